@@ -1,0 +1,199 @@
+/*
+ * turboquant.h — C ABI of libturboquant.so, MI355X (gfx950) build.
+ *
+ * Drop-in replacement for the reference's `extern "C"` surface in
+ * src/tq_capi.cpp.  Every symbol, argument order, struct layout and return
+ * code below is what tq_backend/turboquant_wrapper.py:92-173 binds with
+ * ctypes; each declaration cites the reference entry point it replaces.
+ *
+ * Types are plain C: fp16 buffers are `uint16_t*` (IEEE binary16 bit
+ * patterns; the reference spells them `half*`, which is ABI-identical),
+ * streams are `void*` (a hipStream_t; the reference's cudaStream_t slot;
+ * NULL = the default stream).  All tensor pointers are caller-owned device
+ * memory.  Calls are asynchronous on `stream` unless stated otherwise.
+ *
+ * Return codes (reference src/tq_capi.cpp:9-12):
+ *    0  success
+ *   -1  a required pointer is NULL (checked before anything else)
+ *   -2  invalid configuration or HIP launch/runtime error; the message is in
+ *       the calling thread's buffer returned by tq_last_error()
+ */
+#ifndef TURBOQUANT_H_
+#define TURBOQUANT_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Exported with default visibility; the library builds with
+ * -fvisibility=hidden so only these symbols are public. */
+#if defined(__GNUC__)
+#pragma GCC visibility push(default)
+#endif
+
+/* ---------------------------------------------------------------------- */
+/* Structs: byte-identical to the reference (include/tq_config.h:4-13,      */
+/* include/tq_turbo_prod.cuh:14-27, include/tq_turbo_mse_layout.h:5-15).    */
+/* ---------------------------------------------------------------------- */
+
+/* TQScaleType (include/tq_types.h:8-11) */
+enum { TQ_SCALE_FP16 = 0, TQ_SCALE_FP32 = 1 };
+/* TQQuantMode (include/tq_types.h:13-15) */
+enum { TQ_QUANT_MSE_INT4 = 0 };
+
+typedef struct TQConfig {
+    int block_size;       /* tokens per page (default 16)               */
+    int num_kv_heads;     /* default 8; callers override (e.g. 2)        */
+    int head_dim;         /* D, power of two in [2, 128] (default 128)   */
+    int nbits;            /* default 4                                   */
+    int group_size;       /* default 128                                 */
+    int page_alignment;   /* turbo_mse region alignment (default 256)    */
+    int scale_type;       /* TQ_SCALE_*  (default FP16)                  */
+    int quant_mode;       /* TQ_QUANT_*  (default MSE_INT4)              */
+} TQConfig;
+
+/* turbo_prod page: K nibbles (bits[2:0] = 3-bit code, bit 3 = residual
+ * sign), K residual RMS, K RMS, V nibbles, V RMS; cell c = tib*H + h. */
+typedef struct TQTurboProdPageLayout {
+    size_t page_size_bytes;
+    size_t k4_codes_offset;
+    size_t k_residual_scales_offset;
+    size_t k_scales_offset;
+    size_t v4_codes_offset;
+    size_t v_scales_offset;
+    int k4_bytes_per_token_head;
+    int v4_bytes_per_token_head;
+    int scale_bytes_per_token_head;
+} TQTurboProdPageLayout;
+
+/* turbo_mse page: K codes | V codes | K RMS | V RMS, each region aligned to
+ * cfg.page_alignment. */
+typedef struct TQTurbomsePageLayout {
+    size_t code_bytes_per_token_head;
+    size_t norm_bytes_per_token_head;
+    size_t k_codes_offset;
+    size_t v_codes_offset;
+    size_t k_norms_offset;
+    size_t v_norms_offset;
+    size_t page_size_bytes;
+} TQTurbomsePageLayout;
+
+/* ---------------------------------------------------------------------- */
+/* The reference's 11 entry points                                          */
+/* ---------------------------------------------------------------------- */
+
+/* src/tq_capi.cpp:17 — message of the last failed call on this thread. */
+const char* tq_last_error(void);
+
+/* src/tq_capi.cpp:35 — TQConfig defaults {16, 8, 128, 4, 128, 256, 0, 0}. */
+int tq_make_default_config(TQConfig* out_cfg);
+
+/* src/tq_capi.cpp:41 (factory src/tq_turbo_prod.cpp:7-39). Host only. */
+int tq_make_turbo_prod_layout(const TQConfig* cfg, TQTurboProdPageLayout* out_layout);
+
+/* src/tq_capi.cpp:49 — quantize K,V [num_tokens, H, D] fp16 into the pages
+ * named by slot_mapping[num_tokens] (slot = page*block_size + tib). */
+int tq_launch_turbo_prod_pack_kv(const uint16_t* key, const uint16_t* value,
+                                 const int32_t* slot_mapping, uint8_t* page_pool,
+                                 const TQTurboProdPageLayout* layout, const TQConfig* cfg,
+                                 int num_tokens, void* stream);
+
+/* src/tq_capi.cpp:66 — dequantize to fp16 [num_tokens, H, D]. */
+int tq_launch_turbo_prod_dequant_kv(const uint8_t* page_pool, const int32_t* slot_mapping,
+                                    uint16_t* out_key, uint16_t* out_value,
+                                    const TQTurboProdPageLayout* layout, const TQConfig* cfg,
+                                    int num_tokens, void* stream);
+
+/* src/tq_capi.cpp:82 — logits[num_queries, H, num_kv_tokens] fp32,
+ * query [num_queries, H, D] fp16; logit = <q, k> / sqrt(D). */
+int tq_launch_turbo_prod_fused_attention_logits(const uint16_t* query, const uint8_t* page_pool,
+                                                const int32_t* slot_mapping, float* logits,
+                                                const TQTurboProdPageLayout* layout,
+                                                const TQConfig* cfg, int num_queries,
+                                                int num_kv_tokens, void* stream);
+
+/* src/tq_capi.cpp:99 — softmax(q k^T / sqrt(D)) V over the compressed pages,
+ * output [num_queries, H, D] fp16.  No causal mask (as the reference). */
+int tq_launch_turbo_prod_fused_attention_output(const uint16_t* query, const uint8_t* page_pool,
+                                                const int32_t* slot_mapping, uint16_t* output,
+                                                const TQTurboProdPageLayout* layout,
+                                                const TQConfig* cfg, int num_queries,
+                                                int num_kv_tokens, void* stream);
+
+/* src/tq_capi.cpp:118 (factory src/tq_turbo_mse_layout.cpp:7-28). Host only. */
+int tq_make_turbo_mse_layout(const TQConfig* cfg, TQTurbomsePageLayout* out_layout);
+
+/* src/tq_capi.cpp:126 */
+int tq_launch_turbo_mse_pack_kv(const uint16_t* key, const uint16_t* value,
+                                const int32_t* slot_mapping, uint8_t* page_pool,
+                                const TQTurbomsePageLayout* layout, const TQConfig* cfg,
+                                int num_tokens, void* stream);
+
+/* src/tq_capi.cpp:142 */
+int tq_launch_turbo_mse_dequant_kv(const uint8_t* page_pool, const int32_t* slot_mapping,
+                                   uint16_t* out_key, uint16_t* out_value,
+                                   const TQTurbomsePageLayout* layout, const TQConfig* cfg,
+                                   int num_tokens, void* stream);
+
+/* src/tq_capi.cpp:158 */
+int tq_launch_turbo_mse_fused_attention_output(const uint16_t* query, const uint8_t* page_pool,
+                                               const int32_t* slot_mapping, uint16_t* output,
+                                               const TQTurbomsePageLayout* layout,
+                                               const TQConfig* cfg, int num_queries,
+                                               int num_kv_tokens, void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* Page allocator and block table (host bookkeeping).                       */
+/* Replaces TQAllocator (src/tq_allocator.cpp:5-31, include/tq_allocator.h) */
+/* and TQBlockTable (src/tq_block_table.cpp:4-43), which the reference      */
+/* compiles into the library but never exports; same LIFO semantics.        */
+/* ---------------------------------------------------------------------- */
+
+typedef struct TQAllocator TQAllocator;
+typedef struct TQBlockTable TQBlockTable;
+
+/* TQAllocator::TQAllocator (src/tq_allocator.cpp:5-14): a pool of
+ * num_pages pages of page_size_bytes.  If device_pool is NULL the library
+ * hipMallocs it (and frees it in tq_allocator_destroy); otherwise the
+ * caller's memory is used.  Free list starts [N-1 ... 0] so allocation
+ * order is 0, 1, 2, ... */
+int tq_allocator_create(size_t page_size_bytes, int num_pages, uint8_t* device_pool,
+                        TQAllocator** out);
+int tq_allocator_destroy(TQAllocator* a);
+/* TQAllocator::alloc_block (:22-27): *out_block = page id, or -1 when empty. */
+int tq_allocator_alloc_block(TQAllocator* a, int32_t* out_block);
+/* TQAllocator::free_block (:29-31): pushes the page back (LIFO). */
+int tq_allocator_free_block(TQAllocator* a, int32_t block);
+int tq_allocator_num_free(const TQAllocator* a, int* out_num_free);
+uint8_t* tq_allocator_device_pool(const TQAllocator* a);
+
+/* TQBlockTable (include/tq_block_table.h:9-22) over an allocator. */
+int tq_block_table_create(TQAllocator* a, int block_size, TQBlockTable** out);
+int tq_block_table_destroy(TQBlockTable* t);
+/* TQBlockTable::build_slot_map (src/tq_block_table.cpp:24-39): appends
+ * append_tokens tokens to seq_id, allocating pages on demand, and writes
+ * their slots (phys*block_size + tib) to out_slots.  Out of pages -> -2,
+ * message "out of blocks", and the sequence is left unchanged. */
+int tq_block_table_build_slot_map(TQBlockTable* t, int32_t seq_id, int append_tokens,
+                                  int32_t* out_slots);
+/* SequenceState of seq_id: token count and page ids (copies at most
+ * capacity ids into out_blocks; *out_num_blocks = total). */
+int tq_block_table_num_tokens(const TQBlockTable* t, int32_t seq_id, int* out_num_tokens);
+int tq_block_table_blocks(const TQBlockTable* t, int32_t seq_id, int32_t* out_blocks,
+                          int capacity, int* out_num_blocks);
+/* Releases every page of seq_id back to the allocator (no reference
+ * counterpart: the reference never frees a sequence). */
+int tq_block_table_free_sequence(TQBlockTable* t, int32_t seq_id);
+
+#if defined(__GNUC__)
+#pragma GCC visibility pop
+#endif
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TURBOQUANT_H_ */

@@ -1,0 +1,316 @@
+"""Pins of the CPU oracle against things other than itself (see oracle/oracle.py)."""
+from __future__ import annotations
+
+import subprocess
+
+import numpy as np
+import pytest
+import scipy.linalg
+
+from oracle.oracle import REF_DIR
+
+K3_LITERALS = [-2.1513, -1.34326, -0.755526, -0.244919, 0.244919, 0.755526, 1.34326, 2.1513]
+V4_LITERALS = [-2.7326, -2.0690, -1.6180, -1.2562, -0.9423, -0.6568, -0.3880, -0.1284,
+               0.1284, 0.3880, 0.6568, 0.9423, 1.2562, 1.6180, 2.0690, 2.7326]
+
+
+# ---- fp16 conversion vs numpy (IEEE RNE) -------------------------------------
+
+def test_h2f_all_halves(oracle):
+    h = np.arange(65536, dtype=np.uint16)
+    got = oracle.h2f_array(h)
+    want = h.view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_f2h_matches_numpy(oracle, rng):
+    # random magnitudes over the whole fp16 range and beyond, plus exact ties
+    x = (rng.standard_normal(200_000) * np.exp2(rng.uniform(-30, 18, 200_000))).astype(np.float32)
+    halves = np.arange(65536, dtype=np.uint16).view(np.float16).astype(np.float32)
+    fin = halves[np.isfinite(halves)]
+    mids = ((fin[:-1].astype(np.float64) + fin[1:]) / 2).astype(np.float32)  # ties and near-ties
+    edge = np.array([0.0, -0.0, 65504, 65519.99, 65520, -65520, 1e-8, 2.9802322e-08,
+                     2.9802326e-08, 5.9604645e-08, np.inf, -np.inf, 6.1035156e-05], np.float32)
+    for arr in (x, mids, edge, fin):
+        got = oracle.f2h_array(arr)
+        want = arr.astype(np.float16).view(np.uint16)
+        assert np.array_equal(got, want)
+
+
+# ---- sign flip: the hash equals (-1)^(i+h) -----------------------------------
+
+def test_sign_flip_closed_form(oracle):
+    for h in range(64):
+        for i in range(128):
+            assert oracle.sign_flip(i, h) == (1.0 if (i + h) % 2 == 0 else -1.0)
+
+
+def test_inv_sqrt_d_correctly_rounded(oracle):
+    for k in range(1, 8):
+        D = 1 << k
+        want = np.float32(1.0 / np.sqrt(np.float64(D)))
+        assert np.float32(oracle.inv_sqrt_d(D)) == want
+    assert np.float32(oracle.inv_sqrt_d(128)).view(np.uint32) == 0x3DB504F3
+
+
+# ---- WHT ---------------------------------------------------------------------
+
+@pytest.mark.parametrize("D", [2, 8, 64, 128])
+def test_wht_matches_hadamard_matrix(oracle, rng, D):
+    H = scipy.linalg.hadamard(D).astype(np.float64)
+    assert np.array_equal(H @ H, D * np.eye(D))
+    for _ in range(20):
+        x = rng.standard_normal(D).astype(np.float32) * np.float32(rng.uniform(0.1, 10))
+        got = oracle.wht(x).astype(np.float64)
+        want = H @ x.astype(np.float64)
+        assert np.allclose(got, want, rtol=0, atol=1e-5 * np.abs(x).sum())
+
+
+def test_wht_sign_flip_is_pair_swap(oracle, rng):
+    """WHT(s(., h) * x) = (-1)^h * WHT(x)[j ^ 1], bit for bit: the first
+    butterfly stage of the reference's order turns (x0, -x1) into the swapped
+    pair, and every later stage treats the swap symmetrically."""
+    D = 128
+    for trial in range(50):
+        x = rng.standard_normal(D).astype(np.float32) * np.float32(rng.uniform(1e-3, 1e3))
+        base = oracle.wht(x)
+        for h in (0, 1):
+            s = np.array([oracle.sign_flip(i, h) for i in range(D)], np.float32)
+            got = oracle.wht(x * s)
+            want = base[np.arange(D) ^ 1] * np.float32(1 if h % 2 == 0 else -1)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+# ---- reduction tree order ----------------------------------------------------
+
+def _halving_tree_numpy(r):
+    r = np.array(r, np.float32)
+    s = r.size // 2
+    while s:
+        r[:s] = r[:s] + r[s:2 * s]
+        s //= 2
+    return r[0]
+
+
+def test_tree_sum_is_halving_tree(oracle, rng):
+    # values spanning 2^40 so summation order changes the float32 result
+    diffs_seq = diffs_adj = 0
+    for _ in range(200):
+        r = (rng.standard_normal(128) * np.exp2(rng.integers(-20, 20, 128))).astype(np.float32)
+        got = np.float32(oracle.tree_sum(r))
+        assert got == _halving_tree_numpy(r)
+        seq = np.float32(0)
+        for v in r:
+            seq = np.float32(seq + v)
+        adj = r.copy()
+        while adj.size > 1:
+            adj = (adj[0::2] + adj[1::2]).astype(np.float32)
+        diffs_seq += got != seq
+        diffs_adj += got != adj[0]
+    # the inputs do discriminate between orders
+    assert diffs_seq > 50 and diffs_adj > 50
+
+
+# ---- nearest code --------------------------------------------------------------
+
+def test_nearest_codes_brute_force(oracle, rng):
+    k3 = oracle.k3
+    v4 = oracle.v4
+    assert np.array_equal(k3, np.array(K3_LITERALS, np.float32))
+    assert np.array_equal(v4, np.array(V4_LITERALS, np.float32))
+    x = np.concatenate([rng.uniform(-3.5, 3.5, 4000).astype(np.float32),
+                        ((k3[:-1] + k3[1:]) / 2).astype(np.float32),   # K3 decision ties
+                        ((v4[:-1] + v4[1:]) / 2).astype(np.float32),   # V4 decision ties
+                        np.float32([0.0, -0.0, 2.5, -2.5, 2.75, -2.75])])
+    for xi in x:
+        dk = np.abs(np.float32(xi) - k3)       # float32 distances like the kernel
+        dv = np.abs(np.float32(xi) - v4)
+        assert oracle.nearest_k3(xi) == int(np.argmin(dk))  # argmin = first minimum
+        assert oracle.nearest_v4(xi) == int(np.argmin(dv))
+
+
+# ---- codebook provenance --------------------------------------------------------
+
+def test_k3_from_reference_lloyd_max_binary(oracle):
+    exe = REF_DIR / "gaussian_codebook"
+    if not exe.exists():
+        pytest.skip("oracle/_ref not built (reference tree absent)")
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout
+    levels = [float(v) for v in out.split("levels:")[1].split("thresholds:")[0].split()]
+    assert levels == K3_LITERALS              # the reference program prints the literals
+    mine, _ = oracle.lloyd_max(8)             # this oracle's restatement of the program
+    assert np.allclose(mine, levels, atol=5e-6)
+
+
+def test_v4_is_converged_16_level_lloyd_max(oracle):
+    levels, _ = oracle.lloyd_max(16, max_iter=200_000, tol=1e-15)
+    assert np.abs(levels - np.array(V4_LITERALS)).max() < 1.5e-4
+
+
+# ---- layouts ---------------------------------------------------------------------
+
+def test_prod_layout_closed_form_and_readme_vram(oracle):
+    L = oracle.prod_layout(16, 2, 128)
+    assert (L.k4_off, L.kres_off, L.ks_off, L.v4_off, L.vs_off, L.page_size) == \
+        (0, 2048, 2112, 2176, 4224, 4288)
+    mse = oracle.mse_layout(16, 2, 128)
+    assert (mse.k_codes_off, mse.v_codes_off, mse.k_norms_off, mse.v_norms_off, mse.page_size) \
+        == (0, 2048, 4096, 4352, 4608)
+    # README.md:53-55 / 70-72: 302 / 324 MB at 32K x 36 layers, 75 / 81 MB at 8K x 36
+    for tokens, prod_mb, mse_mb in ((32768, 302, 324), (8192, 75, 81)):
+        pages = tokens // 16
+        assert round(pages * L.page_size * 36 / 1e6) == prod_mb or \
+            round(pages * L.page_size * 36 / 2**20) == prod_mb
+        assert round(pages * mse.page_size * 36 / 1e6) == mse_mb or \
+            round(pages * mse.page_size * 36 / 2**20) == mse_mb
+
+
+def test_mse_layout_matches_reference_factory(oracle):
+    exe = REF_DIR / "ref_layouts"
+    if not exe.exists():
+        pytest.skip("oracle/_ref not built (reference tree absent)")
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout
+    n = 0
+    for line in out.strip().splitlines():
+        head, mse, _legacy = line.split("|")
+        B, H, D, nbits, al = map(int, head.split())
+        ref = list(map(int, mse.split()))
+        L = oracle.mse_layout(B, H, D, nbits, al)
+        assert [L.code_bytes, L.norm_bytes, L.k_codes_off, L.v_codes_off, L.k_norms_off,
+                L.v_norms_off, L.page_size] == ref, line
+        n += 1
+    assert n == 144
+
+
+# ---- pack / dequant statistics and invariants -----------------------------------
+
+def _rel_mse(x, y):
+    x = x.astype(np.float64)
+    y = y.astype(np.float64)
+    return np.mean((x - y) ** 2) / (np.var(x) + 1e-8)
+
+
+@pytest.mark.parametrize("scheme,tol", [("turbo_prod", 0.35), ("turbo_mse", 0.25)])
+def test_roundtrip_relative_mse(oracle, scheme, tol):
+    """The reference's own round-trip bound (tests/test_cag.py:212-246)."""
+    from turborag_amd.synthetic import as_u16, kv_tokens_major
+    k, v = kv_tokens_major(256, 2, 128, seed=11)
+    k16, v16 = as_u16(k), as_u16(v)
+    slots = np.arange(256, dtype=np.int32)
+    if scheme == "turbo_prod":
+        pool = oracle.prod_pack(k16, v16, slots, num_pages=16)
+        ok, ov = oracle.prod_dequant(pool, slots, 2, 128)
+    else:
+        pool = oracle.mse_pack(k16, v16, slots, num_pages=16)
+        ok, ov = oracle.mse_dequant(pool, slots, 2, 128)
+    kf = k16.view(np.float16).astype(np.float32)
+    vf = v16.view(np.float16).astype(np.float32)
+    rk = _rel_mse(kf, ok.view(np.float16).astype(np.float32))
+    rv = _rel_mse(vf, ov.view(np.float16).astype(np.float32))
+    assert rk < tol and rv < tol
+    # and the codec is far better than the bound (4-bit Gaussian quantizer ~1e-2)
+    assert rk < 0.05 and rv < 0.05
+
+
+def test_dequant_is_scaled_hadamard_of_decoded(oracle, rng):
+    """dequant = fp16(s * H(decoded) / sqrt(D)): check against a float64 matrix
+    product (differences only from fp32 rounding inside the butterfly)."""
+    from turborag_amd.synthetic import as_u16, kv_tokens_major
+    D, H = 128, 2
+    k, v = kv_tokens_major(16, H, D, seed=5)
+    slots = np.arange(16, dtype=np.int32)
+    pool = oracle.prod_pack(as_u16(k), as_u16(v), slots, num_pages=1)
+    ok, _ = oracle.prod_dequant(pool, slots, H, D)
+    L = oracle.prod_layout(16, H, D)
+    Hm = scipy.linalg.hadamard(D).astype(np.float64)
+    k3 = oracle.k3.astype(np.float64)
+    for t in range(16):
+        for h in range(H):
+            c = t * H + h
+            nib = pool[L.k4_off + c * 64: L.k4_off + c * 64 + 64]
+            codes = np.stack([nib & 0xF, nib >> 4], 1).reshape(-1)
+            ks = np.float64(pool[L.ks_off + 2 * c: L.ks_off + 2 * c + 2].view(np.float16)[0])
+            re = np.float64(pool[L.kres_off + 2 * c: L.kres_off + 2 * c + 2].view(np.float16)[0])
+            y = (k3[codes & 7] + re * np.where(codes & 8, 1.0, -1.0)) * ks
+            s = np.array([1.0 if (i + h) % 2 == 0 else -1.0 for i in range(D)])
+            want = s * (Hm @ y) / np.sqrt(D)
+            got = ok[t, h].view(np.float16).astype(np.float64)
+            assert np.allclose(got, want, rtol=2e-3, atol=1e-3 * np.abs(want).max())
+
+
+def test_mse_pack_idempotent_away_from_boundaries(oracle):
+    """pack(dequant(pack(x))) reproduces the code bytes of pack(x) almost
+    everywhere (quantize -> dequantize -> quantize is a projection up to fp16
+    rounding and the re-derived RMS)."""
+    from turborag_amd.synthetic import as_u16, kv_tokens_major
+    k, v = kv_tokens_major(64, 2, 128, seed=3)
+    slots = np.arange(64, dtype=np.int32)
+    p1 = oracle.mse_pack(as_u16(k), as_u16(v), slots, num_pages=4)
+    ok, ov = oracle.mse_dequant(p1, slots, 2, 128)
+    p2 = oracle.mse_pack(ok, ov, slots, num_pages=4)
+    L = oracle.mse_layout(16, 2, 128)
+    c1 = p1.reshape(4, -1)[:, :L.k_norms_off]
+    c2 = p2.reshape(4, -1)[:, :L.k_norms_off]
+    assert np.mean(c1 == c2) > 0.9
+
+
+def test_boundary_counts_small(oracle):
+    from turborag_amd.synthetic import as_u16, kv_tokens_major
+    k, v = kv_tokens_major(512, 2, 128, seed=9)
+    kc, ks, vc = oracle.boundary_counts("turbo_prod", as_u16(k), as_u16(v))
+    total = 512 * 2 * 128
+    assert kc / total < 1e-3 and ks / total < 1e-3 and vc / total < 1e-3
+    norm_rows, code_diff, mc = oracle.boundary_counts("turbo_mse", as_u16(k), as_u16(v))
+    assert code_diff / total < 1e-3 and mc / total < 1e-3
+
+
+# ---- attention oracles ----------------------------------------------------------
+
+@pytest.mark.parametrize("scheme", ["turbo_prod", "turbo_mse"])
+def test_attention_f64_vs_sdpa_over_dequant(oracle, scheme):
+    """fp64 rotated-domain attention over the codes == SDPA
+    (src/tq_attention_ref.cpp semantics) over the dequantized fp16 K/V, up to
+    the fp16 rounding of the dequantized values.  That rounding alone moves
+    the output by ~1e-3 relative on this outlier-heavy data (measured 1.06e-3
+    max), so the SDPA cross-check uses 3e-3; the 1e-3 gate applies against
+    the exact oracle (the reference's fp32 algorithm passes it, below)."""
+    from turborag_amd.synthetic import as_u16, gqa_rows, kv_tokens_major, permuted_slots, query
+    N, H, D = 700, 2, 128
+    k, v = kv_tokens_major(N, H, D, seed=21)
+    slots = permuted_slots(N, 16, seed=22).numpy()
+    pages = int(slots.max()) // 16 + 1
+    q = as_u16(gqa_rows(query(16, D, seed=23), H))  # [8, 2, 128]
+    if scheme == "turbo_prod":
+        pool = oracle.prod_pack(as_u16(k), as_u16(v), slots, num_pages=pages)
+        ok, ov = oracle.prod_dequant(pool, slots, H, D)
+        out = oracle.prod_attention_f64(q, pool, slots)
+        ref32 = oracle.prod_attention_f32(q, pool, slots)
+    else:
+        pool = oracle.mse_pack(as_u16(k), as_u16(v), slots, num_pages=pages)
+        ok, ov = oracle.mse_dequant(pool, slots, H, D)
+        out = oracle.mse_attention_f64(q, pool, slots)
+        ref32 = oracle.mse_attention_f32(q, pool, slots)
+    for qi in range(q.shape[0]):
+        for h in range(H):
+            sd = oracle.sdpa_single_head(q[qi, h], ok[:, h].copy(), ov[:, h].copy())
+            o = out[qi, h]
+            err = np.abs(o - sd).max() / np.abs(o).max()
+            assert err < 3e-3, (qi, h, err)
+            r32 = ref32[qi, h].view(np.float16).astype(np.float64)
+            assert np.abs(r32 - o).max() / np.abs(o).max() < 1e-3
+
+
+def test_attention_single_token_is_value(oracle):
+    """With one kv token the softmax weight is exactly 1: the output equals the
+    dequantized V row (up to fp16 rounding of the latter)."""
+    from turborag_amd.synthetic import as_u16, kv_tokens_major
+    k, v = kv_tokens_major(1, 2, 128, seed=4)
+    slots = np.array([5], np.int32)
+    pool = oracle.prod_pack(as_u16(k), as_u16(v), slots, num_pages=1)
+    _, ov = oracle.prod_dequant(pool, slots, 2, 128)
+    q = as_u16(kv_tokens_major(1, 2, 128, seed=8)[0])
+    out = oracle.prod_attention_f64(q, pool, slots)
+    want = ov[0].view(np.float16).astype(np.float64)
+    assert np.allclose(out[0], want, rtol=1e-3, atol=1e-3)

@@ -1,0 +1,315 @@
+// tq_capi.cpp — the extern "C" surface of libturboquant.so (include/turboquant.h).
+//
+// Mirrors src/tq_capi.cpp of the reference: NULL pointers -> -1 before any
+// other check; any tq::Error / std::exception from validation or a launch ->
+// -2 with the message in a thread-local 512-byte buffer (TQ_KERNEL_CALL,
+// src/tq_capi.cpp:14-33).  Exceptions never cross the ABI.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <new>
+#include <utility>
+#include <vector>
+
+#include "tq_internal.h"
+
+namespace {
+
+thread_local char g_last_error[512] = "";
+
+void set_error(const char* msg) { std::snprintf(g_last_error, sizeof(g_last_error), "%.511s", msg); }
+
+template <class F>
+int guarded(F&& f) {
+    try {
+        f();
+        return 0;
+    } catch (const std::exception& e) {
+        set_error(e.what());
+        return -2;
+    } catch (...) {
+        set_error("unknown error");
+        return -2;
+    }
+}
+
+size_t align_up(size_t x, size_t a) { return ((x + a - 1) / a) * a; }
+
+bool is_pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
+
+int log2i(int x) {
+    int k = 0;
+    while ((1 << k) < x) ++k;
+    return k;
+}
+
+void check_common(const TQConfig& cfg, const char* scheme) {
+    // Same message as the reference's launchers for the limit it checks
+    // (tq_turbo_prod_kernels.cu:595, tq_turbo_mse_kernels.cu:431).
+    if (cfg.head_dim > 128)
+        throw tq::Error(std::string(scheme) + ": head_dim > 128 is not supported");
+    if (!is_pow2(cfg.head_dim) || cfg.head_dim < 2)
+        throw tq::Error(std::string(scheme) + ": head_dim must be a power of two in [2, 128]");
+    if (cfg.num_kv_heads <= 0) throw tq::Error(std::string(scheme) + ": num_kv_heads must be > 0");
+    if (cfg.block_size <= 0) throw tq::Error(std::string(scheme) + ": block_size must be > 0");
+}
+
+// Counts that the reference launches as grid dimensions: zero or negative
+// gives "invalid configuration argument" from the CUDA launch check (turbo_prod
+// only — its turbo_mse launchers do not check), preserved here.
+void check_grid(int n, const char* what, bool prod) {
+    if (n < 0 || (n == 0 && prod))
+        throw tq::Error(std::string(what) + ": invalid configuration argument");
+}
+
+}  // namespace
+
+namespace tq {
+
+void set_last_error(const char* msg) { set_error(msg); }
+
+float inv_sqrt_d(int D) {
+    const int k = log2i(D);
+    if ((k & 1) == 0) return std::ldexp(1.0f, -k / 2);
+    return std::ldexp(0x1.6a09e6p-1f, -(k - 1) / 2);  // RN(1/sqrt(2)) * 2^-((k-1)/2)
+}
+
+void check_launch(const char* what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) throw Error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+PageGeom prod_geom(const TQConfig& cfg, const TQTurboProdPageLayout& l) {
+    check_common(cfg, "turbo_prod");
+    const int half = cfg.head_dim / 2;
+    if (l.k4_bytes_per_token_head != half || l.v4_bytes_per_token_head != half ||
+        l.scale_bytes_per_token_head != 2)
+        throw Error("turbo_prod: layout does not match head_dim (use tq_make_turbo_prod_layout)");
+    PageGeom g{};
+    g.page_size = l.page_size_bytes;
+    g.kc_off = l.k4_codes_offset;
+    g.vc_off = l.v4_codes_offset;
+    g.ks_off = l.k_scales_offset;
+    g.kres_off = l.k_residual_scales_offset;
+    g.vs_off = l.v_scales_offset;
+    g.code_stride = half;
+    g.scale_stride = 2;
+    g.H = cfg.num_kv_heads;
+    g.D = cfg.head_dim;
+    g.block_size = cfg.block_size;
+    g.bs_shift = is_pow2(cfg.block_size) ? log2i(cfg.block_size) : -1;
+    return g;
+}
+
+PageGeom mse_geom(const TQConfig& cfg, const TQTurbomsePageLayout& l) {
+    check_common(cfg, "turbo_mse");
+    const int half = cfg.head_dim / 2;
+    if (l.code_bytes_per_token_head != (size_t)half || l.norm_bytes_per_token_head != 2)
+        throw Error("turbo_mse: layout does not match head_dim/nbits=4 (use tq_make_turbo_mse_layout)");
+    PageGeom g{};
+    g.page_size = l.page_size_bytes;
+    g.kc_off = l.k_codes_offset;
+    g.vc_off = l.v_codes_offset;
+    g.ks_off = l.k_norms_offset;
+    g.kres_off = 0;
+    g.vs_off = l.v_norms_offset;
+    g.code_stride = half;
+    g.scale_stride = 2;
+    g.H = cfg.num_kv_heads;
+    g.D = cfg.head_dim;
+    g.block_size = cfg.block_size;
+    g.bs_shift = is_pow2(cfg.block_size) ? log2i(cfg.block_size) : -1;
+    return g;
+}
+
+void* workspace(hipStream_t stream, size_t bytes) {
+    // One buffer per (device, stream): calls on one stream are ordered, so
+    // reuse is safe; outgrown buffers are kept (a kernel may still use them).
+    static std::mutex mu;
+    struct Buf { void* p; size_t n; };
+    static std::map<std::pair<int, hipStream_t>, Buf> bufs;
+    static std::vector<void*> retired;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) throw Error("hipGetDevice failed");
+    std::lock_guard<std::mutex> lock(mu);
+    Buf& b = bufs[{dev, stream}];
+    if (b.n >= bytes && b.p) return b.p;
+    size_t n = std::max<size_t>(bytes, 1 << 20);
+    n = std::max(n, b.n * 2);
+    void* p = nullptr;
+    if (hipMalloc(&p, n) != hipSuccess) {
+        (void)hipGetLastError();
+        throw Error("workspace hipMalloc failed");
+    }
+    if (b.p) retired.push_back(b.p);
+    b.p = p;
+    b.n = n;
+    return p;
+}
+
+}  // namespace tq
+
+// ---------------------------------------------------------------------------
+// Config and layouts (host only)
+// ---------------------------------------------------------------------------
+
+extern "C" const char* tq_last_error(void) { return g_last_error; }
+
+extern "C" int tq_make_default_config(TQConfig* out) {
+    if (!out) return -1;
+    *out = TQConfig{16, 8, 128, 4, 128, 256, TQ_SCALE_FP16, TQ_QUANT_MSE_INT4};
+    return 0;
+}
+
+// src/tq_turbo_prod.cpp:7-39
+extern "C" int tq_make_turbo_prod_layout(const TQConfig* cfg, TQTurboProdPageLayout* out) {
+    if (!cfg || !out) return -1;
+    TQTurboProdPageLayout l{};
+    l.k4_bytes_per_token_head = (cfg->head_dim + 1) / 2;
+    l.v4_bytes_per_token_head = (cfg->head_dim * 4 + 7) / 8;
+    l.scale_bytes_per_token_head = 2;
+    const size_t th = (size_t)cfg->block_size * (size_t)cfg->num_kv_heads;
+    size_t cur = 0;
+    l.k4_codes_offset = cur;
+    cur += th * (size_t)l.k4_bytes_per_token_head;
+    cur = align_up(cur, 2);
+    l.k_residual_scales_offset = cur;
+    cur += th * 2;
+    l.k_scales_offset = cur;
+    cur += th * 2;
+    l.v4_codes_offset = cur;
+    cur += th * (size_t)l.v4_bytes_per_token_head;
+    cur = align_up(cur, 2);
+    l.v_scales_offset = cur;
+    cur += th * 2;
+    l.page_size_bytes = align_up(cur, 2);
+    *out = l;
+    return 0;
+}
+
+// src/tq_turbo_mse_layout.cpp:7-28
+extern "C" int tq_make_turbo_mse_layout(const TQConfig* cfg, TQTurbomsePageLayout* out) {
+    if (!cfg || !out) return -1;
+    TQTurbomsePageLayout l{};
+    l.code_bytes_per_token_head = (size_t)((cfg->head_dim * cfg->nbits + 7) / 8);
+    l.norm_bytes_per_token_head = 2;
+    const size_t th = (size_t)cfg->block_size * (size_t)cfg->num_kv_heads;
+    const size_t a = (size_t)cfg->page_alignment;
+    l.k_codes_offset = 0;
+    l.v_codes_offset = align_up(l.k_codes_offset + th * l.code_bytes_per_token_head, a);
+    l.k_norms_offset = align_up(l.v_codes_offset + th * l.code_bytes_per_token_head, a);
+    l.v_norms_offset = align_up(l.k_norms_offset + th * l.norm_bytes_per_token_head, a);
+    l.page_size_bytes = align_up(l.v_norms_offset + th * l.norm_bytes_per_token_head, a);
+    *out = l;
+    return 0;
+}
+
+// ---------------------------------------------------------------------------
+// turbo_prod
+// ---------------------------------------------------------------------------
+
+extern "C" int tq_launch_turbo_prod_pack_kv(const uint16_t* key, const uint16_t* value,
+                                            const int32_t* slot_mapping, uint8_t* page_pool,
+                                            const TQTurboProdPageLayout* layout,
+                                            const TQConfig* cfg, int num_tokens, void* stream) {
+    if (!key || !value || !slot_mapping || !page_pool || !layout || !cfg) return -1;
+    return guarded([&] {
+        const tq::PageGeom g = tq::prod_geom(*cfg, *layout);
+        check_grid(num_tokens, "turbo_prod_pack_kv_kernel", true);
+        tq::launch_pack(tq::Scheme::Prod, key, value, slot_mapping, page_pool, g, num_tokens,
+                        static_cast<hipStream_t>(stream));
+    });
+}
+
+extern "C" int tq_launch_turbo_prod_dequant_kv(const uint8_t* page_pool,
+                                               const int32_t* slot_mapping, uint16_t* out_key,
+                                               uint16_t* out_value,
+                                               const TQTurboProdPageLayout* layout,
+                                               const TQConfig* cfg, int num_tokens,
+                                               void* stream) {
+    if (!page_pool || !slot_mapping || !out_key || !out_value || !layout || !cfg) return -1;
+    return guarded([&] {
+        const tq::PageGeom g = tq::prod_geom(*cfg, *layout);
+        check_grid(num_tokens, "turbo_prod_dequant_kv_kernel", true);
+        tq::launch_dequant(tq::Scheme::Prod, page_pool, slot_mapping, out_key, out_value, g,
+                           num_tokens, static_cast<hipStream_t>(stream));
+    });
+}
+
+extern "C" int tq_launch_turbo_prod_fused_attention_logits(
+    const uint16_t* query, const uint8_t* page_pool, const int32_t* slot_mapping, float* logits,
+    const TQTurboProdPageLayout* layout, const TQConfig* cfg, int num_queries, int num_kv_tokens,
+    void* stream) {
+    if (!query || !page_pool || !slot_mapping || !logits || !layout || !cfg) return -1;
+    return guarded([&] {
+        const tq::PageGeom g = tq::prod_geom(*cfg, *layout);
+        check_grid(num_queries, "turbo_prod_fused_attention_logits_kernel", true);
+        if (num_kv_tokens < 0) throw tq::Error("turbo_prod logits: num_kv_tokens < 0");
+        tq::launch_logits(query, page_pool, slot_mapping, logits, g, num_queries, num_kv_tokens,
+                          static_cast<hipStream_t>(stream));
+    });
+}
+
+extern "C" int tq_launch_turbo_prod_fused_attention_output(
+    const uint16_t* query, const uint8_t* page_pool, const int32_t* slot_mapping,
+    uint16_t* output, const TQTurboProdPageLayout* layout, const TQConfig* cfg, int num_queries,
+    int num_kv_tokens, void* stream) {
+    if (!query || !page_pool || !slot_mapping || !output || !layout || !cfg) return -1;
+    return guarded([&] {
+        const tq::PageGeom g = tq::prod_geom(*cfg, *layout);
+        check_grid(num_queries, "turbo_prod_fused_attn_online_kernel", true);
+        if (num_kv_tokens < 0) throw tq::Error("turbo_prod attention: num_kv_tokens < 0");
+        tq::launch_attention(tq::Scheme::Prod, query, page_pool, slot_mapping, output, g,
+                             num_queries, num_kv_tokens, static_cast<hipStream_t>(stream));
+    });
+}
+
+// ---------------------------------------------------------------------------
+// turbo_mse
+// ---------------------------------------------------------------------------
+
+extern "C" int tq_launch_turbo_mse_pack_kv(const uint16_t* key, const uint16_t* value,
+                                           const int32_t* slot_mapping, uint8_t* page_pool,
+                                           const TQTurbomsePageLayout* layout,
+                                           const TQConfig* cfg, int num_tokens, void* stream) {
+    if (!key || !value || !slot_mapping || !page_pool || !layout || !cfg) return -1;
+    return guarded([&] {
+        const tq::PageGeom g = tq::mse_geom(*cfg, *layout);
+        check_grid(num_tokens, "turbo_mse_pack_kv_kernel", false);
+        tq::launch_pack(tq::Scheme::Mse, key, value, slot_mapping, page_pool, g, num_tokens,
+                        static_cast<hipStream_t>(stream));
+    });
+}
+
+extern "C" int tq_launch_turbo_mse_dequant_kv(const uint8_t* page_pool,
+                                              const int32_t* slot_mapping, uint16_t* out_key,
+                                              uint16_t* out_value,
+                                              const TQTurbomsePageLayout* layout,
+                                              const TQConfig* cfg, int num_tokens, void* stream) {
+    if (!page_pool || !slot_mapping || !out_key || !out_value || !layout || !cfg) return -1;
+    return guarded([&] {
+        const tq::PageGeom g = tq::mse_geom(*cfg, *layout);
+        check_grid(num_tokens, "turbo_mse_dequant_kv_kernel", false);
+        tq::launch_dequant(tq::Scheme::Mse, page_pool, slot_mapping, out_key, out_value, g,
+                           num_tokens, static_cast<hipStream_t>(stream));
+    });
+}
+
+extern "C" int tq_launch_turbo_mse_fused_attention_output(
+    const uint16_t* query, const uint8_t* page_pool, const int32_t* slot_mapping,
+    uint16_t* output, const TQTurbomsePageLayout* layout, const TQConfig* cfg, int num_queries,
+    int num_kv_tokens, void* stream) {
+    if (!query || !page_pool || !slot_mapping || !output || !layout || !cfg) return -1;
+    return guarded([&] {
+        const tq::PageGeom g = tq::mse_geom(*cfg, *layout);
+        check_grid(num_queries, "turbo_mse_fused_attn_online_kernel", false);
+        if (num_kv_tokens < 0) throw tq::Error("turbo_mse attention: num_kv_tokens < 0");
+        tq::launch_attention(tq::Scheme::Mse, query, page_pool, slot_mapping, output, g,
+                             num_queries, num_kv_tokens, static_cast<hipStream_t>(stream));
+    });
+}

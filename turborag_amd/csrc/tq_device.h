@@ -1,0 +1,146 @@
+// tq_device.h — device-side building blocks for the gfx950 kernels.
+//
+// Row convention: one (token, head) vector of D fp32 values ("row") is held by
+// D/2 consecutive lanes of a wave64, lane j owning elements 2j and 2j+1.  With
+// that assignment the reference's butterfly (len = 1 first, then 2, 4, ...)
+// is: stage 1 in registers, stage len >= 2 an xor-exchange with lane
+// j ^ (len/2); and the reference's shared-memory halving tree
+// r[i] += r[i + s] is an xor-butterfly over lanes followed by r0 + r1.  Both
+// reproduce the reference's float operation order exactly, so results are
+// bit-identical to it (fp32 add is commutative; every lane of an xor pair
+// computes the same sum).
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "tq_internal.h"
+
+namespace tq {
+namespace dev {
+
+// Codebooks: src/cuda/tq_turbo_prod_kernels.cu:26-37 (K3 3-bit Lloyd-Max,
+// V4 4-bit) and src/cuda/tq_turbo_mse_kernels.cu:24-29 (turbo_mse = V4).
+__device__ constexpr float kK3[8] = {-2.1513f, -1.34326f, -0.755526f, -0.244919f,
+                                     0.244919f, 0.755526f, 1.34326f,  2.1513f};
+__device__ constexpr float kV4[16] = {-2.7326f, -2.0690f, -1.6180f, -1.2562f,
+                                      -0.9423f, -0.6568f, -0.3880f, -0.1284f,
+                                      0.1284f,  0.3880f,  0.6568f,  0.9423f,
+                                      1.2562f,  1.6180f,  2.0690f,  2.7326f};
+
+constexpr float kMinRMS = 1e-8f;  // include/tq_shared_device.cuh:9
+
+__device__ __forceinline__ float h2f(uint16_t h) {
+    return __half2float(__ushort_as_half(h));
+}
+__device__ __forceinline__ uint16_t f2h(float f) {  // RNE (v_cvt_f16_f32)
+    return __half_as_ushort(__float2half(f));
+}
+
+// The reference's sign_flip(i, h) (tq_turbo_prod_kernels.cu:19-23) has bit 0
+// of ((h*2654435761) ^ (i*1103515245 + 12345)) = 1 ^ ((i ^ h) & 1), i.e. it
+// is exactly (-1)^(i+h).
+__device__ __forceinline__ float sign_of(int i, int h) { return ((i ^ h) & 1) ? -1.0f : 1.0f; }
+
+__device__ __forceinline__ float clamp_ref(float x, float lo, float hi) {
+    return x < lo ? lo : (x > hi ? hi : x);
+}
+
+__device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
+
+// In-place WHT of a row held two-per-lane (lane index j within its row).
+template <int L>
+__device__ __forceinline__ void wht_pair(float& x0, float& x1, int j) {
+    const float a = x0 + x1, b = x0 - x1;
+    x0 = a;
+    x1 = b;
+#pragma unroll
+    for (int m = 1; m < L; m <<= 1) {
+        const float p0 = shfl_xor(x0, m), p1 = shfl_xor(x1, m);
+        const bool lower = (j & m) == 0;
+        x0 = lower ? x0 + p0 : p0 - x0;
+        x1 = lower ? x1 + p1 : p1 - x1;
+    }
+}
+
+// Halving tree over the row (strides D/2 ... 1); every lane gets r[0].
+template <int L>
+__device__ __forceinline__ float tree_pair(float r0, float r1) {
+#pragma unroll
+    for (int m = L / 2; m >= 1; m >>= 1) {
+        r0 += shfl_xor(r0, m);
+        r1 += shfl_xor(r1, m);
+    }
+    return r0 + r1;
+}
+
+// Halving tree over one value per lane (the turbo_mse pair sums).
+template <int L>
+__device__ __forceinline__ float tree_one(float r) {
+#pragma unroll
+    for (int m = L / 2; m >= 1; m >>= 1) r += shfl_xor(r, m);
+    return r;
+}
+
+template <int L>
+__device__ __forceinline__ float sum_lanes(float r) {
+    return tree_one<L>(r);
+}
+
+template <int L>
+__device__ __forceinline__ float max_lanes(float r) {
+#pragma unroll
+    for (int m = L / 2; m >= 1; m >>= 1) r = fmaxf(r, shfl_xor(r, m));
+    return r;
+}
+
+// nearest_k3_idx / nearest_v4_idx (:39-59): first minimum of fp32 |x - c|.
+__device__ __forceinline__ int nearest_k3(float x, float& level) {
+    int best = 0;
+    float bd = fabsf(x - kK3[0]);
+    level = kK3[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) {
+        const float d = fabsf(x - kK3[i]);
+        if (d < bd) {
+            bd = d;
+            best = i;
+            level = kK3[i];
+        }
+    }
+    return best;
+}
+
+__device__ __forceinline__ int nearest_v4(float x) {
+    int best = 0;
+    float bd = fabsf(x - kV4[0]);
+#pragma unroll
+    for (int i = 1; i < 16; ++i) {
+        const float d = fabsf(x - kV4[i]);
+        if (d < bd) {
+            bd = d;
+            best = i;
+        }
+    }
+    return best;
+}
+
+// slot -> (page, token-in-block).
+__device__ __forceinline__ void split_slot(int slot, const PageGeom& g, int& page, int& tib) {
+    if (g.bs_shift >= 0) {
+        page = slot >> g.bs_shift;
+        tib = slot & ((1 << g.bs_shift) - 1);
+    } else {
+        page = slot / g.block_size;
+        tib = slot % g.block_size;
+    }
+}
+
+__device__ __forceinline__ uint16_t ld_u16(const uint8_t* p) {
+    return *reinterpret_cast<const uint16_t*>(p);
+}
+
+}  // namespace dev
+}  // namespace tq

@@ -1,0 +1,68 @@
+// tq_internal.h — host-side declarations shared by the C ABI and the HIP
+// kernel files of libturboquant.so (gfx950).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+#include "turboquant.h"
+
+namespace tq {
+
+// Error raised by launchers; the C ABI converts it to rc -2 and stores the
+// message for tq_last_error() (the reference's TQ_KERNEL_CALL,
+// src/tq_capi.cpp:25-33).
+struct Error : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+// Stores msg in the calling thread's tq_last_error() buffer.
+void set_last_error(const char* msg);
+
+// Byte geometry of one page, resolved from a TQTurboProdPageLayout or a
+// TQTurbomsePageLayout.  Passed to kernels by value.
+//   cell c = tib * H + h;  K codes at kc_off + c*code_stride, V codes at
+//   vc_off + c*code_stride, scales at {ks,kres,vs}_off + c*scale_stride.
+struct PageGeom {
+    uint64_t page_size;
+    uint64_t kc_off, vc_off;
+    uint64_t ks_off, kres_off, vs_off;  // kres_off unused by turbo_mse
+    int code_stride;
+    int scale_stride;
+    int H, D, block_size;
+    int bs_shift;  // log2(block_size) when block_size is a power of two, else -1
+};
+
+enum class Scheme : int { Prod = 0, Mse = 1 };
+
+// Validates cfg/layout and resolves the geometry (throws tq::Error).
+PageGeom prod_geom(const TQConfig& cfg, const TQTurboProdPageLayout& layout);
+PageGeom mse_geom(const TQConfig& cfg, const TQTurbomsePageLayout& layout);
+
+// RN(1/sqrt(D)) for D a power of two.
+float inv_sqrt_d(int D);
+
+// Throws tq::Error("<what>: <hip error string>") if the last launch failed
+// (the reference's TQ_CHECK_LAUNCH, include/tq_cuda_check.h:18-24).
+void check_launch(const char* what);
+
+// Per-(device, stream) scratch for split-K partials; grows, never shrinks.
+void* workspace(hipStream_t stream, size_t bytes);
+
+// ---- launchers (tq_prod.hip, tq_mse.hip, tq_attention.hip) ---------------
+void launch_pack(Scheme s, const uint16_t* key, const uint16_t* value, const int32_t* slots,
+                 uint8_t* pool, const PageGeom& g, int num_tokens, hipStream_t stream);
+void launch_dequant(Scheme s, const uint8_t* pool, const int32_t* slots, uint16_t* out_key,
+                    uint16_t* out_value, const PageGeom& g, int num_tokens, hipStream_t stream);
+void launch_logits(const uint16_t* query, const uint8_t* pool, const int32_t* slots,
+                   float* logits, const PageGeom& g, int num_queries, int num_kv_tokens,
+                   hipStream_t stream);
+void launch_attention(Scheme s, const uint16_t* query, const uint8_t* pool, const int32_t* slots,
+                      uint16_t* output, const PageGeom& g, int num_queries, int num_kv_tokens,
+                      hipStream_t stream);
+
+}  // namespace tq
