@@ -35,7 +35,12 @@ constexpr float kMinRMS = 1e-8f;  // include/tq_shared_device.cuh:9
 __device__ __forceinline__ float h2f(uint16_t h) {
     return __half2float(__ushort_as_half(h));
 }
-__device__ __forceinline__ uint16_t f2h(float f) {  // RNE (v_cvt_f16_f32)
+// fp32 -> fp16, RNE (v_cvt_f16_f32).  The empty asm pins f as a rounded fp32
+// register value: without it the backend folds fp16(a * b) into
+// v_fma_mixlo_f16(a, b, 0), which rounds a*b once to fp16 (not fp32 then
+// fp16, as the reference does) and turns a -0 product into +0.
+__device__ __forceinline__ uint16_t f2h(float f) {
+    asm volatile("" : "+v"(f));
     return __half_as_ushort(__float2half(f));
 }
 
