@@ -103,6 +103,7 @@ PageGeom prod_geom(const TQConfig& cfg, const TQTurboProdPageLayout& l) {
     g.D = cfg.head_dim;
     g.block_size = cfg.block_size;
     g.bs_shift = is_pow2(cfg.block_size) ? log2i(cfg.block_size) : -1;
+    g.h_shift = is_pow2(cfg.num_kv_heads) ? log2i(cfg.num_kv_heads) : -1;
     return g;
 }
 
@@ -124,7 +125,23 @@ PageGeom mse_geom(const TQConfig& cfg, const TQTurbomsePageLayout& l) {
     g.D = cfg.head_dim;
     g.block_size = cfg.block_size;
     g.bs_shift = is_pow2(cfg.block_size) ? log2i(cfg.block_size) : -1;
+    g.h_shift = is_pow2(cfg.num_kv_heads) ? log2i(cfg.num_kv_heads) : -1;
     return g;
+}
+
+int num_cus() {
+    static std::mutex mu;
+    static std::map<int, int> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) throw Error("hipGetDevice failed");
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find(dev);
+    if (it != cache.end()) return it->second;
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+        n = 256;
+    cache[dev] = n;
+    return n;
 }
 
 void* workspace(hipStream_t stream, size_t bytes) {

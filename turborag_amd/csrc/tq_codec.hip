@@ -8,6 +8,8 @@
 // operation order, so codes, scales and dequantized halves are bit-identical
 // to the reference's CUDA kernels (given correctly rounded / and sqrt, which
 // this library is compiled for).
+#include <algorithm>
+
 #include "tq_device.h"
 
 namespace tq {
@@ -188,6 +190,204 @@ __global__ __launch_bounds__(kBlock) void dequant_kernel(
     *reinterpret_cast<uint32_t*>(out_value + off) = vo;
 }
 
+// ---------------------------------------------------------------------------
+// Dequant, streaming form (D = 32, 64, 128).  A row is owned by LPR = D/32
+// lanes; lane j holds the four 8-element chunks j + LPR*m (m = 0..3), so WHT
+// stages len = 1, 2, 4 and len >= 8*LPR are register butterflies and the
+// stages in between cross lanes (quad DPP moves, VALU rate), and store m of
+// the row's lanes writes 16*LPR contiguous bytes (full 64-byte segments for
+// D = 128; quarter-line strided stores measured 1.4x slower).  The 16
+// possible decoded values of each row — (K3[n&7] + re*(+-1)) * ks for
+// turbo_prod K, V4[n] * rms otherwise, with the reference's exact operations
+// — are tabulated per row in LDS and looked up per nibble.  Waves are
+// persistent: each walks groups of 64/LPR rows with the next group's slot and
+// codes in flight while it transforms and stores the current one.
+// ---------------------------------------------------------------------------
+template <int D, bool PROD>
+__global__ __launch_bounds__(kBlock) void dequant_stream_kernel(
+    const uint8_t* __restrict__ pool, const int32_t* __restrict__ slots,
+    uint16_t* __restrict__ out_key, uint16_t* __restrict__ out_value, PageGeom g, int num_rows,
+    float inv) {
+    constexpr int E = 32;           // elements per lane
+    constexpr int LPR = D / E;      // lanes per row
+    constexpr int RPW = 64 / LPR;   // rows per wave group
+    // Each lane keeps a private copy of its row's two 16-entry tables: entry n
+    // of (wave w, lane l) is word ((n*4 + w)*64 + l), so every lookup of lane l
+    // hits LDS bank l and a wave's 64 lookups never conflict, whatever the
+    // nibbles.  The entry's byte address is 4l + 256*(4n + w): the lane's base
+    // with byte 1 replaced by 4n + w (one v_perm_b32).  V follows K by 16 KiB.
+    constexpr int kWaves = kBlock / 64;
+    static_assert(kWaves == 4, "byte 1 of a table address holds 4*nibble + wave");
+    constexpr uint32_t kTabBytes = 16 * kWaves * 64 * sizeof(float);
+    // The kernel's only LDS object, so it starts at LDS address 0 and the
+    // address bits above byte 1 are those of the 16 KiB table offset alone.
+    __shared__ __attribute__((aligned(1024))) float tab[2][16][kWaves][64];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int j = lane % LPR, rw = lane / LPR;
+    float* TK = &tab[0][0][wave][lane];  // entry n at TK[n * kWaves * 64]
+    float* TV = &tab[1][0][wave][lane];
+    const uint32_t tbase = (uint32_t)reinterpret_cast<uintptr_t>((lds_float*)TK);
+    const uint32_t wsplat = 0x01010101u * (uint32_t)wave;
+    const int groups = (num_rows + RPW - 1) / RPW;
+    const int stride = gridDim.x * (kBlock / 64);
+
+    struct Item {
+        uint4 kw, vw;
+        float ks, re, vs;
+        int row, h;
+        bool live;
+    };
+    auto token_head = [&](int row, int& t, int& h) {
+        if (g.h_shift >= 0) {
+            t = row >> g.h_shift;
+            h = row & (g.H - 1);
+        } else {
+            t = row / g.H;
+            h = row - t * g.H;
+        }
+    };
+    auto load_slot = [&](int grp) -> int {
+        const int row = grp * RPW + rw;
+        if (grp >= groups || row >= num_rows) return -1;
+        int t, h;
+        token_head(row, t, h);
+        return slots[t];
+    };
+    auto fetch = [&](int grp, int slot) -> Item {
+        Item it;
+        it.row = grp * RPW + rw;
+        int t;
+        token_head(min(it.row, num_rows - 1), t, it.h);
+        it.live = grp < groups && it.row < num_rows && slot >= 0;
+        it.kw = make_uint4(0, 0, 0, 0);
+        it.vw = it.kw;
+        it.ks = it.re = it.vs = 0.0f;
+        if (it.live) {
+            int page, tib;
+            split_slot(slot, g, page, tib);
+            const size_t cell = (size_t)(tib * g.H + it.h);
+            const uint8_t* base = pool + (size_t)page * g.page_size;
+            // dword j + LPR*m of the cell holds the nibbles of chunk m
+            const uint32_t* kp =
+                reinterpret_cast<const uint32_t*>(base + g.kc_off + cell * g.code_stride) + j;
+            const uint32_t* vp =
+                reinterpret_cast<const uint32_t*>(base + g.vc_off + cell * g.code_stride) + j;
+            it.kw = make_uint4(kp[0], kp[LPR], kp[2 * LPR], kp[3 * LPR]);
+            it.vw = make_uint4(vp[0], vp[LPR], vp[2 * LPR], vp[3 * LPR]);
+            it.ks = h2f(ld_u16(base + g.ks_off + cell * g.scale_stride));
+            it.vs = h2f(ld_u16(base + g.vs_off + cell * g.scale_stride));
+            if (PROD) it.re = h2f(ld_u16(base + g.kres_off + cell * g.scale_stride));
+        }
+        return it;
+    };
+
+    // One tensor at a time keeps 32 values live per lane.
+    auto transform = [&](const Item& it, uint4 w, uint32_t toff, uint16_t* out) {
+        float x[E];
+        const uint32_t wa[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            // bytes 4*nibble + wave, for even and odd elements
+            const uint32_t ev = ((wa[q] << 2) & 0x3C3C3C3Cu) | wsplat;
+            const uint32_t od = ((wa[q] >> 2) & 0x3C3C3C3Cu) | wsplat;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                // byte 0 and bytes 2..3 from tbase, byte 1 = 4*nibble + wave.
+                const uint32_t sel = 0x03020000u | ((uint32_t)(4 + b) << 8);
+                const uint32_t ae = __builtin_amdgcn_perm(ev, tbase, sel) + toff;
+                const uint32_t ao = __builtin_amdgcn_perm(od, tbase, sel) + toff;
+                x[8 * q + 2 * b] = *reinterpret_cast<const lds_float*>(ae);
+                x[8 * q + 2 * b + 1] = *reinterpret_cast<const lds_float*>(ao);
+            }
+        }
+        // x[8m + i] is element 8*(j + LPR*m) + i.  Stages in the reference's
+        // order: len = 1, 2, 4 pair k and k ^ len in the lane ...
+        auto reg_stage = [&](int kb) {
+#pragma unroll
+            for (int k = 0; k < E; ++k) {
+                if ((k & kb) == 0) {
+                    const float a = x[k], b = x[k + kb];
+                    x[k] = a + b;
+                    x[k + kb] = a - b;
+                }
+            }
+        };
+        reg_stage(1);
+        reg_stage(2);
+        reg_stage(4);
+        // ... len = 8, 16 (LPR = 4; 8 for LPR = 2) pair lanes j and j ^ 1,
+        // j ^ 2.  The lower lane needs mine + partner, the upper partner -
+        // mine: fmaf(mine, +-1, partner) is both, exactly (exact product, one
+        // rounding of the sum) ...
+        if constexpr (LPR >= 2) {
+            const float sg = (j & 1) ? -1.0f : 1.0f;
+#pragma unroll
+            for (int k = 0; k < E; ++k) x[k] = fmaf(x[k], sg, quad_xor<1>(x[k]));
+        }
+        if constexpr (LPR >= 4) {
+            const float sg = (j & 2) ? -1.0f : 1.0f;
+#pragma unroll
+            for (int k = 0; k < E; ++k) x[k] = fmaf(x[k], sg, quad_xor<2>(x[k]));
+        }
+        // ... and the two largest (chunk m ^ 1, m ^ 2) are in the lane again.
+        reg_stage(8);
+        reg_stage(16);
+        if (!it.live) return;
+        // Element 8*(j + LPR*m) + i has sign (-1)^(i + h).
+        const float se = (it.h & 1) ? -inv : inv;
+        uint4* d = reinterpret_cast<uint4*>(out + (size_t)it.row * D) + j;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const float* c = x + 8 * m;
+            d[LPR * m] = make_uint4(f2h2(c[0] * se, c[1] * -se), f2h2(c[2] * se, c[3] * -se),
+                                    f2h2(c[4] * se, c[5] * -se), f2h2(c[6] * se, c[7] * -se));
+        }
+    };
+
+    int grp = blockIdx.x * (kBlock / 64) + wave;
+    Item cur = fetch(grp, load_slot(grp));
+    int s_next = load_slot(grp + stride);
+    while (grp < groups) {  // wave-uniform
+        const Item nxt = fetch(grp + stride, s_next);
+        s_next = load_slot(grp + 2 * stride);
+        // Lane j computes entries j*PER .. j*PER + PER-1 and writes each into
+        // the private copies of all LPR lanes of its row (adjacent words).
+        {
+            typedef float vecL __attribute__((ext_vector_type(LPR)));
+            constexpr int PER = 16 / LPR;
+            float* rowK = &tab[0][0][wave][LPR * rw];
+            float* rowV = &tab[1][0][wave][LPR * rw];
+#pragma unroll
+            for (int q = 0; q < PER; ++q) {
+                const int n = j * PER + q;
+                const float kv = PROD ? (kK3[n & 7] + cur.re * ((n & 8) ? 1.0f : -1.0f)) * cur.ks
+                                      : kV4[n] * cur.ks;
+                const float vv = kV4[n] * cur.vs;
+                *reinterpret_cast<vecL*>(rowK + n * kWaves * 64) = (vecL)(kv);
+                *reinterpret_cast<vecL*>(rowV + n * kWaves * 64) = (vecL)(vv);
+            }
+        }
+        // The table is private to this wave: wave-scope ordering suffices.
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        transform(cur, cur.kw, 0, out_key);
+        transform(cur, cur.vw, kTabBytes, out_value);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        cur = nxt;
+        grp += stride;
+    }
+}
+
+// The streaming kernel reads codes as dwords and writes 16-byte output chunks.
+bool wide_dequant_ok(const PageGeom& g, const void* pool, const void* ok, const void* ov) {
+    const auto al = [](uint64_t v, uint64_t a) { return (v & (a - 1)) == 0; };
+    return (g.D == 32 || g.D == 64 || g.D == 128) && al(g.page_size, 4) && al(g.kc_off, 4) &&
+           al(g.vc_off, 4) && al(reinterpret_cast<uintptr_t>(pool), 4) &&
+           al(reinterpret_cast<uintptr_t>(ok), 16) && al(reinterpret_cast<uintptr_t>(ov), 16);
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -227,9 +427,27 @@ void launch_dequant(Scheme s, const uint8_t* pool, const int32_t* slots, uint16_
                     uint16_t* out_value, const PageGeom& g, int num_tokens, hipStream_t stream) {
     const int rows = num_tokens * g.H;
     if (rows <= 0) return;
+    const float inv = inv_sqrt_d(g.D);
+    if (wide_dequant_ok(g, pool, out_key, out_value)) {
+        // Persistent waves: up to four workgroups (one wave per SIMD each) per
+        // CU, fewer when there is not enough work (measured: 4 per CU beats
+        // 1 or 2 and equals 8 at the 32K-token layer).
+        const int rows_per_block = kBlock / (g.D / 32);
+        const int blocks_needed = (rows + rows_per_block - 1) / rows_per_block;
+        const dim3 grid(std::max(1, std::min(blocks_needed, 4 * num_cus())));
+        const bool prod = s == Scheme::Prod;
+        auto go = [&](auto kernel) {
+            hipLaunchKernelGGL(kernel, grid, dim3(kBlock), 0, stream, pool, slots, out_key,
+                               out_value, g, rows, inv);
+        };
+        if (g.D == 128) prod ? go(dequant_stream_kernel<128, true>) : go(dequant_stream_kernel<128, false>);
+        else if (g.D == 64) prod ? go(dequant_stream_kernel<64, true>) : go(dequant_stream_kernel<64, false>);
+        else prod ? go(dequant_stream_kernel<32, true>) : go(dequant_stream_kernel<32, false>);
+        check_launch(prod ? "turbo_prod_dequant_kv_kernel" : "turbo_mse_dequant_kv_kernel");
+        return;
+    }
     const int rpb = kBlock / (g.D / 2);
     const dim3 grid((rows + rpb - 1) / rpb);
-    const float inv = inv_sqrt_d(g.D);
     if (s == Scheme::Prod) {
         TQ_DISPATCH_D(g.D, hipLaunchKernelGGL((dequant_kernel<kD, true>), grid, dim3(kBlock), 0,
                                               stream, pool, slots, out_key, out_value, g, rows,

@@ -32,6 +32,9 @@ __device__ constexpr float kV4[16] = {-2.7326f, -2.0690f, -1.6180f, -1.2562f,
 
 constexpr float kMinRMS = 1e-8f;  // include/tq_shared_device.cuh:9
 
+// A float in LDS addressed by its 32-bit LDS byte offset.
+typedef __attribute__((address_space(3))) float lds_float;
+
 __device__ __forceinline__ float h2f(uint16_t h) {
     return __half2float(__ushort_as_half(h));
 }
@@ -54,6 +57,25 @@ __device__ __forceinline__ float clamp_ref(float x, float lo, float hi) {
 }
 
 __device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
+
+// Two fp32 -> packed fp16x2 (RNE each, v_cvt_pk_f16_f32), low half = a.  Same
+// fp32 pinning as f2h.
+__device__ __forceinline__ uint32_t f2h2(float a, float b) {
+    typedef float f2v __attribute__((ext_vector_type(2)));
+    typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+    asm volatile("" : "+v"(a), "+v"(b));
+    const h2v h = __builtin_convertvector((f2v){a, b}, h2v);
+    return __builtin_bit_cast(uint32_t, h);
+}
+
+// Lane exchange inside a quad through DPP (a VALU op, no LDS traffic):
+// quad_perm(1,0,3,2) = xor 1, quad_perm(2,3,0,1) = xor 2.
+template <int MASK>
+__device__ __forceinline__ float quad_xor(float v) {
+    static_assert(MASK == 1 || MASK == 2, "quad_xor: mask 1 or 2");
+    constexpr int ctrl = MASK == 1 ? 0xB1 : 0x4E;
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), ctrl, 0xF, 0xF, true));
+}
 
 // In-place WHT of a row held two-per-lane (lane index j within its row).
 template <int L>

@@ -35,7 +35,11 @@ struct PageGeom {
     int scale_stride;
     int H, D, block_size;
     int bs_shift;  // log2(block_size) when block_size is a power of two, else -1
+    int h_shift;   // log2(H) when H is a power of two, else -1
 };
+
+// Number of compute units of the current device (cached per device).
+int num_cus();
 
 enum class Scheme : int { Prod = 0, Mse = 1 };
 
