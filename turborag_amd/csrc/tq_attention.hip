@@ -187,9 +187,416 @@ __global__ __launch_bounds__(256) void prod_logits_kernel(
     logits[(size_t)row * num_kv_tokens + t] = (s1 * ks + s2 * (ks * re)) * inv;
 }
 
+// ===========================================================================
+// Matrix-core path: D = 128, up to 8 query rows per kv head per workgroup.
+//
+// Per kv head h and row group (8 query rows), a workgroup of 4 waves owns a
+// range of tokens; each wave takes 64-token chunks.
+//   QK: S^T[token][col] = sum_d K[token][d] * Q^T[d][col] with
+//       v_mfma_f32_16x16x32_f16.  A = K, decoded from nibbles to fp16 through
+//       256-entry LDS tables indexed by code byte; B = the rotated query split
+//       into fp16 hi + lo parts, columns 2r (hi) and 2r+1 (lo) of row r, so a
+//       single MFMA column pair recovers ~22-bit query precision.  The K3
+//       codebook enters as fp16(aK*K3[c]) with aK = 1.2918981, which makes all
+//       four magnitudes fp16-exact to 1.4e-5 relative (V4 with aV = 1.5982153
+//       to 9.3e-5); the scale is divided out per token.  turbo_prod's residual
+//       sign is a second A matrix (+-1, exact) with its own accumulator.
+//   softmax: base-2 online softmax per row over the chunk, in the MFMA output
+//       layout (lane (col, g) holds tokens 4g..4g+3 of each 16-token tile).
+//   PV: O[col][d] += sum_t P'[col][t] V[t][d] with the same MFMA.  The QK
+//       output layout is exactly the A-operand layout over 32 tokens (two
+//       tiles), so P' = p * vs needs no data movement; it is split hi/lo in
+//       the column pair like q.  B = V, whose contraction index (tokens) must
+//       run inside a lane: each lane loads dword i of 8 tokens' V cells and
+//       interleaves the nibbles of token pairs into bytes, one table lookup
+//       per (token pair, d).
+// Each workgroup merges its waves, applies the inverse WHT and sign flip to
+// its unnormalised partial (linear, so allowed before the split merge), and
+// writes (o[128], m, l) per row; a combine kernel takes the weighted sum.
+// ===========================================================================
+namespace mfma {
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+constexpr float kAlphaK = 1.2918981f;
+constexpr float kAlphaV = 1.5982153f;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kRows = 8;     // query rows per workgroup (16 MFMA columns, hi/lo)
+constexpr int kPartStride = 128 + 2;  // floats per partial row: o[128], m, l
+
+__device__ __forceinline__ uint32_t pack_h2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, (half2v){(_Float16)a, (_Float16)b});
+}
+__device__ __forceinline__ half8 as_h8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    return __builtin_bit_cast(half8, (u32x4){a, b, c, d});
+}
+// fp16 hi or lo part of x: lo = fp16(x - fp32(fp16(x))) (the difference is exact).
+__device__ __forceinline__ _Float16 hi_lo(float x, bool lo) {
+    const _Float16 h = (_Float16)x;
+    return lo ? (_Float16)(x - (float)h) : h;
+}
+}  // namespace mfma
+
+// CH = tokens per wave iteration (32: two QK tiles, one PV step; 64: four and
+// two); NW = waves per workgroup.
+template <bool PROD, int CH, int NW>
+__global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
+    const uint16_t* __restrict__ query, const uint8_t* __restrict__ pool,
+    const int32_t* __restrict__ slots, float* __restrict__ ws, PageGeom g, int num_queries,
+    int num_kv_tokens, int tokens_per_split, int num_splits, float inv) {
+    using namespace mfma;
+    constexpr int kChunk = CH, kWaves = NW;
+    constexpr int kTiles = CH / 16, kSteps = CH / 32;
+    static_assert(CH == 32 || CH == 64, "chunk of 32 or 64 tokens");
+    static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+    __shared__ uint2 lutK[256];     // prod: (aK*K3 pair, sign pair); mse: (aV*V4 pair, -)
+    __shared__ uint32_t lutV[256];  // aV*V4 pair
+    __shared__ float qs[kRows][128];
+    __shared__ uint4 bqs[4][64];  // QK B operand (fp16 hi/lo q) of k-step s for lane l
+    __shared__ uint64_t tko[kWaves][kChunk], tvo[kWaves][kChunk];
+    __shared__ float4 tsc[kWaves][kChunk];  // per token: K scale a, residual scale b, vs, bias
+    __shared__ float mo[kWaves][kRows][128];
+    __shared__ float mm[kWaves][kRows], ml[kWaves][kRows];
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int i = lane & 15, gq = lane >> 4;
+    const int split = blockIdx.x % num_splits;
+    const int hr = blockIdx.x / num_splits;
+    const int h = hr % g.H, rg = hr / g.H;
+    const float ck = inv * kLog2e / (PROD ? kAlphaK : kAlphaV);  // logit scale per unit ks
+    const float cr = inv * kLog2e;                                 // residual: ks * re
+    const int t_begin = split * tokens_per_split;
+    const int t_end = min(num_kv_tokens, t_begin + tokens_per_split);
+
+    // A chunk's codes and per-token scales, loaded ahead of its compute.
+    struct Chunk {
+        uint4 kw[kTiles];        // K: tile tau, token 16*tau + i, bytes [16gq, 16gq + 16)
+        uint32_t vw[kSteps][8];  // V: step p, k-index 8gq + e (token below), dword i
+        uint16_t ks, re, vs;  // this lane's token's fp16 scales (raw: still in flight)
+        bool valid;
+    };
+    // slot -> cell offsets (exchanged through LDS) -> code loads; the scale
+    // loads stay in flight in registers until the chunk is computed.
+    auto fetch = [&](int t0, Chunk& c) {
+        const int t = t0 + (lane & (kChunk - 1));
+        uint64_t ko = 0, vo = 0;  // tokens past the range read page 0 and get bias -inf
+        c.valid = t < t_end;
+        c.ks = c.re = c.vs = 0;
+        if (c.valid) {
+            int page, tib;
+            split_slot(slots[t], g, page, tib);
+            const uint64_t cell = (uint64_t)(tib * g.H + h);
+            const uint64_t pb = (uint64_t)page * g.page_size;
+            ko = pb + g.kc_off + cell * g.code_stride;
+            vo = pb + g.vc_off + cell * g.code_stride;
+            c.ks = ld_u16(pool + pb + g.ks_off + cell * g.scale_stride);
+            c.vs = ld_u16(pool + pb + g.vs_off + cell * g.scale_stride);
+            if (PROD) c.re = ld_u16(pool + pb + g.kres_off + cell * g.scale_stride);
+        }
+        if (lane < kChunk) {
+            tko[w][lane] = ko;
+            tvo[w][lane] = vo;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int tau = 0; tau < kTiles; ++tau)
+            c.kw[tau] = *reinterpret_cast<const uint4*>(pool + tko[w][16 * tau + i] + 16 * gq);
+        // k-step p covers tiles 2p, 2p+1; k-index 8gq + e is token
+        // 32p + 4gq + e (e < 4) or 32p + 16 + 4gq + (e - 4).
+#pragma unroll
+        for (int p = 0; p < kSteps; ++p)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int tok = 32 * p + (e < 4 ? 4 * gq + e : 16 + 4 * gq + (e - 4));
+                c.vw[p][e] = *reinterpret_cast<const uint32_t*>(pool + tvo[w][tok] + 4 * i);
+            }
+    };
+    int t0 = t_begin + w * kChunk;
+    Chunk cur;
+    if (t0 < t_end) fetch(t0, cur);  // in flight during the setup below
+
+    if (tid < 256) {  // decode tables, entry = code byte (low nibble = even d)
+        const int lo = tid & 15, hi = tid >> 4;
+        const float al = PROD ? kAlphaK : kAlphaV;
+        const float vlo = pick(kV4, lo), vhi = pick(kV4, hi);
+        const float klo = PROD ? pick(kK3, lo & 7) : vlo, khi = PROD ? pick(kK3, hi & 7) : vhi;
+        const uint32_t sgn = pack_h2((lo & 8) ? 1.0f : -1.0f, (hi & 8) ? 1.0f : -1.0f);
+        lutK[tid] = make_uint2(pack_h2(al * klo, al * khi), PROD ? sgn : 0u);
+        lutV[tid] = pack_h2(kAlphaV * vlo, kAlphaV * vhi);
+    }
+    // Rotated query rows of this group (wave w: rows w, w + NW, ...):
+    // qrot = WHT(q * s) * inv.
+    for (int r = w; r < kRows; r += kWaves) {
+        const int qi = rg * kRows + r;
+        float q0 = 0.0f, q1 = 0.0f;
+        const uint16_t* qp = query + ((size_t)min(qi, num_queries - 1) * g.H + h) * 128;
+        rotate_query<64>(qp, h, lane, inv, q0, q1);
+        qs[r][2 * lane] = qi < num_queries ? q0 : 0.0f;
+        qs[r][2 * lane + 1] = qi < num_queries ? q1 : 0.0f;
+    }
+    __syncthreads();
+
+    // B operand of QK, built once per workgroup: column i = row i/2, hi (i
+    // even) or lo (i odd) part; k-index 8*gq + e of step s is d = 32*gq + 8*s + e.
+    const bool lo_col = (i & 1) != 0;
+    if (tid < 256) {
+        const int s = tid >> 6;
+        half8 b;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) b[e] = hi_lo(qs[i >> 1][32 * gq + 8 * s + e], lo_col);
+        bqs[s][lane] = __builtin_bit_cast(uint4, b);
+    }
+    __syncthreads();
+    half8 bq[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) bq[s] = __builtin_bit_cast(half8, bqs[s][lane]);
+
+    float m_run = kInitMax, l_run = 0.0f;
+    f32x4 acc[8];
+#pragma unroll
+    for (int v = 0; v < 8; ++v) acc[v] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    bool first = true;
+
+    while (t0 < t_end) {  // wave-uniform
+        const uint4* kw = cur.kw;
+        const uint32_t(*vw)[8] = cur.vw;
+        if (lane < kChunk) {
+            const float ks = h2f(cur.ks), vs = h2f(cur.vs), re = PROD ? h2f(cur.re) : 0.0f;
+            tsc[w][lane] = cur.valid ? make_float4(ks * ck, ks * re * cr, vs, 0.0f)
+                                     : make_float4(0.f, 0.f, 0.f, -INFINITY);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        Chunk nxt;
+        const int t1 = t0 + kWaves * kChunk;
+        if (t1 < t_end) fetch(t1, nxt);
+
+        // QK
+        f32x4 cb[kTiles], cs[kTiles];
+#pragma unroll
+        for (int tau = 0; tau < kTiles; ++tau) {
+            cb[tau] = (f32x4){0.f, 0.f, 0.f, 0.f};
+            cs[tau] = cb[tau];
+            const uint32_t wd[4] = {kw[tau].x, kw[tau].y, kw[tau].z, kw[tau].w};
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const uint2 e0 = lutK[wd[s] & 0xff], e1 = lutK[(wd[s] >> 8) & 0xff];
+                const uint2 e2 = lutK[(wd[s] >> 16) & 0xff], e3 = lutK[wd[s] >> 24];
+                cb[tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(e0.x, e1.x, e2.x, e3.x),
+                                                                bq[s], cb[tau], 0, 0, 0);
+                if (PROD)
+                    cs[tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        as_h8(e0.y, e1.y, e2.y, e3.y), bq[s], cs[tau], 0, 0, 0);
+            }
+        }
+        // Logits (base 2) of tokens 16*tau + 4*gq + e; hi + lo columns summed.
+        float lg[kTiles][4];
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int tau = 0; tau < kTiles; ++tau)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float4 sc = tsc[w][16 * tau + 4 * gq + e];
+                const float sb = cb[tau][e] + quad_xor<1>(cb[tau][e]);
+                const float sr = PROD ? cs[tau][e] + quad_xor<1>(cs[tau][e]) : 0.0f;
+                lg[tau][e] = fmaf(sb, sc.x, fmaf(sr, sc.y, sc.w));
+                mloc = fmaxf(mloc, lg[tau][e]);
+            }
+        mloc = fmaxf(mloc, shfl_xor(mloc, 16));
+        mloc = fmaxf(mloc, shfl_xor(mloc, 32));
+        // v_exp_f32 without denormal handling: arguments are <= 0 and a
+        // weight below 2^-126 of the running maximum is negligible.
+        const float m_new = fmaxf(m_run, mloc);
+        const float alpha = first ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+        m_run = m_new;
+        float lsum = 0.0f;
+#pragma unroll
+        for (int tau = 0; tau < kTiles; ++tau)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                lg[tau][e] = __builtin_amdgcn_exp2f(lg[tau][e] - m_new);
+                lsum += lg[tau][e];
+            }
+        l_run = l_run * alpha + lsum;
+        if (!first && __any(alpha != 1.0f)) {
+            // acc lane (d, gq) holds columns 4gq..4gq+3 = rows 2gq, 2gq+1.
+            const float a0 = __shfl(alpha, 4 * gq), a1 = __shfl(alpha, 4 * gq + 2);
+#pragma unroll
+            for (int v = 0; v < 8; ++v) {
+                acc[v][0] *= a0;
+                acc[v][1] *= a0;
+                acc[v][2] *= a1;
+                acc[v][3] *= a1;
+            }
+        }
+        // PV
+#pragma unroll
+        for (int p = 0; p < kSteps; ++p) {
+            half8 ap;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int tau = 2 * p + (e >> 2), ee = e & 3;
+                const float vs = tsc[w][16 * tau + 4 * gq + ee].z;
+                ap[e] = hi_lo(lg[tau][ee] * vs, lo_col);
+            }
+            uint32_t bv[8][4];  // [N-tile v = d - 8i][token pair]
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t we = vw[p][2 * q], wo = vw[p][2 * q + 1];
+                const uint32_t lob = (we & 0x0F0F0F0Fu) | ((wo & 0x0F0F0F0Fu) << 4);
+                const uint32_t hib = ((we >> 4) & 0x0F0F0F0Fu) | (wo & 0xF0F0F0F0u);
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    bv[2 * b][q] = lutV[(lob >> (8 * b)) & 0xff];
+                    bv[2 * b + 1][q] = lutV[(hib >> (8 * b)) & 0xff];
+                }
+            }
+#pragma unroll
+            for (int v = 0; v < 8; ++v)
+                acc[v] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    ap, as_h8(bv[v][0], bv[v][1], bv[v][2], bv[v][3]), acc[v], 0, 0, 0);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        cur = nxt;
+        t0 = t1;
+        first = false;
+    }
+
+    // Wave results: l summed over the g lanes of each column; o rows from the
+    // hi + lo columns, the V codebook scale divided out.
+    float l_tot = l_run + shfl_xor(l_run, 16);
+    l_tot += shfl_xor(l_tot, 32);
+    if (gq == 0 && !lo_col) {
+        mm[w][i >> 1] = m_run;
+        ml[w][i >> 1] = l_tot;
+    }
+    const float iav = 1.0f / kAlphaV;
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+        mo[w][2 * gq][8 * i + v] = (acc[v][0] + acc[v][1]) * iav;
+        mo[w][2 * gq + 1][8 * i + v] = (acc[v][2] + acc[v][3]) * iav;
+    }
+    __syncthreads();
+
+    // Merge the waves; inverse WHT and sign flip; partial to the workspace.
+    for (int r = w; r < kRows; r += kWaves) {
+        float M = mm[0][r];
+#pragma unroll
+        for (int u = 1; u < kWaves; ++u) M = fmaxf(M, mm[u][r]);
+        float L = 0.f, o0 = 0.f, o1 = 0.f;
+#pragma unroll
+        for (int u = 0; u < kWaves; ++u) {
+            const float wt = exp2f(mm[u][r] - M);
+            L += ml[u][r] * wt;
+            o0 += mo[u][r][2 * lane] * wt;
+            o1 += mo[u][r][2 * lane + 1] * wt;
+        }
+        wht_pair<64>(o0, o1, lane);
+        const float s0 = (h & 1) ? -inv : inv;
+        float* part = ws + ((size_t)blockIdx.x * kRows + r) * kPartStride;
+        part[2 * lane] = o0 * s0;
+        part[2 * lane + 1] = o1 * -s0;
+        if (lane == 0) {
+            part[128] = M;
+            part[129] = L;
+        }
+    }
+}
+
+// Sum of the split partials of one output row (q, h): o = sum_s 2^(m_s - M)
+// o_s / sum_s 2^(m_s - M) l_s.  Block = (row, 32-element slice of d), 256
+// threads = 8 groups x 32 d.  Group g takes splits g, g + 8, ...: it loads up
+// to 16 partials' (m, l, o[d]) in one round, merges them with a running
+// maximum, and the 8 groups are merged in LDS.
+__global__ __launch_bounds__(256) void attn_mfma_combine_kernel(
+    const float* __restrict__ ws, uint16_t* __restrict__ output, int H, int num_splits) {
+    using namespace mfma;
+    constexpr int kBatch = 16;
+    __shared__ float red_m[8], red_l[8];
+    __shared__ float red_o[8][33];
+    const int row = blockIdx.x >> 2, dq = blockIdx.x & 3;  // row = q * H + h
+    const int q = row / H, h = row - q * H;
+    const int rg = q / kRows, r = q % kRows;
+    const int t = threadIdx.x, dd = t & 31, sg = t >> 5;
+    const int d = 32 * dq + dd;
+    const size_t base_bid = (size_t)(rg * H + h) * num_splits;
+    auto part = [&](int s) { return ws + ((base_bid + s) * kRows + r) * kPartStride; };
+
+    float M = kInitMax, L = 0.f, acc = 0.f;
+    for (int base = sg; base < num_splits; base += 8 * kBatch) {
+        float pm[kBatch], pl[kBatch], po[kBatch];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+            const int s = base + 8 * k;
+            const float* p = part(s < num_splits ? s : base);
+            pm[k] = s < num_splits ? p[128] : kInitMax;
+            pl[k] = p[129];
+            po[k] = p[d];
+        }
+        float mb = M;
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) mb = fmaxf(mb, pm[k]);
+        const float sc = exp2f(M - mb);
+        L *= sc;
+        acc *= sc;
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+            const float wt = exp2f(pm[k] - mb);
+            L += pl[k] * wt;
+            acc += po[k] * wt;
+        }
+        M = mb;
+    }
+    if (dd == 0) {
+        red_m[sg] = M;
+        red_l[sg] = L;
+    }
+    red_o[sg][dd] = acc;
+    __syncthreads();
+    if (t < 32) {
+        float Mx = red_m[0];
+#pragma unroll
+        for (int u = 1; u < 8; ++u) Mx = fmaxf(Mx, red_m[u]);
+        float Lt = 0.f, o = 0.f;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const float wt = exp2f(red_m[u] - Mx);
+            Lt += red_l[u] * wt;
+            o += red_o[u][t] * wt;
+        }
+        output[(size_t)row * 128 + 32 * dq + t] = f2h(Lt > 0.f ? o / Lt : o);
+    }
+}
+
+// Split kernel shape: tokens per wave iteration and waves per workgroup.
+#ifndef TQ_SPLIT_CHUNK
+#define TQ_SPLIT_CHUNK 32
+#endif
+#ifndef TQ_SPLIT_WAVES
+#define TQ_SPLIT_WAVES 8
+#endif
+#ifndef TQ_SPLIT_MIN_TOKENS
+#define TQ_SPLIT_MIN_TOKENS 256
+#endif
+#ifndef TQ_SPLIT_BLOCKS_PER_CU
+#define TQ_SPLIT_BLOCKS_PER_CU 2
+#endif
+constexpr int kSplitChunk = TQ_SPLIT_CHUNK, kSplitWaves = TQ_SPLIT_WAVES;
+constexpr int kSplitMinTokens = TQ_SPLIT_MIN_TOKENS, kSplitBlocksPerCU = TQ_SPLIT_BLOCKS_PER_CU;
+
+bool mfma_attention_ok(const PageGeom& g, const void* pool) {
+    const auto al = [](uint64_t v, uint64_t a) { return (v & (a - 1)) == 0; };
+    return g.D == 128 && g.code_stride == 64 && al(g.page_size, 16) && al(g.kc_off, 16) &&
+           al(g.vc_off, 4) && al(reinterpret_cast<uintptr_t>(pool), 16);
+}
+
 }  // namespace
 
-#define TQ_DISPATCH_D(D_, ...)                                                   \
+#define TQ_DISPATCH_D(D_, ...)                                                 \
     switch (D_) {                                                                \
         case 2: { constexpr int kD = 2; __VA_ARGS__; } break;                    \
         case 4: { constexpr int kD = 4; __VA_ARGS__; } break;                    \
@@ -206,6 +613,38 @@ void launch_attention(Scheme s, const uint16_t* query, const uint8_t* pool, cons
                       hipStream_t stream) {
     const int rows = num_queries * g.H;
     if (rows <= 0) return;
+    const float inv = inv_sqrt_d(g.D);
+    if (mfma_attention_ok(g, pool)) {
+        using namespace mfma;
+        const int row_groups = (num_queries + kRows - 1) / kRows;
+        const int heads = g.H * row_groups;
+        // One 256-token split per workgroup, or longer splits once there are
+        // more than ~2 workgroups per CU.
+        const int max_splits =
+            std::max(1, (num_kv_tokens + kSplitMinTokens - 1) / kSplitMinTokens);
+        const int want = std::max(1, (kSplitBlocksPerCU * num_cus() + heads - 1) / heads);
+        int splits = std::min(std::min(max_splits, want), 1024);
+        const int tps = num_kv_tokens > 0 ? (num_kv_tokens + splits - 1) / splits : 0;
+        if (tps > 0) splits = (num_kv_tokens + tps - 1) / tps;
+        const size_t blocks = (size_t)splits * heads;
+        float* ws = static_cast<float*>(
+            workspace(stream, blocks * kRows * kPartStride * sizeof(float)));
+        const bool prod = s == Scheme::Prod;
+        constexpr int kCH = kSplitChunk, kNW = kSplitWaves;
+        if (prod)
+            hipLaunchKernelGGL((attn_mfma_split_kernel<true, kCH, kNW>), dim3(blocks),
+                               dim3(64 * kNW), 0, stream, query, pool, slots, ws, g, num_queries,
+                               num_kv_tokens, tps, splits, inv);
+        else
+            hipLaunchKernelGGL((attn_mfma_split_kernel<false, kCH, kNW>), dim3(blocks),
+                               dim3(64 * kNW), 0, stream, query, pool, slots, ws, g, num_queries,
+                               num_kv_tokens, tps, splits, inv);
+        check_launch(prod ? "turbo_prod_fused_attn_split" : "turbo_mse_fused_attn_split");
+        hipLaunchKernelGGL(attn_mfma_combine_kernel, dim3(4 * rows), dim3(256), 0, stream, ws,
+                           output, g.H, splits);
+        check_launch(prod ? "turbo_prod_fused_attn_combine" : "turbo_mse_fused_attn_combine");
+        return;
+    }
     // Enough waves to cover the chip several times, at least 32 tokens each.
     int splits = (2048 + rows - 1) / rows;
     splits = std::min(splits, std::max(1, (num_kv_tokens + 31) / 32));
@@ -214,7 +653,6 @@ void launch_attention(Scheme s, const uint16_t* query, const uint8_t* pool, cons
     if (tps > 0) splits = (num_kv_tokens + tps - 1) / tps;
     const size_t ws_bytes = (size_t)splits * rows * (g.D + 2) * sizeof(float);
     float* ws = static_cast<float*>(workspace(stream, ws_bytes));
-    const float inv = inv_sqrt_d(g.D);
     const bool prod = s == Scheme::Prod;
     if (prod) {
         TQ_DISPATCH_D(g.D, hipLaunchKernelGGL((attn_partial_kernel<kD, true>),

@@ -361,9 +361,11 @@ __global__ __launch_bounds__(kBlock) void dequant_stream_kernel(
 #pragma unroll
             for (int q = 0; q < PER; ++q) {
                 const int n = j * PER + q;
-                const float kv = PROD ? (kK3[n & 7] + cur.re * ((n & 8) ? 1.0f : -1.0f)) * cur.ks
-                                      : kV4[n] * cur.ks;
-                const float vv = kV4[n] * cur.vs;
+                const float v4n = pick(kV4, n);
+                const float kv =
+                    PROD ? (pick(kK3, n & 7) + cur.re * ((n & 8) ? 1.0f : -1.0f)) * cur.ks
+                         : v4n * cur.ks;
+                const float vv = v4n * cur.vs;
                 *reinterpret_cast<vecL*>(rowK + n * kWaves * 64) = (vecL)(kv);
                 *reinterpret_cast<vecL*>(rowV + n * kWaves * 64) = (vecL)(vv);
             }

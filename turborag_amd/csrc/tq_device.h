@@ -32,6 +32,17 @@ __device__ constexpr float kV4[16] = {-2.7326f, -2.0690f, -1.6180f, -1.2562f,
 
 constexpr float kMinRMS = 1e-8f;  // include/tq_shared_device.cuh:9
 
+// t[idx] for a runtime idx, built from immediates (v_cndmask chain): no
+// memory access, so it never waits behind outstanding global loads (the
+// vector-memory counter is in order).
+template <int N>
+__device__ __forceinline__ float pick(const float (&t)[N], int idx) {
+    float r = t[0];
+#pragma unroll
+    for (int k = 1; k < N; ++k) r = (idx == k) ? t[k] : r;
+    return r;
+}
+
 // A float in LDS addressed by its 32-bit LDS byte offset.
 typedef __attribute__((address_space(3))) float lds_float;
 
