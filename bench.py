@@ -2,19 +2,22 @@
 """bench.py — one MI355X, the TurboCAG KV-compression hot path.
 
 A step is one decode-time pass over a 36-layer Qwen2.5-3B-shaped compressed
-KV cache at 32K context (BASELINE configs 3 and 4): for every layer, dequant
-of its turbo_prod page pool to fp16 K/V [32768, 2, 128] (config 3's work,
+KV cache at 32K context: for every layer, dequant of its turbo_prod page pool
+to fp16 K/V [32768, 2, 128] (the layer load that feeds the model's KV cache,
 inputs resident in HBM) and fused GQA 16/2 decode attention over the same
-pool (config 4).  The 36 distinct pools (316 MB) and fp16 outputs (2.4 GB)
-rotate through more than the 256 MB Infinity Cache.
+pool.  The 36 distinct pools (316 MB) and fp16 outputs (2.4 GB) rotate
+through more than the 256 MB Infinity Cache.  Launches are replayed from HIP
+graphs, so host launch cost is not timed.
 
 value = algorithmic bytes of the step / step time (GB/s).  roofline is the
 dominant kernel (dequant): its algorithmic bytes per launch over its average
-launch duration, from per-launch HIP events on the launch stream.
-cpu_baseline times the CPU oracle (a port of the reference's algorithm) on a
-bounded sample of the same work on this host.
+launch duration, measured with HIP events around replays of a graph of the 36
+per-layer launches, on the stream the graph runs on.  cpu_baseline times the
+CPU oracle (a C port of the reference's algorithm) on a bounded sample of the
+same work on this host.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+       python bench.py --launch-pass   (eager launches only, for rocprofv3)
 """
 from __future__ import annotations
 
@@ -50,6 +53,123 @@ def gpu_kv(N, H, D, seed, dev):
     return k.half(), v.half()
 
 
+class Workload:
+    """The 36-layer pools, outputs and per-layer launches of one step."""
+
+    def __init__(self, layers: int, tokens: int):
+        import torch
+
+        from turborag_amd.synthetic import gqa_rows, permuted_slots, query
+        from turborag_amd.turboquant_wrapper import TurboQuantWrapper
+
+        self.dev = dev = torch.device("cuda", 0)
+        self.tq = tq = TurboQuantWrapper()
+        self.H, self.D, self.B, self.N, self.NL = 2, 128, 16, tokens, layers
+        self.q_heads = 16
+        self.rows = self.q_heads // self.H
+        H, D, B, N, NL = self.H, self.D, self.B, self.N, self.NL
+        cfg = tq.default_config()
+        cfg.num_kv_heads, cfg.head_dim, cfg.block_size = H, D, B
+        self.cfg = cfg
+        self.lp = lp = tq.make_layout_for(cfg)
+        pages = (N + B - 1) // B
+
+        log(f"[bench] setup: {NL} layers x {N} tokens, packing on the GPU")
+        self.slots = permuted_slots(N, B, seed=401).to(dev)
+        self.pools = []
+        for layer in range(NL):
+            k, v = gpu_kv(N, H, D, 300 + layer, dev)
+            pool = torch.zeros(pages * lp.page_size_bytes, dtype=torch.uint8, device=dev)
+            tq.pack(k, v, self.slots, pool, lp, cfg)
+            self.pools.append(pool)
+        del k, v
+        self.out_k = [torch.empty(N, H, D, dtype=torch.float16, device=dev) for _ in range(NL)]
+        self.out_v = [torch.empty(N, H, D, dtype=torch.float16, device=dev) for _ in range(NL)]
+        self.qa = gqa_rows(query(self.q_heads, D, seed=400), H).to(dev)
+        self.att = [torch.empty(self.rows, H, D, dtype=torch.float16, device=dev)
+                    for _ in range(NL)]
+        torch.cuda.synchronize()
+
+        # Algorithmic bytes per layer: pages read + fp16 written + slot map
+        # read (dequant); pages + slot map read + query read + output written
+        # (attention).
+        self.pool_bytes = pages * lp.page_size_bytes
+        slot_bytes = N * 4
+        self.deq_bytes = self.pool_bytes + 2 * N * H * D * 2 + slot_bytes
+        self.att_bytes = self.pool_bytes + slot_bytes + 2 * self.rows * H * D * 2
+        self.step_bytes = NL * (self.deq_bytes + self.att_bytes)
+
+    def _stream(self):
+        import torch
+        return torch.cuda.current_stream().cuda_stream
+
+    def dequant(self, layer):
+        self.tq.dequant(self.pools[layer], self.slots, self.out_k[layer], self.out_v[layer],
+                        self.lp, self.cfg, stream=self._stream())
+
+    def attention(self, layer):
+        self.tq.fused_attn_output(self.qa, self.pools[layer], self.slots, self.att[layer],
+                                  self.lp, self.cfg, self.rows, self.N, stream=self._stream())
+
+    def all_dequant(self):
+        for layer in range(self.NL):
+            self.dequant(layer)
+
+    def all_attention(self):
+        for layer in range(self.NL):
+            self.attention(layer)
+
+    def step(self):
+        self.all_dequant()
+        self.all_attention()
+
+
+def capture(fn, side):
+    """fn's launches as a HIP graph (captured on the side stream), or None."""
+    import torch
+    try:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=side):
+            fn()
+        torch.cuda.synchronize()
+        return g
+    except Exception as e:  # noqa: BLE001 — fall back to eager launches
+        log(f"[bench] graph capture failed ({e}); timing eager launches")
+        return None
+
+
+def event_time_us(run, reps):
+    """Mean duration of run() in µs from HIP events on the current stream."""
+    import torch
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    run()
+    a.record()
+    for _ in range(reps):
+        run()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e3 / reps
+
+
+def launch_pass(w: Workload, reps: int) -> None:
+    """Eager launches only: dequant and attention of every layer, then a plain
+    device copy of the dequant's byte count (the calibration kernel for the
+    FETCH_SIZE / WRITE_SIZE counters)."""
+    import torch
+    half = w.deq_bytes // 4  # fp16 elements copied: deq_bytes / 2 read, / 2 written
+    src = torch.empty(half, dtype=torch.float16, device=w.dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        w.all_dequant()
+        w.all_attention()
+        for _ in range(4):
+            dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"[bench] launch pass: {reps} x {w.NL} layers; copy calibration kernel moves "
+        f"{half * 2} B read + {half * 2} B written")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -59,127 +179,94 @@ def main() -> int:
     ap.add_argument("--tokens", type=int, default=32768)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--launch-pass", action="store_true",
+                    help="eager launches only (for rocprofv3 counter runs); no JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the path has no cross-GPU "
-              "exchange; see DESIGN.md on sharding) — run with --gpus 1", file=sys.stderr)
+              "exchange; each GPU would serve its own layers' pools) — run with --gpus 1",
+              file=sys.stderr)
         return 2
 
-    import numpy as np
     import torch
 
-    from turborag_amd.synthetic import gqa_rows, permuted_slots, query
-    from turborag_amd.turboquant_wrapper import TurboQuantWrapper
+    w = Workload(args.layers, args.tokens)
+    if args.launch_pass:
+        launch_pass(w, max(1, args.steps))
+        return 0
 
-    dev = torch.device("cuda", 0)
-    tq = TurboQuantWrapper()
-    H, D, B, N, NL = 2, 128, 16, args.tokens, args.layers
-    Q_HEADS = 16
-    rows = Q_HEADS // H
-    cfg = tq.default_config()
-    cfg.num_kv_heads, cfg.head_dim, cfg.block_size = H, D, B
-    lp = tq.make_layout_for(cfg)
-    pages = (N + B - 1) // B
-
-    log(f"[bench] setup: {NL} layers x {N} tokens, packing on the GPU")
-    slots = permuted_slots(N, B, seed=401).to(dev)
-    pools = []
-    for layer in range(NL):
-        k, v = gpu_kv(N, H, D, 300 + layer, dev)
-        pool = torch.zeros(pages * lp.page_size_bytes, dtype=torch.uint8, device=dev)
-        tq.pack(k, v, slots, pool, lp, cfg)
-        pools.append(pool)
-    del k, v
-    out_k = [torch.empty(N, H, D, dtype=torch.float16, device=dev) for _ in range(NL)]
-    out_v = [torch.empty(N, H, D, dtype=torch.float16, device=dev) for _ in range(NL)]
-    qa = gqa_rows(query(Q_HEADS, D, seed=400), H).to(dev)
-    att = [torch.empty(rows, H, D, dtype=torch.float16, device=dev) for _ in range(NL)]
-    torch.cuda.synchronize()
-
-    def dequant(layer):
-        tq.dequant(pools[layer], slots, out_k[layer], out_v[layer], lp, cfg,
-                   stream=torch.cuda.current_stream().cuda_stream)
-
-    def attention(layer):
-        tq.fused_attn_output(qa, pools[layer], slots, att[layer], lp, cfg, rows, N,
-                             stream=torch.cuda.current_stream().cuda_stream)
-
-    def step():
-        for layer in range(NL):
-            dequant(layer)
-        for layer in range(NL):
-            attention(layer)
-
-    # Algorithmic bytes: pages read + fp16 written + slot map.
-    pool_bytes = pages * lp.page_size_bytes
-    slot_bytes = N * 4
-    deq_bytes = pool_bytes + 2 * N * H * D * 2 + slot_bytes
-    att_bytes = pool_bytes + slot_bytes + 2 * rows * H * D * 2
-    step_bytes = NL * (deq_bytes + att_bytes)
-
-    # Whole step, replayed from a HIP graph so host launch cost is not timed.
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
-        step()  # sizes this stream's split-K workspace before capture
+        w.step()  # sizes this stream's split-K workspace before capture
     torch.cuda.synchronize()
     use_graph = not args.no_graph
-    graph = None
+    g_step = g_deq = g_att = None
     if use_graph:
-        try:
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph, stream=side):
-                step()
-            torch.cuda.synchronize()
-        except Exception as e:  # fall back to eager launches
-            log(f"[bench] graph capture failed ({e}); timing eager launches")
-            graph, use_graph = None, False
+        g_step = capture(w.step, side)
+        g_deq = capture(w.all_dequant, side)
+        g_att = capture(w.all_attention, side)
+        use_graph = None not in (g_step, g_deq, g_att)
+    run_step = g_step.replay if use_graph else w.step
+    run_deq = g_deq.replay if use_graph else w.all_dequant
+    run_att = g_att.replay if use_graph else w.all_attention
 
-    run = graph.replay if graph is not None else step
+    # The timed region: K whole steps.
     for _ in range(args.warmup):
-        run()
+        run_step()
     torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    ev0.record()
     for _ in range(args.steps):
-        run()
+        run_step()
+    ev1.record()
     torch.cuda.synchronize()
     ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
-    log(f"[bench] step {ms_per_step:.3f} ms ({'graph' if use_graph else 'eager'})")
+    ev_ms_per_step = ev0.elapsed_time(ev1) / args.steps
+    log(f"[bench] step {ms_per_step:.3f} ms wall, {ev_ms_per_step:.3f} ms events "
+        f"({'graph' if use_graph else 'eager'})")
 
-    # Per-launch durations from HIP events bracketing each launch on its stream.
-    def per_launch_us(fn, reps=3):
-        evs = []
-        for _ in range(reps):
-            for layer in range(NL):
-                a = torch.cuda.Event(enable_timing=True)
-                b = torch.cuda.Event(enable_timing=True)
-                a.record()
-                fn(layer)
-                b.record()
-                evs.append((a, b))
-        torch.cuda.synchronize()
-        return statistics.mean(a.elapsed_time(b) * 1e3 for a, b in evs)
-
-    deq_us = per_launch_us(dequant)
-    att_us = per_launch_us(attention)
-    deq_gbps = deq_bytes / (deq_us * 1e-6) / 1e9
-    att_gbps = att_bytes / (att_us * 1e-6) / 1e9
+    # Per-kernel averages: graphs of the 36 dequant launches and of the 36
+    # attention launches (split + combine), replayed and timed with events.
+    reps = max(3, args.steps)
+    deq_us = event_time_us(run_deq, reps) / w.NL
+    att_us = event_time_us(run_att, reps) / w.NL
+    deq_gbps = w.deq_bytes / (deq_us * 1e-6) / 1e9
+    att_gbps = w.att_bytes / (att_us * 1e-6) / 1e9
     log(f"[bench] dequant {deq_us:.2f} us/layer {deq_gbps:.0f} GB/s; "
         f"attention {att_us:.2f} us/layer {att_gbps:.0f} GB/s")
+
+    # A plain device copy of the dequant's byte count, MALL-cold (36 buffers).
+    half = w.deq_bytes // 4
+    srcs = [torch.ones(half, dtype=torch.float16, device=w.dev) for _ in range(8)]
+    dsts = [torch.empty_like(s) for s in srcs]
+
+    def copies():
+        for s, d in zip(srcs, dsts):
+            d.copy_(s)
+    copy_us = event_time_us(copies, reps) / len(srcs)
+    del srcs, dsts
 
     traffic = None
     tf = ROOT / "profiles" / "traffic.json"
     if tf.exists():
+        # HBM bytes per dequant dispatch of this workload, from the two
+        # calibrated counter runs (FETCH_SIZE, WRITE_SIZE) stored beside the
+        # profiles.
         try:
-            traffic = json.loads(tf.read_text()).get("dequant_turbo_prod_32k", {}).get("bytes")
-        except Exception:
+            for name, k in json.loads(tf.read_text()).get("kernels", {}).items():
+                if "dequant" in name and "true" in name:
+                    traffic = k["bytes"]
+        except (ValueError, OSError, KeyError):
             traffic = None
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(tq, pools[0], slots, qa, N, H, D, B, deq_bytes, att_bytes, rows)
+        cpu = cpu_baseline(w)
 
-    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    value = w.step_bytes / (ms_per_step * 1e-3) / 1e9
     line = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -194,10 +281,11 @@ def main() -> int:
         "dtype": "fp32",
         "data": "synthetic",
         "config": {
-            "workload": "C3+C4: per layer, turbo_prod dequant [32768,2,128] + GQA 16/2 decode "
-                        "attention @32K, 36 layers, shuffled 16-token pages",
-            "layers": NL, "tokens": N, "kv_heads": H, "q_heads": Q_HEADS, "head_dim": D,
-            "page_tokens": B, "scheme": "turbo_prod", "graph_replay": use_graph,
+            "workload": "per layer: turbo_prod dequant [32768,2,128] + GQA 16/2 decode "
+                        "attention @32K, 36 layers (Qwen2.5-3B shape), shuffled 16-token pages",
+            "layers": w.NL, "tokens": w.N, "kv_heads": w.H, "q_heads": w.q_heads,
+            "head_dim": w.D, "page_tokens": w.B, "scheme": "turbo_prod",
+            "graph_replay": bool(use_graph),
         },
         "roofline": {
             "bound": "hbm",
@@ -207,56 +295,59 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(deq_gbps / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
-            "algorithmic_bytes": deq_bytes,
+            "algorithmic_bytes": w.deq_bytes,
             "avg_launch_us": round(deq_us, 3),
+            "copy_same_bytes_us": round(copy_us, 3),
         },
         "decode_attn": {
             "us_per_layer": round(att_us, 3),
             "achieved_GBps": round(att_gbps, 1),
             "frac_hbm": round(att_gbps / HBM_PEAK_GBPS, 4),
-            "algorithmic_bytes": att_bytes,
+            "algorithmic_bytes": w.att_bytes,
         },
+        "step_ms_events": round(ev_ms_per_step, 4),
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
     return 0
 
 
-def cpu_baseline(tq, pool, slots, qa, N, H, D, B, deq_bytes, att_bytes, rows):
+def cpu_baseline(w: Workload):
     """The oracle (a C port of the reference's dequant and of its attention
-    kernel's fp32 algorithm) on this host's cores, one layer of each."""
-    import numpy as np
-
+    kernel's fp32 algorithm) on this host's cores: whole layers of the same
+    step, cycling through the 36 pools, for about 10 s of CPU time."""
     from oracle.oracle import load
     from turborag_amd.synthetic import as_u16
     orc = load()
     cores = max(1, min(16, os.cpu_count() or 1))
     orc.nthreads = cores
-    pool_np = pool.cpu().numpy()
-    slots_np = slots.cpu().numpy()
-    q_np = as_u16(qa)
-    times = []
+    slots_np = w.slots.cpu().numpy()
+    q_np = as_u16(w.qa)
+    td = ta = 0.0
+    layers = 0
     t_start = time.perf_counter()
-    while len(times) < 5 and (time.perf_counter() - t_start) < 20:
+    while layers < 8 * w.NL and (layers < 2 or time.perf_counter() - t_start < 10.0):
+        pool_np = w.pools[layers % w.NL].cpu().numpy()
         t0 = time.perf_counter()
-        orc.prod_dequant(pool_np, slots_np, H, D, B)
+        orc.prod_dequant(pool_np, slots_np, w.H, w.D, w.B)
         t1 = time.perf_counter()
-        orc.prod_attention_f32(q_np, pool_np, slots_np, B)
+        orc.prod_attention_f32(q_np, pool_np, slots_np, w.B)
         t2 = time.perf_counter()
-        times.append((t1 - t0, t2 - t1))
-    td = statistics.median(t[0] for t in times)
-    ta = statistics.median(t[1] for t in times)
-    log(f"[bench] cpu oracle ({cores} threads): dequant {td*1e3:.1f} ms, attention {ta*1e3:.1f} ms")
+        td += t1 - t0
+        ta += t2 - t1
+        layers += 1
+    log(f"[bench] cpu oracle ({cores} threads, {layers} layers): dequant "
+        f"{td / layers * 1e3:.1f} ms/layer, attention {ta / layers * 1e3:.1f} ms/layer")
     return {
-        "value": round((deq_bytes + att_bytes) / (td + ta) / 1e9, 3),
+        "value": round(layers * (w.deq_bytes + w.att_bytes) / (td + ta) / 1e9, 3),
         "unit": "GB/s",
         "cores": cores,
         "kind": "port",
-        "sample": f"one layer: turbo_prod dequant of {N} tokens x {H} heads + the reference "
-                  f"kernel's fp32 attention algorithm for {rows} GQA rows x {H} heads over "
-                  f"{N} tokens; median of {len(times)} runs",
-        "dequant_ms": round(td * 1e3, 2),
-        "attention_ms": round(ta * 1e3, 2),
+        "sample": f"{layers} layers (cycling the step's 36 pools): turbo_prod dequant of {w.N} tokens x {w.H} "
+                  f"heads + the reference kernel's fp32 attention algorithm for {w.rows} GQA "
+                  f"rows x {w.H} heads over {w.N} tokens, per layer",
+        "dequant_ms_per_layer": round(td / layers * 1e3, 2),
+        "attention_ms_per_layer": round(ta / layers * 1e3, 2),
     }
 
 
