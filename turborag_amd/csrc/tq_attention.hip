@@ -224,7 +224,7 @@ constexpr float kAlphaK = 1.2918981f;
 constexpr float kAlphaV = 1.5982153f;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kRows = 8;     // query rows per workgroup (16 MFMA columns, hi/lo)
-constexpr int kPartStride = 128 + 2;  // floats per partial row: o[128], m, l
+constexpr int kPartStride = 128 + 4;  // floats per partial row: o[128], m, l, pad (16-B rows)
 
 __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
     return __builtin_bit_cast(uint32_t, (half2v){(_Float16)a, (_Float16)b});
@@ -251,14 +251,21 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     constexpr int kTiles = CH / 16, kSteps = CH / 32;
     static_assert(CH == 32 || CH == 64, "chunk of 32 or 64 tokens");
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
-    __shared__ uint2 lutK[256];     // prod: (aK*K3 pair, sign pair); mse: (aV*V4 pair, -)
-    __shared__ uint32_t lutV[256];  // aV*V4 pair
+    // Decode tables indexed by a code byte (low nibble = even d), fp16 pairs:
+    // table 0 = K (prod: aK*K3, mse: aV*V4), table 1 = V (aV*V4), 32 copies
+    // each.  Entry e of table t, copy c is word e*64 + 32t + c and lane l
+    // reads copy l % 32, so a half-wave's 32 random lookups hit 32 distinct
+    // banks.  After the token loop the space holds the per-wave results for
+    // the merge.
+    __shared__ __attribute__((aligned(256))) uint32_t lut[256][64];
     __shared__ float qs[kRows][128];
     __shared__ uint4 bqs[4][64];  // QK B operand (fp16 hi/lo q) of k-step s for lane l
     __shared__ uint64_t tko[kWaves][kChunk], tvo[kWaves][kChunk];
     __shared__ float4 tsc[kWaves][kChunk];  // per token: K scale a, residual scale b, vs, bias
-    __shared__ float mo[kWaves][kRows][128];
     __shared__ float mm[kWaves][kRows], ml[kWaves][kRows];
+    __shared__ uint32_t kstage[256], vstage[256];
+    static_assert(sizeof(float) * kWaves * kRows * 128 <= sizeof(lut), "merge space");
+    float(*mo)[kRows][128] = reinterpret_cast<float(*)[kRows][128]>(&lut[0][0]);
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int i = lane & 15, gq = lane >> 4;
@@ -318,15 +325,36 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     Chunk cur;
     if (t0 < t_end) fetch(t0, cur);  // in flight during the setup below
 
-    if (tid < 256) {  // decode tables, entry = code byte (low nibble = even d)
-        const int lo = tid & 15, hi = tid >> 4;
-        const float al = PROD ? kAlphaK : kAlphaV;
-        const float vlo = pick(kV4, lo), vhi = pick(kV4, hi);
-        const float klo = PROD ? pick(kK3, lo & 7) : vlo, khi = PROD ? pick(kK3, hi & 7) : vhi;
-        const uint32_t sgn = pack_h2((lo & 8) ? 1.0f : -1.0f, (hi & 8) ? 1.0f : -1.0f);
-        lutK[tid] = make_uint2(pack_h2(al * klo, al * khi), PROD ? sgn : 0u);
-        lutV[tid] = pack_h2(kAlphaV * vlo, kAlphaV * vhi);
+    {  // decode tables: one entry per thread into a staging row, then every
+       // wave replicates rows with conflict-free 1 KB stores (4 rows each).
+        if (tid < 256) {
+            const int lo = tid & 15, hi = tid >> 4;
+            const float vlo = pick(kV4, lo), vhi = pick(kV4, hi);
+            const uint32_t vv = pack_h2(kAlphaV * vlo, kAlphaV * vhi);
+            const uint32_t kv =
+                PROD ? pack_h2(kAlphaK * pick(kK3, lo & 7), kAlphaK * pick(kK3, hi & 7)) : vv;
+            kstage[tid] = kv;
+            vstage[tid] = vv;
+        }
+        __syncthreads();
+        constexpr int kRowsPerWave = 256 / kWaves;
+#pragma unroll
+        for (int k = 0; k < kRowsPerWave; k += 4) {
+            const int e = w * kRowsPerWave + k + (lane >> 4);
+            const uint32_t v = (lane & 8) ? vstage[e] : kstage[e];  // words 32..63: V
+            *reinterpret_cast<uint4*>(&lut[e][4 * (lane & 15)]) = make_uint4(v, v, v, v);
+        }
     }
+    // Byte address of this lane's copy of entry 0 of each table; a lookup
+    // puts the code byte into byte 1 (entry stride 256 B) with one v_perm.
+    const uint32_t lutk = (uint32_t)reinterpret_cast<uintptr_t>((lds_u32*)&lut[0][lane & 31]);
+    const uint32_t lutv = lutk + 128u;
+    const uint32_t lut_hi = lutk & 0xFF00u;  // byte 1 of the base, re-added after the perm
+    auto lookup = [&](uint32_t word, int b, int table) -> uint32_t {
+        const uint32_t base = table ? lutv : lutk;
+        const uint32_t a = __builtin_amdgcn_perm(word, base, 0x03020000u | ((4u + b) << 8)) + lut_hi;
+        return *reinterpret_cast<const lds_u32*>(a);
+    };
     // Rotated query rows of this group (wave w: rows w, w + NW, ...):
     // qrot = WHT(q * s) * inv.
     for (int r = w; r < kRows; r += kWaves) {
@@ -383,13 +411,22 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
             const uint32_t wd[4] = {kw[tau].x, kw[tau].y, kw[tau].z, kw[tau].w};
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                const uint2 e0 = lutK[wd[s] & 0xff], e1 = lutK[(wd[s] >> 8) & 0xff];
-                const uint2 e2 = lutK[(wd[s] >> 16) & 0xff], e3 = lutK[wd[s] >> 24];
-                cb[tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(e0.x, e1.x, e2.x, e3.x),
-                                                                bq[s], cb[tau], 0, 0, 0);
-                if (PROD)
+                cb[tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    as_h8(lookup(wd[s], 0, 0), lookup(wd[s], 1, 0), lookup(wd[s], 2, 0),
+                          lookup(wd[s], 3, 0)),
+                    bq[s], cb[tau], 0, 0, 0);
+                if (PROD) {
+                    // Residual signs (nibble bit 3: 1 -> +1) as fp16 pairs in
+                    // registers: high bytes 0x3C / 0xBC, low bytes 0.
+                    const uint32_t he = ((wd[s] << 4) & 0x80808080u) ^ 0xBCBCBCBCu;  // even d
+                    const uint32_t ho = (wd[s] & 0x80808080u) ^ 0xBCBCBCBCu;         // odd d
                     cs[tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                        as_h8(e0.y, e1.y, e2.y, e3.y), bq[s], cs[tau], 0, 0, 0);
+                        as_h8(__builtin_amdgcn_perm(ho, he, 0x040C000Cu),
+                              __builtin_amdgcn_perm(ho, he, 0x050C010Cu),
+                              __builtin_amdgcn_perm(ho, he, 0x060C020Cu),
+                              __builtin_amdgcn_perm(ho, he, 0x070C030Cu)),
+                        bq[s], cs[tau], 0, 0, 0);
+                }
             }
         }
         // Logits (base 2) of tokens 16*tau + 4*gq + e; hi + lo columns summed.
@@ -450,8 +487,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                 const uint32_t hib = ((we >> 4) & 0x0F0F0F0Fu) | (wo & 0xF0F0F0F0u);
 #pragma unroll
                 for (int b = 0; b < 4; ++b) {
-                    bv[2 * b][q] = lutV[(lob >> (8 * b)) & 0xff];
-                    bv[2 * b + 1][q] = lutV[(hib >> (8 * b)) & 0xff];
+                    bv[2 * b][q] = lookup(lob, b, 1);
+                    bv[2 * b + 1][q] = lookup(hib, b, 1);
                 }
             }
 #pragma unroll
@@ -474,6 +511,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
         mm[w][i >> 1] = m_run;
         ml[w][i >> 1] = l_tot;
     }
+    __syncthreads();  // every wave is done with the tables that mo overwrites
     const float iav = 1.0f / kAlphaV;
 #pragma unroll
     for (int v = 0; v < 8; ++v) {

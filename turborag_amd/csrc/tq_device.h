@@ -45,6 +45,7 @@ __device__ __forceinline__ float pick(const float (&t)[N], int idx) {
 
 // A float in LDS addressed by its 32-bit LDS byte offset.
 typedef __attribute__((address_space(3))) float lds_float;
+typedef __attribute__((address_space(3))) uint32_t lds_u32;
 
 __device__ __forceinline__ float h2f(uint16_t h) {
     return __half2float(__ushort_as_half(h));
