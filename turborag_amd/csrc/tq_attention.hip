@@ -232,6 +232,13 @@ __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
 __device__ __forceinline__ half8 as_h8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
     return __builtin_bit_cast(half8, (u32x4){a, b, c, d});
 }
+// Workgroup barrier for LDS traffic only: waits for this wave's LDS accesses,
+// not for its outstanding global loads (which __syncthreads() would drain).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 // fp16 hi or lo part of x: lo = fp16(x - fp32(fp16(x))) (the difference is exact).
 __device__ __forceinline__ _Float16 hi_lo(float x, bool lo) {
     const _Float16 h = (_Float16)x;
@@ -267,7 +274,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     static_assert(sizeof(float) * kWaves * kRows * 128 <= sizeof(lut), "merge space");
     float(*mo)[kRows][128] = reinterpret_cast<float(*)[kRows][128]>(&lut[0][0]);
 
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
     const int i = lane & 15, gq = lane >> 4;
     const int split = blockIdx.x % num_splits;
     const int hr = blockIdx.x / num_splits;
@@ -284,33 +292,39 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
         uint16_t ks, re, vs;  // this lane's token's fp16 scales (raw: still in flight)
         bool valid;
     };
-    // slot -> cell offsets (exchanged through LDS) -> code loads; the scale
-    // loads stay in flight in registers until the chunk is computed.
-    auto fetch = [&](int t0, Chunk& c) {
-        const int t = t0 + (lane & (kChunk - 1));
-        uint64_t ko = 0, vo = 0;  // tokens past the range read page 0 and get bias -inf
-        c.valid = t < t_end;
-        c.ks = c.re = c.vs = 0;
-        if (c.valid) {
-            int page, tib;
-            split_slot(slots[t], g, page, tib);
-            const uint64_t cell = (uint64_t)(tib * g.H + h);
-            const uint64_t pb = (uint64_t)page * g.page_size;
-            ko = pb + g.kc_off + cell * g.code_stride;
-            vo = pb + g.vc_off + cell * g.code_stride;
-            c.ks = ld_u16(pool + pb + g.ks_off + cell * g.scale_stride);
-            c.vs = ld_u16(pool + pb + g.vs_off + cell * g.scale_stride);
-            if (PROD) c.re = ld_u16(pool + pb + g.kres_off + cell * g.scale_stride);
-        }
-        if (lane < kChunk) {
-            tko[w][lane] = ko;
-            tvo[w][lane] = vo;
-        }
+    // Token of this lane in the chunk at t0 and its slot (the load is issued
+    // here and consumed by fetch, so other work can run in between).  Lanes
+    // past the range re-read the last token of the range.
+    auto load_slot = [&](int t0) -> int {
+        return slots[max(min(t0 + (lane & (kChunk - 1)), t_end - 1), 0)];
+    };
+    // slot -> cell offsets (exchanged through LDS) -> scale and code loads,
+    // issued for every lane.  Tokens past the range or with a negative slot
+    // read the first bytes of the query instead (always valid memory: the
+    // offset of the query from the pool) and get bias -inf.  The loads stay in
+    // flight until the chunk is computed.
+    const uint64_t dummy_off =
+        (uint64_t)(reinterpret_cast<uintptr_t>(query) - reinterpret_cast<uintptr_t>(pool));
+    auto fetch = [&](int t0, int slot, Chunk& c) {
+        c.valid = t0 + (lane & (kChunk - 1)) < t_end && slot >= 0;
+        int page, tib;
+        split_slot(c.valid ? slot : 0, g, page, tib);
+        const uint64_t cell = (uint64_t)(tib * g.H + h);
+        const uint64_t pb = (uint64_t)page * g.page_size;
+        // Byte offsets from pool (integer selects: no branches around loads).
+        // (distinct dummy bytes per field, so the three loads stay separate)
+        const uint64_t so = pb + cell * g.scale_stride;
+        c.ks = ld_u16(pool + (c.valid ? so + g.ks_off : dummy_off));
+        c.vs = ld_u16(pool + (c.valid ? so + g.vs_off : dummy_off + 2));
+        c.re = PROD ? ld_u16(pool + (c.valid ? so + g.kres_off : dummy_off + 4)) : (uint16_t)0;
+        // (with 32-token chunks lanes l and l + 32 hold the same token)
+        tko[w][lane & (kChunk - 1)] = c.valid ? pb + g.kc_off + cell * g.code_stride : dummy_off;
+        tvo[w][lane & (kChunk - 1)] = c.valid ? pb + g.vc_off + cell * g.code_stride : dummy_off;
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
         for (int tau = 0; tau < kTiles; ++tau)
-            c.kw[tau] = *reinterpret_cast<const uint4*>(pool + tko[w][16 * tau + i] + 16 * gq);
+            c.kw[tau] = *reinterpret_cast<const uint4*>(pool + (tko[w][16 * tau + i] + 16 * gq));
         // k-step p covers tiles 2p, 2p+1; k-index 8gq + e is token
         // 32p + 4gq + e (e < 4) or 32p + 16 + 4gq + (e - 4).
 #pragma unroll
@@ -318,25 +332,64 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const int tok = 32 * p + (e < 4 ? 4 * gq + e : 16 + 4 * gq + (e - 4));
-                c.vw[p][e] = *reinterpret_cast<const uint32_t*>(pool + tvo[w][tok] + 4 * i);
+                c.vw[p][e] = *reinterpret_cast<const uint32_t*>(pool + (tvo[w][tok] + 4 * i));
             }
     };
-    int t0 = t_begin + w * kChunk;
-    Chunk cur;
-    if (t0 < t_end) fetch(t0, cur);  // in flight during the setup below
 
-    {  // decode tables: one entry per thread into a staging row, then every
-       // wave replicates rows with conflict-free 1 KB stores (4 rows each).
-        if (tid < 256) {
-            const int lo = tid & 15, hi = tid >> 4;
-            const float vlo = pick(kV4, lo), vhi = pick(kV4, hi);
-            const uint32_t vv = pack_h2(kAlphaV * vlo, kAlphaV * vhi);
-            const uint32_t kv =
-                PROD ? pack_h2(kAlphaK * pick(kK3, lo & 7), kAlphaK * pick(kK3, hi & 7)) : vv;
-            kstage[tid] = kv;
-            vstage[tid] = vv;
+    // Issue order matters (the vector-memory counter is in order): query
+    // rows first, then the first chunk's slots; the decode tables are built
+    // while they are in flight.
+    constexpr int kQPerWave = kRows / kWaves;
+    static_assert(kRows % kWaves == 0, "rows per wave");
+    uint32_t qraw[kQPerWave];
+#pragma unroll
+    for (int k = 0; k < kQPerWave; ++k) {
+        const int qi = min(rg * kRows + w + k * kWaves, num_queries - 1);
+        qraw[k] = *reinterpret_cast<const uint32_t*>(query + ((size_t)qi * g.H + h) * 128 +
+                                                      2 * lane);
+    }
+    int t0 = t_begin + w * kChunk;
+    const int slot0 = load_slot(t0);
+
+    // Decode tables: one entry per thread into a staging row (waves 0-3).
+    if (w < 4) {
+        const int lo = tid & 15, hi = tid >> 4;
+        const float vlo = pick(kV4, lo), vhi = pick(kV4, hi);
+        const uint32_t vv = pack_h2(kAlphaV * vlo, kAlphaV * vhi);
+        const uint32_t kv =
+            PROD ? pack_h2(kAlphaK * pick(kK3, lo & 7), kAlphaK * pick(kK3, hi & 7)) : vv;
+        kstage[tid] = kv;
+        vstage[tid] = vv;
+    }
+    // Query halves to fp32 (times the sign flip) before the code loads are
+    // issued, so waiting for them never waits for the codes.
+    float qf[kQPerWave][2];
+    {
+        const float sh = (h & 1) ? -1.0f : 1.0f;
+#pragma unroll
+        for (int k = 0; k < kQPerWave; ++k) {
+            qf[k][0] = h2f(qraw[k] & 0xffff) * sh;
+            qf[k][1] = h2f(qraw[k] >> 16) * (-sh);
         }
-        __syncthreads();
+    }
+    Chunk cur;
+    fetch(t0, slot0, cur);  // in flight during the setup below (empty waves: all invalid)
+
+    // Rotated query rows of this group (wave w: rows w, w + NW, ...):
+    // qrot = WHT(q * s) * inv.
+#pragma unroll
+    for (int k = 0; k < kQPerWave; ++k) {
+        const int r = w + k * kWaves;
+        float q0 = qf[k][0], q1 = qf[k][1];
+        wht_pair_wave(q0, q1, lane);
+        const bool live = rg * kRows + r < num_queries;
+        qs[r][2 * lane] = live ? q0 * inv : 0.0f;
+        qs[r][2 * lane + 1] = live ? q1 * inv : 0.0f;
+    }
+    lds_barrier();  // staged table rows and rotated queries visible
+
+    // Every wave replicates staged rows with conflict-free 1 KB stores.
+    {
         constexpr int kRowsPerWave = 256 / kWaves;
 #pragma unroll
         for (int k = 0; k < kRowsPerWave; k += 4) {
@@ -345,6 +398,20 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
             *reinterpret_cast<uint4*>(&lut[e][4 * (lane & 15)]) = make_uint4(v, v, v, v);
         }
     }
+    // B operand of QK, built once per workgroup: column i = row i/2, hi (i
+    // even) or lo (i odd) part; k-index 8*gq + e of step s is d = 32*gq + 8*s + e.
+    const bool lo_col = (i & 1) != 0;
+    if (w < 4) {
+        const int s = w;
+        half8 b;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) b[e] = hi_lo(qs[i >> 1][32 * gq + 8 * s + e], lo_col);
+        bqs[s][lane] = __builtin_bit_cast(uint4, b);
+    }
+    lds_barrier();
+    half8 bq[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) bq[s] = __builtin_bit_cast(half8, bqs[s][lane]);
     // Byte address of this lane's copy of entry 0 of each table; a lookup
     // puts the code byte into byte 1 (entry stride 256 B) with one v_perm.
     const uint32_t lutk = (uint32_t)reinterpret_cast<uintptr_t>((lds_u32*)&lut[0][lane & 31]);
@@ -355,52 +422,30 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
         const uint32_t a = __builtin_amdgcn_perm(word, base, 0x03020000u | ((4u + b) << 8)) + lut_hi;
         return *reinterpret_cast<const lds_u32*>(a);
     };
-    // Rotated query rows of this group (wave w: rows w, w + NW, ...):
-    // qrot = WHT(q * s) * inv.
-    for (int r = w; r < kRows; r += kWaves) {
-        const int qi = rg * kRows + r;
-        float q0 = 0.0f, q1 = 0.0f;
-        const uint16_t* qp = query + ((size_t)min(qi, num_queries - 1) * g.H + h) * 128;
-        rotate_query<64>(qp, h, lane, inv, q0, q1);
-        qs[r][2 * lane] = qi < num_queries ? q0 : 0.0f;
-        qs[r][2 * lane + 1] = qi < num_queries ? q1 : 0.0f;
-    }
-    __syncthreads();
-
-    // B operand of QK, built once per workgroup: column i = row i/2, hi (i
-    // even) or lo (i odd) part; k-index 8*gq + e of step s is d = 32*gq + 8*s + e.
-    const bool lo_col = (i & 1) != 0;
-    if (tid < 256) {
-        const int s = tid >> 6;
-        half8 b;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) b[e] = hi_lo(qs[i >> 1][32 * gq + 8 * s + e], lo_col);
-        bqs[s][lane] = __builtin_bit_cast(uint4, b);
-    }
-    __syncthreads();
-    half8 bq[4];
-#pragma unroll
-    for (int s = 0; s < 4; ++s) bq[s] = __builtin_bit_cast(half8, bqs[s][lane]);
 
     float m_run = kInitMax, l_run = 0.0f;
     f32x4 acc[8];
 #pragma unroll
     for (int v = 0; v < 8; ++v) acc[v] = (f32x4){0.f, 0.f, 0.f, 0.f};
     bool first = true;
+    int slot_nx = load_slot(t0 + kWaves * kChunk);
 
     while (t0 < t_end) {  // wave-uniform
         const uint4* kw = cur.kw;
         const uint32_t(*vw)[8] = cur.vw;
-        if (lane < kChunk) {
+        {
             const float ks = h2f(cur.ks), vs = h2f(cur.vs), re = PROD ? h2f(cur.re) : 0.0f;
-            tsc[w][lane] = cur.valid ? make_float4(ks * ck, ks * re * cr, vs, 0.0f)
-                                     : make_float4(0.f, 0.f, 0.f, -INFINITY);
+            tsc[w][lane & (kChunk - 1)] = cur.valid ? make_float4(ks * ck, ks * re * cr, vs, 0.0f)
+                                                    : make_float4(0.f, 0.f, 0.f, -INFINITY);
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         Chunk nxt;
         const int t1 = t0 + kWaves * kChunk;
-        if (t1 < t_end) fetch(t1, nxt);
+        if (t1 < t_end) {  // codes of the next chunk, slots of the one after
+            fetch(t1, slot_nx, nxt);
+            slot_nx = load_slot(t1 + kWaves * kChunk);
+        }
 
         // QK
         f32x4 cb[kTiles], cs[kTiles];
@@ -533,7 +578,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
             o0 += mo[u][r][2 * lane] * wt;
             o1 += mo[u][r][2 * lane + 1] * wt;
         }
-        wht_pair<64>(o0, o1, lane);
+        wht_pair_wave(o0, o1, lane);
         const float s0 = (h & 1) ? -inv : inv;
         float* part = ws + ((size_t)blockIdx.x * kRows + r) * kPartStride;
         part[2 * lane] = o0 * s0;
@@ -669,6 +714,12 @@ void launch_attention(Scheme s, const uint16_t* query, const uint8_t* pool, cons
             workspace(stream, blocks * kRows * kPartStride * sizeof(float)));
         const bool prod = s == Scheme::Prod;
         constexpr int kCH = kSplitChunk, kNW = kSplitWaves;
+        if (num_kv_tokens == 0) {  // no partials: the combine writes the zero output
+            hipLaunchKernelGGL(attn_mfma_combine_kernel, dim3(4 * rows), dim3(256), 0, stream, ws,
+                               output, g.H, 0);
+            check_launch(prod ? "turbo_prod_fused_attn_combine" : "turbo_mse_fused_attn_combine");
+            return;
+        }
         if (prod)
             hipLaunchKernelGGL((attn_mfma_split_kernel<true, kCH, kNW>), dim3(blocks),
                                dim3(64 * kNW), 0, stream, query, pool, slots, ws, g, num_queries,

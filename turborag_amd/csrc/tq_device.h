@@ -89,6 +89,48 @@ __device__ __forceinline__ float quad_xor(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), ctrl, 0xF, 0xF, true));
 }
 
+// v of lane j ^ M across a full wave64, without LDS: DPP quad permutes for
+// M = 1, 2; half-row mirror then quad reverse for 4; row rotate by 8 for 8;
+// the gfx950 permlane16 / permlane32 swaps for 16 and 32.
+template <int M>
+__device__ __forceinline__ float lane_xor(float v, int j) {
+    const int x = __float_as_int(v);
+    if constexpr (M == 1 || M == 2) {
+        return quad_xor<M>(v);
+    } else if constexpr (M == 4) {
+        const int t = __builtin_amdgcn_mov_dpp(x, 0x141, 0xF, 0xF, true);  // row_half_mirror
+        return __int_as_float(__builtin_amdgcn_mov_dpp(t, 0x1B, 0xF, 0xF, true));  // quad 3210
+    } else if constexpr (M == 8) {
+        return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, true));  // row_ror:8
+    } else if constexpr (M == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap((unsigned)x, (unsigned)x, false, false);
+        return __uint_as_float((j & 16) ? r[0] : r[1]);
+    } else {
+        static_assert(M == 32, "lane_xor: M in 1..32");
+        const auto r = __builtin_amdgcn_permlane32_swap((unsigned)x, (unsigned)x, false, false);
+        return __uint_as_float((j & 32) ? r[0] : r[1]);
+    }
+}
+
+// wht_pair<64> with the lane exchanges done by lane_xor (same arithmetic, so
+// the same bits); every lane of the wave must be active.
+__device__ __forceinline__ void wht_pair_wave(float& x0, float& x1, int j) {
+    const float a = x0 + x1, b = x0 - x1;
+    x0 = a;
+    x1 = b;
+    auto stage = [&](float p0, float p1, int m) {
+        const bool lower = (j & m) == 0;
+        x0 = lower ? x0 + p0 : p0 - x0;
+        x1 = lower ? x1 + p1 : p1 - x1;
+    };
+    stage(lane_xor<1>(x0, j), lane_xor<1>(x1, j), 1);
+    stage(lane_xor<2>(x0, j), lane_xor<2>(x1, j), 2);
+    stage(lane_xor<4>(x0, j), lane_xor<4>(x1, j), 4);
+    stage(lane_xor<8>(x0, j), lane_xor<8>(x1, j), 8);
+    stage(lane_xor<16>(x0, j), lane_xor<16>(x1, j), 16);
+    stage(lane_xor<32>(x0, j), lane_xor<32>(x1, j), 32);
+}
+
 // In-place WHT of a row held two-per-lane (lane index j within its row).
 template <int L>
 __device__ __forceinline__ void wht_pair(float& x0, float& x1, int j) {
