@@ -421,6 +421,10 @@ static void prod_logits_one(void* p, long long row) {
     float inv = tqo_inv_sqrt_d(D);
     for (int t = 0; t < c->N; ++t) {
         cell_t ce;
+        if (c->slots[t] < 0) { /* this build's extension: unmapped token */
+            c->logits_f[((size_t)qi * c->H + h) * (size_t)c->N + t] = -INFINITY;
+            continue;
+        }
         prod_cell(c, t, h, &ce);
         float res_ks = ce.ks * ce.re;
         for (int i = 0; i < D; ++i) red[i] = qrot[i] * kK3[nib_get(ce.k, i) & 7] * ce.ks;
@@ -455,6 +459,7 @@ static void attention_f64_one(att_ctx* c, long long row, int is_prod) {
     double mx = -INFINITY;
     for (int t = 0; t < N; ++t) {
         cell_t ce;
+        if (c->slots[t] < 0) { lg[t] = -INFINITY; continue; } /* unmapped token */
         if (is_prod) prod_cell(c, t, h, &ce); else mse_cell(c, t, h, &ce);
         double s1 = 0.0, s2 = 0.0;
         for (int i = 0; i < D; ++i) {
@@ -472,6 +477,7 @@ static void attention_f64_one(att_ctx* c, long long row, int is_prod) {
     double l = 0.0;
     for (int t = 0; t < N; ++t) {
         cell_t ce;
+        if (c->slots[t] < 0) continue;
         if (is_prod) prod_cell(c, t, h, &ce); else mse_cell(c, t, h, &ce);
         double w = exp(lg[t] - mx);
         l += w;
@@ -512,6 +518,7 @@ static void attention_f32_one(att_ctx* c, long long row, int is_prod) {
     for (int t = 0; t < c->N; ++t) {
         cell_t ce;
         float logit;
+        if (c->slots[t] < 0) continue; /* unmapped token (this build's extension) */
         if (is_prod) {
             prod_cell(c, t, h, &ce);
             float res_ks = ce.ks * ce.re;

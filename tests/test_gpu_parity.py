@@ -137,6 +137,36 @@ def test_attention_vs_exact_oracle(tq, oracle, cuda, scheme, Q, H, D, N, B, seed
 
 
 @pytest.mark.parametrize("scheme", ["turbo_prod", "turbo_mse"])
+@pytest.mark.parametrize("Q,H,D,N,seed", [(8, 2, 128, 3000, 51), (3, 2, 64, 700, 52)])
+def test_attention_skips_unmapped_tokens(tq, oracle, cuda, scheme, Q, H, D, N, seed):
+    """Slots < 0 (unmapped tokens) are excluded from the softmax: every 7th
+    token unmapped, and one split range with no mapped token at all."""
+    print(f"[attention holes {scheme}] Q={Q} H={H} D={D} N={N}", flush=True)
+    B = 16
+    k, v = kv_tokens_major(N, H, D, seed=seed)
+    slots = permuted_slots(N, B, seed=seed + 1)
+    pages = int(slots.max()) // B + 1
+    q = kv_tokens_major(Q, H, D, seed=seed + 2)[0]
+    cfg, lp, lm = _cfg(tq, H, D, B)
+    if scheme == "turbo_prod":
+        pool_np = oracle.prod_pack(as_u16(k), as_u16(v), slots.numpy(), pages, B)
+    else:
+        pool_np = oracle.mse_pack(as_u16(k), as_u16(v), slots.numpy(), pages, B)
+    slots[::7] = -1
+    slots[256:600] = -1
+    ref = (oracle.prod_attention_f64 if scheme == "turbo_prod" else oracle.mse_attention_f64)(
+        as_u16(q), pool_np, slots.numpy(), B)
+    out = torch.zeros(Q, H, D, dtype=torch.float16, device=cuda)
+    fn = tq.fused_attn_output if scheme == "turbo_prod" else tq.mse_fused_attn_output
+    fn(q.to(cuda), torch.from_numpy(pool_np).to(cuda), slots.to(cuda), out,
+       lp if scheme == "turbo_prod" else lm, cfg, Q, N)
+    torch.cuda.synchronize()
+    err = _rel_err(out.cpu().float().numpy(), ref)
+    print(f"    rel err {err:.3e}", flush=True)
+    assert err < ATT_TOL
+
+
+@pytest.mark.parametrize("scheme", ["turbo_prod", "turbo_mse"])
 def test_attention_empty_context_is_zero(tq, cuda, scheme):
     """num_kv_tokens == 0: l = 0 -> 1/l taken as 1, output +-0 (:562)."""
     cfg, lp, lm = _cfg(tq, 2, 128)
@@ -197,6 +227,28 @@ def test_logits_vs_oracle(tq, oracle, cuda, Q, H, D, N, B, seed):
     scale = np.abs(ref64).max(axis=-1, keepdims=True) + 1e-30
     assert (np.abs(got - ref64) / scale).max() < 1e-5
     assert (np.abs(ref32 - ref64) / scale).max() < 1e-5
+
+
+def test_logits_unmapped_tokens_are_neg_inf(tq, oracle, cuda):
+    Q, H, D, N, B = 4, 2, 128, 300, 16
+    k, v = kv_tokens_major(N, H, D, seed=61)
+    slots = permuted_slots(N, B, seed=62)
+    pages = int(slots.max()) // B + 1
+    q = kv_tokens_major(Q, H, D, seed=63)[0]
+    cfg, lp, _ = _cfg(tq, H, D, B)
+    pool_np = oracle.prod_pack(as_u16(k), as_u16(v), slots.numpy(), pages, B)
+    slots[::5] = -1
+    ref32 = oracle.prod_logits(as_u16(q), pool_np, slots.numpy(), B)
+    logits = torch.zeros(Q * H * N, dtype=torch.float32, device=cuda)
+    tq.fused_attn_logits(q.to(cuda), torch.from_numpy(pool_np).to(cuda), slots.to(cuda), logits,
+                         lp, cfg, Q, N)
+    torch.cuda.synchronize()
+    got = logits.cpu().numpy().reshape(Q, H, N)
+    hole = slots.numpy() < 0
+    assert np.all(np.isneginf(got[:, :, hole])) and np.all(np.isneginf(ref32[:, :, hole]))
+    live = ~hole
+    scale = np.abs(ref32[:, :, live]).max(axis=-1, keepdims=True)
+    assert (np.abs(got[:, :, live] - ref32[:, :, live]) / scale).max() < 1e-5
 
 
 # ---- full-size properties (BASELINE configs 2 and 3), sampled against the oracle ---

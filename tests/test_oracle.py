@@ -8,6 +8,7 @@ import pytest
 import scipy.linalg
 
 from oracle.oracle import REF_DIR
+from turborag_amd.synthetic import as_u16, kv_tokens_major, permuted_slots
 
 K3_LITERALS = [-2.1513, -1.34326, -0.755526, -0.244919, 0.244919, 0.755526, 1.34326, 2.1513]
 V4_LITERALS = [-2.7326, -2.0690, -1.6180, -1.2562, -0.9423, -0.6568, -0.3880, -0.1284,
@@ -314,3 +315,22 @@ def test_attention_single_token_is_value(oracle):
     out = oracle.prod_attention_f64(q, pool, slots)
     want = ov[0].view(np.float16).astype(np.float64)
     assert np.allclose(out[0], want, rtol=1e-3, atol=1e-3)
+
+
+def test_attention_unmapped_tokens_equal_compacted_list(oracle):
+    """This build's extension: a token with slot < 0 is excluded, so the
+    result equals attention over the list with those tokens removed
+    (fp64 and the reference-order fp32 restatement, both schemes)."""
+    N, H, D, B = 300, 2, 128, 16
+    k, v = kv_tokens_major(N, H, D, seed=5)
+    s = permuted_slots(N, B, seed=6)
+    pages = int(s.max()) // B + 1
+    q = kv_tokens_major(4, H, D, seed=7)[0]
+    holes = s.numpy().copy()
+    holes[::3] = -1
+    kept = holes[holes >= 0].copy()
+    for pack, f64, f32 in ((oracle.prod_pack, oracle.prod_attention_f64, oracle.prod_attention_f32),
+                           (oracle.mse_pack, oracle.mse_attention_f64, oracle.mse_attention_f32)):
+        pool = pack(as_u16(k), as_u16(v), s.numpy(), pages, B)
+        assert np.array_equal(f64(as_u16(q), pool, holes, B), f64(as_u16(q), pool, kept, B))
+        assert np.array_equal(f32(as_u16(q), pool, holes, B), f32(as_u16(q), pool, kept, B))

@@ -76,6 +76,7 @@ __global__ __launch_bounds__(64) void attn_partial_kernel(
     const int t1 = min(num_kv_tokens, t0 + tokens_per_split);
     float m = kInitMax, l = 0.0f, a0 = 0.0f, a1 = 0.0f;
     for (int t = t0; t < t1; ++t) {
+        if (slots[t] < 0) continue;  // unmapped token (wave-uniform)
         const CellPtrs c = cell_of(pool, slots, t, h, g);
         const uint32_t kb = c.base[g.kc_off + c.cell * g.code_stride + j];
         const float ks = h2f(ld_u16(c.base + g.ks_off + c.cell * g.scale_stride));
@@ -170,6 +171,10 @@ __global__ __launch_bounds__(256) void prod_logits_kernel(
     __syncthreads();
     const int t = tile * 256 + threadIdx.x;
     if (t >= num_kv_tokens) return;
+    if (slots[t] < 0) {  // unmapped token: excluded, like a -inf logit
+        logits[(size_t)row * num_kv_tokens + t] = -INFINITY;
+        return;
+    }
     const CellPtrs c = cell_of(pool, slots, t, h, g);
     const uint8_t* kc = c.base + g.kc_off + c.cell * g.code_stride;
     const float ks = h2f(ld_u16(c.base + g.ks_off + c.cell * g.scale_stride));
