@@ -351,23 +351,18 @@ __global__ __launch_bounds__(kBlock) void dequant_stream_kernel(
     while (grp < groups) {  // wave-uniform
         const Item nxt = fetch(grp + stride, s_next);
         s_next = load_slot(grp + 2 * stride);
-        // Lane j computes entries j*PER .. j*PER + PER-1 and writes each into
-        // the private copies of all LPR lanes of its row (adjacent words).
+        // Every lane writes all 16 entries of its own copies (one b32 store
+        // per entry and tensor; a wave's 64 stores fill 64 distinct banks).
         {
-            typedef float vecL __attribute__((ext_vector_type(LPR)));
-            constexpr int PER = 16 / LPR;
-            float* rowK = &tab[0][0][wave][LPR * rw];
-            float* rowV = &tab[1][0][wave][LPR * rw];
+            float* myK = &tab[0][0][wave][lane];
+            float* myV = &tab[1][0][wave][lane];
 #pragma unroll
-            for (int q = 0; q < PER; ++q) {
-                const int n = j * PER + q;
-                const float v4n = pick(kV4, n);
+            for (int n = 0; n < 16; ++n) {
                 const float kv =
-                    PROD ? (pick(kK3, n & 7) + cur.re * ((n & 8) ? 1.0f : -1.0f)) * cur.ks
-                         : v4n * cur.ks;
-                const float vv = v4n * cur.vs;
-                *reinterpret_cast<vecL*>(rowK + n * kWaves * 64) = (vecL)(kv);
-                *reinterpret_cast<vecL*>(rowV + n * kWaves * 64) = (vecL)(vv);
+                    PROD ? (kK3[n & 7] + cur.re * ((n & 8) ? 1.0f : -1.0f)) * cur.ks
+                         : kV4[n] * cur.ks;
+                myK[n * kWaves * 64] = kv;
+                myV[n * kWaves * 64] = kV4[n] * cur.vs;
             }
         }
         // The table is private to this wave: wave-scope ordering suffices.
