@@ -146,6 +146,44 @@ int tq_launch_turbo_mse_fused_attention_output(const uint16_t* query, const uint
                                                int num_kv_tokens, void* stream);
 
 /* ---------------------------------------------------------------------- */
+/* Layer loading into the cache layout (superset of the reference ABI).     */
+/* Replaces the load path of tq_backend/cag_store.py:161-288: per layer a   */
+/* synchronous pageable copy of the .bin pages, dequant to [N, H, D], then  */
+/* a permute copy to the DynamicCache layout [1, H, N, D] (:248-252).        */
+/* ---------------------------------------------------------------------- */
+
+/* As tq_launch_turbo_prod_dequant_kv, but out_key / out_value are
+ * [1, H, num_tokens, D] fp16 (token t of head h at (h * num_tokens + t) * D). */
+int tq_launch_turbo_prod_dequant_kv_hnd(const uint8_t* page_pool, const int32_t* slot_mapping,
+                                        uint16_t* out_key, uint16_t* out_value,
+                                        const TQTurboProdPageLayout* layout, const TQConfig* cfg,
+                                        int num_tokens, void* stream);
+int tq_launch_turbo_mse_dequant_kv_hnd(const uint8_t* page_pool, const int32_t* slot_mapping,
+                                       uint16_t* out_key, uint16_t* out_value,
+                                       const TQTurbomsePageLayout* layout, const TQConfig* cfg,
+                                       int num_tokens, void* stream);
+
+/* For each layer l < num_layers: copies pool_bytes bytes from host_pools[l]
+ * to device_pools[l] on copy_stream and dequantizes device_pools[l] into
+ * out_key[l] / out_value[l] ([1, H, num_tokens, D] fp16) on compute_stream,
+ * which waits for layer l's copy only; layer l's dequant overlaps layer
+ * l+1's copy.  Copies start after the work already on compute_stream.
+ * slot_mapping is device int32[num_tokens].  Asynchronous: completion is
+ * ordered on compute_stream.  Host pages in pinned memory overlap fully;
+ * pageable pages are correct but copied at the runtime's staging rate.
+ * copy_stream == compute_stream is allowed (no overlap). */
+int tq_load_turbo_prod_layers(const uint8_t* const* host_pools, uint8_t* const* device_pools,
+                              size_t pool_bytes, int num_layers, const int32_t* slot_mapping,
+                              int num_tokens, uint16_t* const* out_key,
+                              uint16_t* const* out_value, const TQTurboProdPageLayout* layout,
+                              const TQConfig* cfg, void* copy_stream, void* compute_stream);
+int tq_load_turbo_mse_layers(const uint8_t* const* host_pools, uint8_t* const* device_pools,
+                             size_t pool_bytes, int num_layers, const int32_t* slot_mapping,
+                             int num_tokens, uint16_t* const* out_key, uint16_t* const* out_value,
+                             const TQTurbomsePageLayout* layout, const TQConfig* cfg,
+                             void* copy_stream, void* compute_stream);
+
+/* ---------------------------------------------------------------------- */
 /* Page allocator and block table (host bookkeeping).                       */
 /* Replaces TQAllocator (src/tq_allocator.cpp:5-31, include/tq_allocator.h) */
 /* and TQBlockTable (src/tq_block_table.cpp:4-43), which the reference      */

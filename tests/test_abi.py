@@ -104,6 +104,37 @@ def test_null_pointers_return_minus_one(tq):
                                             None) == -1
     assert L.tq_launch_turbo_mse_fused_attention_output(fake, u8, i32, nul, byref(lm),
                                                         byref(cfg), 1, 1, None) == -1
+    assert L.tq_launch_turbo_prod_dequant_kv_hnd(u8, nul, fake, fake, byref(lp), byref(cfg), 1,
+                                                 None) == -1
+    assert L.tq_launch_turbo_mse_dequant_kv_hnd(u8, i32, fake, fake, byref(lm), nul, 1,
+                                                None) == -1
+    arr = (c_void_p * 1)(fake)
+    assert L.tq_load_turbo_prod_layers(nul, arr, 8, 1, i32, 1, arr, arr, byref(lp), byref(cfg),
+                                       None, None) == -1
+    assert L.tq_load_turbo_mse_layers(arr, arr, 8, 1, i32, 1, arr, nul, byref(lm), byref(cfg),
+                                      None, None) == -1
+
+
+def test_loader_argument_errors_before_any_hip_call(tq):
+    """Zero layers is a no-op; negative counts and bad layouts are rc -2,
+    all decided on the host."""
+    L = tq.lib
+    cfg, lp, lm = _cfg_layout(tq)
+    fake = c_void_p(0x1000)
+    i32 = ctypes.cast(fake, ctypes.POINTER(c_int32))
+    arr = (c_void_p * 1)(fake)
+    assert L.tq_load_turbo_prod_layers(arr, arr, 8, 0, i32, 16, arr, arr, byref(lp), byref(cfg),
+                                       None, None) == 0
+    assert L.tq_load_turbo_prod_layers(arr, arr, 8, -1, i32, 16, arr, arr, byref(lp),
+                                       byref(cfg), None, None) == -2
+    assert b"num_layers" in L.tq_last_error()
+    bad = type(lp)()
+    ctypes.memmove(byref(bad), byref(lp), ctypes.sizeof(lp))
+    bad.k4_bytes_per_token_head = 32
+    assert L.tq_load_turbo_prod_layers(arr, arr, 8, 1, i32, 16, arr, arr, byref(bad),
+                                       byref(cfg), None, None) == -2
+    assert L.tq_load_turbo_mse_layers(arr, arr, 8, 0, i32, 16, arr, arr, byref(lm), byref(cfg),
+                                      None, None) == 0
 
 
 def test_head_dim_errors_return_minus_two(tq):

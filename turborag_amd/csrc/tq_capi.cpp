@@ -286,6 +286,43 @@ extern "C" int tq_launch_turbo_prod_fused_attention_output(
     });
 }
 
+extern "C" int tq_launch_turbo_prod_dequant_kv_hnd(const uint8_t* page_pool,
+                                                   const int32_t* slot_mapping,
+                                                   uint16_t* out_key, uint16_t* out_value,
+                                                   const TQTurboProdPageLayout* layout,
+                                                   const TQConfig* cfg, int num_tokens,
+                                                   void* stream) {
+    if (!page_pool || !slot_mapping || !out_key || !out_value || !layout || !cfg) return -1;
+    return guarded([&] {
+        const tq::PageGeom g = tq::prod_geom(*cfg, *layout);
+        check_grid(num_tokens, "turbo_prod_dequant_kv_kernel", true);
+        tq::launch_dequant(tq::Scheme::Prod, page_pool, slot_mapping, out_key, out_value, g,
+                           num_tokens, static_cast<hipStream_t>(stream), /*head_major=*/true);
+    });
+}
+
+extern "C" int tq_load_turbo_prod_layers(const uint8_t* const* host_pools,
+                                         uint8_t* const* device_pools, size_t pool_bytes,
+                                         int num_layers, const int32_t* slot_mapping,
+                                         int num_tokens, uint16_t* const* out_key,
+                                         uint16_t* const* out_value,
+                                         const TQTurboProdPageLayout* layout,
+                                         const TQConfig* cfg, void* copy_stream,
+                                         void* compute_stream) {
+    if (!host_pools || !device_pools || !slot_mapping || !out_key || !out_value || !layout ||
+        !cfg)
+        return -1;
+    return guarded([&] {
+        const tq::PageGeom g = tq::prod_geom(*cfg, *layout);
+        if (num_layers < 0 || num_tokens < 0)
+            throw tq::Error("turbo_prod load: num_layers and num_tokens must be >= 0");
+        tq::load_layers(tq::Scheme::Prod, host_pools, device_pools, pool_bytes, num_layers,
+                        slot_mapping, num_tokens, out_key, out_value, g,
+                        static_cast<hipStream_t>(copy_stream),
+                        static_cast<hipStream_t>(compute_stream));
+    });
+}
+
 // ---------------------------------------------------------------------------
 // turbo_mse
 // ---------------------------------------------------------------------------
@@ -328,5 +365,41 @@ extern "C" int tq_launch_turbo_mse_fused_attention_output(
         if (num_kv_tokens < 0) throw tq::Error("turbo_mse attention: num_kv_tokens < 0");
         tq::launch_attention(tq::Scheme::Mse, query, page_pool, slot_mapping, output, g,
                              num_queries, num_kv_tokens, static_cast<hipStream_t>(stream));
+    });
+}
+
+extern "C" int tq_launch_turbo_mse_dequant_kv_hnd(const uint8_t* page_pool,
+                                                  const int32_t* slot_mapping, uint16_t* out_key,
+                                                  uint16_t* out_value,
+                                                  const TQTurbomsePageLayout* layout,
+                                                  const TQConfig* cfg, int num_tokens,
+                                                  void* stream) {
+    if (!page_pool || !slot_mapping || !out_key || !out_value || !layout || !cfg) return -1;
+    return guarded([&] {
+        const tq::PageGeom g = tq::mse_geom(*cfg, *layout);
+        check_grid(num_tokens, "turbo_mse_dequant_kv_kernel", false);
+        tq::launch_dequant(tq::Scheme::Mse, page_pool, slot_mapping, out_key, out_value, g,
+                           num_tokens, static_cast<hipStream_t>(stream), /*head_major=*/true);
+    });
+}
+
+extern "C" int tq_load_turbo_mse_layers(const uint8_t* const* host_pools,
+                                        uint8_t* const* device_pools, size_t pool_bytes,
+                                        int num_layers, const int32_t* slot_mapping,
+                                        int num_tokens, uint16_t* const* out_key,
+                                        uint16_t* const* out_value,
+                                        const TQTurbomsePageLayout* layout, const TQConfig* cfg,
+                                        void* copy_stream, void* compute_stream) {
+    if (!host_pools || !device_pools || !slot_mapping || !out_key || !out_value || !layout ||
+        !cfg)
+        return -1;
+    return guarded([&] {
+        const tq::PageGeom g = tq::mse_geom(*cfg, *layout);
+        if (num_layers < 0 || num_tokens < 0)
+            throw tq::Error("turbo_mse load: num_layers and num_tokens must be >= 0");
+        tq::load_layers(tq::Scheme::Mse, host_pools, device_pools, pool_bytes, num_layers,
+                        slot_mapping, num_tokens, out_key, out_value, g,
+                        static_cast<hipStream_t>(copy_stream),
+                        static_cast<hipStream_t>(compute_stream));
     });
 }

@@ -141,7 +141,7 @@ template <int D, bool PROD>
 __global__ __launch_bounds__(kBlock) void dequant_kernel(
     const uint8_t* __restrict__ pool, const int32_t* __restrict__ slots,
     uint16_t* __restrict__ out_key, uint16_t* __restrict__ out_value, PageGeom g, int num_rows,
-    float inv) {
+    float inv, OutLayout ol) {
     constexpr int L = D / 2;
     __shared__ float tk[16], tv[16];
     if (threadIdx.x < 16) {
@@ -185,7 +185,7 @@ __global__ __launch_bounds__(kBlock) void dequant_kernel(
     const float s0 = (h & 1) ? -inv : inv;  // s(2j, h) * inv; s(2j+1, h) = -s(2j, h)
     const uint32_t ko = (uint32_t)f2h(k0 * s0) | ((uint32_t)f2h(k1 * -s0) << 16);
     const uint32_t vo = (uint32_t)f2h(v0 * s0) | ((uint32_t)f2h(v1 * -s0) << 16);
-    const size_t off = (size_t)rr * D + 2 * j;
+    const size_t off = ol.offset(t, h) + 2 * j;
     *reinterpret_cast<uint32_t*>(out_key + off) = ko;
     *reinterpret_cast<uint32_t*>(out_value + off) = vo;
 }
@@ -207,7 +207,7 @@ template <int D, bool PROD>
 __global__ __launch_bounds__(kBlock) void dequant_stream_kernel(
     const uint8_t* __restrict__ pool, const int32_t* __restrict__ slots,
     uint16_t* __restrict__ out_key, uint16_t* __restrict__ out_value, PageGeom g, int num_rows,
-    float inv) {
+    float inv, OutLayout ol) {
     constexpr int E = 32;           // elements per lane
     constexpr int LPR = D / E;      // lanes per row
     constexpr int RPW = 64 / LPR;   // rows per wave group
@@ -235,7 +235,7 @@ __global__ __launch_bounds__(kBlock) void dequant_stream_kernel(
     struct Item {
         uint4 kw, vw;
         float ks, re, vs;
-        int row, h;
+        int row, t, h;
         bool live;
     };
     auto token_head = [&](int row, int& t, int& h) {
@@ -257,8 +257,7 @@ __global__ __launch_bounds__(kBlock) void dequant_stream_kernel(
     auto fetch = [&](int grp, int slot) -> Item {
         Item it;
         it.row = grp * RPW + rw;
-        int t;
-        token_head(min(it.row, num_rows - 1), t, it.h);
+        token_head(min(it.row, num_rows - 1), it.t, it.h);
         it.live = grp < groups && it.row < num_rows && slot >= 0;
         it.kw = make_uint4(0, 0, 0, 0);
         it.vw = it.kw;
@@ -336,7 +335,7 @@ __global__ __launch_bounds__(kBlock) void dequant_stream_kernel(
         if (!it.live) return;
         // Element 8*(j + LPR*m) + i has sign (-1)^(i + h).
         const float se = (it.h & 1) ? -inv : inv;
-        uint4* d = reinterpret_cast<uint4*>(out + (size_t)it.row * D) + j;
+        uint4* d = reinterpret_cast<uint4*>(out + ol.offset(it.t, it.h)) + j;
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
             const float* c = x + 8 * m;
@@ -421,10 +420,14 @@ void launch_pack(Scheme s, const uint16_t* key, const uint16_t* value, const int
 }
 
 void launch_dequant(Scheme s, const uint8_t* pool, const int32_t* slots, uint16_t* out_key,
-                    uint16_t* out_value, const PageGeom& g, int num_tokens, hipStream_t stream) {
+                    uint16_t* out_value, const PageGeom& g, int num_tokens, hipStream_t stream,
+                    bool head_major) {
     const int rows = num_tokens * g.H;
     if (rows <= 0) return;
     const float inv = inv_sqrt_d(g.D);
+    OutLayout ol;  // element offset of row (t, h): [N, H, D] or [H, N, D]
+    ol.tok = head_major ? (uint64_t)g.D : (uint64_t)g.H * g.D;
+    ol.head = head_major ? (uint64_t)num_tokens * g.D : (uint64_t)g.D;
     if (wide_dequant_ok(g, pool, out_key, out_value)) {
         // Persistent waves: up to four workgroups (one wave per SIMD each) per
         // CU, fewer when there is not enough work (measured: 4 per CU beats
@@ -435,7 +438,7 @@ void launch_dequant(Scheme s, const uint8_t* pool, const int32_t* slots, uint16_
         const bool prod = s == Scheme::Prod;
         auto go = [&](auto kernel) {
             hipLaunchKernelGGL(kernel, grid, dim3(kBlock), 0, stream, pool, slots, out_key,
-                               out_value, g, rows, inv);
+                               out_value, g, rows, inv, ol);
         };
         if (g.D == 128) prod ? go(dequant_stream_kernel<128, true>) : go(dequant_stream_kernel<128, false>);
         else if (g.D == 64) prod ? go(dequant_stream_kernel<64, true>) : go(dequant_stream_kernel<64, false>);
@@ -448,12 +451,12 @@ void launch_dequant(Scheme s, const uint8_t* pool, const int32_t* slots, uint16_
     if (s == Scheme::Prod) {
         TQ_DISPATCH_D(g.D, hipLaunchKernelGGL((dequant_kernel<kD, true>), grid, dim3(kBlock), 0,
                                               stream, pool, slots, out_key, out_value, g, rows,
-                                              inv));
+                                              inv, ol));
         check_launch("turbo_prod_dequant_kv_kernel");
     } else {
         TQ_DISPATCH_D(g.D, hipLaunchKernelGGL((dequant_kernel<kD, false>), grid, dim3(kBlock), 0,
                                               stream, pool, slots, out_key, out_value, g, rows,
-                                              inv));
+                                              inv, ol));
         check_launch("turbo_mse_dequant_kv_kernel");
     }
 }

@@ -38,6 +38,15 @@ struct PageGeom {
     int h_shift;   // log2(H) when H is a power of two, else -1
 };
 
+// Element offset of output row (token t, head h) of a dequant: t * tok +
+// h * head ([N, H, D]: tok = H*D, head = D; [H, N, D]: tok = D, head = N*D).
+struct OutLayout {
+    uint64_t tok, head;
+    __host__ __device__ uint64_t offset(int t, int h) const {
+        return (uint64_t)t * tok + (uint64_t)h * head;
+    }
+};
+
 // Number of compute units of the current device (cached per device).
 int num_cus();
 
@@ -60,8 +69,15 @@ void* workspace(hipStream_t stream, size_t bytes);
 // ---- launchers (tq_prod.hip, tq_mse.hip, tq_attention.hip) ---------------
 void launch_pack(Scheme s, const uint16_t* key, const uint16_t* value, const int32_t* slots,
                  uint8_t* pool, const PageGeom& g, int num_tokens, hipStream_t stream);
+// head_major: outputs [H, N, D] (a [1, H, N, D] cache tensor) instead of [N, H, D].
 void launch_dequant(Scheme s, const uint8_t* pool, const int32_t* slots, uint16_t* out_key,
-                    uint16_t* out_value, const PageGeom& g, int num_tokens, hipStream_t stream);
+                    uint16_t* out_value, const PageGeom& g, int num_tokens, hipStream_t stream,
+                    bool head_major = false);
+// Layer-pipelined host -> device copy + dequant into [1, H, N, D] (tq_loader.cpp).
+void load_layers(Scheme s, const uint8_t* const* host_pools, uint8_t* const* device_pools,
+                 size_t pool_bytes, int num_layers, const int32_t* slots, int num_tokens,
+                 uint16_t* const* out_key, uint16_t* const* out_value, const PageGeom& g,
+                 hipStream_t copy_stream, hipStream_t compute_stream);
 void launch_logits(const uint16_t* query, const uint8_t* pool, const int32_t* slots,
                    float* logits, const PageGeom& g, int num_queries, int num_kv_tokens,
                    hipStream_t stream);

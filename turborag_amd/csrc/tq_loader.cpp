@@ -1,0 +1,79 @@
+// tq_loader.cpp — layer-pipelined load of compressed KV into cache layout.
+//
+// The reference loads a document layer by layer (tq_backend/cag_store.py:
+// 161-288): read the layer's .bin pages, copy them to the GPU (pageable,
+// synchronous), dequantize to [N, H, D], then permute to the DynamicCache
+// layout [1, H, N, D] with an extra copy.  Here one call enqueues every
+// layer: layer l's pages go host -> device on the copy stream while layer
+// l-1 is dequantized on the compute stream straight into [1, H, N, D]; the
+// compute stream waits for each layer's copy through an event.  With pinned
+// host pages (hipHostMalloc / torch pin_memory) the copies run at link rate
+// and overlap the dequant.
+#include <mutex>
+#include <vector>
+
+#include "tq_internal.h"
+
+namespace {
+
+// Per-device pool of reusable events (a stream wait captures the event's
+// state when it is enqueued, so an event may be re-recorded afterwards).
+std::vector<hipEvent_t>& device_events(int dev, size_t need) {
+    static std::mutex mu;
+    static std::vector<std::vector<hipEvent_t>> pools;
+    std::lock_guard<std::mutex> lock(mu);
+    if ((size_t)dev >= pools.size()) pools.resize(dev + 1);
+    auto& v = pools[dev];
+    while (v.size() < need) {
+        hipEvent_t e = nullptr;
+        if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
+            (void)hipGetLastError();
+            throw tq::Error("hipEventCreateWithFlags failed");
+        }
+        v.push_back(e);
+    }
+    return v;
+}
+
+void check(hipError_t e, const char* what) {
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        throw tq::Error(std::string(what) + ": " + hipGetErrorString(e));
+    }
+}
+
+}  // namespace
+
+namespace tq {
+
+void load_layers(Scheme s, const uint8_t* const* host_pools, uint8_t* const* device_pools,
+                 size_t pool_bytes, int num_layers, const int32_t* slots, int num_tokens,
+                 uint16_t* const* out_key, uint16_t* const* out_value, const PageGeom& g,
+                 hipStream_t copy_stream, hipStream_t compute_stream) {
+    if (num_layers <= 0) return;
+    for (int l = 0; l < num_layers; ++l)
+        if (!host_pools[l] || !device_pools[l] || !out_key[l] || !out_value[l])
+            throw Error("load_layers: null pool or output pointer for a layer");
+    int dev = 0;
+    check(hipGetDevice(&dev), "hipGetDevice");
+    std::vector<hipEvent_t>& ev = device_events(dev, (size_t)num_layers + 1);
+    const bool two = copy_stream != compute_stream;
+    if (two) {
+        // Copies must not overwrite pools that earlier compute work still reads.
+        check(hipEventRecord(ev[num_layers], compute_stream), "hipEventRecord");
+        check(hipStreamWaitEvent(copy_stream, ev[num_layers], 0), "hipStreamWaitEvent");
+    }
+    for (int l = 0; l < num_layers; ++l) {
+        check(hipMemcpyAsync(device_pools[l], host_pools[l], pool_bytes, hipMemcpyHostToDevice,
+                             copy_stream),
+              "hipMemcpyAsync");
+        if (two) {
+            check(hipEventRecord(ev[l], copy_stream), "hipEventRecord");
+            check(hipStreamWaitEvent(compute_stream, ev[l], 0), "hipStreamWaitEvent");
+        }
+        launch_dequant(s, device_pools[l], slots, out_key[l], out_value[l], g, num_tokens,
+                       compute_stream, /*head_major=*/true);
+    }
+}
+
+}  // namespace tq

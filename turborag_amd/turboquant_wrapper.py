@@ -95,6 +95,19 @@ SIGNATURES: dict[str, tuple[list, object]] = {
                                                     c_void_p, _P(TQTurbomsePageLayout),
                                                     _P(TQConfig), c_int, c_int, c_void_p],
                                                    c_int),
+    # cache-layout dequant and layer loading (superset of the reference ABI)
+    "tq_launch_turbo_prod_dequant_kv_hnd": ([_P(c_uint8), _P(c_int32), c_void_p, c_void_p,
+                                             _P(TQTurboProdPageLayout), _P(TQConfig), c_int,
+                                             c_void_p], c_int),
+    "tq_launch_turbo_mse_dequant_kv_hnd": ([_P(c_uint8), _P(c_int32), c_void_p, c_void_p,
+                                            _P(TQTurbomsePageLayout), _P(TQConfig), c_int,
+                                            c_void_p], c_int),
+    "tq_load_turbo_prod_layers": ([_P(c_void_p), _P(c_void_p), c_size_t, c_int, _P(c_int32),
+                                   c_int, _P(c_void_p), _P(c_void_p), _P(TQTurboProdPageLayout),
+                                   _P(TQConfig), c_void_p, c_void_p], c_int),
+    "tq_load_turbo_mse_layers": ([_P(c_void_p), _P(c_void_p), c_size_t, c_int, _P(c_int32),
+                                  c_int, _P(c_void_p), _P(c_void_p), _P(TQTurbomsePageLayout),
+                                  _P(TQConfig), c_void_p, c_void_p], c_int),
     # page allocator / block table
     "tq_allocator_create": ([c_size_t, c_int, c_void_p, _P(c_void_p)], c_int),
     "tq_allocator_destroy": ([c_void_p], c_int),
@@ -310,6 +323,67 @@ class TurboQuantWrapper:
             self._stream(stream))
         if rc != 0:
             self._kernel_raise(rc, "turbo_mse", "fused_attn_output")
+
+    # ── cache layout [1, H, N, D] and layer loading (this build) ────── #
+
+    def _dequant_hnd(self, scheme, page_pool, slot_mapping, out_key, out_value, layout, cfg,
+                     num_tokens, stream):
+        thd = num_tokens * cfg.num_kv_heads * cfg.head_dim
+        self._check(scheme, "dequant_kv_hnd", page_pool=(page_pool, torch.uint8, 0),
+                    slot_mapping=(slot_mapping, torch.int32, num_tokens),
+                    out_key=(out_key, torch.float16, thd), out_value=(out_value, torch.float16, thd))
+        fn = (self._lib.tq_launch_turbo_prod_dequant_kv_hnd if scheme == "turbo_prod"
+              else self._lib.tq_launch_turbo_mse_dequant_kv_hnd)
+        rc = fn(self._u8p(page_pool), self._i32p(slot_mapping), self._vp(out_key),
+                self._vp(out_value), ctypes.byref(layout), ctypes.byref(cfg), num_tokens,
+                self._stream(stream))
+        if rc != 0:
+            self._kernel_raise(rc, scheme, "dequant_kv_hnd")
+
+    def dequant_hnd(self, page_pool, slot_mapping, out_key, out_value, layout, cfg,
+                    num_tokens: int, stream: int = 0) -> None:
+        """turbo_prod dequant straight into the cache layout [1, H, N, D]."""
+        self._dequant_hnd("turbo_prod", page_pool, slot_mapping, out_key, out_value, layout,
+                          cfg, num_tokens, stream)
+
+    def mse_dequant_hnd(self, page_pool, slot_mapping, out_key, out_value, layout, cfg,
+                        num_tokens: int, stream: int = 0) -> None:
+        self._dequant_hnd("turbo_mse", page_pool, slot_mapping, out_key, out_value, layout,
+                          cfg, num_tokens, stream)
+
+    def load_layers(self, scheme: str, host_pools, device_pools, slot_mapping, out_keys,
+                    out_values, layout, cfg, num_tokens: int, copy_stream: int = 0,
+                    compute_stream: int = 0) -> None:
+        """Copy each layer's pages host -> device and dequantize it into
+        out_keys[l] / out_values[l] ([1, H, N, D] fp16), layer l's dequant
+        overlapping layer l+1's copy (pinned host_pools overlap fully)."""
+        L = len(host_pools)
+        if not (len(device_pools) == len(out_keys) == len(out_values) == L):
+            raise ValueError(f"{scheme} load_layers: per-layer lists differ in length")
+        nbytes = host_pools[0].numel() if L else 0
+        thd = num_tokens * cfg.num_kv_heads * cfg.head_dim
+        for l in range(L):
+            hp = host_pools[l]
+            if hp.device.type != "cpu" or hp.dtype != torch.uint8 or not hp.is_contiguous() \
+                    or hp.numel() != nbytes:
+                raise ValueError(f"{scheme} load_layers: host_pools[{l}] must be a contiguous "
+                                 f"CPU uint8 tensor of {nbytes} bytes")
+            self._check(scheme, "load_layers", device_pool=(device_pools[l], torch.uint8, nbytes),
+                        out_key=(out_keys[l], torch.float16, thd),
+                        out_value=(out_values[l], torch.float16, thd))
+        self._check(scheme, "load_layers", slot_mapping=(slot_mapping, torch.int32, num_tokens))
+        arr = c_void_p * max(L, 1)
+        hps = arr(*[t.data_ptr() for t in host_pools])
+        dps = arr(*[t.data_ptr() for t in device_pools])
+        oks = arr(*[t.data_ptr() for t in out_keys])
+        ovs = arr(*[t.data_ptr() for t in out_values])
+        fn = (self._lib.tq_load_turbo_prod_layers if scheme == "turbo_prod"
+              else self._lib.tq_load_turbo_mse_layers)
+        rc = fn(hps, dps, nbytes, L, self._i32p(slot_mapping), num_tokens, oks, ovs,
+                ctypes.byref(layout), ctypes.byref(cfg), self._stream(copy_stream),
+                self._stream(compute_stream))
+        if rc != 0:
+            self._kernel_raise(rc, scheme, "load_layers")
 
     # ── allocation helpers (reference :385-415) ─────────────────────── #
 
