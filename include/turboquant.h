@@ -184,6 +184,35 @@ int tq_load_turbo_mse_layers(const uint8_t* const* host_pools, uint8_t* const* d
                              void* copy_stream, void* compute_stream);
 
 /* ---------------------------------------------------------------------- */
+/* Batched decode over paged sequences (superset of the reference ABI).     */
+/* The reference serves a batch with one fused_attention_output call per    */
+/* sequence and speculative position, each with a per-token slot_mapping    */
+/* (src/tq_capi.cpp:99, :158); this is one launch for all of them.          */
+/* ---------------------------------------------------------------------- */
+
+/* query / output [num_rows, H, D] fp16.  Row r belongs to sequence
+ * row_seq[r] and attends that sequence's first row_kv_len[r] tokens (a
+ * per-row causal limit, e.g. L + j + 1 for speculative position j); the 8
+ * rows of each aligned group (rows 8k .. 8k+7, padding rows with kv length
+ * 0 allowed) must share one sequence.  Token t of sequence s is at position
+ * t % block_size of page block_tables[s * max_blocks_per_seq + t /
+ * block_size]; pages for every token a row attends must be valid.
+ * max_kv_len >= every row_kv_len sizes the launch and must fit in
+ * max_blocks_per_seq pages.  Rows with kv length 0 get 0.  head_dim 128. */
+int tq_launch_turbo_prod_paged_attention(const uint16_t* query, const uint8_t* page_pool,
+                                         const int32_t* block_tables, int max_blocks_per_seq,
+                                         const int32_t* row_seq, const int32_t* row_kv_len,
+                                         uint16_t* output, const TQTurboProdPageLayout* layout,
+                                         const TQConfig* cfg, int num_rows, int max_kv_len,
+                                         void* stream);
+int tq_launch_turbo_mse_paged_attention(const uint16_t* query, const uint8_t* page_pool,
+                                        const int32_t* block_tables, int max_blocks_per_seq,
+                                        const int32_t* row_seq, const int32_t* row_kv_len,
+                                        uint16_t* output, const TQTurbomsePageLayout* layout,
+                                        const TQConfig* cfg, int num_rows, int max_kv_len,
+                                        void* stream);
+
+/* ---------------------------------------------------------------------- */
 /* Page allocator and block table (host bookkeeping).                       */
 /* Replaces TQAllocator (src/tq_allocator.cpp:5-31, include/tq_allocator.h) */
 /* and TQBlockTable (src/tq_block_table.cpp:4-43), which the reference      */

@@ -237,6 +237,17 @@ __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
 __device__ __forceinline__ half8 as_h8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
     return __builtin_bit_cast(half8, (u32x4){a, b, c, d});
 }
+// Batched decode over paged sequences: query row r belongs to sequence
+// row_seq[r] (the 8 rows of an aligned group share one) and attends its
+// first row_kv_len[r] tokens; token t of sequence s is in page
+// block_tables[s * max_blocks + t / B].
+struct PagedRows {
+    const int32_t* block_tables;
+    const int32_t* row_seq;
+    const int32_t* row_kv_len;
+    int max_blocks;
+};
+
 // Workgroup barrier for LDS traffic only: waits for this wave's LDS accesses,
 // not for its outstanding global loads (which __syncthreads() would drain).
 __device__ __forceinline__ void lds_barrier() {
@@ -253,11 +264,11 @@ __device__ __forceinline__ _Float16 hi_lo(float x, bool lo) {
 
 // CH = tokens per wave iteration (32: two QK tiles, one PV step; 64: four and
 // two); NW = waves per workgroup.
-template <bool PROD, int CH, int NW>
+template <bool PROD, int CH, int NW, bool PAGED>
 __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     const uint16_t* __restrict__ query, const uint8_t* __restrict__ pool,
     const int32_t* __restrict__ slots, float* __restrict__ ws, PageGeom g, int num_queries,
-    int num_kv_tokens, int tokens_per_split, int num_splits, float inv) {
+    int num_kv_tokens, int tokens_per_split, int num_splits, float inv, mfma::PagedRows pr) {
     using namespace mfma;
     constexpr int kChunk = CH, kWaves = NW;
     constexpr int kTiles = CH / 16, kSteps = CH / 32;
@@ -288,7 +299,22 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     const float ck = inv * kLog2e / (PROD ? kAlphaK : kAlphaV);  // logit scale per unit ks
     const float cr = inv * kLog2e;                                 // residual: ks * re
     const int t_begin = split * tokens_per_split;
-    const int t_end = min(num_kv_tokens, t_begin + tokens_per_split);
+    // Paged rows: the group's sequence and per-row kv lengths (causal limit);
+    // rowlen is that of this lane's MFMA column row.  A split past every row's
+    // length has no partial (the combine does not read it).
+    int kv_end = num_kv_tokens, seq = 0, rowlen = 0;
+    if constexpr (PAGED) {
+        const int rr = rg * kRows + (lane & 7);
+        const int lv = rr < num_queries ? pr.row_kv_len[rr] : 0;
+        rowlen = __shfl(lv, i >> 1);
+        int m = max(lv, __shfl_xor(lv, 1));
+        m = max(m, __shfl_xor(m, 2));
+        m = max(m, __shfl_xor(m, 4));
+        kv_end = __builtin_amdgcn_readfirstlane(m);
+        seq = __builtin_amdgcn_readfirstlane(pr.row_seq[rg * kRows]);
+        if (t_begin >= kv_end) return;  // uniform over the workgroup, before any barrier
+    }
+    const int t_end = min(kv_end, t_begin + tokens_per_split);
 
     // A chunk's codes and per-token scales, loaded ahead of its compute.
     struct Chunk {
@@ -301,7 +327,15 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     // here and consumed by fetch, so other work can run in between).  Lanes
     // past the range re-read the last token of the range.
     auto load_slot = [&](int t0) -> int {
-        return slots[max(min(t0 + (lane & (kChunk - 1)), t_end - 1), 0)];
+        const int t = max(min(t0 + (lane & (kChunk - 1)), t_end - 1), 0);
+        if constexpr (PAGED) {  // token t of sequence seq: page table entry t / B
+            const int blk = min(g.bs_shift >= 0 ? t >> g.bs_shift : t / g.block_size,
+                                pr.max_blocks - 1);
+            const int page = pr.block_tables[(size_t)seq * pr.max_blocks + blk];
+            return page < 0 ? -1 : page * g.block_size + (t - blk * g.block_size);
+        } else {
+            return slots[t];
+        }
     };
     // slot -> cell offsets (exchanged through LDS) -> scale and code loads,
     // issued for every lane.  Tokens past the range or with a negative slot
@@ -490,6 +524,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                 const float sb = cb[tau][e] + quad_xor<1>(cb[tau][e]);
                 const float sr = PROD ? cs[tau][e] + quad_xor<1>(cs[tau][e]) : 0.0f;
                 lg[tau][e] = fmaf(sb, sc.x, fmaf(sr, sc.y, sc.w));
+                if constexpr (PAGED)  // causal limit of this column's row
+                    if (t0 + 16 * tau + 4 * gq + e >= rowlen) lg[tau][e] = -INFINITY;
                 mloc = fmaxf(mloc, lg[tau][e]);
             }
         mloc = fmaxf(mloc, shfl_xor(mloc, 16));
@@ -600,8 +636,12 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
 // threads = 8 groups x 32 d.  Group g takes splits g, g + 8, ...: it loads up
 // to 16 partials' (m, l, o[d]) in one round, merges them with a running
 // maximum, and the 8 groups are merged in LDS.
+// PAGED: the group's splits stop at its longest row (later splits wrote no
+// partial); num_queries and tokens_per_split are only used then.
+template <bool PAGED>
 __global__ __launch_bounds__(256) void attn_mfma_combine_kernel(
-    const float* __restrict__ ws, uint16_t* __restrict__ output, int H, int num_splits) {
+    const float* __restrict__ ws, uint16_t* __restrict__ output, int H, int num_splits,
+    int num_queries, int tokens_per_split, mfma::PagedRows pr) {
     using namespace mfma;
     constexpr int kBatch = 16;
     __shared__ float red_m[8], red_l[8];
@@ -613,15 +653,23 @@ __global__ __launch_bounds__(256) void attn_mfma_combine_kernel(
     const int d = 32 * dq + dd;
     const size_t base_bid = (size_t)(rg * H + h) * num_splits;
     auto part = [&](int s) { return ws + ((base_bid + s) * kRows + r) * kPartStride; };
+    int S = num_splits;
+    if constexpr (PAGED) {
+        int kv = 0;
+#pragma unroll
+        for (int k = 0; k < kRows; ++k)
+            kv = max(kv, rg * kRows + k < num_queries ? pr.row_kv_len[rg * kRows + k] : 0);
+        S = min(num_splits, (kv + tokens_per_split - 1) / tokens_per_split);
+    }
 
     float M = kInitMax, L = 0.f, acc = 0.f;
-    for (int base = sg; base < num_splits; base += 8 * kBatch) {
+    for (int base = sg; base < S; base += 8 * kBatch) {
         float pm[kBatch], pl[kBatch], po[kBatch];
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
             const int s = base + 8 * k;
-            const float* p = part(s < num_splits ? s : base);
-            pm[k] = s < num_splits ? p[128] : kInitMax;
+            const float* p = part(s < S ? s : base);
+            pm[k] = s < S ? p[128] : kInitMax;
             pl[k] = p[129];
             po[k] = p[d];
         }
@@ -719,23 +767,24 @@ void launch_attention(Scheme s, const uint16_t* query, const uint8_t* pool, cons
             workspace(stream, blocks * kRows * kPartStride * sizeof(float)));
         const bool prod = s == Scheme::Prod;
         constexpr int kCH = kSplitChunk, kNW = kSplitWaves;
+        const PagedRows none{};
         if (num_kv_tokens == 0) {  // no partials: the combine writes the zero output
-            hipLaunchKernelGGL(attn_mfma_combine_kernel, dim3(4 * rows), dim3(256), 0, stream, ws,
-                               output, g.H, 0);
+            hipLaunchKernelGGL(attn_mfma_combine_kernel<false>, dim3(4 * rows), dim3(256), 0,
+                               stream, ws, output, g.H, 0, num_queries, 1, none);
             check_launch(prod ? "turbo_prod_fused_attn_combine" : "turbo_mse_fused_attn_combine");
             return;
         }
         if (prod)
-            hipLaunchKernelGGL((attn_mfma_split_kernel<true, kCH, kNW>), dim3(blocks),
+            hipLaunchKernelGGL((attn_mfma_split_kernel<true, kCH, kNW, false>), dim3(blocks),
                                dim3(64 * kNW), 0, stream, query, pool, slots, ws, g, num_queries,
-                               num_kv_tokens, tps, splits, inv);
+                               num_kv_tokens, tps, splits, inv, none);
         else
-            hipLaunchKernelGGL((attn_mfma_split_kernel<false, kCH, kNW>), dim3(blocks),
+            hipLaunchKernelGGL((attn_mfma_split_kernel<false, kCH, kNW, false>), dim3(blocks),
                                dim3(64 * kNW), 0, stream, query, pool, slots, ws, g, num_queries,
-                               num_kv_tokens, tps, splits, inv);
+                               num_kv_tokens, tps, splits, inv, none);
         check_launch(prod ? "turbo_prod_fused_attn_split" : "turbo_mse_fused_attn_split");
-        hipLaunchKernelGGL(attn_mfma_combine_kernel, dim3(4 * rows), dim3(256), 0, stream, ws,
-                           output, g.H, splits);
+        hipLaunchKernelGGL(attn_mfma_combine_kernel<false>, dim3(4 * rows), dim3(256), 0, stream,
+                           ws, output, g.H, splits, num_queries, tps, none);
         check_launch(prod ? "turbo_prod_fused_attn_combine" : "turbo_mse_fused_attn_combine");
         return;
     }
@@ -763,6 +812,47 @@ void launch_attention(Scheme s, const uint16_t* query, const uint8_t* pool, cons
     TQ_DISPATCH_D(g.D, hipLaunchKernelGGL(attn_combine_kernel<kD>, dim3(rows), dim3(64), 0,
                                           stream, ws, output, g, rows, splits, inv));
     check_launch(prod ? "turbo_prod_fused_attn_combine" : "turbo_mse_fused_attn_combine");
+}
+
+void launch_paged_attention(Scheme s, const uint16_t* query, const uint8_t* pool,
+                            const int32_t* block_tables, int max_blocks, const int32_t* row_seq,
+                            const int32_t* row_kv_len, uint16_t* output, const PageGeom& g,
+                            int num_rows, int max_kv_len, hipStream_t stream) {
+    const int rows = num_rows * g.H;
+    if (rows <= 0) return;
+    if (!mfma_attention_ok(g, pool))
+        throw Error("paged attention: needs head_dim 128 and 16-byte aligned pages and pool");
+    using namespace mfma;
+    const float inv = inv_sqrt_d(g.D);
+    const int row_groups = (num_rows + kRows - 1) / kRows;
+    const int heads = g.H * row_groups;
+    // Split length: a multiple of one workgroup pass (waves x chunk) sized so
+    // that the longest group yields about 8 workgroups per CU in total.
+    constexpr int kPass = kSplitChunk * kSplitWaves;
+    const long long want_tokens =
+        ((long long)std::max(max_kv_len, 1) * heads + 8LL * num_cus() - 1) / (8LL * num_cus());
+    const int tps = (int)std::max<long long>(
+        kPass, ((want_tokens + kPass - 1) / kPass) * kPass);
+    const int splits = std::max(1, (max_kv_len + tps - 1) / tps);
+    const size_t blocks = (size_t)splits * heads;
+    float* ws = static_cast<float*>(workspace(stream, blocks * kRows * kPartStride * sizeof(float)));
+    const PagedRows pr{block_tables, row_seq, row_kv_len, max_blocks};
+    const bool prod = s == Scheme::Prod;
+    constexpr int kCH = kSplitChunk, kNW = kSplitWaves;
+    if (max_kv_len > 0) {
+        if (prod)
+            hipLaunchKernelGGL((attn_mfma_split_kernel<true, kCH, kNW, true>), dim3(blocks),
+                               dim3(64 * kNW), 0, stream, query, pool, nullptr, ws, g, num_rows,
+                               max_kv_len, tps, splits, inv, pr);
+        else
+            hipLaunchKernelGGL((attn_mfma_split_kernel<false, kCH, kNW, true>), dim3(blocks),
+                               dim3(64 * kNW), 0, stream, query, pool, nullptr, ws, g, num_rows,
+                               max_kv_len, tps, splits, inv, pr);
+        check_launch(prod ? "turbo_prod_paged_attn_split" : "turbo_mse_paged_attn_split");
+    }
+    hipLaunchKernelGGL(attn_mfma_combine_kernel<true>, dim3(4 * rows), dim3(256), 0, stream, ws,
+                       output, g.H, max_kv_len > 0 ? splits : 0, num_rows, tps, pr);
+    check_launch(prod ? "turbo_prod_paged_attn_combine" : "turbo_mse_paged_attn_combine");
 }
 
 void launch_logits(const uint16_t* query, const uint8_t* pool, const int32_t* slots,

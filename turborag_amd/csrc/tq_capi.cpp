@@ -403,3 +403,51 @@ extern "C" int tq_load_turbo_mse_layers(const uint8_t* const* host_pools,
                         static_cast<hipStream_t>(compute_stream));
     });
 }
+
+// ---------------------------------------------------------------------------
+// Batched decode over paged sequences (superset of the reference ABI)
+// ---------------------------------------------------------------------------
+
+namespace {
+template <class Layout>
+int paged_attention(tq::Scheme scheme, const uint16_t* query, const uint8_t* page_pool,
+                    const int32_t* block_tables, int max_blocks, const int32_t* row_seq,
+                    const int32_t* row_kv_len, uint16_t* output, const Layout* layout,
+                    const TQConfig* cfg, int num_rows, int max_kv_len, void* stream) {
+    if (!query || !page_pool || !block_tables || !row_seq || !row_kv_len || !output || !layout ||
+        !cfg)
+        return -1;
+    return guarded([&] {
+        const bool prod = scheme == tq::Scheme::Prod;
+        const tq::PageGeom g = prod ? tq::prod_geom(*cfg, *reinterpret_cast<const TQTurboProdPageLayout*>(layout))
+                                    : tq::mse_geom(*cfg, *reinterpret_cast<const TQTurbomsePageLayout*>(layout));
+        const char* name = prod ? "turbo_prod paged attention" : "turbo_mse paged attention";
+        if (num_rows < 0 || max_kv_len < 0 || max_blocks <= 0)
+            throw tq::Error(std::string(name) +
+                            ": num_rows, max_kv_len >= 0 and max_blocks_per_seq > 0 required");
+        if ((long long)max_kv_len > (long long)max_blocks * cfg->block_size)
+            throw tq::Error(std::string(name) + ": max_kv_len exceeds max_blocks_per_seq pages");
+        tq::launch_paged_attention(scheme, query, page_pool, block_tables, max_blocks, row_seq,
+                                   row_kv_len, output, g, num_rows, max_kv_len,
+                                   static_cast<hipStream_t>(stream));
+    });
+}
+}  // namespace
+
+extern "C" int tq_launch_turbo_prod_paged_attention(
+    const uint16_t* query, const uint8_t* page_pool, const int32_t* block_tables,
+    int max_blocks_per_seq, const int32_t* row_seq, const int32_t* row_kv_len, uint16_t* output,
+    const TQTurboProdPageLayout* layout, const TQConfig* cfg, int num_rows, int max_kv_len,
+    void* stream) {
+    return paged_attention(tq::Scheme::Prod, query, page_pool, block_tables, max_blocks_per_seq,
+                           row_seq, row_kv_len, output, layout, cfg, num_rows, max_kv_len, stream);
+}
+
+extern "C" int tq_launch_turbo_mse_paged_attention(
+    const uint16_t* query, const uint8_t* page_pool, const int32_t* block_tables,
+    int max_blocks_per_seq, const int32_t* row_seq, const int32_t* row_kv_len, uint16_t* output,
+    const TQTurbomsePageLayout* layout, const TQConfig* cfg, int num_rows, int max_kv_len,
+    void* stream) {
+    return paged_attention(tq::Scheme::Mse, query, page_pool, block_tables, max_blocks_per_seq,
+                           row_seq, row_kv_len, output, layout, cfg, num_rows, max_kv_len, stream);
+}

@@ -81,6 +81,11 @@ void load_layers(Scheme s, const uint8_t* const* host_pools, uint8_t* const* dev
 void launch_logits(const uint16_t* query, const uint8_t* pool, const int32_t* slots,
                    float* logits, const PageGeom& g, int num_queries, int num_kv_tokens,
                    hipStream_t stream);
+// Batched decode over paged sequences (see tq_launch_*_paged_attention).
+void launch_paged_attention(Scheme s, const uint16_t* query, const uint8_t* pool,
+                            const int32_t* block_tables, int max_blocks, const int32_t* row_seq,
+                            const int32_t* row_kv_len, uint16_t* output, const PageGeom& g,
+                            int num_rows, int max_kv_len, hipStream_t stream);
 void launch_attention(Scheme s, const uint16_t* query, const uint8_t* pool, const int32_t* slots,
                       uint16_t* output, const PageGeom& g, int num_queries, int num_kv_tokens,
                       hipStream_t stream);

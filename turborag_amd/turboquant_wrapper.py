@@ -108,6 +108,15 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "tq_load_turbo_mse_layers": ([_P(c_void_p), _P(c_void_p), c_size_t, c_int, _P(c_int32),
                                   c_int, _P(c_void_p), _P(c_void_p), _P(TQTurbomsePageLayout),
                                   _P(TQConfig), c_void_p, c_void_p], c_int),
+    # batched decode over paged sequences (superset of the reference ABI)
+    "tq_launch_turbo_prod_paged_attention": ([c_void_p, _P(c_uint8), _P(c_int32), c_int,
+                                              _P(c_int32), _P(c_int32), c_void_p,
+                                              _P(TQTurboProdPageLayout), _P(TQConfig), c_int,
+                                              c_int, c_void_p], c_int),
+    "tq_launch_turbo_mse_paged_attention": ([c_void_p, _P(c_uint8), _P(c_int32), c_int,
+                                             _P(c_int32), _P(c_int32), c_void_p,
+                                             _P(TQTurbomsePageLayout), _P(TQConfig), c_int,
+                                             c_int, c_void_p], c_int),
     # page allocator / block table
     "tq_allocator_create": ([c_size_t, c_int, c_void_p, _P(c_void_p)], c_int),
     "tq_allocator_destroy": ([c_void_p], c_int),
@@ -384,6 +393,35 @@ class TurboQuantWrapper:
                 self._stream(compute_stream))
         if rc != 0:
             self._kernel_raise(rc, scheme, "load_layers")
+
+    def paged_attn_output(self, scheme: str, query, page_pool, block_tables, row_seq,
+                          row_kv_len, output, layout, cfg, max_kv_len: int,
+                          stream: int = 0) -> None:
+        """One launch of decode attention for a batch of paged sequences.
+
+        query / output [num_rows, H, D] fp16; row r belongs to sequence
+        row_seq[r] (aligned groups of 8 rows share one) and attends its first
+        row_kv_len[r] tokens; block_tables [num_seqs, max_blocks] int32 page
+        ids.  head_dim 128."""
+        H, D = cfg.num_kv_heads, cfg.head_dim
+        num_rows = query.shape[0]
+        if block_tables.dim() != 2:
+            raise ValueError(f"{scheme} paged_attn_output: block_tables must be [num_seqs, "
+                             f"max_blocks]")
+        self._check(scheme, "paged_attn_output", query=(query, torch.float16, num_rows * H * D),
+                    page_pool=(page_pool, torch.uint8, 0),
+                    block_tables=(block_tables, torch.int32, block_tables.numel()),
+                    row_seq=(row_seq, torch.int32, num_rows),
+                    row_kv_len=(row_kv_len, torch.int32, num_rows),
+                    output=(output, torch.float16, num_rows * H * D))
+        fn = (self._lib.tq_launch_turbo_prod_paged_attention if scheme == "turbo_prod"
+              else self._lib.tq_launch_turbo_mse_paged_attention)
+        rc = fn(self._vp(query), self._u8p(page_pool), self._i32p(block_tables),
+                block_tables.shape[1], self._i32p(row_seq), self._i32p(row_kv_len),
+                self._vp(output), ctypes.byref(layout), ctypes.byref(cfg), num_rows, max_kv_len,
+                self._stream(stream))
+        if rc != 0:
+            self._kernel_raise(rc, scheme, "paged_attn_output")
 
     # ── allocation helpers (reference :385-415) ─────────────────────── #
 
