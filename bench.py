@@ -267,6 +267,10 @@ def main() -> int:
         f"{loader['ms']:.2f} ms ({loader['host_GBps']:.1f} GB/s of pages); copies alone "
         f"{loader['h2d_only_ms']:.2f} ms")
 
+    batched = measure_batched(w)
+    log(f"[bench] batched decode: {batched['sequences']} sequences, {batched['rows']} rows: "
+        f"append {batched['append_us']:.1f} us + attention {batched['attention_us']:.1f} us")
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(w)
@@ -311,6 +315,7 @@ def main() -> int:
             "algorithmic_bytes": w.att_bytes,
         },
         "loader": loader,
+        "batched_decode": batched,
         "step_ms_events": round(ev_ms_per_step, 4),
         "cpu_baseline": cpu,
     }
@@ -348,6 +353,41 @@ def measure_loader(w: Workload, reps: int = 3) -> dict:
     return {"layers": w.NL, "ms": round(ms, 3), "host_GBps": round(page_bytes / ms / 1e6, 2),
             "h2d_only_ms": round(h2d, 3), "h2d_GBps": round(page_bytes / h2d / 1e6, 2),
             "output": "[1, H, N, D] fp16 per layer", "host_memory": "pinned"}
+
+
+def measure_batched(w: Workload, reps: int = 10) -> dict:
+    """One serving step of a batch of paged sequences (32 sequences, lengths
+    U[1024, 32768], 1-8 new tokens each, pages scattered by the allocator):
+    one pack launch appending every new token, then one paged-attention
+    launch for 8 GQA rows per new token (causal over the new tokens)."""
+    import numpy as np
+    import torch
+
+    from turborag_amd.batched import PagedBatch
+    lens = np.random.default_rng(500).integers(1024, 32769, size=32)
+    widths = np.random.default_rng(501).integers(1, 9, size=32)
+    b = PagedBatch(w.tq, "turbo_prod", lens, widths, seed=500, device=w.dev)
+    b.append_new_tokens(seed=503)
+    query, row_seq, row_len = b.decode_rows(seed=504)
+    bt = b.block_tables()
+    out = torch.empty_like(query)
+    torch.cuda.synchronize()
+    att_us = event_time_us(lambda: b.attention(query, row_seq, row_len, bt, out), reps)
+    app_us = event_time_us(b.repack, reps)
+    rows = int(query.shape[0])
+    # Algorithmic bytes: each sequence's cells once per kv head (+4 B slot
+    # per token), the new tokens' fp16 K/V in and cells out, query and output.
+    cell = 134 * w.H  # 64 + 64 + 3 * 2 bytes per (token, head)
+    kv_tokens = int((lens + widths).sum())
+    alg = kv_tokens * (cell + 4) + int(widths.sum()) * (2 * w.H * 128 * 2 + cell) + 2 * rows * w.H * 256
+    # What this kernel reads: every new-token row group reads its own range.
+    read = int(sum(sum(L + j + 1 for j in range(wd)) for L, wd in zip(lens, widths))) * cell
+    b.close()
+    return {"sequences": 32, "rows": rows, "kv_tokens": kv_tokens,
+            "new_tokens": int(widths.sum()), "append_us": round(app_us, 2),
+            "attention_us": round(att_us, 2), "step_us": round(app_us + att_us, 2),
+            "algorithmic_bytes": alg, "GBps_algorithmic": round(alg / (app_us + att_us) / 1e3, 1),
+            "cells_read_bytes": read}
 
 
 def cpu_baseline(w: Workload):

@@ -52,9 +52,16 @@ class PagedBatch:
     # ── helpers ─────────────────────────────────────────────────────── #
 
     def _pack(self, k: torch.Tensor, v: torch.Tensor, slots: list[int]) -> None:
-        s = torch.tensor(slots, dtype=torch.int32, device=self.dev)
-        (self.tq.pack if self.prod else self.tq.mse_pack)(
-            k.to(self.dev), v.to(self.dev), s, self.pool, self.layout, self.cfg)
+        self._last_pack = (k.to(self.dev), v.to(self.dev),
+                           torch.tensor(slots, dtype=torch.int32, device=self.dev))
+        self.repack()
+
+    def repack(self, stream: int = 0) -> None:
+        """Issue the last pack launch again (same tokens into the same slots:
+        idempotent), e.g. to time the append of a step."""
+        k, v, s = self._last_pack
+        (self.tq.pack if self.prod else self.tq.mse_pack)(k, v, s, self.pool, self.layout,
+                                                          self.cfg, stream=stream)
 
     def _prefill(self) -> None:
         """Every sequence's first L_s tokens, appended one page at a time in a
