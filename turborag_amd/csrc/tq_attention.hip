@@ -293,9 +293,33 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
     const int i = lane & 15, gq = lane >> 4;
-    const int split = blockIdx.x % num_splits;
-    const int hr = blockIdx.x / num_splits;
-    const int h = hr % g.H, rg = hr / g.H;
+    // Work item of this workgroup.  Paged rows: items are ordered row group
+    // fastest (the row groups of one sequence's new tokens are adjacent and
+    // read the same pages), cut into runs of kRun items, and the runs are dealt
+    // to the 8 XCDs round robin (workgroup b runs on XCD b % 8): a run's
+    // workgroups share one XCD and start together, so its L2 serves the
+    // repeated page reads, and every XCD gets an even share of the splits.
+    // The partial's slot in the workspace (pid) keeps the split-fastest
+    // order the combine reads.
+    int split, h, rg;
+    size_t pid = blockIdx.x;
+    if constexpr (PAGED) {
+        constexpr int kRun = 8;
+        const int groups = (num_queries + kRows - 1) / kRows;
+        const int items = num_splits * g.H * groups;
+        const int x = blockIdx.x & 7, li = blockIdx.x >> 3;
+        const int v = (((li / kRun) * 8 + x) * kRun) + li % kRun;
+        if (v >= items) return;
+        rg = v % groups;
+        h = (v / groups) % g.H;
+        split = v / (groups * g.H);
+        pid = (size_t)split + (size_t)num_splits * (h + (size_t)g.H * rg);
+    } else {
+        split = blockIdx.x % num_splits;
+        const int hr = blockIdx.x / num_splits;
+        h = hr % g.H;
+        rg = hr / g.H;
+    }
     const float ck = inv * kLog2e / (PROD ? kAlphaK : kAlphaV);  // logit scale per unit ks
     const float cr = inv * kLog2e;                                 // residual: ks * re
     const int t_begin = split * tokens_per_split;
@@ -621,7 +645,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
         }
         wht_pair_wave(o0, o1, lane);
         const float s0 = (h & 1) ? -inv : inv;
-        float* part = ws + ((size_t)blockIdx.x * kRows + r) * kPartStride;
+        float* part = ws + (pid * kRows + r) * kPartStride;
         part[2 * lane] = o0 * s0;
         part[2 * lane + 1] = o1 * -s0;
         if (lane == 0) {
@@ -834,8 +858,9 @@ void launch_paged_attention(Scheme s, const uint16_t* query, const uint8_t* pool
     const int tps = (int)std::max<long long>(
         kPass, ((want_tokens + kPass - 1) / kPass) * kPass);
     const int splits = std::max(1, (max_kv_len + tps - 1) / tps);
-    const size_t blocks = (size_t)splits * heads;
-    float* ws = static_cast<float*>(workspace(stream, blocks * kRows * kPartStride * sizeof(float)));
+    const size_t items = (size_t)splits * heads;
+    const size_t blocks = 64 * ((items + 63) / 64);  // runs of 8 dealt to 8 XCDs (see the kernel)
+    float* ws = static_cast<float*>(workspace(stream, items * kRows * kPartStride * sizeof(float)));
     const PagedRows pr{block_tables, row_seq, row_kv_len, max_blocks};
     const bool prod = s == Scheme::Prod;
     constexpr int kCH = kSplitChunk, kNW = kSplitWaves;
