@@ -444,7 +444,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     for (int k = 0; k < kQPerWave; ++k) {
         const int r = w + k * kWaves;
         float q0 = qf[k][0], q1 = qf[k][1];
-        wht_pair_wave(q0, q1, lane);
+        wht_pair<64>(q0, q1, lane);
         const bool live = rg * kRows + r < num_queries;
         qs[r][2 * lane] = live ? q0 * inv : 0.0f;
         qs[r][2 * lane + 1] = live ? q1 * inv : 0.0f;
@@ -552,8 +552,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                     if (t0 + 16 * tau + 4 * gq + e >= rowlen) lg[tau][e] = -INFINITY;
                 mloc = fmaxf(mloc, lg[tau][e]);
             }
-        mloc = fmaxf(mloc, shfl_xor(mloc, 16));
-        mloc = fmaxf(mloc, shfl_xor(mloc, 32));
+        mloc = fmaxf(mloc, lane_xor<16>(mloc));
+        mloc = fmaxf(mloc, lane_xor<32>(mloc));
         // v_exp_f32 without denormal handling: arguments are <= 0 and a
         // weight below 2^-126 of the running maximum is negligible.
         const float m_new = fmaxf(m_run, mloc);
@@ -615,8 +615,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
 
     // Wave results: l summed over the g lanes of each column; o rows from the
     // hi + lo columns, the V codebook scale divided out.
-    float l_tot = l_run + shfl_xor(l_run, 16);
-    l_tot += shfl_xor(l_tot, 32);
+    float l_tot = l_run + lane_xor<16>(l_run);
+    l_tot += lane_xor<32>(l_tot);
     if (gq == 0 && !lo_col) {
         mm[w][i >> 1] = m_run;
         ml[w][i >> 1] = l_tot;
@@ -643,7 +643,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
             o0 += mo[u][r][2 * lane] * wt;
             o1 += mo[u][r][2 * lane + 1] * wt;
         }
-        wht_pair_wave(o0, o1, lane);
+        wht_pair<64>(o0, o1, lane);
         const float s0 = (h & 1) ? -inv : inv;
         float* part = ws + (pid * kRows + r) * kPartStride;
         part[2 * lane] = o0 * s0;

@@ -89,11 +89,12 @@ __device__ __forceinline__ float quad_xor(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), ctrl, 0xF, 0xF, true));
 }
 
-// v of lane j ^ M across a full wave64, without LDS: DPP quad permutes for
-// M = 1, 2; half-row mirror then quad reverse for 4; row rotate by 8 for 8;
-// the gfx950 permlane16 / permlane32 swaps for 16 and 32.
+// v of lane (this lane) ^ M across a full wave64, without LDS: DPP quad
+// permutes for M = 1, 2; half-row mirror then quad reverse for 4; row rotate
+// by 8 for 8; the gfx950 permlane16 / permlane32 swaps for 16 and 32.  Every
+// lane of the wave must be active (the DPP reads use bound_ctrl).
 template <int M>
-__device__ __forceinline__ float lane_xor(float v, int j) {
+__device__ __forceinline__ float lane_xor(float v) {
     const int x = __float_as_int(v);
     if constexpr (M == 1 || M == 2) {
         return quad_xor<M>(v);
@@ -104,31 +105,24 @@ __device__ __forceinline__ float lane_xor(float v, int j) {
         return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, true));  // row_ror:8
     } else if constexpr (M == 16) {
         const auto r = __builtin_amdgcn_permlane16_swap((unsigned)x, (unsigned)x, false, false);
-        return __uint_as_float((j & 16) ? r[0] : r[1]);
+        return __uint_as_float((__lane_id() & 16) ? r[0] : r[1]);
     } else {
         static_assert(M == 32, "lane_xor: M in 1..32");
         const auto r = __builtin_amdgcn_permlane32_swap((unsigned)x, (unsigned)x, false, false);
-        return __uint_as_float((j & 32) ? r[0] : r[1]);
+        return __uint_as_float((__lane_id() & 32) ? r[0] : r[1]);
     }
 }
 
-// wht_pair<64> with the lane exchanges done by lane_xor (same arithmetic, so
-// the same bits); every lane of the wave must be active.
-__device__ __forceinline__ void wht_pair_wave(float& x0, float& x1, int j) {
-    const float a = x0 + x1, b = x0 - x1;
-    x0 = a;
-    x1 = b;
-    auto stage = [&](float p0, float p1, int m) {
-        const bool lower = (j & m) == 0;
-        x0 = lower ? x0 + p0 : p0 - x0;
-        x1 = lower ? x1 + p1 : p1 - x1;
-    };
-    stage(lane_xor<1>(x0, j), lane_xor<1>(x1, j), 1);
-    stage(lane_xor<2>(x0, j), lane_xor<2>(x1, j), 2);
-    stage(lane_xor<4>(x0, j), lane_xor<4>(x1, j), 4);
-    stage(lane_xor<8>(x0, j), lane_xor<8>(x1, j), 8);
-    stage(lane_xor<16>(x0, j), lane_xor<16>(x1, j), 16);
-    stage(lane_xor<32>(x0, j), lane_xor<32>(x1, j), 32);
+// lane_xor for an m known after loop unrolling.
+__device__ __forceinline__ float xor_lane(float v, int m) {
+    switch (m) {
+        case 1: return lane_xor<1>(v);
+        case 2: return lane_xor<2>(v);
+        case 4: return lane_xor<4>(v);
+        case 8: return lane_xor<8>(v);
+        case 16: return lane_xor<16>(v);
+        default: return lane_xor<32>(v);
+    }
 }
 
 // In-place WHT of a row held two-per-lane (lane index j within its row).
@@ -139,7 +133,7 @@ __device__ __forceinline__ void wht_pair(float& x0, float& x1, int j) {
     x1 = b;
 #pragma unroll
     for (int m = 1; m < L; m <<= 1) {
-        const float p0 = shfl_xor(x0, m), p1 = shfl_xor(x1, m);
+        const float p0 = xor_lane(x0, m), p1 = xor_lane(x1, m);
         const bool lower = (j & m) == 0;
         x0 = lower ? x0 + p0 : p0 - x0;
         x1 = lower ? x1 + p1 : p1 - x1;
@@ -151,8 +145,8 @@ template <int L>
 __device__ __forceinline__ float tree_pair(float r0, float r1) {
 #pragma unroll
     for (int m = L / 2; m >= 1; m >>= 1) {
-        r0 += shfl_xor(r0, m);
-        r1 += shfl_xor(r1, m);
+        r0 += xor_lane(r0, m);
+        r1 += xor_lane(r1, m);
     }
     return r0 + r1;
 }
@@ -161,7 +155,7 @@ __device__ __forceinline__ float tree_pair(float r0, float r1) {
 template <int L>
 __device__ __forceinline__ float tree_one(float r) {
 #pragma unroll
-    for (int m = L / 2; m >= 1; m >>= 1) r += shfl_xor(r, m);
+    for (int m = L / 2; m >= 1; m >>= 1) r += xor_lane(r, m);
     return r;
 }
 
@@ -173,7 +167,7 @@ __device__ __forceinline__ float sum_lanes(float r) {
 template <int L>
 __device__ __forceinline__ float max_lanes(float r) {
 #pragma unroll
-    for (int m = L / 2; m >= 1; m >>= 1) r = fmaxf(r, shfl_xor(r, m));
+    for (int m = L / 2; m >= 1; m >>= 1) r = fmaxf(r, xor_lane(r, m));
     return r;
 }
 
