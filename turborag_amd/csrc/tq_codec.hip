@@ -79,6 +79,158 @@ __global__ __launch_bounds__(kBlock) void prod_pack_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Pack, wide form (D = 64, 128): 16 lanes per (token, head) row, lane j owns
+// the E = D/16 contiguous elements E*j .. E*j + E-1, so four rows share a
+// wave.  The reference's butterfly stage len pairs elements i and i + len:
+// in-lane for len < E, lanes j and j ^ (len/E) otherwise; its halving trees
+// (r[i] += r[i + s], s = n/2 .. 1) likewise cross lanes for s >= E and end
+// in-lane.  Operation order per element is the reference's, so codes and
+// scales are bit-identical to the one-row-per-wave form above; codes leave as
+// one dword (K) and one dword (V) per lane (E = 8).
+// ---------------------------------------------------------------------------
+template <int E>
+__device__ __forceinline__ void wht_wide(float (&x)[E], int j) {
+#pragma unroll
+    for (int len = 1; len < E; len <<= 1)
+#pragma unroll
+        for (int k = 0; k < E; ++k)
+            if ((k & len) == 0) {
+                const float a = x[k], b = x[k + len];
+                x[k] = a + b;
+                x[k + len] = a - b;
+            }
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) {
+        const bool lower = (j & m) == 0;
+#pragma unroll
+        for (int k = 0; k < E; ++k) {
+            const float p = xor_lane(x[k], m);
+            x[k] = lower ? x[k] + p : p - x[k];
+        }
+    }
+}
+
+// Halving-tree sum of the row's N = 16 * n values, n per lane (contiguous):
+// stages s >= n cross lanes (xor s/n, largest first), then in-lane.  Every
+// lane of the row ends with the total.
+template <int n>
+__device__ __forceinline__ float tree_wide(float (&r)[n]) {
+#pragma unroll
+    for (int m = 8; m >= 1; m >>= 1)
+#pragma unroll
+        for (int k = 0; k < n; ++k) r[k] += xor_lane(r[k], m);
+#pragma unroll
+    for (int s = n / 2; s >= 1; s >>= 1)
+#pragma unroll
+        for (int k = 0; k < s; ++k) r[k] += r[k + s];
+    return r[0];
+}
+
+template <int D, bool PROD>
+__global__ __launch_bounds__(kBlock) void pack_wide_kernel(
+    const uint16_t* __restrict__ key, const uint16_t* __restrict__ value,
+    const int32_t* __restrict__ slots, uint8_t* __restrict__ pool, PageGeom g, int num_rows,
+    float inv) {
+    constexpr int E = D / 16;
+    static_assert(E == 4 || E == 8, "D = 64 or 128");
+    typedef uint16_t h4 __attribute__((ext_vector_type(E)));
+    const int j = threadIdx.x & 15;
+    const int row = blockIdx.x * (kBlock / 16) + (threadIdx.x >> 4);
+    const bool valid = row < num_rows;
+    const int rr = valid ? row : num_rows - 1;
+    const int t = rr / g.H, h = rr % g.H;
+    const size_t off = (size_t)rr * D + E * j;
+    const h4 kr = *reinterpret_cast<const h4*>(key + off);
+    const h4 vr = *reinterpret_cast<const h4*>(value + off);
+    // s(i, h) = (-1)^(i + h); E*j is even, so element k has sign (-1)^(k + h).
+    const float sh = (h & 1) ? -1.0f : 1.0f;
+    float xk[E], xv[E];
+#pragma unroll
+    for (int k = 0; k < E; ++k) {
+        const float sg = (k & 1) ? -sh : sh;
+        xk[k] = h2f(kr[k]) * sg;
+        xv[k] = h2f(vr[k]) * sg;
+    }
+    wht_wide<E>(xk, j);
+    wht_wide<E>(xv, j);
+    uint32_t kcode = 0, vcode = 0;
+    float krms, vrms, rms_e = 0.0f;
+    if constexpr (PROD) {
+        float r[E];
+#pragma unroll
+        for (int k = 0; k < E; ++k) {
+            xk[k] *= inv;
+            xv[k] *= inv;
+            r[k] = xk[k] * xk[k];
+        }
+        krms = sqrtf(tree_wide<E>(r) / (float)D);
+        if (krms < kMinRMS) krms = kMinRMS;
+#pragma unroll
+        for (int k = 0; k < E; ++k) r[k] = xv[k] * xv[k];
+        vrms = sqrtf(tree_wide<E>(r) / (float)D);
+        if (vrms < kMinRMS) vrms = kMinRMS;
+        float e[E];
+#pragma unroll
+        for (int k = 0; k < E; ++k) {
+            const float kn = clamp_ref(xk[k] / krms, -2.5f, 2.5f);
+            const float vn = clamp_ref(xv[k] / vrms, -2.75f, 2.75f);
+            float lv;
+            const uint32_t c = (uint32_t)nearest_k3(kn, lv);
+            e[k] = kn - lv;
+            kcode |= (((e[k] >= 0.0f) ? 8u : 0u) | c) << (4 * k);
+            vcode |= (uint32_t)nearest_v4(vn) << (4 * k);
+            r[k] = e[k] * e[k];
+        }
+        rms_e = sqrtf(tree_wide<E>(r) / (float)D);
+        if (rms_e < kMinRMS) rms_e = kMinRMS;
+    } else {
+        // Pair sums fmaf(x0, x0, x1 * x1) (tq_turbo_mse_kernels.cu:108, contracted).
+        float rk[E / 2], rv[E / 2];
+#pragma unroll
+        for (int k = 0; k < E; ++k) {
+            xk[k] *= inv;
+            xv[k] *= inv;
+        }
+#pragma unroll
+        for (int p = 0; p < E / 2; ++p) {
+            rk[p] = fmaf(xk[2 * p], xk[2 * p], xk[2 * p + 1] * xk[2 * p + 1]);
+            rv[p] = fmaf(xv[2 * p], xv[2 * p], xv[2 * p + 1] * xv[2 * p + 1]);
+        }
+        krms = sqrtf(tree_wide<E / 2>(rk) / (float)D);
+        if (krms < kMinRMS) krms = kMinRMS;
+        vrms = sqrtf(tree_wide<E / 2>(rv) / (float)D);
+        if (vrms < kMinRMS) vrms = kMinRMS;
+#pragma unroll
+        for (int k = 0; k < E; ++k) {
+            kcode |= (uint32_t)nearest_v4(clamp_ref(xk[k] / krms, -2.75f, 2.75f)) << (4 * k);
+            vcode |= (uint32_t)nearest_v4(clamp_ref(xv[k] / vrms, -2.75f, 2.75f)) << (4 * k);
+        }
+    }
+    if (!valid) return;
+    const int slot = slots[t];
+    if (slot < 0) return;
+    int page, tib;
+    split_slot(slot, g, page, tib);
+    const size_t cell = (size_t)(tib * g.H + h);
+    uint8_t* base = pool + (size_t)page * g.page_size;
+    // Element pair (2b, 2b+1) is byte b (low nibble even); the lane's E/2
+    // bytes are contiguous at byte E*j/2 of the cell.
+    if constexpr (E == 8) {
+        *reinterpret_cast<uint32_t*>(base + g.kc_off + cell * g.code_stride + 4 * j) = kcode;
+        *reinterpret_cast<uint32_t*>(base + g.vc_off + cell * g.code_stride + 4 * j) = vcode;
+    } else {
+        *reinterpret_cast<uint16_t*>(base + g.kc_off + cell * g.code_stride + 2 * j) = (uint16_t)kcode;
+        *reinterpret_cast<uint16_t*>(base + g.vc_off + cell * g.code_stride + 2 * j) = (uint16_t)vcode;
+    }
+    if (j == 0) {
+        *reinterpret_cast<uint16_t*>(base + g.ks_off + cell * g.scale_stride) = f2h(krms);
+        if (PROD)
+            *reinterpret_cast<uint16_t*>(base + g.kres_off + cell * g.scale_stride) = f2h(rms_e);
+        *reinterpret_cast<uint16_t*>(base + g.vs_off + cell * g.scale_stride) = f2h(vrms);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // turbo_mse pack — src/cuda/tq_turbo_mse_kernels.cu:65-136, 186-237.
 // The pair sum red[t] = x0*x0 + x1*x1 (:108) is evaluated as
 // fmaf(x0, x0, x1*x1), the contraction nvcc applies at its default -fmad=true.
@@ -413,6 +565,21 @@ void launch_pack(Scheme s, const uint16_t* key, const uint16_t* value, const int
     const int rpb = kBlock / (g.D / 2);
     const dim3 grid((rows + rpb - 1) / rpb);
     const float inv = inv_sqrt_d(g.D);
+    const auto al = [](uint64_t v, uint64_t a) { return (v & (a - 1)) == 0; };
+    if ((g.D == 64 || g.D == 128) && al(g.kc_off, 4) && al(g.vc_off, 4) && al(g.page_size, 4) &&
+        al(reinterpret_cast<uintptr_t>(pool), 4) && al(reinterpret_cast<uintptr_t>(key), 16) &&
+        al(reinterpret_cast<uintptr_t>(value), 16)) {
+        const dim3 wgrid((rows + kBlock / 16 - 1) / (kBlock / 16));
+        const bool prod = s == Scheme::Prod;
+        auto go = [&](auto kernel) {
+            hipLaunchKernelGGL(kernel, wgrid, dim3(kBlock), 0, stream, key, value, slots, pool, g,
+                               rows, inv);
+        };
+        if (g.D == 128) prod ? go(pack_wide_kernel<128, true>) : go(pack_wide_kernel<128, false>);
+        else prod ? go(pack_wide_kernel<64, true>) : go(pack_wide_kernel<64, false>);
+        check_launch(prod ? "turbo_prod_pack_kv_kernel" : "turbo_mse_pack_kv_kernel");
+        return;
+    }
     if (s == Scheme::Prod) {
         TQ_DISPATCH_D(g.D, hipLaunchKernelGGL(prod_pack_kernel<kD>, grid, dim3(kBlock), 0, stream,
                                               key, value, slots, pool, g, rows, inv));
