@@ -338,17 +338,21 @@ __global__ __launch_bounds__(kBlock) void dequant_kernel(
     const uint32_t ko = (uint32_t)f2h(k0 * s0) | ((uint32_t)f2h(k1 * -s0) << 16);
     const uint32_t vo = (uint32_t)f2h(v0 * s0) | ((uint32_t)f2h(v1 * -s0) << 16);
     const size_t off = ol.offset(t, h) + 2 * j;
-    __builtin_nontemporal_store(ko, reinterpret_cast<uint32_t*>(out_key + off));
-    __builtin_nontemporal_store(vo, reinterpret_cast<uint32_t*>(out_value + off));
+    // Plain stores: rows of fewer than 64 elements share 128-byte lines with
+    // their neighbours, and non-temporal pieces of a line each go to memory.
+    *reinterpret_cast<uint32_t*>(out_key + off) = ko;
+    *reinterpret_cast<uint32_t*>(out_value + off) = vo;
 }
 
 // ---------------------------------------------------------------------------
 // Dequant, streaming form (D = 32, 64, 128).  A row is owned by LPR = D/32
 // lanes; lane j holds the four 8-element chunks j + LPR*m (m = 0..3), so WHT
 // stages len = 1, 2, 4 and len >= 8*LPR are register butterflies and the
-// stages in between cross lanes (quad DPP moves, VALU rate), and store m of
-// the row's lanes writes 16*LPR contiguous bytes (full 64-byte segments for
-// D = 128; quarter-line strided stores measured 1.4x slower).  The 16
+// stages in between cross lanes (quad DPP moves, VALU rate).  For D = 128
+// the output leaves as non-temporal stores of whole 128-byte lines (two rows
+// trade chunks first); for D = 32, 64 store m of the row's lanes writes
+// 16*LPR contiguous bytes with plain stores, which the L2 merges into lines
+// (non-temporal pieces of lines measured 2-3x slower there).  The 16
 // possible decoded values of each row — (K3[n&7] + re*(+-1)) * ks for
 // turbo_prod K, V4[n] * rms otherwise, with the reference's exact operations
 // — are tabulated per row in LDS and looked up per nibble.  Waves are
@@ -390,7 +394,8 @@ __global__ __launch_bounds__(kBlock) void dequant_stream_kernel(
         uint4 kw, vw;
         float ks, re, vs;
         int row, t, h;
-        bool live;
+        int pt, ph;  // token and head of row ^ 1 (the store partner when LPR = 4)
+        bool live, plive;
     };
     auto token_head = [&](int row, int& t, int& h) {
         if (g.h_shift >= 0) {
@@ -431,6 +436,10 @@ __global__ __launch_bounds__(kBlock) void dequant_stream_kernel(
             it.ks = h2f(ld_u16(base + g.ks_off + cell * g.scale_stride));
             it.vs = h2f(ld_u16(base + g.vs_off + cell * g.scale_stride));
             if (PROD) it.re = h2f(ld_u16(base + g.kres_off + cell * g.scale_stride));
+        }
+        if constexpr (LPR == 4) {
+            token_head(min(it.row ^ 1, num_rows - 1), it.pt, it.ph);
+            it.plive = lane_xor<4>(it.live ? 1.0f : 0.0f) != 0.0f;
         }
         return it;
     };
@@ -486,18 +495,50 @@ __global__ __launch_bounds__(kBlock) void dequant_stream_kernel(
         // ... and the two largest (chunk m ^ 1, m ^ 2) are in the lane again.
         reg_stage(8);
         reg_stage(16);
-        if (!it.live) return;
         // Element 8*(j + LPR*m) + i has sign (-1)^(i + h).
         const float se = (it.h & 1) ? -inv : inv;
-        uint4* d = reinterpret_cast<uint4*>(out + ol.offset(it.t, it.h)) + j;
+        u32x4 v[4];
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
             const float* c = x + 8 * m;
-            // Streaming (non-temporal) stores: the fp16 output is written once
-            // and is far larger than the caches (measured 13% faster per layer).
-            const u32x4 val = {f2h2(c[0] * se, c[1] * -se), f2h2(c[2] * se, c[3] * -se),
-                               f2h2(c[4] * se, c[5] * -se), f2h2(c[6] * se, c[7] * -se)};
-            __builtin_nontemporal_store(val, reinterpret_cast<u32x4*>(d + LPR * m));
+            v[m] = u32x4{f2h2(c[0] * se, c[1] * -se), f2h2(c[2] * se, c[3] * -se),
+                         f2h2(c[4] * se, c[5] * -se), f2h2(c[6] * se, c[7] * -se)};
+        }
+        if constexpr (LPR == 4) {
+            // Streaming (non-temporal) stores of whole 128-byte lines: the
+            // fp16 output is written once and is far larger than the caches,
+            // and a line that reaches the L2 in two non-temporal pieces is
+            // written to memory twice.  Rows 2p and 2p + 1 (lanes 8p..8p+3
+            // and 8p+4..8p+7) trade half their chunks across lane ^ 4, so
+            // store k writes line k >> 1 of row 2p + (k & 1) with all 8
+            // lanes: lane j of the even row chunk j, of the odd row chunk
+            // 4 + j (of the line).
+            const int odd = rw & 1;
+            const u32x4 s0 = odd ? v[0] : v[1], s1 = odd ? v[2] : v[3];
+            u32x4 r0, r1;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                r0[q] = __float_as_uint(lane_xor<4>(__uint_as_float(s0[q])));
+                r1[q] = __float_as_uint(lane_xor<4>(__uint_as_float(s1[q])));
+            }
+            // store k: own row when (k & 1) == odd, else the partner's
+            const u32x4 val[4] = {odd ? r0 : v[0], odd ? v[1] : r0, odd ? r1 : v[2],
+                                  odd ? v[3] : r1};
+            uint4* const mine = reinterpret_cast<uint4*>(out + ol.offset(it.t, it.h));
+            uint4* const other = reinterpret_cast<uint4*>(out + ol.offset(it.pt, it.ph));
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const bool own = (k & 1) == odd;
+                if (own ? it.live : it.plive)
+                    __builtin_nontemporal_store(
+                        val[k], reinterpret_cast<u32x4*>((own ? mine : other) + 8 * (k >> 1) +
+                                                         4 * odd + j));
+            }
+        } else {
+            if (!it.live) return;
+            uint4* d = reinterpret_cast<uint4*>(out + ol.offset(it.t, it.h)) + j;
+#pragma unroll
+            for (int m = 0; m < 4; ++m) reinterpret_cast<u32x4*>(d + LPR * m)[0] = v[m];
         }
     };
 
