@@ -732,6 +732,68 @@ __global__ __launch_bounds__(256) void attn_mfma_combine_kernel(
     }
 }
 
+// The same merge for few splits: one block per (row group, kv head) item,
+// thread t takes row t / 32 and elements 4(t % 32) .. +3 over every split
+// (8 in flight).  One block per item instead of 4 per row: for the many short
+// items of a batched decode step the block count, not the bytes, is the cost.
+constexpr int kItemCombineMaxSplits = 16;
+template <bool PAGED>
+__global__ __launch_bounds__(256) void attn_mfma_combine_items_kernel(
+    const float* __restrict__ ws, uint16_t* __restrict__ output, int H, int num_splits,
+    int num_queries, int tokens_per_split, mfma::PagedRows pr) {
+    using namespace mfma;
+    const int item = blockIdx.x;  // h + H * rg
+    const int h = item % H, rg = item / H;
+    const int t = threadIdx.x, r = t >> 5, d0 = 4 * (t & 31);
+    int S = num_splits;
+    if constexpr (PAGED) {
+        int kv = 0;
+#pragma unroll
+        for (int k = 0; k < kRows; ++k)
+            kv = max(kv, rg * kRows + k < num_queries ? pr.row_kv_len[rg * kRows + k] : 0);
+        S = min(num_splits, (kv + tokens_per_split - 1) / tokens_per_split);
+    }
+    const float* base = ws + ((size_t)item * num_splits * kRows + r) * kPartStride;
+    float M = kInitMax, L = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int b = 0; b < S; b += 8) {
+        float pm[8], pl[8];
+        float4 po[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const bool ok = b + k < S;
+            const float* p = base + (size_t)min(b + k, S - 1) * kRows * kPartStride;
+            pm[k] = ok ? p[128] : kInitMax;
+            pl[k] = ok ? p[129] : 0.f;
+            po[k] = ok ? *reinterpret_cast<const float4*>(p + d0) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        float mb = M;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) mb = fmaxf(mb, pm[k]);
+        const float sc = exp2f(M - mb);
+        L *= sc;
+        acc.x *= sc;
+        acc.y *= sc;
+        acc.z *= sc;
+        acc.w *= sc;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float wt = exp2f(pm[k] - mb);
+            L += pl[k] * wt;
+            acc.x += po[k].x * wt;
+            acc.y += po[k].y * wt;
+            acc.z += po[k].z * wt;
+            acc.w += po[k].w * wt;
+        }
+        M = mb;
+    }
+    const int q = rg * kRows + r;
+    if (q >= num_queries) return;
+    const auto fin = [&](float o) { return (uint32_t)f2h(L > 0.f ? o / L : o); };
+    *reinterpret_cast<uint2*>(output + ((size_t)q * H + h) * 128 + d0) =
+        make_uint2(fin(acc.x) | (fin(acc.y) << 16), fin(acc.z) | (fin(acc.w) << 16));
+}
+
 // Split kernel shape: tokens per wave iteration and waves per workgroup.
 #ifndef TQ_SPLIT_CHUNK
 #define TQ_SPLIT_CHUNK 32
@@ -807,8 +869,12 @@ void launch_attention(Scheme s, const uint16_t* query, const uint8_t* pool, cons
                                dim3(64 * kNW), 0, stream, query, pool, slots, ws, g, num_queries,
                                num_kv_tokens, tps, splits, inv, none);
         check_launch(prod ? "turbo_prod_fused_attn_split" : "turbo_mse_fused_attn_split");
-        hipLaunchKernelGGL(attn_mfma_combine_kernel<false>, dim3(4 * rows), dim3(256), 0, stream,
-                           ws, output, g.H, splits, num_queries, tps, none);
+        if (splits <= kItemCombineMaxSplits)
+            hipLaunchKernelGGL(attn_mfma_combine_items_kernel<false>, dim3(heads), dim3(256), 0,
+                               stream, ws, output, g.H, splits, num_queries, tps, none);
+        else
+            hipLaunchKernelGGL(attn_mfma_combine_kernel<false>, dim3(4 * rows), dim3(256), 0,
+                               stream, ws, output, g.H, splits, num_queries, tps, none);
         check_launch(prod ? "turbo_prod_fused_attn_combine" : "turbo_mse_fused_attn_combine");
         return;
     }
@@ -875,8 +941,13 @@ void launch_paged_attention(Scheme s, const uint16_t* query, const uint8_t* pool
                                max_kv_len, tps, splits, inv, pr);
         check_launch(prod ? "turbo_prod_paged_attn_split" : "turbo_mse_paged_attn_split");
     }
-    hipLaunchKernelGGL(attn_mfma_combine_kernel<true>, dim3(4 * rows), dim3(256), 0, stream, ws,
-                       output, g.H, max_kv_len > 0 ? splits : 0, num_rows, tps, pr);
+    if (splits <= kItemCombineMaxSplits)
+        hipLaunchKernelGGL(attn_mfma_combine_items_kernel<true>, dim3(heads), dim3(256), 0,
+                           stream, ws, output, g.H, max_kv_len > 0 ? splits : 0, num_rows, tps,
+                           pr);
+    else
+        hipLaunchKernelGGL(attn_mfma_combine_kernel<true>, dim3(4 * rows), dim3(256), 0, stream,
+                           ws, output, g.H, max_kv_len > 0 ? splits : 0, num_rows, tps, pr);
     check_launch(prod ? "turbo_prod_paged_attn_combine" : "turbo_mse_paged_attn_combine");
 }
 
