@@ -267,6 +267,11 @@ def main() -> int:
         f"{loader['ms']:.2f} ms ({loader['host_GBps']:.1f} GB/s of pages); copies alone "
         f"{loader['h2d_only_ms']:.2f} ms")
 
+    store = measure_store(w)
+    log(f"[bench] store: {w.NL} layers .bin/.meta -> [1,H,N,D] in {store['ms']:.2f} ms; "
+        f"the reference's per-layer load path {store['reference_path_ms']:.2f} ms "
+        f"(outputs identical: {store['identical']})")
+
     batched = measure_batched(w)
     log(f"[bench] batched decode: {batched['sequences']} sequences, {batched['rows']} rows: "
         f"append {batched['append_us']:.1f} us + attention {batched['attention_us']:.1f} us")
@@ -315,6 +320,7 @@ def main() -> int:
             "algorithmic_bytes": w.att_bytes,
         },
         "loader": loader,
+        "store": store,
         "batched_decode": batched,
         "step_ms_events": round(ev_ms_per_step, 4),
         "cpu_baseline": cpu,
@@ -353,6 +359,80 @@ def measure_loader(w: Workload, reps: int = 3) -> dict:
     return {"layers": w.NL, "ms": round(ms, 3), "host_GBps": round(page_bytes / ms / 1e6, 2),
             "h2d_only_ms": round(h2d, 3), "h2d_GBps": round(page_bytes / h2d / 1e6, 2),
             "output": "[1, H, N, D] fp16 per layer", "host_memory": "pinned"}
+
+
+def measure_store(w: Workload, reps: int = 3) -> dict:
+    """The on-disk store: the step's 36 layers written as .bin/.meta files
+    (CAGStore format) to a temporary directory, then loaded into [1, H, N, D]
+    by CAGStore.load_layers_hnd (parallel file reads into pinned staging, a
+    group of layers at a time, overlapped with the copies and dequant).
+    Beside it, the reference's per-layer path (cag_store.py:161-254: manifest
+    check, read_bytes -> bytearray -> frombuffer -> clone -> pageable copy,
+    meta load, dequant to [N, H, D], permute copy), with this library's
+    dequant.  Host wall clock, page cache warm; both outputs compared."""
+    import hashlib
+    import shutil
+    import tempfile
+
+    import torch
+
+    from turborag_amd.cag_store import CAGStore
+    d = tempfile.mkdtemp(prefix="tqstore_", dir=os.environ.get("TMPDIR", "/tmp"))
+    try:
+        st = CAGStore(d, tq=w.tq)
+        fmt = st._format("turbo_prod", w.cfg, w.lp, w.N)
+        slots_cpu = w.slots.cpu()
+        layers = list(range(w.NL))
+        for l in layers:
+            st.io.write_pool(st._pool_path("doc", l, "turbo_prod"), w.pools[l], fmt)
+            st.io.write_meta(st._meta_path("doc", l, "turbo_prod"), w.N, slots_cpu, fmt)
+            st._update_manifest("doc", l, "turbo_prod", w.N)
+        manifest = os.path.join(d, "manifest.json")
+
+        def ours():
+            ks, vs, _ = st.load_layers_hnd("doc", layers, "turbo_prod", (w.H, w.D))
+            torch.cuda.synchronize()
+            return ks, vs
+
+        def reference_path():
+            ks, vs = [], []
+            for l in layers:
+                m = json.loads(open(manifest).read())
+                assert m["entries"]["doc"]["sha256"] == hashlib.sha256(b"doc").hexdigest()
+                meta = torch.load(st._meta_path("doc", l, "turbo_prod"), weights_only=True)
+                raw = st._pool_path("doc", l, "turbo_prod").read_bytes()
+                pool = torch.frombuffer(bytearray(raw[:w.pool_bytes]), dtype=torch.uint8).clone()
+                pool = pool.to("cuda", non_blocking=True)
+                slots = meta["slots"].to("cuda")
+                ok = torch.zeros(w.N, w.H, w.D, dtype=torch.float16, device="cuda")
+                ov = torch.zeros_like(ok)
+                w.tq.dequant(pool, slots, ok, ov, w.lp, w.cfg)
+                ks.append(ok.permute(1, 0, 2).unsqueeze(0).contiguous())
+                vs.append(ov.permute(1, 0, 2).unsqueeze(0).contiguous())
+            torch.cuda.synchronize()
+            return ks, vs
+
+        def best(fn):
+            fn()
+            ts = []
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                out = fn()
+                ts.append((time.perf_counter() - t0) * 1e3)
+                del out
+            return min(ts)
+
+        a, b = ours(), reference_path()
+        same = all(torch.equal(x, y) for x, y in zip(a[0] + a[1], b[0] + b[1]))
+        del a, b
+        ms, ref_ms = best(ours), best(reference_path)
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+    page_bytes = w.NL * w.pool_bytes
+    return {"layers": w.NL, "ms": round(ms, 2), "reference_path_ms": round(ref_ms, 2),
+            "speedup": round(ref_ms / ms, 2), "pages_GBps": round(page_bytes / ms / 1e6, 2),
+            "identical": bool(same), "files": "page cache (written just before)",
+            "output": "[1, H, N, D] fp16 per layer"}
 
 
 def measure_batched(w: Workload, reps: int = 10) -> dict:

@@ -255,6 +255,81 @@ int tq_block_table_blocks(const TQBlockTable* t, int32_t seq_id, int32_t* out_bl
  * counterpart: the reference never frees a sequence). */
 int tq_block_table_free_sequence(TQBlockTable* t, int32_t seq_id);
 
+/* ---------------------------------------------------------------------- */
+/* On-disk CAG store (superset of the reference ABI).  The reference reads  */
+/* and writes these files in Python (tq_backend/cag_store.py); these        */
+/* entries produce and consume the same files from C/C++:                   */
+/*   <key>.bin   raw page pool (:147-149), here followed by a versioned      */
+/*               64-byte footer that the reference's reader ignores (it      */
+/*               slices raw[:pool_bytes], :189-190); fp16 scheme: a          */
+/*               torch.save dict (:128-131);                                 */
+/*   <key>.meta  torch.save({"num_tokens", "slots"}) (:150);                 */
+/*   manifest.json (:33-95).                                                 */
+/* All return 0, -1 for a null argument, -2 with tq_last_error().           */
+/* ---------------------------------------------------------------------- */
+#define TQ_STORE_FORMAT_VERSION 1
+#define TQ_SCHEME_TURBO_PROD 1
+#define TQ_SCHEME_TURBO_MSE 2
+
+typedef struct TQStoreFormat {
+    int32_t version;          /* TQ_STORE_FORMAT_VERSION */
+    int32_t scheme;           /* TQ_SCHEME_TURBO_PROD / TQ_SCHEME_TURBO_MSE */
+    int32_t num_kv_heads;
+    int32_t head_dim;
+    int32_t block_size;
+    int32_t page_size_bytes;
+    int64_t num_pages;
+    int64_t num_tokens;
+} TQStoreFormat;
+
+/* Lower-case hex SHA-256 of data into out_hex65 (64 digits + NUL)
+ * (cag_store.py:47-49, hashlib.sha256(doc_id.encode()).hexdigest()). */
+int tq_store_sha256_hex(const void* data, size_t n, char* out_hex65);
+/* cag_store.py:97-100 — "<sha256(doc_id)[:16]>_L<layer, %02d>_<scheme>". */
+int tq_store_key(const char* doc_id, int layer, const char* scheme, char* out, size_t cap);
+/* CRC-32C (Castagnoli), the checksum of the pages in a .bin footer. */
+int tq_store_crc32c(const void* data, size_t n, uint32_t* out);
+/* cag_store.py:150 — torch.save({"num_tokens": num_tokens, "slots":
+ * int32[num_slots]}) to path (atomically: path.tmp, then rename).  With fmt,
+ * the dict also carries the format record (tq_format, tq_scheme,
+ * num_kv_heads, head_dim, block_size, page_size_bytes). */
+int tq_store_write_meta(const char* path, int64_t num_tokens, const int32_t* slots,
+                        int64_t num_slots, const TQStoreFormat* fmt);
+/* cag_store.py:172-174 — num_tokens, *num_slots and the first min(cap,
+ * *num_slots) slots (slots may be NULL with cap 0, to size a buffer);
+ * *has_fmt / *fmt from the format record when present.  The pickle reader
+ * accepts only what torch.save writes for dicts of ints, strings, lists and
+ * tensors (no code runs; the reference calls torch.load(weights_only=False)). */
+int tq_store_read_meta(const char* path, int64_t* num_tokens, int32_t* slots, int64_t cap,
+                       int64_t* num_slots, TQStoreFormat* fmt, int* has_fmt);
+/* cag_store.py:147-149 — the pool bytes, then the footer (fmt, pool_bytes
+ * and the CRC-32C of the pool). */
+int tq_store_write_pool(const char* path, const uint8_t* pool, size_t pool_bytes,
+                        const TQStoreFormat* fmt);
+/* Size of a .bin and, when it has a footer, its format record. */
+int tq_store_pool_info(const char* path, size_t* file_bytes, TQStoreFormat* fmt, int* has_footer);
+/* cag_store.py:189-191 for n files at once: the first pool_bytes bytes of
+ * paths[k] into host_dst[k] (e.g. pinned memory for tq_load_*_layers), files
+ * spread over `threads` threads.  verify != 0 checks the page checksum of
+ * files that have a footer. */
+int tq_store_read_pools(const char* const* paths, uint8_t* const* host_dst, size_t pool_bytes,
+                        int n, int threads, int verify);
+/* cag_store.py:127-131 — fp16 scheme .bin: torch.save({"num_tokens", "kv":
+ * fp16[numel], "shape": [shape...]}). */
+int tq_store_write_fp16(const char* path, int64_t num_tokens, const uint16_t* kv, int64_t numel,
+                        const int64_t* shape, int ndim);
+/* cag_store.py:176-181 — reads that file (kv / shape may be NULL with cap 0). */
+int tq_store_read_fp16(const char* path, int64_t* num_tokens, uint16_t* kv, int64_t cap,
+                       int64_t* numel, int64_t* shape, int shape_cap, int* ndim);
+/* cag_store.py:51-67 — records (layer, scheme, num_tokens) of doc_id in
+ * <store_dir>/manifest.json (written like json.dumps(indent=2), atomically). */
+int tq_store_manifest_update(const char* store_dir, const char* doc_id, int layer,
+                             const char* scheme, int64_t num_tokens);
+/* cag_store.py:69-95 — rc -2 with the reference's message on a hash or key
+ * mismatch; a missing entry or manifest passes. */
+int tq_store_manifest_verify(const char* store_dir, const char* doc_id, int layer,
+                             const char* scheme);
+
 #if defined(__GNUC__)
 #pragma GCC visibility pop
 #endif

@@ -35,7 +35,8 @@ HIPCC_FLAGS = [
     f"-I{ROOT / 'include'}", f"-I{CSRC}",
 ]
 
-SOURCES = ["tq_capi.cpp", "tq_pool.cpp", "tq_loader.cpp", "tq_codec.hip", "tq_attention.hip"]
+SOURCES = ["tq_capi.cpp", "tq_pool.cpp", "tq_loader.cpp", "tq_store.cpp", "tq_codec.hip",
+           "tq_attention.hip"]
 
 
 def _hipcc() -> str:

@@ -52,7 +52,10 @@ def kernels_md(prefix: str, command: str) -> str:
            "| kernel | calls | avg µs | min µs | median µs | max µs |",
            "|---|---:|---:|---:|---:|---:|"]
     order = sorted(d.items(), key=lambda kv: -sum(kv[1]))
-    for n, v in order[:16]:
+    # every kernel of this library, then the busiest others (torch, copies)
+    ours = [kv for kv in order if kv[0].startswith("tq::")]
+    others = [kv for kv in order if not kv[0].startswith("tq::")][:8]
+    for n, v in ours + others:
         out.append(f"| `{n}` | {len(v)} | {statistics.mean(v):.3f} | {min(v):.3f} | "
                    f"{statistics.median(v):.3f} | {max(v):.3f} |")
     return "\n".join(out) + "\n"

@@ -64,8 +64,24 @@ class TQTurbomsePageLayout(ctypes.Structure):
     ]
 
 
+class TQStoreFormat(ctypes.Structure):
+    """Format record of the on-disk store (.bin footer, .meta keys)."""
+
+    _fields_ = [
+        ("version", c_int32),
+        ("scheme", c_int32),  # 1 turbo_prod, 2 turbo_mse
+        ("num_kv_heads", c_int32),
+        ("head_dim", c_int32),
+        ("block_size", c_int32),
+        ("page_size_bytes", c_int32),
+        ("num_pages", ctypes.c_int64),
+        ("num_tokens", ctypes.c_int64),
+    ]
+
+
 # Every exported symbol and its ctypes signature (argtypes, restype).
 _P = POINTER
+_I64 = ctypes.c_int64
 SIGNATURES: dict[str, tuple[list, object]] = {
     "tq_last_error": ([], ctypes.c_char_p),
     "tq_make_default_config": ([_P(TQConfig)], c_int),
@@ -130,6 +146,25 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "tq_block_table_num_tokens": ([c_void_p, c_int32, _P(c_int)], c_int),
     "tq_block_table_blocks": ([c_void_p, c_int32, _P(c_int32), c_int, _P(c_int)], c_int),
     "tq_block_table_free_sequence": ([c_void_p, c_int32], c_int),
+    # on-disk store (tq_backend/cag_store.py formats)
+    "tq_store_sha256_hex": ([c_void_p, c_size_t, ctypes.c_char_p], c_int),
+    "tq_store_key": ([ctypes.c_char_p, c_int, ctypes.c_char_p, ctypes.c_char_p, c_size_t], c_int),
+    "tq_store_crc32c": ([c_void_p, c_size_t, _P(ctypes.c_uint32)], c_int),
+    "tq_store_write_meta": ([ctypes.c_char_p, _I64, _P(c_int32), _I64, _P(TQStoreFormat)],
+                            c_int),
+    "tq_store_read_meta": ([ctypes.c_char_p, _P(_I64), _P(c_int32), _I64, _P(_I64),
+                           _P(TQStoreFormat), _P(c_int)], c_int),
+    "tq_store_write_pool": ([ctypes.c_char_p, c_void_p, c_size_t, _P(TQStoreFormat)], c_int),
+    "tq_store_pool_info": ([ctypes.c_char_p, _P(c_size_t), _P(TQStoreFormat), _P(c_int)], c_int),
+    "tq_store_read_pools": ([_P(ctypes.c_char_p), _P(c_void_p), c_size_t, c_int, c_int, c_int],
+                            c_int),
+    "tq_store_write_fp16": ([ctypes.c_char_p, _I64, c_void_p, _I64, _P(_I64), c_int], c_int),
+    "tq_store_read_fp16": ([ctypes.c_char_p, _P(_I64), c_void_p, _I64, _P(_I64), _P(_I64), c_int,
+                           _P(c_int)], c_int),
+    "tq_store_manifest_update": ([ctypes.c_char_p, ctypes.c_char_p, c_int, ctypes.c_char_p, _I64],
+                                 c_int),
+    "tq_store_manifest_verify": ([ctypes.c_char_p, ctypes.c_char_p, c_int, ctypes.c_char_p],
+                                 c_int),
 }
 
 
