@@ -272,6 +272,11 @@ def main() -> int:
         f"the reference's per-layer load path {store['reference_path_ms']:.2f} ms "
         f"(outputs identical: {store['identical']})")
 
+    legacy = measure_legacy(w)
+    log(f"[bench] unexported kernels @32K: qjl dequant {legacy['qjl_dequant_us']:.1f} us, "
+        f"qjl attention {legacy['qjl_attention_us']:.1f} us, int4 dequant "
+        f"{legacy['int4_dequant_us']:.1f} us")
+
     batched = measure_batched(w)
     log(f"[bench] batched decode: {batched['sequences']} sequences, {batched['rows']} rows: "
         f"append {batched['append_us']:.1f} us + attention {batched['attention_us']:.1f} us")
@@ -321,6 +326,7 @@ def main() -> int:
         },
         "loader": loader,
         "store": store,
+        "unexported_kernels": legacy,
         "batched_decode": batched,
         "step_ms_events": round(ev_ms_per_step, 4),
         "cpu_baseline": cpu,
@@ -433,6 +439,47 @@ def measure_store(w: Workload, reps: int = 3) -> dict:
             "speedup": round(ref_ms / ms, 2), "pages_GBps": round(page_bytes / ms / 1e6, 2),
             "identical": bool(same), "files": "page cache (written just before)",
             "output": "[1, H, N, D] fp16 per layer"}
+
+
+def measure_legacy(w: Workload, reps: int = 10) -> dict:
+    """The kernels the reference compiles but does not export, on one layer
+    of the step's shape (32K tokens, H = 2, D = 128, the step's shuffled
+    slots): QJL-1b pack / dequant / GQA 16/2 attention and legacy INT4 pack /
+    dequant.  Event-timed eager launches on the current stream."""
+    import torch
+    tq = w.tq
+    cfg = tq.default_config()
+    cfg.num_kv_heads, cfg.head_dim, cfg.block_size, cfg.group_size = w.H, w.D, w.B, w.D
+    k, v = gpu_kv(w.N, w.H, w.D, 999, w.dev)
+    pages = (w.N + w.B - 1) // w.B
+    lq, li = tq.make_qjl_layout_for(cfg), tq.make_int4_layout_for(cfg)
+    pq = torch.zeros(pages * lq.page_size_bytes, dtype=torch.uint8, device=w.dev)
+    pi = torch.zeros(pages * li.page_size_bytes, dtype=torch.uint8, device=w.dev)
+    ok = torch.empty(w.N, w.H, w.D, dtype=torch.float16, device=w.dev)
+    ov = torch.empty_like(ok)
+    out = torch.empty_like(w.att[0])
+    st = w._stream
+    t = {
+        "qjl_pack_us": event_time_us(lambda: tq.qjl_pack(k, v, w.slots, pq, lq, cfg, st()), reps),
+        "qjl_dequant_us": event_time_us(
+            lambda: tq.qjl_dequant(pq, w.slots, ok, ov, lq, cfg, st()), reps),
+        "qjl_attention_us": event_time_us(
+            lambda: tq.qjl_fused_attn_output(w.qa, pq, w.slots, out, lq, cfg, w.rows, w.N, st()),
+            reps),
+        "int4_pack_us": event_time_us(lambda: tq.int4_pack(k, v, w.slots, pi, li, cfg, st()),
+                                      reps),
+        "int4_dequant_us": event_time_us(
+            lambda: tq.int4_dequant(pi, w.slots, ok, ov, li, cfg, st()), reps),
+    }
+    fp16 = 2 * w.N * w.H * w.D * 2
+    t = {k_: round(v_, 2) for k_, v_ in t.items()}
+    t["qjl_dequant_GBps"] = round((pages * lq.page_size_bytes + fp16 + w.N * 4)
+                                  / t["qjl_dequant_us"] / 1e3, 1)
+    t["int4_dequant_GBps"] = round((pages * li.page_size_bytes + fp16 + w.N * 4)
+                                   / t["int4_dequant_us"] / 1e3, 1)
+    t["shape"] = "32768 tokens x 2 kv heads x 128, 8 GQA rows per kv head for attention"
+    del k, v, pq, pi, ok, ov
+    return t
 
 
 def measure_batched(w: Workload, reps: int = 10) -> dict:

@@ -256,6 +256,103 @@ int tq_block_table_blocks(const TQBlockTable* t, int32_t seq_id, int32_t* out_bl
 int tq_block_table_free_sequence(TQBlockTable* t, int32_t seq_id);
 
 /* ---------------------------------------------------------------------- */
+/* Kernels the reference compiles but never exports (superset of its ABI): */
+/* QJL-1b (include/tq_qjl.cuh, src/cuda/tq_qjl_kernels.cu), the legacy     */
+/* INT4 and dense pages (include/tq_layout.h, include/tq_dense_layout.h,   */
+/* src/cuda/tq_{pack,dequant,dense}_kernels.cu) and the GPU SDPA reference  */
+/* (include/tq_attention_ref.h:24-45).  Same return codes as above; tokens  */
+/* with a negative slot are skipped; head_dim a power of two in [2, 128].    */
+/* ---------------------------------------------------------------------- */
+
+/* TQQJLPageLayout (include/tq_qjl.cuh:21-33): 1-bit K signs, K RMS, 4-bit
+ * V codes, V RMS. */
+typedef struct TQQJLPageLayout {
+    size_t page_size_bytes;
+    size_t k1_codes_offset;
+    size_t k_scales_offset;
+    size_t v4_codes_offset;
+    size_t v_scales_offset;
+    int k1_bytes_per_token_head;
+    int v4_bytes_per_token_head;
+    int scale_bytes_per_token_head;
+} TQQJLPageLayout;
+
+/* TQPageLayout (include/tq_layout.h:11-23): the legacy INT4 page (absmax
+ * scales, no rotation). */
+typedef struct TQPageLayout {
+    size_t code_bytes_per_token_head;
+    size_t scale_bytes_per_token_head;
+    size_t k_codes_offset;
+    size_t v_codes_offset;
+    size_t k_scales_offset;
+    size_t v_scales_offset;
+    size_t k_codes_bytes;
+    size_t v_codes_bytes;
+    size_t k_scales_bytes;
+    size_t v_scales_bytes;
+    size_t page_size_bytes;
+} TQPageLayout;
+
+/* TQDensePageLayout (include/tq_dense_layout.h:5-12): fp16 K and V. */
+typedef struct TQDensePageLayout {
+    size_t elem_bytes;
+    size_t k_offset;
+    size_t v_offset;
+    size_t k_bytes;
+    size_t v_bytes;
+    size_t page_size_bytes;
+} TQDensePageLayout;
+
+/* make_tq_qjl_page_layout, src/tq_qjl.cpp:7-33. */
+int tq_make_qjl_layout(const TQConfig* cfg, TQQJLPageLayout* out_layout);
+/* launch_tq_qjl_pack_kv, src/cuda/tq_qjl_kernels.cu:382-398. */
+int tq_launch_qjl_pack_kv(const uint16_t* key, const uint16_t* value,
+                          const int32_t* slot_mapping, uint8_t* page_pool,
+                          const TQQJLPageLayout* layout, const TQConfig* cfg, int num_tokens,
+                          void* stream);
+/* launch_tq_qjl_dequant_kv, :400-416. */
+int tq_launch_qjl_dequant_kv(const uint8_t* page_pool, const int32_t* slot_mapping,
+                             uint16_t* out_key, uint16_t* out_value,
+                             const TQQJLPageLayout* layout, const TQConfig* cfg, int num_tokens,
+                             void* stream);
+/* launch_tq_qjl_fused_attention_output, :418-437: logits <q, k> without
+ * 1/sqrt(D) (the QJL kernel's convention). */
+int tq_launch_qjl_fused_attention_output(const uint16_t* query, const uint8_t* page_pool,
+                                         const int32_t* slot_mapping, uint16_t* output,
+                                         const TQQJLPageLayout* layout, const TQConfig* cfg,
+                                         int num_queries, int num_kv_tokens, void* stream);
+/* make_tq_page_layout, src/tq_layout.cpp:8-36 (rc -2 unless nbits == 4 and
+ * group_size == head_dim, where the reference throws). */
+int tq_make_int4_layout(const TQConfig* cfg, TQPageLayout* out_layout);
+/* launch_tq_pack_kv, src/cuda/tq_pack_kernels.cu:112-128. */
+int tq_launch_int4_pack_kv(const uint16_t* key, const uint16_t* value,
+                           const int32_t* slot_mapping, uint8_t* page_pool,
+                           const TQPageLayout* layout, const TQConfig* cfg, int num_tokens,
+                           void* stream);
+/* launch_tq_dequant_kv, src/cuda/tq_dequant_kernels.cu:57-70. */
+int tq_launch_int4_dequant_kv(const uint8_t* page_pool, const int32_t* slot_mapping,
+                              uint16_t* out_key, uint16_t* out_value, const TQPageLayout* layout,
+                              const TQConfig* cfg, int num_tokens, void* stream);
+/* make_tq_dense_page_layout, src/tq_dense_layout.cpp:7-18. */
+int tq_make_dense_layout(const TQConfig* cfg, TQDensePageLayout* out_layout);
+/* launch_dense_store_kv / launch_dense_load_kv, src/cuda/tq_dense_kernels.cu:72-99. */
+int tq_launch_dense_store_kv(const uint16_t* key, const uint16_t* value,
+                             const int32_t* slot_mapping, uint8_t* page_pool,
+                             const TQDensePageLayout* layout, const TQConfig* cfg, int num_tokens,
+                             void* stream);
+int tq_launch_dense_load_kv(const uint8_t* page_pool, const int32_t* slot_mapping,
+                            uint16_t* out_key, uint16_t* out_value,
+                            const TQDensePageLayout* layout, const TQConfig* cfg, int num_tokens,
+                            void* stream);
+/* launch_attention_ref_gpu, src/cuda/tq_attention_ref_kernel.cu:116-139:
+ * softmax(q k^T / sqrt(D)) V over contiguous fp16 K/V [num_kv_tokens, H, D];
+ * logit_scratch (num_queries * H * num_kv_tokens floats) receives the
+ * scaled logits. */
+int tq_launch_attention_ref(const uint16_t* query, const uint16_t* key, const uint16_t* value,
+                            uint16_t* output, float* logit_scratch, const TQConfig* cfg,
+                            int num_queries, int num_kv_tokens, void* stream);
+
+/* ---------------------------------------------------------------------- */
 /* On-disk CAG store (superset of the reference ABI).  The reference reads  */
 /* and writes these files in Python (tq_backend/cag_store.py); these        */
 /* entries produce and consume the same files from C/C++:                   */

@@ -6,6 +6,8 @@
 #                       Lloyd-Max 8-level design that produced kK3Codebook)
 #   ref_layouts         src/tq_turbo_mse_layout.cpp + src/tq_layout.cpp with
 #                       oracle/ref_layout_driver.cpp
+#   ref_legacy_layouts  src/tq_layout.cpp + src/tq_dense_layout.cpp with
+#                       oracle/ref_legacy_layout_driver.cpp (every field)
 # Everything else on the path includes <cuda_runtime.h>/<cuda_fp16.h> and is
 # not buildable here.  Silently does nothing when /root/reference is absent.
 set -euo pipefail
@@ -16,4 +18,6 @@ mkdir -p "$here/_ref"
 g++ -O2 -std=c++17 -o "$here/_ref/gaussian_codebook" "$ref/src/gaussian_codebook.cpp"
 g++ -O2 -std=c++17 -I"$ref/include" -o "$here/_ref/ref_layouts" \
     "$here/ref_layout_driver.cpp" "$ref/src/tq_turbo_mse_layout.cpp" "$ref/src/tq_layout.cpp"
+g++ -O2 -std=c++17 -I"$ref/include" -o "$here/_ref/ref_legacy_layouts" \
+    "$here/ref_legacy_layout_driver.cpp" "$ref/src/tq_layout.cpp" "$ref/src/tq_dense_layout.cpp"
 echo "build_ref: ok"

@@ -58,7 +58,8 @@ HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "libtq_oracle.so"
 REF_DIR = HERE / "_ref"
 
-__all__ = ["Oracle", "ProdLayout", "MseLayout", "load", "REF_DIR"]
+__all__ = ["Oracle", "ProdLayout", "MseLayout", "QjlLayout", "Int4Layout", "DenseLayout",
+           "load", "REF_DIR"]
 
 
 class ProdLayout(Structure):
@@ -71,6 +72,23 @@ class MseLayout(Structure):
     _fields_ = [("code_bytes", c_size_t), ("norm_bytes", c_size_t), ("k_codes_off", c_size_t),
                 ("v_codes_off", c_size_t), ("k_norms_off", c_size_t), ("v_norms_off", c_size_t),
                 ("page_size", c_size_t)]
+
+
+class QjlLayout(Structure):
+    _fields_ = [("page_size", c_size_t), ("k1_off", c_size_t), ("ks_off", c_size_t),
+                ("v4_off", c_size_t), ("vs_off", c_size_t), ("k1_bytes", c_int),
+                ("v4_bytes", c_int), ("scale_bytes", c_int)]
+
+
+class Int4Layout(Structure):
+    _fields_ = [(n, c_size_t) for n in (
+        "code_bytes", "scale_bytes", "k_codes_off", "v_codes_off", "k_scales_off", "v_scales_off",
+        "k_codes_bytes", "v_codes_bytes", "k_scales_bytes", "v_scales_bytes", "page_size")]
+
+
+class DenseLayout(Structure):
+    _fields_ = [(n, c_size_t) for n in ("elem_bytes", "k_off", "v_off", "k_bytes", "v_bytes",
+                                        "page_size")]
 
 
 def _p(a: np.ndarray):
@@ -140,6 +158,23 @@ class Oracle:
         L.tqo_prod_boundary_count.argtypes = [vp, vp, c_int, c_int, c_int, POINTER(c_longlong)]
         L.tqo_mse_boundary_count.argtypes = [vp, vp, c_int, c_int, c_int, POINTER(c_longlong)]
         L.tqo_sdpa_single_head.argtypes = [vp, vp, vp, c_int, c_int, vp]
+        L.tqo_make_qjl_layout.argtypes = [c_int, c_int, c_int, POINTER(QjlLayout)]
+        L.tqo_make_int4_layout.argtypes = [c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+                                           POINTER(Int4Layout)]
+        L.tqo_make_int4_layout.restype = c_int
+        L.tqo_make_dense_layout.argtypes = [c_int, c_int, c_int, c_int, POINTER(DenseLayout)]
+        L.tqo_qjl_pack_row.argtypes = [vp, vp, c_int, vp, vp, vp, vp]
+        L.tqo_int4_pack_row.argtypes = [vp, vp, c_int, vp, vp, vp, vp]
+        for name, lay in (("tqo_qjl_pack", QjlLayout), ("tqo_int4_pack", Int4Layout)):
+            getattr(L, name).argtypes = [vp, vp, vp, c_int, c_int, c_int, c_int, POINTER(lay),
+                                         vp, c_int]
+        for name, lay in (("tqo_qjl_dequant", QjlLayout), ("tqo_int4_dequant", Int4Layout)):
+            getattr(L, name).argtypes = [vp, vp, c_int, c_int, c_int, c_int, POINTER(lay), vp,
+                                         vp, c_int]
+        for name in ("tqo_qjl_attention_f64", "tqo_qjl_attention_f32"):
+            getattr(L, name).argtypes = [vp, vp, vp, c_int, c_int, c_int, c_int, c_int,
+                                         POINTER(QjlLayout), vp, c_int]
+        L.tqo_sdpa_gpu_ref.argtypes = [vp, vp, vp, vp, vp, c_int, c_int, c_int, c_int, c_int]
         L.tqo_lloyd_max_gaussian.argtypes = [c_int, c_int, c_double, vp, vp]
         self.nthreads = int(os.environ.get("TQ_ORACLE_THREADS", "1"))
 
@@ -336,6 +371,115 @@ class Oracle:
         self.lib.tqo_mse_attention_f32(_p(query), _p(pool), _p(slots), Q, slots.size, H, D,
                                        block_size, ctypes.byref(L), _p(out), self.nthreads)
         return out
+
+    # ---- QJL-1b, legacy INT4, dense, GPU SDPA reference ------------------------
+    def qjl_layout(self, block_size: int, H: int, D: int) -> QjlLayout:
+        L = QjlLayout()
+        self.lib.tqo_make_qjl_layout(block_size, H, D, ctypes.byref(L))
+        return L
+
+    def int4_layout(self, block_size: int, H: int, D: int, nbits: int = 4,
+                    group_size: int | None = None, align: int = 256,
+                    scale_fp32: bool = False) -> Int4Layout | None:
+        L = Int4Layout()
+        rc = self.lib.tqo_make_int4_layout(block_size, H, D, nbits,
+                                           D if group_size is None else group_size, align,
+                                           int(scale_fp32), ctypes.byref(L))
+        return L if rc == 0 else None
+
+    def dense_layout(self, block_size: int, H: int, D: int, align: int = 256) -> DenseLayout:
+        L = DenseLayout()
+        self.lib.tqo_make_dense_layout(block_size, H, D, align, ctypes.byref(L))
+        return L
+
+    def qjl_pack_row(self, k, v):
+        k, v = _u16(k), _u16(v)
+        D = k.size
+        k1 = np.zeros((D + 7) // 8, np.uint8)
+        v4 = np.zeros(D // 2, np.uint8)
+        sc = np.zeros(2, np.uint16)
+        self.lib.tqo_qjl_pack_row(_p(k), _p(v), D, _p(k1), _p(v4), _p(sc[0:]), _p(sc[1:]))
+        return dict(k1=k1, v4=v4, ks=int(sc[0]), vs=int(sc[1]))
+
+    def int4_pack_row(self, k, v):
+        k, v = _u16(k), _u16(v)
+        D = k.size
+        kc = np.zeros((D + 1) // 2, np.uint8)
+        vc = np.zeros((D + 1) // 2, np.uint8)
+        sc = np.zeros(2, np.uint16)
+        self.lib.tqo_int4_pack_row(_p(k), _p(v), D, _p(kc), _p(vc), _p(sc[0:]), _p(sc[1:]))
+        return dict(kc=kc, vc=vc, ks=int(sc[0]), vs=int(sc[1]))
+
+    def _pack_any(self, fn, L, key, value, slots, num_pages, block_size, pool):
+        key, value = _u16(key), _u16(value)
+        N, H, D = key.shape
+        slots = np.ascontiguousarray(slots, dtype=np.int32)
+        if pool is None:
+            pool = np.zeros(num_pages * L.page_size, np.uint8)
+        fn(_p(key), _p(value), _p(slots), N, H, D, block_size, ctypes.byref(L), _p(pool),
+           self.nthreads)
+        return pool
+
+    def _dequant_any(self, fn, L, pool, slots, H, D, block_size):
+        pool = np.ascontiguousarray(pool, dtype=np.uint8)
+        slots = np.ascontiguousarray(slots, dtype=np.int32)
+        N = slots.size
+        ok = np.zeros((N, H, D), np.uint16)
+        ov = np.zeros((N, H, D), np.uint16)
+        fn(_p(pool), _p(slots), N, H, D, block_size, ctypes.byref(L), _p(ok), _p(ov),
+           self.nthreads)
+        return ok, ov
+
+    def qjl_pack(self, key, value, slots, num_pages: int, block_size: int = 16, pool=None):
+        _, H, D = np.shape(key)
+        return self._pack_any(self.lib.tqo_qjl_pack, self.qjl_layout(block_size, H, D), key,
+                              value, slots, num_pages, block_size, pool)
+
+    def qjl_dequant(self, pool, slots, H: int, D: int, block_size: int = 16):
+        return self._dequant_any(self.lib.tqo_qjl_dequant, self.qjl_layout(block_size, H, D),
+                                 pool, slots, H, D, block_size)
+
+    def int4_pack(self, key, value, slots, num_pages: int, block_size: int = 16, pool=None,
+                  align: int = 256, scale_fp32: bool = False):
+        _, H, D = np.shape(key)
+        L = self.int4_layout(block_size, H, D, align=align, scale_fp32=scale_fp32)
+        return self._pack_any(self.lib.tqo_int4_pack, L, key, value, slots, num_pages,
+                              block_size, pool)
+
+    def int4_dequant(self, pool, slots, H: int, D: int, block_size: int = 16, align: int = 256,
+                     scale_fp32: bool = False):
+        L = self.int4_layout(block_size, H, D, align=align, scale_fp32=scale_fp32)
+        return self._dequant_any(self.lib.tqo_int4_dequant, L, pool, slots, H, D, block_size)
+
+    def _qjl_att(self, fn, dtype, query, pool, slots, block_size):
+        query = _u16(query)
+        Q, H, D = query.shape
+        slots = np.ascontiguousarray(slots, dtype=np.int32)
+        pool = np.ascontiguousarray(pool, dtype=np.uint8)
+        out = np.zeros((Q, H, D), dtype)
+        fn(_p(query), _p(pool), _p(slots), Q, slots.size, H, D, block_size,
+           ctypes.byref(self.qjl_layout(block_size, H, D)), _p(out), self.nthreads)
+        return out
+
+    def qjl_attention_f64(self, query, pool, slots, block_size: int = 16) -> np.ndarray:
+        return self._qjl_att(self.lib.tqo_qjl_attention_f64, np.float64, query, pool, slots,
+                             block_size)
+
+    def qjl_attention_f32(self, query, pool, slots, block_size: int = 16) -> np.ndarray:
+        return self._qjl_att(self.lib.tqo_qjl_attention_f32, np.uint16, query, pool, slots,
+                             block_size)
+
+    def sdpa_gpu_ref(self, query, key, value):
+        """(fp16 output bits [Q,H,D], fp32 logits [Q,H,N]) of the GPU SDPA
+        reference kernel's algorithm."""
+        query, key, value = _u16(query), _u16(key), _u16(value)
+        Q, H, D = query.shape
+        N = key.shape[0]
+        out = np.zeros((Q, H, D), np.uint16)
+        lg = np.zeros((Q, H, max(N, 1)), np.float32)
+        self.lib.tqo_sdpa_gpu_ref(_p(query), _p(key), _p(value), _p(out), _p(lg), Q, N, H, D,
+                                  self.nthreads)
+        return out, lg[:, :, :N]
 
     # ---- misc ------------------------------------------------------------------
     def boundary_counts(self, scheme: str, key, value) -> tuple[int, int, int]:

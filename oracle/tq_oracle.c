@@ -784,3 +784,420 @@ void tqo_lloyd_max_gaussian(int M, int max_iter, double tol, double* levels, dou
     memcpy(levels, c, sizeof(double) * (size_t)M);
     memcpy(thr, t, sizeof(double) * (size_t)(M - 1));
 }
+
+/* ======================================================================== */
+/* Kernels the reference compiles but does not export:       */
+/* QJL-1b, the legacy INT4 and dense pages, and the GPU SDPA reference.       */
+/* ======================================================================== */
+
+/* src/tq_qjl.cpp:7-33 */
+void tqo_make_qjl_layout(int block_size, int H, int D, tqo_qjl_layout* L) {
+    memset(L, 0, sizeof(*L));
+    L->k1_bytes = (D + 7) / 8;
+    L->v4_bytes = (D * 4 + 7) / 8;
+    L->scale_bytes = 2;
+    size_t th = (size_t)block_size * (size_t)H, cur = 0;
+    L->k1_off = cur; cur += th * (size_t)L->k1_bytes;
+    cur = align_up(cur, 2);
+    L->ks_off = cur; cur += th * 2;
+    L->v4_off = cur; cur += th * (size_t)L->v4_bytes;
+    cur = align_up(cur, 2);
+    L->vs_off = cur; cur += th * 2;
+    L->page_size = align_up(cur, 2);
+}
+
+/* src/tq_layout.cpp:8-36; returns -1 where the reference throws (nbits != 4,
+ * group_size != head_dim).  scale_fp32: TQScaleType::FP32 (4-byte scales). */
+int tqo_make_int4_layout(int block_size, int H, int D, int nbits, int group_size,
+                         int page_alignment, int scale_fp32, tqo_int4_layout* L) {
+    memset(L, 0, sizeof(*L));
+    if (nbits != 4 || group_size != D) return -1;
+    size_t th = (size_t)block_size * (size_t)H, a = (size_t)page_alignment;
+    L->code_bytes = (size_t)D * (size_t)nbits / 8;
+    L->scale_bytes = scale_fp32 ? 4 : 2;
+    L->k_codes_off = 0;
+    L->k_codes_bytes = th * L->code_bytes;
+    L->v_codes_off = align_up(L->k_codes_off + L->k_codes_bytes, a);
+    L->v_codes_bytes = th * L->code_bytes;
+    L->k_scales_off = align_up(L->v_codes_off + L->v_codes_bytes, a);
+    L->k_scales_bytes = th * L->scale_bytes;
+    L->v_scales_off = align_up(L->k_scales_off + L->k_scales_bytes, a);
+    L->v_scales_bytes = th * L->scale_bytes;
+    L->page_size = align_up(L->v_scales_off + L->v_scales_bytes, a);
+    return 0;
+}
+
+/* src/tq_dense_layout.cpp:7-18 */
+void tqo_make_dense_layout(int block_size, int H, int D, int page_alignment,
+                           tqo_dense_layout* L) {
+    memset(L, 0, sizeof(*L));
+    size_t th = (size_t)block_size * (size_t)H, a = (size_t)page_alignment;
+    L->elem_bytes = 2;
+    L->k_off = 0;
+    L->k_bytes = th * (size_t)D * 2;
+    L->v_off = align_up(L->k_bytes, a);
+    L->v_bytes = th * (size_t)D * 2;
+    L->page_size = align_up(L->v_off + L->v_bytes, a);
+}
+
+/* ---- QJL-1b (src/cuda/tq_qjl_kernels.cu) -------------------------------- */
+/* The QJL kernels call sign_flip(idx) without the head (:16-19): (-1)^idx. */
+static float qjl_sign(int i) { return tqo_sign_flip(i, 0); }
+
+/* qjl_pack_kv_kernel, :72-181, one (token, head). */
+void tqo_qjl_pack_row(const uint16_t* k, const uint16_t* v, int D, uint8_t* k1, uint8_t* v4,
+                      uint16_t* ks, uint16_t* vs) {
+    float sk[TQO_MAX_D], sv[TQO_MAX_D], red[TQO_MAX_D];
+    int bits[TQO_MAX_D], vidx[TQO_MAX_D];
+    float inv = tqo_inv_sqrt_d(D);
+    for (int i = 0; i < D; ++i) {
+        sk[i] = tqo_h2f(k[i]) * qjl_sign(i);
+        sv[i] = tqo_h2f(v[i]) * qjl_sign(i);
+    }
+    tqo_wht(sk, D);
+    tqo_wht(sv, D);
+    for (int i = 0; i < D; ++i) { sk[i] *= inv; sv[i] *= inv; }
+    for (int i = 0; i < D; ++i) red[i] = sk[i] * sk[i];
+    float krms = rms_of(red, D, D);
+    *ks = tqo_f2h(krms);
+    for (int i = 0; i < D; ++i) red[i] = sv[i] * sv[i];
+    float vrms = rms_of(red, D, D);
+    *vs = tqo_f2h(vrms);
+    for (int i = 0; i < D; ++i) {
+        bits[i] = (sk[i] / krms >= 0.0f) ? 1 : 0;
+        vidx[i] = tqo_nearest_v4(clampf_ref(sv[i] / vrms, -2.75f, 2.75f));
+    }
+    for (int b = 0; b < (D + 7) / 8; ++b) { /* pack_1bit_byte_from_bits, shared_device :22-31 */
+        uint8_t o = 0;
+        for (int i = 0; i < 8; ++i)
+            if (8 * b + i < D) o |= (uint8_t)((bits[8 * b + i] & 1) << i);
+        k1[b] = o;
+    }
+    for (int j = 0; j < D / 2; ++j) v4[j] = (uint8_t)((vidx[2 * j + 1] << 4) | vidx[2 * j]);
+}
+
+typedef struct {
+    const uint16_t *k, *v;
+    const int32_t* slots;
+    int H, D, bs;
+    const tqo_qjl_layout* L;
+    uint8_t* pool;
+    const uint8_t* cpool;
+    uint16_t *ok, *ov;
+} qjl_ctx;
+
+static void qjl_pack_one(void* p, long long row) {
+    qjl_ctx* c = (qjl_ctx*)p;
+    int t = (int)(row / c->H), h = (int)(row % c->H);
+    int slot = c->slots[t];
+    if (slot < 0) return; /* this build's extension: unmapped token */
+    int page = slot / c->bs, tib = slot % c->bs;
+    size_t cell = (size_t)tib * c->H + h;
+    uint8_t* base = c->pool + (size_t)page * c->L->page_size;
+    uint16_t ks, vs;
+    const size_t off = (size_t)row * c->D;
+    tqo_qjl_pack_row(c->k + off, c->v + off, c->D, base + c->L->k1_off + cell * c->L->k1_bytes,
+                     base + c->L->v4_off + cell * c->L->v4_bytes, &ks, &vs);
+    put_h(base + c->L->ks_off + cell * 2, ks);
+    put_h(base + c->L->vs_off + cell * 2, vs);
+}
+
+void tqo_qjl_pack(const uint16_t* key, const uint16_t* value, const int32_t* slots,
+                  int num_tokens, int H, int D, int block_size, const tqo_qjl_layout* L,
+                  uint8_t* pool, int nthreads) {
+    qjl_ctx c = {key, value, slots, H, D, block_size, L, pool, NULL, NULL, NULL};
+    parallel_rows((long long)num_tokens * H, nthreads, qjl_pack_one, &c);
+}
+
+static int bit_get(const uint8_t* src, int i) { return (src[i >> 3] >> (i & 7)) & 1; }
+
+typedef struct {
+    const uint8_t *k1, *v4;
+    float ks, vs;
+} qjl_cell_t;
+
+static void qjl_cell(const uint8_t* pool, const int32_t* slots, int t, int h, int H, int bs,
+                     const tqo_qjl_layout* L, qjl_cell_t* o) {
+    int slot = slots[t], page = slot / bs, tib = slot % bs;
+    size_t cell = (size_t)tib * H + h;
+    const uint8_t* base = pool + (size_t)page * L->page_size;
+    o->k1 = base + L->k1_off + cell * L->k1_bytes;
+    o->v4 = base + L->v4_off + cell * L->v4_bytes;
+    o->ks = tqo_h2f(get_h(base + L->ks_off + cell * 2));
+    o->vs = tqo_h2f(get_h(base + L->vs_off + cell * 2));
+}
+
+/* qjl_dequant_kv_kernel, :189-245. */
+static void qjl_dequant_one(void* p, long long row) {
+    qjl_ctx* c = (qjl_ctx*)p;
+    int t = (int)(row / c->H), h = (int)(row % c->H), D = c->D;
+    if (c->slots[t] < 0) return;
+    qjl_cell_t ce;
+    qjl_cell(c->cpool, c->slots, t, h, c->H, c->bs, c->L, &ce);
+    float sk[TQO_MAX_D], sv[TQO_MAX_D];
+    for (int i = 0; i < D; ++i) {
+        sk[i] = (bit_get(ce.k1, i) ? 1.0f : -1.0f) * ce.ks;
+        sv[i] = kV4[nib_get(ce.v4, i)] * ce.vs;
+    }
+    tqo_wht(sk, D);
+    tqo_wht(sv, D);
+    float inv = tqo_inv_sqrt_d(D);
+    for (int i = 0; i < D; ++i) {
+        c->ok[(size_t)row * D + i] = tqo_f2h(sk[i] * inv * qjl_sign(i));
+        c->ov[(size_t)row * D + i] = tqo_f2h(sv[i] * inv * qjl_sign(i));
+    }
+}
+
+void tqo_qjl_dequant(const uint8_t* pool, const int32_t* slots, int num_tokens, int H, int D,
+                     int block_size, const tqo_qjl_layout* L, uint16_t* out_key,
+                     uint16_t* out_value, int nthreads) {
+    qjl_ctx c = {NULL, NULL, slots, H, D, block_size, L, NULL, pool, out_key, out_value};
+    parallel_rows((long long)num_tokens * H, nthreads, qjl_dequant_one, &c);
+}
+
+typedef struct {
+    const uint16_t* q;
+    const uint8_t* pool;
+    const int32_t* slots;
+    int Q, N, H, D, bs;
+    const tqo_qjl_layout* L;
+    double* out_d;
+    uint16_t* out_h;
+} qjl_att_ctx;
+
+/* Exact: logit = <qrot, +-ks> (no 1/sqrt(D), :254 "Logit convention"),
+ * softmax, acc = sum p * vs * V4, acc / l, inverse WHT, * s_i / sqrt(D). */
+static void qjl_att64_one(void* p, long long row) {
+    qjl_att_ctx* c = (qjl_att_ctx*)p;
+    int qi = (int)(row / c->H), h = (int)(row % c->H), D = c->D, N = c->N;
+    float qrot[TQO_MAX_D];
+    double qd[TQO_MAX_D], acc[TQO_MAX_D];
+    float inv = tqo_inv_sqrt_d(D);
+    const uint16_t* q = c->q + ((size_t)qi * c->H + h) * (size_t)D;
+    for (int i = 0; i < D; ++i) qrot[i] = tqo_h2f(q[i]) * qjl_sign(i);
+    tqo_wht(qrot, D);
+    for (int i = 0; i < D; ++i) { qd[i] = (double)(qrot[i] * inv); acc[i] = 0.0; }
+    double* lg = (double*)malloc(sizeof(double) * (size_t)(N > 0 ? N : 1));
+    double mx = -INFINITY;
+    for (int t = 0; t < N; ++t) {
+        if (c->slots[t] < 0) { lg[t] = -INFINITY; continue; }
+        qjl_cell_t ce;
+        qjl_cell(c->pool, c->slots, t, h, c->H, c->bs, c->L, &ce);
+        double s = 0.0;
+        for (int i = 0; i < D; ++i) s += bit_get(ce.k1, i) ? qd[i] : -qd[i];
+        lg[t] = s * (double)ce.ks;
+        if (lg[t] > mx) mx = lg[t];
+    }
+    double l = 0.0;
+    for (int t = 0; t < N; ++t) {
+        if (c->slots[t] < 0) continue;
+        qjl_cell_t ce;
+        qjl_cell(c->pool, c->slots, t, h, c->H, c->bs, c->L, &ce);
+        double w = exp(lg[t] - mx);
+        l += w;
+        for (int i = 0; i < D; ++i) acc[i] += w * (double)ce.vs * (double)kV4[nib_get(ce.v4, i)];
+    }
+    free(lg);
+    if (l > 0.0)
+        for (int i = 0; i < D; ++i) acc[i] /= l;
+    wht_f64(acc, D);
+    double invd = 1.0 / sqrt((double)D);
+    double* o = c->out_d + ((size_t)qi * c->H + h) * (size_t)D;
+    for (int i = 0; i < D; ++i) o[i] = acc[i] * invd * (double)qjl_sign(i);
+}
+
+/* qjl_fused_attn_online_kernel, :262-378, in fp32 in the kernel's order. */
+static void qjl_att32_one(void* p, long long row) {
+    qjl_att_ctx* c = (qjl_att_ctx*)p;
+    int qi = (int)(row / c->H), h = (int)(row % c->H), D = c->D;
+    float qrot[TQO_MAX_D], vacc[TQO_MAX_D], red[TQO_MAX_D];
+    float inv = tqo_inv_sqrt_d(D);
+    const uint16_t* q = c->q + ((size_t)qi * c->H + h) * (size_t)D;
+    for (int i = 0; i < D; ++i) qrot[i] = tqo_h2f(q[i]) * qjl_sign(i);
+    tqo_wht(qrot, D);
+    for (int i = 0; i < D; ++i) { qrot[i] *= inv; vacc[i] = 0.0f; }
+    float m = -1e30f, l = 0.0f;
+    for (int t = 0; t < c->N; ++t) {
+        if (c->slots[t] < 0) continue;
+        qjl_cell_t ce;
+        qjl_cell(c->pool, c->slots, t, h, c->H, c->bs, c->L, &ce);
+        for (int i = 0; i < D; ++i) red[i] = qrot[i] * ((bit_get(ce.k1, i) ? 1.0f : -1.0f) * ce.ks);
+        float logit = tqo_tree_sum(red, D);
+        float m_new = fmaxf(m, logit);
+        float a = expf(m - m_new), b = expf(logit - m_new);
+        l = l * a + b;
+        m = m_new;
+        for (int i = 0; i < D; ++i) {
+            vacc[i] *= a;
+            vacc[i] += b * (kV4[nib_get(ce.v4, i)] * ce.vs);
+        }
+    }
+    float inv_l = (l > 0.0f) ? (1.0f / l) : 1.0f;
+    for (int i = 0; i < D; ++i) vacc[i] *= inv_l;
+    tqo_wht(vacc, D);
+    uint16_t* o = c->out_h + ((size_t)qi * c->H + h) * (size_t)D;
+    for (int i = 0; i < D; ++i) o[i] = tqo_f2h(vacc[i] * inv * qjl_sign(i));
+}
+
+void tqo_qjl_attention_f64(const uint16_t* query, const uint8_t* pool, const int32_t* slots,
+                           int num_queries, int num_kv_tokens, int H, int D, int block_size,
+                           const tqo_qjl_layout* L, double* out, int nthreads) {
+    qjl_att_ctx c = {query, pool, slots, num_queries, num_kv_tokens, H, D, block_size, L, out, NULL};
+    parallel_rows((long long)num_queries * H, nthreads, qjl_att64_one, &c);
+}
+
+void tqo_qjl_attention_f32(const uint16_t* query, const uint8_t* pool, const int32_t* slots,
+                           int num_queries, int num_kv_tokens, int H, int D, int block_size,
+                           const tqo_qjl_layout* L, uint16_t* out, int nthreads) {
+    qjl_att_ctx c = {query, pool, slots, num_queries, num_kv_tokens, H, D, block_size, L, NULL, out};
+    parallel_rows((long long)num_queries * H, nthreads, qjl_att32_one, &c);
+}
+
+/* ---- legacy INT4 (src/cuda/tq_pack_kernels.cu, tq_dequant_kernels.cu) ---- */
+
+/* __float2int_rn: round half to even; NaN converts to 0 (PTX cvt.rni). */
+static int f2i_rn(float x) {
+    if (x != x) return 0;
+    float r = rintf(x);
+    if (r >= 2147483647.0f) return 2147483647;
+    if (r <= -2147483648.0f) return (-2147483647 - 1);
+    return (int)r;
+}
+
+/* quantize_to_int4, tq_pack_kernels.cu:30-34 */
+static int q_int4(float x, float scale) {
+    if (scale <= 1e-12f) return 0;
+    int q = f2i_rn(x / scale);
+    return q < -8 ? -8 : (q > 7 ? 7 : q);
+}
+
+/* tq_pack_kv_kernel, :36-110, one (token, head): scale = max(absmax / 7, 1e-8)
+ * (fp32; the fp16 copy is what is stored), codes two's-complement nibbles. */
+void tqo_int4_pack_row(const uint16_t* k, const uint16_t* v, int D, uint8_t* kc, uint8_t* vc,
+                       uint16_t* ks, uint16_t* vs) {
+    float ka = 0.0f, va = 0.0f;
+    for (int i = 0; i < D; ++i) {
+        ka = fmaxf(ka, fabsf(tqo_h2f(k[i])));
+        va = fmaxf(va, fabsf(tqo_h2f(v[i])));
+    }
+    float kscale = fmaxf(ka / 7.0f, 1e-8f), vscale = fmaxf(va / 7.0f, 1e-8f);
+    *ks = tqo_f2h(kscale);
+    *vs = tqo_f2h(vscale);
+    for (int i = 0; i < D; i += 2) {
+        int k0 = q_int4(tqo_h2f(k[i]), kscale), v0 = q_int4(tqo_h2f(v[i]), vscale);
+        int k1 = 0, v1 = 0;
+        if (i + 1 < D) {
+            k1 = q_int4(tqo_h2f(k[i + 1]), kscale);
+            v1 = q_int4(tqo_h2f(v[i + 1]), vscale);
+        }
+        kc[i / 2] = (uint8_t)((k0 & 0xF) | ((k1 & 0xF) << 4)); /* pack_int4, tq_quant.h:8-10 */
+        vc[i / 2] = (uint8_t)((v0 & 0xF) | ((v1 & 0xF) << 4));
+    }
+}
+
+typedef struct {
+    const uint16_t *k, *v;
+    const int32_t* slots;
+    int H, D, bs;
+    const tqo_int4_layout* L;
+    uint8_t* pool;
+    const uint8_t* cpool;
+    uint16_t *ok, *ov;
+} int4_ctx;
+
+static void int4_pack_one(void* p, long long row) {
+    int4_ctx* c = (int4_ctx*)p;
+    int t = (int)(row / c->H), h = (int)(row % c->H), slot = c->slots[t];
+    if (slot < 0) return;
+    int page = slot / c->bs, tib = slot % c->bs;
+    size_t cell = (size_t)tib * c->H + h;
+    uint8_t* base = c->pool + (size_t)page * c->L->page_size;
+    uint16_t ks, vs;
+    tqo_int4_pack_row(c->k + (size_t)row * c->D, c->v + (size_t)row * c->D, c->D,
+                      base + c->L->k_codes_off + cell * c->L->code_bytes,
+                      base + c->L->v_codes_off + cell * c->L->code_bytes, &ks, &vs);
+    /* a half at the scale cell, whatever the cell size (:84-88) */
+    put_h(base + c->L->k_scales_off + cell * c->L->scale_bytes, ks);
+    put_h(base + c->L->v_scales_off + cell * c->L->scale_bytes, vs);
+}
+
+void tqo_int4_pack(const uint16_t* key, const uint16_t* value, const int32_t* slots,
+                   int num_tokens, int H, int D, int block_size, const tqo_int4_layout* L,
+                   uint8_t* pool, int nthreads) {
+    int4_ctx c = {key, value, slots, H, D, block_size, L, pool, NULL, NULL, NULL};
+    parallel_rows((long long)num_tokens * H, nthreads, int4_pack_one, &c);
+}
+
+static int s4(int n) { return n >= 8 ? n - 16 : n; } /* unpack_int4_low/high, tq_quant.h:12-20 */
+
+/* tq_dequant_kv_kernel, tq_dequant_kernels.cu:6-55: f2h(q * f32(scale)). */
+static void int4_dequant_one(void* p, long long row) {
+    int4_ctx* c = (int4_ctx*)p;
+    int t = (int)(row / c->H), h = (int)(row % c->H), slot = c->slots[t], D = c->D;
+    if (slot < 0) return;
+    int page = slot / c->bs, tib = slot % c->bs;
+    size_t cell = (size_t)tib * c->H + h;
+    const uint8_t* base = c->cpool + (size_t)page * c->L->page_size;
+    const uint8_t* kc = base + c->L->k_codes_off + cell * c->L->code_bytes;
+    const uint8_t* vc = base + c->L->v_codes_off + cell * c->L->code_bytes;
+    float ks = tqo_h2f(get_h(base + c->L->k_scales_off + cell * c->L->scale_bytes));
+    float vs = tqo_h2f(get_h(base + c->L->v_scales_off + cell * c->L->scale_bytes));
+    for (int i = 0; i < D; ++i) {
+        int kn = (i & 1) ? kc[i / 2] >> 4 : kc[i / 2] & 0xF;
+        int vn = (i & 1) ? vc[i / 2] >> 4 : vc[i / 2] & 0xF;
+        c->ok[(size_t)row * D + i] = tqo_f2h((float)s4(kn) * ks);
+        c->ov[(size_t)row * D + i] = tqo_f2h((float)s4(vn) * vs);
+    }
+}
+
+void tqo_int4_dequant(const uint8_t* pool, const int32_t* slots, int num_tokens, int H, int D,
+                      int block_size, const tqo_int4_layout* L, uint16_t* out_key,
+                      uint16_t* out_value, int nthreads) {
+    int4_ctx c = {NULL, NULL, slots, H, D, block_size, L, NULL, pool, out_key, out_value};
+    parallel_rows((long long)num_tokens * H, nthreads, int4_dequant_one, &c);
+}
+
+/* ---- GPU SDPA reference (src/cuda/tq_attention_ref_kernel.cu:24-112) ----- */
+/* Per (query, head): logits = tree-sum(q * k) * inv into logit_scratch, max,
+ * sum of expf in token order, 1/sum, then V accumulated in token order with
+ * weight expf(l - max) * (1/sum); fp16 output.  fp32 throughout. */
+typedef struct {
+    const uint16_t *q, *k, *v;
+    uint16_t* out;
+    float* logits;
+    int Q, N, H, D;
+} sdpa_ctx;
+
+static void sdpa_gpu_one(void* p, long long row) {
+    sdpa_ctx* c = (sdpa_ctx*)p;
+    int qi = (int)(row / c->H), h = (int)(row % c->H), D = c->D, N = c->N;
+    float q[TQO_MAX_D], red[TQO_MAX_D], vacc[TQO_MAX_D];
+    float inv = tqo_inv_sqrt_d(D);
+    for (int i = 0; i < D; ++i) q[i] = tqo_h2f(c->q[((size_t)qi * c->H + h) * D + i]);
+    float* lg = c->logits + ((size_t)qi * c->H + h) * (size_t)N;
+    float mx = -1e30f;
+    for (int t = 0; t < N; ++t) {
+        const uint16_t* kr = c->k + ((size_t)t * c->H + h) * D;
+        for (int i = 0; i < D; ++i) red[i] = q[i] * tqo_h2f(kr[i]);
+        float logit = tqo_tree_sum(red, D) * inv;
+        lg[t] = logit;
+        if (logit > mx) mx = logit;
+    }
+    float s = 0.0f;
+    for (int t = 0; t < N; ++t) s += expf(lg[t] - mx);
+    float inv_sum = (s > 0.0f) ? (1.0f / s) : 1.0f;
+    for (int i = 0; i < D; ++i) vacc[i] = 0.0f;
+    for (int t = 0; t < N; ++t) {
+        float w = expf(lg[t] - mx) * inv_sum;
+        const uint16_t* vr = c->v + ((size_t)t * c->H + h) * D;
+        for (int i = 0; i < D; ++i) vacc[i] += w * tqo_h2f(vr[i]);
+    }
+    for (int i = 0; i < D; ++i) c->out[((size_t)qi * c->H + h) * D + i] = tqo_f2h(vacc[i]);
+}
+
+void tqo_sdpa_gpu_ref(const uint16_t* query, const uint16_t* key, const uint16_t* value,
+                      uint16_t* out, float* logits, int num_queries, int num_kv_tokens, int H,
+                      int D, int nthreads) {
+    sdpa_ctx c = {query, key, value, out, logits, num_queries, num_kv_tokens, H, D};
+    parallel_rows((long long)num_queries * H, nthreads, sdpa_gpu_one, &c);
+}

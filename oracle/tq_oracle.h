@@ -123,6 +123,52 @@ void tqo_mse_boundary_count(const uint16_t* key, const uint16_t* value, int num_
 void tqo_sdpa_single_head(const uint16_t* q, const uint16_t* k_all, const uint16_t* v_all,
                           int num_tokens, int head_dim, float* out);
 
+/* ---- QJL-1b, legacy INT4, dense, GPU SDPA reference --------------------- */
+typedef struct {
+    size_t page_size, k1_off, ks_off, v4_off, vs_off;
+    int k1_bytes, v4_bytes, scale_bytes;
+} tqo_qjl_layout;
+
+typedef struct {
+    size_t code_bytes, scale_bytes, k_codes_off, v_codes_off, k_scales_off, v_scales_off,
+        k_codes_bytes, v_codes_bytes, k_scales_bytes, v_scales_bytes, page_size;
+} tqo_int4_layout;
+
+typedef struct {
+    size_t elem_bytes, k_off, v_off, k_bytes, v_bytes, page_size;
+} tqo_dense_layout;
+
+void tqo_make_qjl_layout(int block_size, int H, int D, tqo_qjl_layout* out);
+int tqo_make_int4_layout(int block_size, int H, int D, int nbits, int group_size,
+                         int page_alignment, int scale_fp32, tqo_int4_layout* out);
+void tqo_make_dense_layout(int block_size, int H, int D, int page_alignment,
+                           tqo_dense_layout* out);
+void tqo_qjl_pack_row(const uint16_t* k, const uint16_t* v, int D, uint8_t* k1, uint8_t* v4,
+                      uint16_t* ks, uint16_t* vs);
+void tqo_qjl_pack(const uint16_t* key, const uint16_t* value, const int32_t* slots,
+                  int num_tokens, int H, int D, int block_size, const tqo_qjl_layout* L,
+                  uint8_t* pool, int nthreads);
+void tqo_qjl_dequant(const uint8_t* pool, const int32_t* slots, int num_tokens, int H, int D,
+                     int block_size, const tqo_qjl_layout* L, uint16_t* out_key,
+                     uint16_t* out_value, int nthreads);
+void tqo_qjl_attention_f64(const uint16_t* query, const uint8_t* pool, const int32_t* slots,
+                           int num_queries, int num_kv_tokens, int H, int D, int block_size,
+                           const tqo_qjl_layout* L, double* out, int nthreads);
+void tqo_qjl_attention_f32(const uint16_t* query, const uint8_t* pool, const int32_t* slots,
+                           int num_queries, int num_kv_tokens, int H, int D, int block_size,
+                           const tqo_qjl_layout* L, uint16_t* out, int nthreads);
+void tqo_int4_pack_row(const uint16_t* k, const uint16_t* v, int D, uint8_t* kc, uint8_t* vc,
+                       uint16_t* ks, uint16_t* vs);
+void tqo_int4_pack(const uint16_t* key, const uint16_t* value, const int32_t* slots,
+                   int num_tokens, int H, int D, int block_size, const tqo_int4_layout* L,
+                   uint8_t* pool, int nthreads);
+void tqo_int4_dequant(const uint8_t* pool, const int32_t* slots, int num_tokens, int H, int D,
+                      int block_size, const tqo_int4_layout* L, uint16_t* out_key,
+                      uint16_t* out_value, int nthreads);
+void tqo_sdpa_gpu_ref(const uint16_t* query, const uint16_t* key, const uint16_t* value,
+                      uint16_t* out, float* logits, int num_queries, int num_kv_tokens, int H,
+                      int D, int nthreads);
+
 /* ---- Lloyd-Max, src/gaussian_codebook.cpp:43-83 (M levels) -------------- */
 void tqo_lloyd_max_gaussian(int M, int max_iter, double tol, double* levels, double* thresholds);
 

@@ -9,6 +9,12 @@ oracle/build_ref.sh):
   ref_layouts.txt            the reference's make_tq_turbo_mse_page_layout
                              (src/tq_turbo_mse_layout.cpp:7-28) over 144
                              configs, via oracle/ref_layout_driver.cpp.
+  ref_legacy_layouts.txt     every field of the reference's make_tq_page_layout
+                             (src/tq_layout.cpp:8-36) and
+                             make_tq_dense_page_layout (src/tq_dense_layout.cpp)
+                             over 288 configs (FP16 and FP32 scales) and the
+                             configs the legacy factory rejects, via
+                             oracle/ref_legacy_layout_driver.cpp.
 
 Oracle-produced (seeded inputs, this build's CPU restatement as the checker;
 they pin the oracle against regressions and give the GPU tests fixed data):
@@ -43,7 +49,8 @@ N, H, D, B, PAGES = 37, 2, 128, 16, 5
 def reference_outputs() -> None:
     ref = ROOT / "oracle" / "_ref"
     for exe, name in (("gaussian_codebook", "ref_gaussian_codebook.txt"),
-                      ("ref_layouts", "ref_layouts.txt")):
+                      ("ref_layouts", "ref_layouts.txt"),
+                      ("ref_legacy_layouts", "ref_legacy_layouts.txt")):
         path = ref / exe
         if not path.exists():
             raise SystemExit(f"{path} missing: run oracle/build_ref.sh first")

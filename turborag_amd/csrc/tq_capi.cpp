@@ -129,6 +129,98 @@ PageGeom mse_geom(const TQConfig& cfg, const TQTurbomsePageLayout& l) {
     return g;
 }
 
+// src/tq_qjl.cpp:7-33 (host factory, also used to validate a caller's layout)
+TQQJLPageLayout make_qjl_layout(const TQConfig& cfg) {
+    TQQJLPageLayout l{};
+    l.k1_bytes_per_token_head = (cfg.head_dim + 7) / 8;
+    l.v4_bytes_per_token_head = (cfg.head_dim * 4 + 7) / 8;
+    l.scale_bytes_per_token_head = 2;
+    const size_t th = (size_t)cfg.block_size * (size_t)cfg.num_kv_heads;
+    size_t cur = 0;
+    l.k1_codes_offset = cur;
+    cur += th * (size_t)l.k1_bytes_per_token_head;
+    cur = align_up(cur, 2);
+    l.k_scales_offset = cur;
+    cur += th * 2;
+    l.v4_codes_offset = cur;
+    cur += th * (size_t)l.v4_bytes_per_token_head;
+    cur = align_up(cur, 2);
+    l.v_scales_offset = cur;
+    cur += th * 2;
+    l.page_size_bytes = align_up(cur, 2);
+    return l;
+}
+
+// src/tq_layout.cpp:8-36
+TQPageLayout make_int4_layout(const TQConfig& cfg) {
+    if (cfg.nbits != 4) throw Error("Only int4 is supported in MVP");
+    if (cfg.group_size != cfg.head_dim) throw Error("MVP expects group_size == head_dim");
+    TQPageLayout l{};
+    l.code_bytes_per_token_head = (size_t)(cfg.head_dim * cfg.nbits) / 8;
+    l.scale_bytes_per_token_head = cfg.scale_type == TQ_SCALE_FP16 ? 2 : 4;
+    const size_t th = (size_t)cfg.block_size * (size_t)cfg.num_kv_heads;
+    const size_t a = (size_t)cfg.page_alignment;
+    l.k_codes_offset = 0;
+    l.k_codes_bytes = th * l.code_bytes_per_token_head;
+    l.v_codes_offset = align_up(l.k_codes_offset + l.k_codes_bytes, a);
+    l.v_codes_bytes = th * l.code_bytes_per_token_head;
+    l.k_scales_offset = align_up(l.v_codes_offset + l.v_codes_bytes, a);
+    l.k_scales_bytes = th * l.scale_bytes_per_token_head;
+    l.v_scales_offset = align_up(l.k_scales_offset + l.k_scales_bytes, a);
+    l.v_scales_bytes = th * l.scale_bytes_per_token_head;
+    l.page_size_bytes = align_up(l.v_scales_offset + l.v_scales_bytes, a);
+    return l;
+}
+
+// src/tq_dense_layout.cpp:7-18
+TQDensePageLayout make_dense_layout(const TQConfig& cfg) {
+    TQDensePageLayout l{};
+    l.elem_bytes = 2;
+    const size_t th = (size_t)cfg.block_size * (size_t)cfg.num_kv_heads;
+    const size_t a = (size_t)cfg.page_alignment;
+    l.k_offset = 0;
+    l.k_bytes = th * (size_t)cfg.head_dim * 2;
+    l.v_offset = align_up(l.k_offset + l.k_bytes, a);
+    l.v_bytes = th * (size_t)cfg.head_dim * 2;
+    l.page_size_bytes = align_up(l.v_offset + l.v_bytes, a);
+    return l;
+}
+
+QjlGeom qjl_geom(const TQConfig& cfg, const TQQJLPageLayout& l) {
+    check_common(cfg, "QJL");
+    const TQQJLPageLayout want = make_qjl_layout(cfg);
+    if (l.k1_bytes_per_token_head != want.k1_bytes_per_token_head ||
+        l.v4_bytes_per_token_head != want.v4_bytes_per_token_head ||
+        l.scale_bytes_per_token_head != 2 || l.page_size_bytes < want.page_size_bytes)
+        throw Error("QJL: layout does not match head_dim (use tq_make_qjl_layout)");
+    return QjlGeom{l.page_size_bytes, l.k1_codes_offset, l.k_scales_offset, l.v4_codes_offset,
+                   l.v_scales_offset, l.k1_bytes_per_token_head, l.v4_bytes_per_token_head,
+                   cfg.num_kv_heads, cfg.head_dim, cfg.block_size};
+}
+
+Int4Geom int4_geom(const TQConfig& cfg, const TQPageLayout& l) {
+    check_common(cfg, "int4");
+    const TQPageLayout want = make_int4_layout(cfg);
+    if (l.code_bytes_per_token_head != want.code_bytes_per_token_head ||
+        l.scale_bytes_per_token_head != want.scale_bytes_per_token_head ||
+        l.page_size_bytes < want.page_size_bytes)
+        throw Error("int4: layout does not match cfg (use tq_make_int4_layout)");
+    return Int4Geom{l.page_size_bytes, l.k_codes_offset, l.v_codes_offset, l.k_scales_offset,
+                    l.v_scales_offset, (int)l.code_bytes_per_token_head,
+                    (int)l.scale_bytes_per_token_head, cfg.num_kv_heads, cfg.head_dim,
+                    cfg.block_size};
+}
+
+DenseGeom dense_geom(const TQConfig& cfg, const TQDensePageLayout& l) {
+    check_common(cfg, "dense");
+    const TQDensePageLayout want = make_dense_layout(cfg);
+    if (l.elem_bytes != 2 || l.k_bytes != want.k_bytes || l.page_size_bytes < want.page_size_bytes ||
+        (l.k_offset & 3) || (l.v_offset & 3) || (l.page_size_bytes & 3))
+        throw Error("dense: layout does not match cfg (use tq_make_dense_layout)");
+    return DenseGeom{l.page_size_bytes, l.k_offset, l.v_offset, cfg.num_kv_heads, cfg.head_dim,
+                     cfg.block_size};
+}
+
 int num_cus() {
     static std::mutex mu;
     static std::map<int, int> cache;
@@ -450,4 +542,166 @@ extern "C" int tq_launch_turbo_mse_paged_attention(
     void* stream) {
     return paged_attention(tq::Scheme::Mse, query, page_pool, block_tables, max_blocks_per_seq,
                            row_seq, row_kv_len, output, layout, cfg, num_rows, max_kv_len, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Kernels the reference compiles but does not export (QJL-1b, legacy INT4,
+// dense pages, GPU SDPA reference).  Zero tokens or queries do nothing.
+// ---------------------------------------------------------------------------
+namespace {
+void need_aligned4(const void* p, const char* what) {
+    if (reinterpret_cast<uintptr_t>(p) & 3) throw tq::Error(std::string(what) + ": pointer not 4-byte aligned");
+}
+void check_count(int n, const char* what) {
+    if (n < 0) throw tq::Error(std::string(what) + ": negative count");
+}
+}  // namespace
+
+extern "C" int tq_make_qjl_layout(const TQConfig* cfg, TQQJLPageLayout* out) {
+    if (!cfg || !out) return -1;
+    *out = tq::make_qjl_layout(*cfg);
+    return 0;
+}
+
+extern "C" int tq_launch_qjl_pack_kv(const uint16_t* key, const uint16_t* value,
+                                     const int32_t* slot_mapping, uint8_t* page_pool,
+                                     const TQQJLPageLayout* layout, const TQConfig* cfg,
+                                     int num_tokens, void* stream) {
+    if (!key || !value || !slot_mapping || !page_pool || !layout || !cfg) return -1;
+    return guarded([&] {
+        const tq::QjlGeom g = tq::qjl_geom(*cfg, *layout);
+        check_count(num_tokens, "qjl_pack_kv");
+        need_aligned4(key, "qjl_pack_kv key");
+        need_aligned4(value, "qjl_pack_kv value");
+        tq::launch_qjl_pack(key, value, slot_mapping, page_pool, g, num_tokens,
+                            static_cast<hipStream_t>(stream));
+    });
+}
+
+extern "C" int tq_launch_qjl_dequant_kv(const uint8_t* page_pool, const int32_t* slot_mapping,
+                                        uint16_t* out_key, uint16_t* out_value,
+                                        const TQQJLPageLayout* layout, const TQConfig* cfg,
+                                        int num_tokens, void* stream) {
+    if (!page_pool || !slot_mapping || !out_key || !out_value || !layout || !cfg) return -1;
+    return guarded([&] {
+        const tq::QjlGeom g = tq::qjl_geom(*cfg, *layout);
+        check_count(num_tokens, "qjl_dequant_kv");
+        need_aligned4(out_key, "qjl_dequant_kv out_key");
+        need_aligned4(out_value, "qjl_dequant_kv out_value");
+        tq::launch_qjl_dequant(page_pool, slot_mapping, out_key, out_value, g, num_tokens,
+                               static_cast<hipStream_t>(stream));
+    });
+}
+
+extern "C" int tq_launch_qjl_fused_attention_output(const uint16_t* query,
+                                                    const uint8_t* page_pool,
+                                                    const int32_t* slot_mapping, uint16_t* output,
+                                                    const TQQJLPageLayout* layout,
+                                                    const TQConfig* cfg, int num_queries,
+                                                    int num_kv_tokens, void* stream) {
+    if (!query || !page_pool || !slot_mapping || !output || !layout || !cfg) return -1;
+    return guarded([&] {
+        const tq::QjlGeom g = tq::qjl_geom(*cfg, *layout);
+        check_count(num_queries, "qjl_fused_attention_output");
+        check_count(num_kv_tokens, "qjl_fused_attention_output");
+        need_aligned4(query, "qjl_fused_attention_output query");
+        need_aligned4(output, "qjl_fused_attention_output output");
+        tq::launch_qjl_attention(query, page_pool, slot_mapping, output, g, num_queries,
+                                 num_kv_tokens, static_cast<hipStream_t>(stream));
+    });
+}
+
+extern "C" int tq_make_int4_layout(const TQConfig* cfg, TQPageLayout* out) {
+    if (!cfg || !out) return -1;
+    return guarded([&] { *out = tq::make_int4_layout(*cfg); });
+}
+
+extern "C" int tq_launch_int4_pack_kv(const uint16_t* key, const uint16_t* value,
+                                      const int32_t* slot_mapping, uint8_t* page_pool,
+                                      const TQPageLayout* layout, const TQConfig* cfg,
+                                      int num_tokens, void* stream) {
+    if (!key || !value || !slot_mapping || !page_pool || !layout || !cfg) return -1;
+    return guarded([&] {
+        const tq::Int4Geom g = tq::int4_geom(*cfg, *layout);
+        check_count(num_tokens, "int4_pack_kv");
+        need_aligned4(key, "int4_pack_kv key");
+        need_aligned4(value, "int4_pack_kv value");
+        tq::launch_int4_pack(key, value, slot_mapping, page_pool, g, num_tokens,
+                             static_cast<hipStream_t>(stream));
+    });
+}
+
+extern "C" int tq_launch_int4_dequant_kv(const uint8_t* page_pool, const int32_t* slot_mapping,
+                                         uint16_t* out_key, uint16_t* out_value,
+                                         const TQPageLayout* layout, const TQConfig* cfg,
+                                         int num_tokens, void* stream) {
+    if (!page_pool || !slot_mapping || !out_key || !out_value || !layout || !cfg) return -1;
+    return guarded([&] {
+        const tq::Int4Geom g = tq::int4_geom(*cfg, *layout);
+        check_count(num_tokens, "int4_dequant_kv");
+        need_aligned4(out_key, "int4_dequant_kv out_key");
+        need_aligned4(out_value, "int4_dequant_kv out_value");
+        tq::launch_int4_dequant(page_pool, slot_mapping, out_key, out_value, g, num_tokens,
+                                static_cast<hipStream_t>(stream));
+    });
+}
+
+extern "C" int tq_make_dense_layout(const TQConfig* cfg, TQDensePageLayout* out) {
+    if (!cfg || !out) return -1;
+    *out = tq::make_dense_layout(*cfg);
+    return 0;
+}
+
+extern "C" int tq_launch_dense_store_kv(const uint16_t* key, const uint16_t* value,
+                                        const int32_t* slot_mapping, uint8_t* page_pool,
+                                        const TQDensePageLayout* layout, const TQConfig* cfg,
+                                        int num_tokens, void* stream) {
+    if (!key || !value || !slot_mapping || !page_pool || !layout || !cfg) return -1;
+    return guarded([&] {
+        const tq::DenseGeom g = tq::dense_geom(*cfg, *layout);
+        check_count(num_tokens, "dense_store_kv");
+        need_aligned4(key, "dense_store_kv key");
+        need_aligned4(value, "dense_store_kv value");
+        need_aligned4(page_pool, "dense_store_kv page_pool");
+        tq::launch_dense_copy(true, key, value, nullptr, nullptr, slot_mapping, page_pool, g,
+                              num_tokens, static_cast<hipStream_t>(stream));
+    });
+}
+
+extern "C" int tq_launch_dense_load_kv(const uint8_t* page_pool, const int32_t* slot_mapping,
+                                       uint16_t* out_key, uint16_t* out_value,
+                                       const TQDensePageLayout* layout, const TQConfig* cfg,
+                                       int num_tokens, void* stream) {
+    if (!page_pool || !slot_mapping || !out_key || !out_value || !layout || !cfg) return -1;
+    return guarded([&] {
+        const tq::DenseGeom g = tq::dense_geom(*cfg, *layout);
+        check_count(num_tokens, "dense_load_kv");
+        need_aligned4(out_key, "dense_load_kv out_key");
+        need_aligned4(out_value, "dense_load_kv out_value");
+        need_aligned4(page_pool, "dense_load_kv page_pool");
+        tq::launch_dense_copy(false, nullptr, nullptr, out_key, out_value, slot_mapping,
+                              const_cast<uint8_t*>(page_pool), g, num_tokens,
+                              static_cast<hipStream_t>(stream));
+    });
+}
+
+extern "C" int tq_launch_attention_ref(const uint16_t* query, const uint16_t* key,
+                                       const uint16_t* value, uint16_t* output,
+                                       float* logit_scratch, const TQConfig* cfg,
+                                       int num_queries, int num_kv_tokens, void* stream) {
+    if (!query || !key || !value || !output || !logit_scratch || !cfg) return -1;
+    return guarded([&] {
+        // tq_attention_ref_kernel.cu:127-128
+        if (cfg->head_dim > 128)
+            throw tq::Error("attention_ref_gpu: head_dim > 128 is not supported");
+        check_common(*cfg, "attention_ref_gpu");
+        check_count(num_queries, "attention_ref_gpu");
+        check_count(num_kv_tokens, "attention_ref_gpu");
+        for (const void* p : {(const void*)query, (const void*)key, (const void*)value,
+                              (const void*)output})
+            need_aligned4(p, "attention_ref_gpu");
+        tq::launch_attention_ref(query, key, value, output, logit_scratch, cfg->num_kv_heads,
+                                 cfg->head_dim, num_queries, num_kv_tokens,
+                                 static_cast<hipStream_t>(stream));
+    });
 }

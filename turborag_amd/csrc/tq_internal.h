@@ -90,4 +90,50 @@ void launch_attention(Scheme s, const uint16_t* query, const uint8_t* pool, cons
                       uint16_t* output, const PageGeom& g, int num_queries, int num_kv_tokens,
                       hipStream_t stream);
 
+// ---- the reference's unexported kernels (tq_legacy.hip) -------------------
+// Byte geometry of a QJL-1b page (cell c = tib * H + h; K signs at
+// k1_off + c * k1_bytes, V codes at v4_off + c * v4_bytes, fp16 scales at
+// ks_off / vs_off + 2c).
+struct QjlGeom {
+    uint64_t page_size, k1_off, ks_off, v4_off, vs_off;
+    int k1_bytes, v4_bytes;
+    int H, D, block_size;
+};
+// Legacy INT4 page: codes at kc_off / vc_off + c * code_bytes, an fp16 scale
+// at the start of each scale cell (ks_off / vs_off + c * scale_bytes).
+struct Int4Geom {
+    uint64_t page_size, kc_off, vc_off, ks_off, vs_off;
+    int code_bytes, scale_bytes;
+    int H, D, block_size;
+};
+// Dense page: fp16 rows at k_off / v_off + c * 2D.
+struct DenseGeom {
+    uint64_t page_size, k_off, v_off;
+    int H, D, block_size;
+};
+QjlGeom qjl_geom(const TQConfig& cfg, const TQQJLPageLayout& layout);
+Int4Geom int4_geom(const TQConfig& cfg, const TQPageLayout& layout);
+DenseGeom dense_geom(const TQConfig& cfg, const TQDensePageLayout& layout);
+
+void launch_qjl_pack(const uint16_t* key, const uint16_t* value, const int32_t* slots,
+                     uint8_t* pool, const QjlGeom& g, int num_tokens, hipStream_t stream);
+void launch_qjl_dequant(const uint8_t* pool, const int32_t* slots, uint16_t* out_key,
+                        uint16_t* out_value, const QjlGeom& g, int num_tokens,
+                        hipStream_t stream);
+void launch_qjl_attention(const uint16_t* query, const uint8_t* pool, const int32_t* slots,
+                          uint16_t* output, const QjlGeom& g, int num_queries, int num_kv_tokens,
+                          hipStream_t stream);
+void launch_int4_pack(const uint16_t* key, const uint16_t* value, const int32_t* slots,
+                      uint8_t* pool, const Int4Geom& g, int num_tokens, hipStream_t stream);
+void launch_int4_dequant(const uint8_t* pool, const int32_t* slots, uint16_t* out_key,
+                         uint16_t* out_value, const Int4Geom& g, int num_tokens,
+                         hipStream_t stream);
+// store: [N, H, D] key/value -> pages; otherwise pages -> out_key/out_value.
+void launch_dense_copy(bool store, const uint16_t* key, const uint16_t* value, uint16_t* out_key,
+                       uint16_t* out_value, const int32_t* slots, uint8_t* pool,
+                       const DenseGeom& g, int num_tokens, hipStream_t stream);
+void launch_attention_ref(const uint16_t* query, const uint16_t* key, const uint16_t* value,
+                          uint16_t* output, float* logits, int H, int D, int num_queries,
+                          int num_kv_tokens, hipStream_t stream);
+
 }  // namespace tq

@@ -64,6 +64,37 @@ class TQTurbomsePageLayout(ctypes.Structure):
     ]
 
 
+class TQQJLPageLayout(ctypes.Structure):
+    """include/tq_qjl.cuh:21-33."""
+
+    _fields_ = [
+        ("page_size_bytes", c_size_t),
+        ("k1_codes_offset", c_size_t),
+        ("k_scales_offset", c_size_t),
+        ("v4_codes_offset", c_size_t),
+        ("v_scales_offset", c_size_t),
+        ("k1_bytes_per_token_head", c_int),
+        ("v4_bytes_per_token_head", c_int),
+        ("scale_bytes_per_token_head", c_int),
+    ]
+
+
+class TQPageLayout(ctypes.Structure):
+    """include/tq_layout.h:11-23 (the legacy INT4 page)."""
+
+    _fields_ = [(n, c_size_t) for n in (
+        "code_bytes_per_token_head", "scale_bytes_per_token_head", "k_codes_offset",
+        "v_codes_offset", "k_scales_offset", "v_scales_offset", "k_codes_bytes", "v_codes_bytes",
+        "k_scales_bytes", "v_scales_bytes", "page_size_bytes")]
+
+
+class TQDensePageLayout(ctypes.Structure):
+    """include/tq_dense_layout.h:5-12."""
+
+    _fields_ = [(n, c_size_t) for n in (
+        "elem_bytes", "k_offset", "v_offset", "k_bytes", "v_bytes", "page_size_bytes")]
+
+
 class TQStoreFormat(ctypes.Structure):
     """Format record of the on-disk store (.bin footer, .meta keys)."""
 
@@ -146,6 +177,27 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "tq_block_table_num_tokens": ([c_void_p, c_int32, _P(c_int)], c_int),
     "tq_block_table_blocks": ([c_void_p, c_int32, _P(c_int32), c_int, _P(c_int)], c_int),
     "tq_block_table_free_sequence": ([c_void_p, c_int32], c_int),
+    # the reference's unexported kernels: QJL-1b, legacy INT4, dense, SDPA reference
+    "tq_make_qjl_layout": ([_P(TQConfig), _P(TQQJLPageLayout)], c_int),
+    "tq_launch_qjl_pack_kv": ([c_void_p, c_void_p, _P(c_int32), _P(c_uint8), _P(TQQJLPageLayout),
+                               _P(TQConfig), c_int, c_void_p], c_int),
+    "tq_launch_qjl_dequant_kv": ([_P(c_uint8), _P(c_int32), c_void_p, c_void_p,
+                                  _P(TQQJLPageLayout), _P(TQConfig), c_int, c_void_p], c_int),
+    "tq_launch_qjl_fused_attention_output": ([c_void_p, _P(c_uint8), _P(c_int32), c_void_p,
+                                              _P(TQQJLPageLayout), _P(TQConfig), c_int, c_int,
+                                              c_void_p], c_int),
+    "tq_make_int4_layout": ([_P(TQConfig), _P(TQPageLayout)], c_int),
+    "tq_launch_int4_pack_kv": ([c_void_p, c_void_p, _P(c_int32), _P(c_uint8), _P(TQPageLayout),
+                                _P(TQConfig), c_int, c_void_p], c_int),
+    "tq_launch_int4_dequant_kv": ([_P(c_uint8), _P(c_int32), c_void_p, c_void_p,
+                                   _P(TQPageLayout), _P(TQConfig), c_int, c_void_p], c_int),
+    "tq_make_dense_layout": ([_P(TQConfig), _P(TQDensePageLayout)], c_int),
+    "tq_launch_dense_store_kv": ([c_void_p, c_void_p, _P(c_int32), _P(c_uint8),
+                                  _P(TQDensePageLayout), _P(TQConfig), c_int, c_void_p], c_int),
+    "tq_launch_dense_load_kv": ([_P(c_uint8), _P(c_int32), c_void_p, c_void_p,
+                                 _P(TQDensePageLayout), _P(TQConfig), c_int, c_void_p], c_int),
+    "tq_launch_attention_ref": ([c_void_p, c_void_p, c_void_p, c_void_p, _P(c_float),
+                                 _P(TQConfig), c_int, c_int, c_void_p], c_int),
     # on-disk store (tq_backend/cag_store.py formats)
     "tq_store_sha256_hex": ([c_void_p, c_size_t, ctypes.c_char_p], c_int),
     "tq_store_key": ([ctypes.c_char_p, c_int, ctypes.c_char_p, ctypes.c_char_p, c_size_t], c_int),
@@ -457,6 +509,113 @@ class TurboQuantWrapper:
                 self._stream(stream))
         if rc != 0:
             self._kernel_raise(rc, scheme, "paged_attn_output")
+
+    # ── the reference's unexported kernels ──────────────────────────── #
+    # QJL-1b (include/tq_qjl.cuh), legacy INT4 (include/tq_layout.h), dense
+    # (include/tq_dense_layout.h), GPU SDPA reference (include/tq_attention_ref.h).
+
+    def _layout(self, fn: str, cls, cfg):
+        layout = cls()
+        rc = getattr(self._lib, fn)(ctypes.byref(cfg), ctypes.byref(layout))
+        if rc != 0:
+            raise RuntimeError(f"{fn} failed: {self._last_cuda_error()}")
+        return layout
+
+    def make_qjl_layout_for(self, cfg: TQConfig) -> TQQJLPageLayout:
+        return self._layout("tq_make_qjl_layout", TQQJLPageLayout, cfg)
+
+    def make_int4_layout_for(self, cfg: TQConfig) -> TQPageLayout:
+        return self._layout("tq_make_int4_layout", TQPageLayout, cfg)
+
+    def make_dense_layout_for(self, cfg: TQConfig) -> TQDensePageLayout:
+        return self._layout("tq_make_dense_layout", TQDensePageLayout, cfg)
+
+    def _store_pages(self, scheme, fn, key, value, slot_mapping, page_pool, layout, cfg, stream):
+        N = key.shape[0]
+        thd = N * cfg.num_kv_heads * cfg.head_dim
+        self._check(scheme, "pack_kv", key=(key, torch.float16, thd),
+                    value=(value, torch.float16, thd), slot_mapping=(slot_mapping, torch.int32, N),
+                    page_pool=(page_pool, torch.uint8, 0))
+        rc = getattr(self._lib, fn)(self._vp(key), self._vp(value), self._i32p(slot_mapping),
+                                    self._u8p(page_pool), ctypes.byref(layout), ctypes.byref(cfg),
+                                    N, self._stream(stream))
+        if rc != 0:
+            self._kernel_raise(rc, scheme, "pack_kv")
+
+    def _load_pages(self, scheme, fn, page_pool, slot_mapping, out_key, out_value, layout, cfg,
+                    stream):
+        N = out_key.shape[0]
+        thd = N * cfg.num_kv_heads * cfg.head_dim
+        self._check(scheme, "dequant_kv", page_pool=(page_pool, torch.uint8, 0),
+                    slot_mapping=(slot_mapping, torch.int32, N),
+                    out_key=(out_key, torch.float16, thd), out_value=(out_value, torch.float16, thd))
+        rc = getattr(self._lib, fn)(self._u8p(page_pool), self._i32p(slot_mapping),
+                                    self._vp(out_key), self._vp(out_value), ctypes.byref(layout),
+                                    ctypes.byref(cfg), N, self._stream(stream))
+        if rc != 0:
+            self._kernel_raise(rc, scheme, "dequant_kv")
+
+    def qjl_pack(self, key, value, slot_mapping, page_pool, layout, cfg, stream: int = 0) -> None:
+        self._store_pages("qjl", "tq_launch_qjl_pack_kv", key, value, slot_mapping, page_pool,
+                          layout, cfg, stream)
+
+    def qjl_dequant(self, page_pool, slot_mapping, out_key, out_value, layout, cfg,
+                    stream: int = 0) -> None:
+        self._load_pages("qjl", "tq_launch_qjl_dequant_kv", page_pool, slot_mapping, out_key,
+                         out_value, layout, cfg, stream)
+
+    def qjl_fused_attn_output(self, query, page_pool, slot_mapping, output, layout, cfg,
+                              num_queries: int, num_kv_tokens: int, stream: int = 0) -> None:
+        """Logit convention <q, k> without 1/sqrt(D), as the QJL kernel
+        (src/cuda/tq_qjl_kernels.cu:254)."""
+        H, D = cfg.num_kv_heads, cfg.head_dim
+        self._check("qjl", "fused_attn_output", query=(query, torch.float16, num_queries * H * D),
+                    page_pool=(page_pool, torch.uint8, 0),
+                    slot_mapping=(slot_mapping, torch.int32, num_kv_tokens),
+                    output=(output, torch.float16, num_queries * H * D))
+        rc = self._lib.tq_launch_qjl_fused_attention_output(
+            self._vp(query), self._u8p(page_pool), self._i32p(slot_mapping), self._vp(output),
+            ctypes.byref(layout), ctypes.byref(cfg), num_queries, num_kv_tokens,
+            self._stream(stream))
+        if rc != 0:
+            self._kernel_raise(rc, "qjl", "fused_attn_output")
+
+    def int4_pack(self, key, value, slot_mapping, page_pool, layout, cfg, stream: int = 0) -> None:
+        self._store_pages("int4", "tq_launch_int4_pack_kv", key, value, slot_mapping, page_pool,
+                          layout, cfg, stream)
+
+    def int4_dequant(self, page_pool, slot_mapping, out_key, out_value, layout, cfg,
+                     stream: int = 0) -> None:
+        self._load_pages("int4", "tq_launch_int4_dequant_kv", page_pool, slot_mapping, out_key,
+                         out_value, layout, cfg, stream)
+
+    def dense_store(self, key, value, slot_mapping, page_pool, layout, cfg,
+                    stream: int = 0) -> None:
+        self._store_pages("dense", "tq_launch_dense_store_kv", key, value, slot_mapping,
+                          page_pool, layout, cfg, stream)
+
+    def dense_load(self, page_pool, slot_mapping, out_key, out_value, layout, cfg,
+                   stream: int = 0) -> None:
+        self._load_pages("dense", "tq_launch_dense_load_kv", page_pool, slot_mapping, out_key,
+                         out_value, layout, cfg, stream)
+
+    def attention_ref(self, query, key, value, output, logit_scratch, cfg, num_queries: int,
+                      num_kv_tokens: int, stream: int = 0) -> None:
+        """softmax(q k^T / sqrt(D)) V over contiguous fp16 K/V; logit_scratch
+        (float32, num_queries * H * num_kv_tokens) receives the logits."""
+        H, D = cfg.num_kv_heads, cfg.head_dim
+        self._check("sdpa", "attention_ref", query=(query, torch.float16, num_queries * H * D),
+                    key=(key, torch.float16, num_kv_tokens * H * D),
+                    value=(value, torch.float16, num_kv_tokens * H * D),
+                    output=(output, torch.float16, num_queries * H * D),
+                    logit_scratch=(logit_scratch, torch.float32,
+                                   num_queries * H * num_kv_tokens))
+        rc = self._lib.tq_launch_attention_ref(
+            self._vp(query), self._vp(key), self._vp(value), self._vp(output),
+            self._f32p(logit_scratch), ctypes.byref(cfg), num_queries, num_kv_tokens,
+            self._stream(stream))
+        if rc != 0:
+            self._kernel_raise(rc, "sdpa", "attention_ref")
 
     # ── allocation helpers (reference :385-415) ─────────────────────── #
 
