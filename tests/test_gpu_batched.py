@@ -85,3 +85,34 @@ def test_paged_matches_slot_map_attention(tq, cuda):
     err = (out.float() - ref.float()).abs().max() / ref.float().abs().max()
     assert err.item() < 2e-3
     b.close()
+
+
+def test_paged_many_sequences_against_slot_map_attention(tq, cuda):
+    """Over a hundred row groups (the pairing of groups runs over several
+    64-group chunks, with runs of odd and even length): every row group equals
+    the reference-ABI fused_attention_output over its sequence's slot map."""
+    rng = np.random.default_rng(540)
+    lens = rng.integers(20, 700, size=41)
+    widths = rng.integers(1, 6, size=41)
+    print(f"[batched many] groups={int(widths.sum())}", flush=True)
+    b = PagedBatch(tq, "turbo_prod", lens, widths, seed=541, device=cuda)
+    b.append_new_tokens(seed=906)
+    query, row_seq, row_len = b.decode_rows(seed=907)
+    out = torch.zeros_like(query)
+    b.attention(query, row_seq, row_len, b.block_tables(), out)
+    r = 0
+    worst = 0.0
+    for s, (L, w) in enumerate(zip(lens, widths)):
+        for j in range(w):
+            n = int(L) + j + 1
+            slots = torch.from_numpy(b.slots_of(s, n)).to(cuda)
+            ref = torch.zeros_like(query[r:r + 8])
+            tq.fused_attn_output(query[r:r + 8].contiguous(), b.pool, slots, ref, b.layout, b.cfg,
+                                 8, n)
+            torch.cuda.synchronize()
+            err = ((out[r:r + 8].float() - ref.float()).abs().max() / ref.float().abs().max()).item()
+            worst = max(worst, err)
+            r += 8
+    print(f"    worst rel diff {worst:.3e}", flush=True)
+    assert worst < 2e-3
+    b.close()

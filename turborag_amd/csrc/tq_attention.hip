@@ -12,6 +12,7 @@
 // Logits follow the reference's convention <q, k> / sqrt(D) (:426, :531,
 // turbo_mse :378).
 #include <algorithm>
+#include <type_traits>
 
 #include "tq_device.h"
 
@@ -246,6 +247,11 @@ struct PagedRows {
     const int32_t* row_seq;
     const int32_t* row_kv_len;
     int max_blocks;
+    // Two-position form: pair k covers row groups pair_first[k] and, when
+    // pair_count[k] == 2, the next group of the same sequence.
+    const int32_t* pair_first;
+    const int32_t* pair_count;
+    const int32_t* num_pairs;
 };
 
 // Workgroup barrier for LDS traffic only: waits for this wave's LDS accesses,
@@ -263,8 +269,10 @@ __device__ __forceinline__ _Float16 hi_lo(float x, bool lo) {
 }  // namespace mfma
 
 // CH = tokens per wave iteration (32: two QK tiles, one PV step; 64: four and
-// two); NW = waves per workgroup.
-template <bool PROD, int CH, int NW, bool PAGED>
+// two); NW = waves per workgroup; NP = row groups per workgroup (2: two new
+// tokens of one paged sequence share every decoded K/V chunk, each with its
+// own MFMA columns, softmax state and accumulators).
+template <bool PROD, int CH, int NW, bool PAGED, int NP = 1>
 __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     const uint16_t* __restrict__ query, const uint8_t* __restrict__ pool,
     const int32_t* __restrict__ slots, float* __restrict__ ws, PageGeom g, int num_queries,
@@ -274,6 +282,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     constexpr int kTiles = CH / 16, kSteps = CH / 32;
     static_assert(CH == 32 || CH == 64, "chunk of 32 or 64 tokens");
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+    static_assert(NP == 1 || (NP == 2 && PAGED), "two positions: paged rows only");
+    constexpr int kR = kRows * NP;  // query rows of the workgroup
     // Decode tables indexed by a code byte (low nibble = even d), fp16 pairs:
     // table 0 = K (prod: aK*K3, mse: aV*V4), table 1 = V (aV*V4), 32 copies
     // each.  Entry e of table t, copy c is word e*64 + 32t + c and lane l
@@ -281,14 +291,14 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     // banks.  After the token loop the space holds the per-wave results for
     // the merge.
     __shared__ __attribute__((aligned(256))) uint32_t lut[256][64];
-    __shared__ float qs[kRows][128];
-    __shared__ uint4 bqs[4][64];  // QK B operand (fp16 hi/lo q) of k-step s for lane l
+    __shared__ float qs[kR][128];
+    __shared__ uint4 bqs[NP][4][64];  // QK B operand (fp16 hi/lo q) of k-step s for lane l
     __shared__ uint64_t tko[kWaves][kChunk], tvo[kWaves][kChunk];
     __shared__ float4 tsc[kWaves][kChunk];  // per token: K scale a, residual scale b, vs, bias
-    __shared__ float mm[kWaves][kRows], ml[kWaves][kRows];
+    __shared__ float mm[kWaves][kR], ml[kWaves][kR];
     __shared__ uint32_t kstage[256], vstage[256];
-    static_assert(sizeof(float) * kWaves * kRows * 128 <= sizeof(lut), "merge space");
-    float(*mo)[kRows][128] = reinterpret_cast<float(*)[kRows][128]>(&lut[0][0]);
+    static_assert(sizeof(float) * kWaves * kR * 128 <= sizeof(lut), "merge space");
+    float(*mo)[kR][128] = reinterpret_cast<float(*)[kR][128]>(&lut[0][0]);
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
@@ -301,18 +311,27 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     // repeated page reads, and every XCD gets an even share of the splits.
     // The partial's slot in the workspace (pid) keeps the split-fastest
     // order the combine reads.
-    int split, h, rg;
+    int split, h, rg, npos = 1;
     size_t pid = blockIdx.x;
     if constexpr (PAGED) {
         constexpr int kRun = 8;
-        const int groups = (num_queries + kRows - 1) / kRows;
-        const int items = num_splits * g.H * groups;
+        // work units: row groups, or pairs of them (NP = 2; the grid is sized
+        // for one unit per group, the items past the pair count exit)
+        const int units = NP == 2 ? __builtin_amdgcn_readfirstlane(pr.num_pairs[0])
+                                  : (num_queries + kRows - 1) / kRows;
+        const int items = num_splits * g.H * units;
         const int x = blockIdx.x & 7, li = blockIdx.x >> 3;
         const int v = (((li / kRun) * 8 + x) * kRun) + li % kRun;
         if (v >= items) return;
-        rg = v % groups;
-        h = (v / groups) % g.H;
-        split = v / (groups * g.H);
+        const int unit = v % units;
+        h = (v / units) % g.H;
+        split = v / (units * g.H);
+        if constexpr (NP == 2) {
+            rg = __builtin_amdgcn_readfirstlane(pr.pair_first[unit]);
+            npos = __builtin_amdgcn_readfirstlane(pr.pair_count[unit]);
+        } else {
+            rg = unit;
+        }
         pid = (size_t)split + (size_t)num_splits * (h + (size_t)g.H * rg);
     } else {
         split = blockIdx.x % num_splits;
@@ -326,15 +345,26 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     // Paged rows: the group's sequence and per-row kv lengths (causal limit);
     // rowlen is that of this lane's MFMA column row.  A split past every row's
     // length has no partial (the combine does not read it).
-    int kv_end = num_kv_tokens, seq = 0, rowlen = 0;
+    int kv_end = num_kv_tokens, seq = 0;
+    // per position: this lane's column row length, the group's longest and
+    // shortest row
+    int rowlen[NP] = {}, gend[NP] = {}, gmin[NP] = {};
     if constexpr (PAGED) {
-        const int rr = rg * kRows + (lane & 7);
-        const int lv = rr < num_queries ? pr.row_kv_len[rr] : 0;
-        rowlen = __shfl(lv, i >> 1);
-        int m = max(lv, __shfl_xor(lv, 1));
-        m = max(m, __shfl_xor(m, 2));
-        m = max(m, __shfl_xor(m, 4));
-        kv_end = __builtin_amdgcn_readfirstlane(m);
+        kv_end = 0;
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            const int rr = (rg + p) * kRows + (lane & 7);
+            const int lv = p < npos && rr < num_queries ? pr.row_kv_len[rr] : 0;
+            rowlen[p] = __shfl(lv, i >> 1);
+            int m = max(lv, __shfl_xor(lv, 1)), n = min(lv, __shfl_xor(lv, 1));
+            m = max(m, __shfl_xor(m, 2));
+            n = min(n, __shfl_xor(n, 2));
+            m = max(m, __shfl_xor(m, 4));
+            n = min(n, __shfl_xor(n, 4));
+            gend[p] = __builtin_amdgcn_readfirstlane(m);
+            gmin[p] = __builtin_amdgcn_readfirstlane(n);
+            kv_end = max(kv_end, gend[p]);
+        }
         seq = __builtin_amdgcn_readfirstlane(pr.row_seq[rg * kRows]);
         if (t_begin >= kv_end) return;  // uniform over the workgroup, before any barrier
     }
@@ -402,8 +432,10 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     // Issue order matters (the vector-memory counter is in order): query
     // rows first, then the first chunk's slots; the decode tables are built
     // while they are in flight.
-    constexpr int kQPerWave = kRows / kWaves;
-    static_assert(kRows % kWaves == 0, "rows per wave");
+    constexpr int kQPerWave = kR / kWaves;
+    static_assert(kR % kWaves == 0, "rows per wave");
+    // Row r of the workgroup is row r % 8 of group rg + r / 8 (consecutive
+    // groups: rows rg * 8 + r).
     uint32_t qraw[kQPerWave];
 #pragma unroll
     for (int k = 0; k < kQPerWave; ++k) {
@@ -445,7 +477,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
         const int r = w + k * kWaves;
         float q0 = qf[k][0], q1 = qf[k][1];
         wht_pair<64>(q0, q1, lane);
-        const bool live = rg * kRows + r < num_queries;
+        const bool live = r / kRows < npos && rg * kRows + r < num_queries;
         qs[r][2 * lane] = live ? q0 * inv : 0.0f;
         qs[r][2 * lane + 1] = live ? q1 * inv : 0.0f;
     }
@@ -464,17 +496,20 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     // B operand of QK, built once per workgroup: column i = row i/2, hi (i
     // even) or lo (i odd) part; k-index 8*gq + e of step s is d = 32*gq + 8*s + e.
     const bool lo_col = (i & 1) != 0;
-    if (w < 4) {
-        const int s = w;
+    for (int ps = w; ps < 4 * NP; ps += kWaves) {  // (position, k-step) of the B operand
+        const int p = ps >> 2, s = ps & 3;
         half8 b;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) b[e] = hi_lo(qs[i >> 1][32 * gq + 8 * s + e], lo_col);
-        bqs[s][lane] = __builtin_bit_cast(uint4, b);
+        for (int e = 0; e < 8; ++e)
+            b[e] = hi_lo(qs[p * kRows + (i >> 1)][32 * gq + 8 * s + e], lo_col);
+        bqs[p][s][lane] = __builtin_bit_cast(uint4, b);
     }
     lds_barrier();
-    half8 bq[4];
+    half8 bq[NP][4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) bq[s] = __builtin_bit_cast(half8, bqs[s][lane]);
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) bq[p][s] = __builtin_bit_cast(half8, bqs[p][s][lane]);
     // Byte address of this lane's copy of entry 0 of each table; a lookup
     // puts the code byte into byte 1 (entry stride 256 B) with one v_perm.
     const uint32_t lutk = (uint32_t)reinterpret_cast<uintptr_t>((lds_u32*)&lut[0][lane & 31]);
@@ -486,152 +521,195 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
         return *reinterpret_cast<const lds_u32*>(a);
     };
 
-    float m_run = kInitMax, l_run = 0.0f;
-    f32x4 acc[8];
+    float m_run[NP], l_run[NP];
+    f32x4 acc[NP][8];
 #pragma unroll
-    for (int v = 0; v < 8; ++v) acc[v] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int p = 0; p < NP; ++p) {
+        m_run[p] = kInitMax;
+        l_run[p] = 0.0f;
+#pragma unroll
+        for (int v = 0; v < 8; ++v) acc[p][v] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    }
     bool first = true;
     int slot_nx = load_slot(t0 + kWaves * kChunk);
 
-    while (t0 < t_end) {  // wave-uniform
-        const uint4* kw = cur.kw;
-        const uint32_t(*vw)[8] = cur.vw;
-        {
-            const float ks = h2f(cur.ks), vs = h2f(cur.vs), re = PROD ? h2f(cur.re) : 0.0f;
-            tsc[w][lane & (kChunk - 1)] = cur.valid ? make_float4(ks * ck, ks * re * cr, vs, 0.0f)
-                                                    : make_float4(0.f, 0.f, 0.f, -INFINITY);
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        Chunk nxt;
-        const int t1 = t0 + kWaves * kChunk;
-        if (t1 < t_end) {  // codes of the next chunk, slots of the one after
-            fetch(t1, slot_nx, nxt);
-            slot_nx = load_slot(t1 + kWaves * kChunk);
-        }
+    // The chunk loop, for the positions the workgroup has (a pair unit of a
+    // single group runs the one-position loop).
+    auto chunk_loop = [&](auto npa) {
+        constexpr int NPA = decltype(npa)::value;
+        while (t0 < t_end) {  // wave-uniform
+            const uint4* kw = cur.kw;
+            const uint32_t(*vw)[8] = cur.vw;
+            {
+                const float ks = h2f(cur.ks), vs = h2f(cur.vs), re = PROD ? h2f(cur.re) : 0.0f;
+                tsc[w][lane & (kChunk - 1)] = cur.valid ? make_float4(ks * ck, ks * re * cr, vs, 0.0f)
+                                                        : make_float4(0.f, 0.f, 0.f, -INFINITY);
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            Chunk nxt;
+            const int t1 = t0 + kWaves * kChunk;
+            if (t1 < t_end) {  // codes of the next chunk, slots of the one after
+                fetch(t1, slot_nx, nxt);
+                slot_nx = load_slot(t1 + kWaves * kChunk);
+            }
 
-        // QK
-        f32x4 cb[kTiles], cs[kTiles];
-#pragma unroll
-        for (int tau = 0; tau < kTiles; ++tau) {
-            cb[tau] = (f32x4){0.f, 0.f, 0.f, 0.f};
-            cs[tau] = cb[tau];
-            const uint32_t wd[4] = {kw[tau].x, kw[tau].y, kw[tau].z, kw[tau].w};
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                cb[tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    as_h8(lookup(wd[s], 0, 0), lookup(wd[s], 1, 0), lookup(wd[s], 2, 0),
-                          lookup(wd[s], 3, 0)),
-                    bq[s], cb[tau], 0, 0, 0);
-                if (PROD) {
-                    // Residual signs (nibble bit 3: 1 -> +1) as fp16 pairs in
-                    // registers: high bytes 0x3C / 0xBC, low bytes 0.
-                    const uint32_t he = ((wd[s] << 4) & 0x80808080u) ^ 0xBCBCBCBCu;  // even d
-                    const uint32_t ho = (wd[s] & 0x80808080u) ^ 0xBCBCBCBCu;         // odd d
-                    cs[tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                        as_h8(__builtin_amdgcn_perm(ho, he, 0x040C000Cu),
-                              __builtin_amdgcn_perm(ho, he, 0x050C010Cu),
-                              __builtin_amdgcn_perm(ho, he, 0x060C020Cu),
-                              __builtin_amdgcn_perm(ho, he, 0x070C030Cu)),
-                        bq[s], cs[tau], 0, 0, 0);
+            // QK: one decoded A operand per k-step, an MFMA per position
+            f32x4 cb[NPA][kTiles], cs[NPA][kTiles];
+    #pragma unroll
+            for (int tau = 0; tau < kTiles; ++tau) {
+    #pragma unroll
+                for (int p = 0; p < NPA; ++p) {
+                    cb[p][tau] = (f32x4){0.f, 0.f, 0.f, 0.f};
+                    cs[p][tau] = cb[p][tau];
+                }
+                const uint32_t wd[4] = {kw[tau].x, kw[tau].y, kw[tau].z, kw[tau].w};
+    #pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const half8 a = as_h8(lookup(wd[s], 0, 0), lookup(wd[s], 1, 0),
+                                          lookup(wd[s], 2, 0), lookup(wd[s], 3, 0));
+    #pragma unroll
+                    for (int p = 0; p < NPA; ++p)
+                        cb[p][tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[p][s], cb[p][tau],
+                                                                            0, 0, 0);
+                    if (PROD) {
+                        // Residual signs (nibble bit 3: 1 -> +1) as fp16 pairs in
+                        // registers: high bytes 0x3C / 0xBC, low bytes 0.
+                        const uint32_t he = ((wd[s] << 4) & 0x80808080u) ^ 0xBCBCBCBCu;  // even d
+                        const uint32_t ho = (wd[s] & 0x80808080u) ^ 0xBCBCBCBCu;         // odd d
+                        const half8 sa = as_h8(__builtin_amdgcn_perm(ho, he, 0x040C000Cu),
+                                               __builtin_amdgcn_perm(ho, he, 0x050C010Cu),
+                                               __builtin_amdgcn_perm(ho, he, 0x060C020Cu),
+                                               __builtin_amdgcn_perm(ho, he, 0x070C030Cu));
+    #pragma unroll
+                        for (int p = 0; p < NPA; ++p)
+                            cs[p][tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sa, bq[p][s],
+                                                                                cs[p][tau], 0, 0, 0);
+                    }
                 }
             }
-        }
-        // Logits (base 2) of tokens 16*tau + 4*gq + e; hi + lo columns summed.
-        float lg[kTiles][4];
-        float mloc = -INFINITY;
-#pragma unroll
-        for (int tau = 0; tau < kTiles; ++tau)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float4 sc = tsc[w][16 * tau + 4 * gq + e];
-                const float sb = cb[tau][e] + quad_xor<1>(cb[tau][e]);
-                const float sr = PROD ? cs[tau][e] + quad_xor<1>(cs[tau][e]) : 0.0f;
-                lg[tau][e] = fmaf(sb, sc.x, fmaf(sr, sc.y, sc.w));
-                if constexpr (PAGED)  // causal limit of this column's row
-                    if (t0 + 16 * tau + 4 * gq + e >= rowlen) lg[tau][e] = -INFINITY;
-                mloc = fmaxf(mloc, lg[tau][e]);
-            }
-        mloc = fmaxf(mloc, lane_xor<16>(mloc));
-        mloc = fmaxf(mloc, lane_xor<32>(mloc));
-        // v_exp_f32 without denormal handling: arguments are <= 0 and a
-        // weight below 2^-126 of the running maximum is negligible.
-        const float m_new = fmaxf(m_run, mloc);
-        const float alpha = first ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-        m_run = m_new;
-        float lsum = 0.0f;
-#pragma unroll
-        for (int tau = 0; tau < kTiles; ++tau)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                lg[tau][e] = __builtin_amdgcn_exp2f(lg[tau][e] - m_new);
-                lsum += lg[tau][e];
-            }
-        l_run = l_run * alpha + lsum;
-        if (!first && __any(alpha != 1.0f)) {
-            // acc lane (d, gq) holds columns 4gq..4gq+3 = rows 2gq, 2gq+1.
-            const float a0 = __shfl(alpha, 4 * gq), a1 = __shfl(alpha, 4 * gq + 2);
-#pragma unroll
-            for (int v = 0; v < 8; ++v) {
-                acc[v][0] *= a0;
-                acc[v][1] *= a0;
-                acc[v][2] *= a1;
-                acc[v][3] *= a1;
-            }
-        }
-        // PV
-#pragma unroll
-        for (int p = 0; p < kSteps; ++p) {
-            half8 ap;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int tau = 2 * p + (e >> 2), ee = e & 3;
-                const float vs = tsc[w][16 * tau + 4 * gq + ee].z;
-                ap[e] = hi_lo(lg[tau][ee] * vs, lo_col);
-            }
-            uint32_t bv[8][4];  // [N-tile v = d - 8i][token pair]
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const uint32_t we = vw[p][2 * q], wo = vw[p][2 * q + 1];
-                const uint32_t lob = (we & 0x0F0F0F0Fu) | ((wo & 0x0F0F0F0Fu) << 4);
-                const uint32_t hib = ((we >> 4) & 0x0F0F0F0Fu) | (wo & 0xF0F0F0F0u);
-#pragma unroll
-                for (int b = 0; b < 4; ++b) {
-                    bv[2 * b][q] = lookup(lob, b, 1);
-                    bv[2 * b + 1][q] = lookup(hib, b, 1);
+            // Logits (base 2) of tokens 16*tau + 4*gq + e; hi + lo columns summed.
+            float lg[NPA][kTiles][4];
+    #pragma unroll
+            for (int p = 0; p < NPA; ++p) {
+                // rows shorter than the chunk's end need the causal mask
+                const bool masked = PAGED && t0 + kChunk > gmin[p];
+                float mloc = -INFINITY;
+    #pragma unroll
+                for (int tau = 0; tau < kTiles; ++tau)
+    #pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float4 sc = tsc[w][16 * tau + 4 * gq + e];
+                        const float sb = cb[p][tau][e] + quad_xor<1>(cb[p][tau][e]);
+                        const float sr = PROD ? cs[p][tau][e] + quad_xor<1>(cs[p][tau][e]) : 0.0f;
+                        lg[p][tau][e] = fmaf(sb, sc.x, fmaf(sr, sc.y, sc.w));
+                        if (masked)  // causal limit of this column's row
+                            if (t0 + 16 * tau + 4 * gq + e >= rowlen[p]) lg[p][tau][e] = -INFINITY;
+                        mloc = fmaxf(mloc, lg[p][tau][e]);
+                    }
+                mloc = fmaxf(mloc, lane_xor<16>(mloc));
+                mloc = fmaxf(mloc, lane_xor<32>(mloc));
+                // v_exp_f32 without denormal handling: arguments are <= 0 and a
+                // weight below 2^-126 of the running maximum is negligible.
+                const float m_new = fmaxf(m_run[p], mloc);
+                const float alpha = first ? 0.0f : __builtin_amdgcn_exp2f(m_run[p] - m_new);
+                m_run[p] = m_new;
+                float lsum = 0.0f;
+    #pragma unroll
+                for (int tau = 0; tau < kTiles; ++tau)
+    #pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        lg[p][tau][e] = __builtin_amdgcn_exp2f(lg[p][tau][e] - m_new);
+                        lsum += lg[p][tau][e];
+                    }
+                l_run[p] = l_run[p] * alpha + lsum;
+                if (!first && __any(alpha != 1.0f)) {
+                    // acc lane (d, gq) holds columns 4gq..4gq+3 = rows 2gq, 2gq+1.
+                    const float a0 = __shfl(alpha, 4 * gq), a1 = __shfl(alpha, 4 * gq + 2);
+    #pragma unroll
+                    for (int v = 0; v < 8; ++v) {
+                        acc[p][v][0] *= a0;
+                        acc[p][v][1] *= a0;
+                        acc[p][v][2] *= a1;
+                        acc[p][v][3] *= a1;
+                    }
                 }
             }
-#pragma unroll
-            for (int v = 0; v < 8; ++v)
-                acc[v] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    ap, as_h8(bv[v][0], bv[v][1], bv[v][2], bv[v][3]), acc[v], 0, 0, 0);
+            // PV: one decoded B operand per N-tile, an MFMA per position
+    #pragma unroll
+            for (int st = 0; st < kSteps; ++st) {
+                half8 ap[NPA];
+    #pragma unroll
+                for (int p = 0; p < NPA; ++p)
+    #pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const int tau = 2 * st + (e >> 2), ee = e & 3;
+                        const float vs = tsc[w][16 * tau + 4 * gq + ee].z;
+                        ap[p][e] = hi_lo(lg[p][tau][ee] * vs, lo_col);
+                    }
+                uint32_t bv[8][4];  // [N-tile v = d - 8i][token pair]
+    #pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const uint32_t we = vw[st][2 * q], wo = vw[st][2 * q + 1];
+                    const uint32_t lob = (we & 0x0F0F0F0Fu) | ((wo & 0x0F0F0F0Fu) << 4);
+                    const uint32_t hib = ((we >> 4) & 0x0F0F0F0Fu) | (wo & 0xF0F0F0F0u);
+    #pragma unroll
+                    for (int b = 0; b < 4; ++b) {
+                        bv[2 * b][q] = lookup(lob, b, 1);
+                        bv[2 * b + 1][q] = lookup(hib, b, 1);
+                    }
+                }
+    #pragma unroll
+                for (int v = 0; v < 8; ++v) {
+                    const half8 bvv = as_h8(bv[v][0], bv[v][1], bv[v][2], bv[v][3]);
+    #pragma unroll
+                    for (int p = 0; p < NPA; ++p)
+                        acc[p][v] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ap[p], bvv, acc[p][v], 0, 0,
+                                                                           0);
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            cur = nxt;
+            t0 = t1;
+            first = false;
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        cur = nxt;
-        t0 = t1;
-        first = false;
-    }
+    };
+    if (NP == 2 && npos == 2)
+        chunk_loop(std::integral_constant<int, NP>{});
+    else
+        chunk_loop(std::integral_constant<int, 1>{});
 
     // Wave results: l summed over the g lanes of each column; o rows from the
     // hi + lo columns, the V codebook scale divided out.
-    float l_tot = l_run + lane_xor<16>(l_run);
-    l_tot += lane_xor<32>(l_tot);
-    if (gq == 0 && !lo_col) {
-        mm[w][i >> 1] = m_run;
-        ml[w][i >> 1] = l_tot;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        float l_tot = l_run[p] + lane_xor<16>(l_run[p]);
+        l_tot += lane_xor<32>(l_tot);
+        if (gq == 0 && !lo_col) {
+            mm[w][p * kRows + (i >> 1)] = m_run[p];
+            ml[w][p * kRows + (i >> 1)] = l_tot;
+        }
     }
     __syncthreads();  // every wave is done with the tables that mo overwrites
     const float iav = 1.0f / kAlphaV;
 #pragma unroll
-    for (int v = 0; v < 8; ++v) {
-        mo[w][2 * gq][8 * i + v] = (acc[v][0] + acc[v][1]) * iav;
-        mo[w][2 * gq + 1][8 * i + v] = (acc[v][2] + acc[v][3]) * iav;
-    }
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+            mo[w][p * kRows + 2 * gq][8 * i + v] = (acc[p][v][0] + acc[p][v][1]) * iav;
+            mo[w][p * kRows + 2 * gq + 1][8 * i + v] = (acc[p][v][2] + acc[p][v][3]) * iav;
+        }
     __syncthreads();
 
     // Merge the waves; inverse WHT and sign flip; partial to the workspace.
-    for (int r = w; r < kRows; r += kWaves) {
+    // A group whose rows all end before this split has no partial (its
+    // combine reads only the splits below its longest row).
+    for (int r = w; r < kR; r += kWaves) {
+        const int p = r / kRows;
+        bool keep = p < npos;
+        if constexpr (PAGED) keep = keep && t_begin < gend[p];
+        if (!keep) continue;  // wave-uniform
         float M = mm[0][r];
 #pragma unroll
         for (int u = 1; u < kWaves; ++u) M = fmaxf(M, mm[u][r]);
@@ -645,7 +723,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
         }
         wht_pair<64>(o0, o1, lane);
         const float s0 = (h & 1) ? -inv : inv;
-        float* part = ws + (pid * kRows + r) * kPartStride;
+        float* part = ws + ((pid + (size_t)num_splits * g.H * p) * kRows + r % kRows) * kPartStride;
         part[2 * lane] = o0 * s0;
         part[2 * lane + 1] = o1 * -s0;
         if (lane == 0) {
@@ -654,7 +732,6 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
         }
     }
 }
-
 // Sum of the split partials of one output row (q, h): o = sum_s 2^(m_s - M)
 // o_s / sum_s 2^(m_s - M) l_s.  Block = (row, 32-element slice of d), 256
 // threads = 8 groups x 32 d.  Group g takes splits g, g + 8, ...: it loads up
@@ -736,7 +813,7 @@ __global__ __launch_bounds__(256) void attn_mfma_combine_kernel(
 // thread t takes row t / 32 and elements 4(t % 32) .. +3 over every split
 // (8 in flight).  One block per item instead of 4 per row: for the many short
 // items of a batched decode step the block count, not the bytes, is the cost.
-constexpr int kItemCombineMaxSplits = 16;
+constexpr int kItemCombineMaxSplits = 32;
 template <bool PAGED>
 __global__ __launch_bounds__(256) void attn_mfma_combine_items_kernel(
     const float* __restrict__ ws, uint16_t* __restrict__ output, int H, int num_splits,
@@ -792,6 +869,42 @@ __global__ __launch_bounds__(256) void attn_mfma_combine_items_kernel(
     const auto fin = [&](float o) { return (uint32_t)f2h(L > 0.f ? o / L : o); };
     *reinterpret_cast<uint2*>(output + ((size_t)q * H + h) * 128 + d0) =
         make_uint2(fin(acc.x) | (fin(acc.y) << 16), fin(acc.z) | (fin(acc.w) << 16));
+}
+
+// Pairs of row groups for the two-position paged kernel, from row_seq (rows
+// in aligned groups of 8 share a sequence): each run of consecutive groups of
+// one sequence is cut into pairs from its start, the last one single when the
+// run is odd.  One wave walks the groups 64 at a time: a group starts a run
+// when its sequence differs from the previous group's, and starts a pair when
+// its distance from its run's start is even.
+__global__ __launch_bounds__(64) void pair_groups_kernel(const int32_t* __restrict__ row_seq,
+                                                         int groups, int32_t* __restrict__ first,
+                                                         int32_t* __restrict__ count,
+                                                         int32_t* __restrict__ num_pairs) {
+    using mfma::kRows;
+    const int lane = threadIdx.x;
+    int run_start = 0, out = 0;
+    for (int g0 = 0; g0 < groups; g0 += 64) {
+        const int gi = g0 + lane;
+        const bool in = gi < groups;
+        const int sq = in ? row_seq[(size_t)gi * kRows] : 0;
+        const int before = in && gi > 0 ? row_seq[(size_t)(gi - 1) * kRows] : 0;
+        const int after = gi + 1 < groups ? row_seq[(size_t)(gi + 1) * kRows] : 0;
+        const bool new_run = in && (gi == 0 || sq != before);
+        const uint64_t runs = __ballot(new_run);
+        const uint64_t upto = runs & (lane == 63 ? ~0ull : ((2ull << lane) - 1));
+        const int rs = upto ? g0 + 63 - __builtin_clzll(upto) : run_start;
+        const bool start = in && ((gi - rs) & 1) == 0;
+        const uint64_t starts = __ballot(start);
+        if (start) {
+            const int k = out + __builtin_popcountll(starts & ((1ull << lane) - 1));
+            first[k] = gi;
+            count[k] = gi + 1 < groups && after == sq ? 2 : 1;
+        }
+        out += __builtin_popcountll(starts);
+        run_start = __shfl(rs, 63);
+    }
+    if (lane == 0) num_pairs[0] = out;
 }
 
 // Split kernel shape: tokens per wave iteration and waves per workgroup.
@@ -917,26 +1030,40 @@ void launch_paged_attention(Scheme s, const uint16_t* query, const uint8_t* pool
     const int row_groups = (num_rows + kRows - 1) / kRows;
     const int heads = g.H * row_groups;
     // Split length: a multiple of one workgroup pass (waves x chunk) sized so
-    // that the longest group yields about 8 workgroups per CU in total.
+    // that the longest group would yield about 8 workgroups per CU in total
+    // (pairs of groups then take about half that: the per-workgroup setup is
+    // amortised over as many passes as with one group per workgroup).
     constexpr int kPass = kSplitChunk * kSplitWaves;
     const long long want_tokens =
         ((long long)std::max(max_kv_len, 1) * heads + 8LL * num_cus() - 1) / (8LL * num_cus());
     const int tps = (int)std::max<long long>(
         kPass, ((want_tokens + kPass - 1) / kPass) * kPass);
     const int splits = std::max(1, (max_kv_len + tps - 1) / tps);
-    const size_t items = (size_t)splits * heads;
+    const size_t items = (size_t)splits * heads;  // partial slots: (split, head, group)
     const size_t blocks = 64 * ((items + 63) / 64);  // runs of 8 dealt to 8 XCDs (see the kernel)
-    float* ws = static_cast<float*>(workspace(stream, items * kRows * kPartStride * sizeof(float)));
-    const PagedRows pr{block_tables, row_seq, row_kv_len, max_blocks};
+    // Workspace: the partials, then the pair table of the row groups.
+    const size_t part_bytes = items * kRows * kPartStride * sizeof(float);
+    char* wsb = static_cast<char*>(
+        workspace(stream, part_bytes + (2 * (size_t)row_groups + 1) * sizeof(int32_t)));
+    float* ws = reinterpret_cast<float*>(wsb);
+    int32_t* pair_first = reinterpret_cast<int32_t*>(wsb + part_bytes);
+    int32_t* pair_count = pair_first + row_groups;
+    int32_t* num_pairs = pair_count + row_groups;
+    const PagedRows pr{block_tables, row_seq, row_kv_len, max_blocks,
+                       pair_first, pair_count, num_pairs};
     const bool prod = s == Scheme::Prod;
     constexpr int kCH = kSplitChunk, kNW = kSplitWaves;
     if (max_kv_len > 0) {
+        hipLaunchKernelGGL(pair_groups_kernel, dim3(1), dim3(64), 0, stream, row_seq, row_groups,
+                           pair_first, pair_count, num_pairs);
+        check_launch(prod ? "turbo_prod_paged_attn_pairs" : "turbo_mse_paged_attn_pairs");
+        // The grid covers every row group as a unit; units past the pair count exit.
         if (prod)
-            hipLaunchKernelGGL((attn_mfma_split_kernel<true, kCH, kNW, true>), dim3(blocks),
+            hipLaunchKernelGGL((attn_mfma_split_kernel<true, kCH, kNW, true, 2>), dim3(blocks),
                                dim3(64 * kNW), 0, stream, query, pool, nullptr, ws, g, num_rows,
                                max_kv_len, tps, splits, inv, pr);
         else
-            hipLaunchKernelGGL((attn_mfma_split_kernel<false, kCH, kNW, true>), dim3(blocks),
+            hipLaunchKernelGGL((attn_mfma_split_kernel<false, kCH, kNW, true, 2>), dim3(blocks),
                                dim3(64 * kNW), 0, stream, query, pool, nullptr, ws, g, num_rows,
                                max_kv_len, tps, splits, inv, pr);
         check_launch(prod ? "turbo_prod_paged_attn_split" : "turbo_mse_paged_attn_split");
