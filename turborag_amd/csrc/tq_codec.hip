@@ -99,14 +99,16 @@ __device__ __forceinline__ void wht_wide(float (&x)[E], int j) {
                 x[k] = a + b;
                 x[k + len] = a - b;
             }
+    // Cross-lane stages: partner + (+-mine), the signed copies made for all
+    // E values first so that no DPP add waits on the VALU op just before it.
 #pragma unroll
     for (int m = 1; m < 16; m <<= 1) {
         const bool lower = (j & m) == 0;
+        float t[E];
 #pragma unroll
-        for (int k = 0; k < E; ++k) {
-            const float p = xor_lane(x[k], m);
-            x[k] = lower ? x[k] + p : p - x[k];
-        }
+        for (int k = 0; k < E; ++k) t[k] = lower ? x[k] : -x[k];
+#pragma unroll
+        for (int k = 0; k < E; ++k) x[k] = xor_lane(x[k], m) + t[k];
     }
 }
 
@@ -170,15 +172,15 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
         vrms = sqrtf(tree_wide<E>(r) / (float)D);
         if (vrms < kMinRMS) vrms = kMinRMS;
         float e[E];
+        const float ky = 1.0f / krms, vy = 1.0f / vrms;
 #pragma unroll
         for (int k = 0; k < E; ++k) {
-            const float kn = clamp_ref(xk[k] / krms, -2.5f, 2.5f);
-            const float vn = clamp_ref(xv[k] / vrms, -2.75f, 2.75f);
-            float lv;
-            const uint32_t c = (uint32_t)nearest_k3(kn, lv);
-            e[k] = kn - lv;
-            kcode |= (((e[k] >= 0.0f) ? 8u : 0u) | c) << (4 * k);
-            vcode |= (uint32_t)nearest_v4(vn) << (4 * k);
+            const float kn = clamp_ref(div_by(xk[k], krms, ky), -2.5f, 2.5f);
+            const float vn = clamp_ref(div_by(xv[k], vrms, vy), -2.75f, 2.75f);
+            const int c = nearest_k3_count(kn);
+            e[k] = kn - pick(kK3, c);
+            kcode |= (((e[k] >= 0.0f) ? 8u : 0u) | (uint32_t)c) << (4 * k);
+            vcode |= (uint32_t)nearest_v4_count(vn) << (4 * k);
             r[k] = e[k] * e[k];
         }
         rms_e = sqrtf(tree_wide<E>(r) / (float)D);
@@ -200,10 +202,13 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
         if (krms < kMinRMS) krms = kMinRMS;
         vrms = sqrtf(tree_wide<E / 2>(rv) / (float)D);
         if (vrms < kMinRMS) vrms = kMinRMS;
+        const float ky = 1.0f / krms, vy = 1.0f / vrms;
 #pragma unroll
         for (int k = 0; k < E; ++k) {
-            kcode |= (uint32_t)nearest_v4(clamp_ref(xk[k] / krms, -2.75f, 2.75f)) << (4 * k);
-            vcode |= (uint32_t)nearest_v4(clamp_ref(xv[k] / vrms, -2.75f, 2.75f)) << (4 * k);
+            kcode |= (uint32_t)nearest_v4_count(clamp_ref(div_by(xk[k], krms, ky), -2.75f, 2.75f))
+                     << (4 * k);
+            vcode |= (uint32_t)nearest_v4_count(clamp_ref(div_by(xv[k], vrms, vy), -2.75f, 2.75f))
+                     << (4 * k);
         }
     }
     if (!valid) return;

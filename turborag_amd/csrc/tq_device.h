@@ -202,6 +202,47 @@ __device__ __forceinline__ int nearest_v4(float x) {
     return best;
 }
 
+// Counting forms of nearest_k3 / nearest_v4 for clamped inputs (|x| <= 2.5,
+// 2.75).  The codebooks are sorted and their levels at least 0.25 apart, far
+// above the fp32 spacing of the distances, so the fp32 distances |x - c_i|
+// fall strictly up to the first minimum and rise strictly after it: the
+// index of the first minimum (the reference's strict '<' scan) is the number
+// of strict decreases of consecutive distances.  NaN compares false in both.
+__device__ __forceinline__ int nearest_k3_count(float x) {
+    float prev = fabsf(x - kK3[0]);
+    int n = 0;
+#pragma unroll
+    for (int i = 1; i < 8; ++i) {
+        const float d = fabsf(x - kK3[i]);
+        n += d < prev ? 1 : 0;
+        prev = d;
+    }
+    return n;
+}
+
+__device__ __forceinline__ int nearest_v4_count(float x) {
+    float prev = fabsf(x - kV4[0]);
+    int n = 0;
+#pragma unroll
+    for (int i = 1; i < 16; ++i) {
+        const float d = fabsf(x - kV4[i]);
+        n += d < prev ? 1 : 0;
+        prev = d;
+    }
+    return n;
+}
+
+// a / b rounded correctly, given y = RN(1/b) (Markstein's FMA division:
+// q0 = RN(a * y) is within one ulp of a / b, the remainder a - b * q0 is then
+// exact in one fma, and RN(q0 + remainder * y) is the correctly rounded
+// quotient; P. Markstein, IBM J. Res. Dev. 34(1), 1990).  Valid while no
+// step underflows or overflows: the pack divides rotated values by their
+// row's RMS (>= 1e-8), quotients between 1e-14 and 1e14 or zero.
+__device__ __forceinline__ float div_by(float a, float b, float y) {
+    const float q0 = a * y;
+    return fmaf(fmaf(-q0, b, a), y, q0);
+}
+
 // slot -> (page, token-in-block).
 __device__ __forceinline__ void split_slot(int slot, const PageGeom& g, int& page, int& tib) {
     if (g.bs_shift >= 0) {
