@@ -297,6 +297,10 @@ def main() -> int:
         f"the reference's per-layer load path {store['reference_path_ms']:.2f} ms "
         f"(outputs identical: {store['identical']})")
 
+    pack = measure_pack(w)
+    log(f"[bench] pack (36 layers x 8192 tokens): turbo_prod {pack['turbo_prod_us_per_layer']:.1f} "
+        f"us/layer, turbo_mse {pack['turbo_mse_us_per_layer']:.1f} us/layer")
+
     legacy = measure_legacy(w)
     log(f"[bench] unexported kernels @32K: qjl dequant {legacy['qjl_dequant_us']:.1f} us, "
         f"qjl attention {legacy['qjl_attention_us']:.1f} us, int4 dequant "
@@ -352,6 +356,7 @@ def main() -> int:
         },
         "loader": loader,
         "store": store,
+        "pack": pack,
         "unexported_kernels": legacy,
         "batched_decode": batched,
         "step_ms_events": round(ev_ms_per_step, 4),
@@ -466,6 +471,50 @@ def measure_store(w: Workload, reps: int = 3) -> dict:
             "speedup": round(ref_ms / ms, 2), "pages_GBps": round(page_bytes / ms / 1e6, 2),
             "identical": bool(same), "files": "page cache (written just before)",
             "output": "[1, H, N, D] fp16 per layer"}
+
+
+def measure_pack(w: Workload, reps: int = 5) -> dict:
+    """Quantize on append: 36 layers x 8192 tokens of K/V (H = 2, D = 128,
+    shuffled 16-token pages) packed into turbo_prod and turbo_mse pools, one
+    graph of 36 pack launches per scheme.  Algorithmic bytes per layer: fp16
+    K/V and slots read, pages written."""
+    import torch
+
+    from turborag_amd.synthetic import permuted_slots
+    tq, N, NL = w.tq, 8192, w.NL
+    cfg = tq.default_config()
+    cfg.num_kv_heads, cfg.head_dim, cfg.block_size = w.H, w.D, w.B
+    lp, lm = tq.make_layout_for(cfg), tq.make_mse_layout_for(cfg)
+    slots = permuted_slots(N, w.B, seed=402).to(w.dev)
+    kv = [gpu_kv(N, w.H, w.D, 700 + l, w.dev) for l in range(NL)]
+    pages = (N + w.B - 1) // w.B
+    pp = [torch.zeros(pages * lp.page_size_bytes, dtype=torch.uint8, device=w.dev)
+          for _ in range(NL)]
+    pm = [torch.zeros(pages * lm.page_size_bytes, dtype=torch.uint8, device=w.dev)
+          for _ in range(NL)]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+
+    def prod():
+        for (k, v), p in zip(kv, pp):
+            tq.pack(k, v, slots, p, lp, cfg, stream=torch.cuda.current_stream().cuda_stream)
+
+    def mse():
+        for (k, v), p in zip(kv, pm):
+            tq.mse_pack(k, v, slots, p, lm, cfg, stream=torch.cuda.current_stream().cuda_stream)
+
+    out = {"layers": NL, "tokens": N}
+    fp16 = 2 * N * w.H * w.D * 2
+    for name, fn, lay in (("turbo_prod", prod, lp), ("turbo_mse", mse, lm)):
+        g = capture(fn, side)
+        us = event_time_us(g.replay if g is not None else fn, reps) / NL
+        alg = fp16 + N * 4 + pages * lay.page_size_bytes
+        out[f"{name}_us_per_layer"] = round(us, 2)
+        out[f"{name}_GBps"] = round(alg / us / 1e3, 1)
+        out[f"{name}_frac_hbm"] = round(alg / us / 1e3 / HBM_PEAK_GBPS, 4)
+    out["algorithmic_bytes_per_layer_turbo_prod"] = fp16 + N * 4 + pages * lp.page_size_bytes
+    del kv, pp, pm
+    return out
 
 
 def measure_legacy(w: Workload, reps: int = 10) -> dict:
