@@ -136,6 +136,9 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
     constexpr int E = D / 16;
     static_assert(E == 4 || E == 8, "D = 64 or 128");
     typedef uint16_t h4 __attribute__((ext_vector_type(E)));
+    __shared__ float tab[kTabFloats];
+    if (threadIdx.x < kTabFloats) tab[threadIdx.x] = pack_table_entry(threadIdx.x);
+    __syncthreads();
     const int j = threadIdx.x & 15;
     const int row = blockIdx.x * (kBlock / 16) + (threadIdx.x >> 4);
     const bool valid = row < num_rows;
@@ -177,10 +180,10 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
         for (int k = 0; k < E; ++k) {
             const float kn = clamp_ref(div_by(xk[k], krms, ky), -2.5f, 2.5f);
             const float vn = clamp_ref(div_by(xv[k], vrms, vy), -2.75f, 2.75f);
-            const int c = nearest_k3_count(kn);
-            e[k] = kn - pick(kK3, c);
-            kcode |= (((e[k] >= 0.0f) ? 8u : 0u) | (uint32_t)c) << (4 * k);
-            vcode |= (uint32_t)nearest_v4_count(vn) << (4 * k);
+            const uint32_t c4 = search_x4<3>(kn, tab + kTabK3T);
+            e[k] = kn - *reinterpret_cast<const float*>(reinterpret_cast<const char*>(tab + kTabK3) + c4);
+            kcode |= (((e[k] >= 0.0f) ? 8u : 0u) | (c4 >> 2)) << (4 * k);
+            vcode |= (search_x4<4>(vn, tab + kTabV4T) >> 2) << (4 * k);
             r[k] = e[k] * e[k];
         }
         rms_e = sqrtf(tree_wide<E>(r) / (float)D);
@@ -205,10 +208,10 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
         const float ky = 1.0f / krms, vy = 1.0f / vrms;
 #pragma unroll
         for (int k = 0; k < E; ++k) {
-            kcode |= (uint32_t)nearest_v4_count(clamp_ref(div_by(xk[k], krms, ky), -2.75f, 2.75f))
-                     << (4 * k);
-            vcode |= (uint32_t)nearest_v4_count(clamp_ref(div_by(xv[k], vrms, vy), -2.75f, 2.75f))
-                     << (4 * k);
+            kcode |= (search_x4<4>(clamp_ref(div_by(xk[k], krms, ky), -2.75f, 2.75f), tab + kTabV4T)
+                      >> 2) << (4 * k);
+            vcode |= (search_x4<4>(clamp_ref(div_by(xv[k], vrms, vy), -2.75f, 2.75f), tab + kTabV4T)
+                      >> 2) << (4 * k);
         }
     }
     if (!valid) return;

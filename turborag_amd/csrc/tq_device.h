@@ -232,6 +232,84 @@ __device__ __forceinline__ int nearest_v4_count(float x) {
     return n;
 }
 
+// Decision thresholds of the nearest-level scans.  For neighbouring levels
+// a < b, closer(x) = fp32 |x - b| < fp32 |x - a| is false up to a and true
+// from b on, and monotone in between (fp32 subtraction rounds monotonically),
+// so on the clamped domain it is x >= T for T = the smallest float with
+// closer(T).  The strict-decrease count above is then #{i : x >= T_i}: a
+// branchless binary search over the sorted T_i.  The T_i are computed here at
+// compile time by bisection over floats with the same fp32 operations.
+namespace thr {
+constexpr float cabs(float v) { return v < 0.0f ? -v : v; }
+constexpr bool closer(float x, float a, float b) { return cabs(x - b) < cabs(x - a); }
+// No float lies strictly between lo < hi exactly when their rounded midpoint
+// is lo or hi.
+constexpr bool adjacent(float lo, float hi) {
+    return (lo + hi) * 0.5f == lo || (lo + hi) * 0.5f == hi;
+}
+template <int N>
+struct Table {
+    float t[N];      // t[i]: smallest float with closer(., c[i-1], c[i]); t[0] unused
+    float below[N];  // the float just below t[i]
+};
+// Bisection keeps closer(lo) false and closer(hi) true until they are
+// adjacent floats.
+template <int N>
+constexpr Table<N> thresholds(const float (&c)[N]) {
+    Table<N> r{};
+    for (int i = 1; i < N; ++i) {
+        float lo = c[i - 1], hi = c[i];
+        while (!adjacent(lo, hi)) {
+            const float m = (lo + hi) * 0.5f;
+            if (closer(m, c[i - 1], c[i]))
+                hi = m;
+            else
+                lo = m;
+        }
+        r.t[i] = hi;
+        r.below[i] = lo;
+    }
+    return r;
+}
+template <int N>
+constexpr bool well_formed(const float (&c)[N], const Table<N>& T) {
+    for (int i = 1; i < N; ++i) {
+        if (!(c[i] - c[i - 1] >= 0.25f)) return false;  // the spacing the argument needs
+        if (!(T.t[i] > c[i - 1] && T.t[i] <= c[i])) return false;
+        if (!closer(T.t[i], c[i - 1], c[i]) || closer(T.below[i], c[i - 1], c[i])) return false;
+        if (!(T.below[i] < T.t[i]) || !adjacent(T.below[i], T.t[i])) return false;
+    }
+    return true;
+}
+}  // namespace thr
+
+__device__ constexpr thr::Table<8> kK3T = thr::thresholds(kK3);
+__device__ constexpr thr::Table<16> kV4T = thr::thresholds(kV4);
+static_assert(thr::well_formed(kK3, kK3T) && thr::well_formed(kV4, kV4T),
+              "codebook thresholds");
+
+// The 32-float LDS table of the wide pack: [0, 16) V4 thresholds, [16, 24)
+// K3 thresholds, [24, 32) K3 levels (index 0 of each threshold run unused).
+constexpr int kTabV4T = 0, kTabK3T = 16, kTabK3 = 24, kTabFloats = 32;
+__device__ __forceinline__ float pack_table_entry(int i) {
+    return i < kTabK3T ? kV4T.t[i] : (i < kTabK3 ? kK3T.t[i - kTabK3T] : kK3[i - kTabK3]);
+}
+
+// 4 * #{1 <= i < 2^BITS : x >= T[i]}: the nearest level's index times 4 (its
+// byte offset in a float table), by binary search over the thresholds T in
+// LDS.  Equal to 4 * nearest_*_count(x) for clamped x; NaN gives 0.
+template <int BITS>
+__device__ __forceinline__ uint32_t search_x4(float x, const float* T) {
+    uint32_t b = 0;
+#pragma unroll
+    for (int s = 1 << (BITS - 1); s >= 1; s >>= 1) {
+        const float t = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(T) + b +
+                                                        4 * s);
+        b += (x >= t) ? 4u * s : 0u;
+    }
+    return b;
+}
+
 // a / b rounded correctly, given y = RN(1/b) (Markstein's FMA division:
 // q0 = RN(a * y) is within one ulp of a / b, the remainder a - b * q0 is then
 // exact in one fma, and RN(q0 + remainder * y) is the correctly rounded
