@@ -93,6 +93,69 @@ def test_mse_pack_dequant_bit_exact(tq, oracle, cuda, N, H, D, B, seed, slot_kin
     assert np.array_equal(as_u16(ov)[live], wv[live])
 
 
+def _special_rows(N, H, D, seed):
+    """Seeded K/V whose first rows hold non-finite and extreme fp16 values:
+    +-inf, NaN, all zeros, +-65504, fp16 subnormals, a single spike."""
+    k, v = kv_tokens_major(N, H, D, seed=seed)
+    specials = []
+    for t in (k, v):
+        f = t.float()
+        f[0, 0, 3] = float("inf")
+        f[1, 0, 0] = float("-inf")
+        f[2, 0, 5] = float("nan")
+        f[3] = 0.0
+        f[4, 0] = 65504.0
+        f[4, -1, ::2] = -65504.0
+        f[5, 0] = 2.0 ** -24 * torch.arange(1, D + 1, dtype=torch.float32)
+        f[6, 0] = 0.0
+        f[6, 0, D // 2] = 1.0
+        f[7, :, :] = float("nan")
+        specials.append(f.half())
+    return specials[0], specials[1]
+
+
+def _scale_mask(pool_len, page_size, regions):
+    """True at the bytes of the fp16 scale fields (offset, length per page)."""
+    m = np.zeros(pool_len, bool)
+    for p0 in range(0, pool_len, page_size):
+        for off, n in regions:
+            m[p0 + off: p0 + off + n] = True
+    return m
+
+
+def _equal_nan_scales(got, want, scale_mask):
+    """Codes bit-exact; scale fields bit-exact or NaN in both (the NaN payload an
+    fp32 -> fp16 conversion produces is the platform's own)."""
+    diff = got != want
+    assert not np.any(diff & ~scale_mask), "code bytes differ"
+    g16, w16 = got.view(np.uint16), want.view(np.uint16)
+    bad = np.flatnonzero(g16 != w16)
+    nan = lambda h: ((h & 0x7C00) == 0x7C00) & ((h & 0x03FF) != 0)  # noqa: E731
+    assert np.all(nan(g16[bad]) & nan(w16[bad])), f"scale halves differ at {bad[:8]}"
+
+
+@pytest.mark.parametrize("D", [128, 64, 32])
+def test_pack_non_finite_and_extreme_rows(tq, oracle, cuda, D):
+    print(f"[codec specials] D={D}", flush=True)
+    N, H, B = 40, 2, 16
+    k, v = _special_rows(N, H, D, seed=120 + D)
+    slots = permuted_slots(N, B, seed=121)
+    pages = int(slots.max()) // B + 1
+    cfg, lp, lm = _cfg(tq, H, D, B)
+    sb = B * H * 2
+    pool = torch.zeros(pages * lp.page_size_bytes, dtype=torch.uint8, device=cuda)
+    tq.pack(k.to(cuda), v.to(cuda), slots.to(cuda), pool, lp, cfg)
+    want = oracle.prod_pack(as_u16(k), as_u16(v), slots.numpy(), pages, B)
+    _equal_nan_scales(pool.cpu().numpy(), want, _scale_mask(
+        want.size, lp.page_size_bytes, [(lp.k_scales_offset, sb), (lp.k_residual_scales_offset, sb),
+                                        (lp.v_scales_offset, sb)]))
+    pool = torch.zeros(pages * lm.page_size_bytes, dtype=torch.uint8, device=cuda)
+    tq.mse_pack(k.to(cuda), v.to(cuda), slots.to(cuda), pool, lm, cfg)
+    want = oracle.mse_pack(as_u16(k), as_u16(v), slots.numpy(), pages, B, fused_pairsum=True)
+    _equal_nan_scales(pool.cpu().numpy(), want, _scale_mask(
+        want.size, lm.page_size_bytes, [(lm.k_norms_offset, sb), (lm.v_norms_offset, sb)]))
+
+
 def _rel_err(got: np.ndarray, ref: np.ndarray) -> float:
     """max over (row, head) of max|o - r| / max|r|."""
     g = got.reshape(-1, got.shape[-1]).astype(np.float64)
