@@ -88,10 +88,10 @@ __global__ __launch_bounds__(kBlock) void prod_pack_kernel(
 // scales are bit-identical to the one-row-per-wave form above; codes leave as
 // one dword (K) and one dword (V) per lane (E = 8).
 // ---------------------------------------------------------------------------
-template <int E>
+template <int E, int FROM = 1>
 __device__ __forceinline__ void wht_wide(float (&x)[E], int j) {
 #pragma unroll
-    for (int len = 1; len < E; len <<= 1)
+    for (int len = FROM; len < E; len <<= 1)
 #pragma unroll
         for (int k = 0; k < E; ++k)
             if ((k & len) == 0) {
@@ -136,8 +136,10 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
     constexpr int E = D / 16;
     static_assert(E == 4 || E == 8, "D = 64 or 128");
     typedef uint16_t h4 __attribute__((ext_vector_type(E)));
-    __shared__ float tab[kTabFloats];
-    if (threadIdx.x < kTabFloats) tab[threadIdx.x] = pack_table_entry(threadIdx.x);
+    __shared__ PackTables tab;
+    if (threadIdx.x < kPackTableWords)
+        reinterpret_cast<uint32_t*>(&tab)[threadIdx.x] =
+            reinterpret_cast<const uint32_t*>(&kPackTables)[threadIdx.x];
     __syncthreads();
     const int j = threadIdx.x & 15;
     const int row = blockIdx.x * (kBlock / 16) + (threadIdx.x >> 4);
@@ -147,25 +149,32 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
     const size_t off = (size_t)rr * D + E * j;
     const h4 kr = *reinterpret_cast<const h4*>(key + off);
     const h4 vr = *reinterpret_cast<const h4*>(value + off);
-    // s(i, h) = (-1)^(i + h); E*j is even, so element k has sign (-1)^(k + h).
-    const float sh = (h & 1) ? -1.0f : 1.0f;
+    // s(i, h) = (-1)^(i + h) = sh * (-1)^k (E*j is even).  The first butterfly
+    // stage on (sh*a, -sh*b) gives (sh*(a - b), sh*(a + b)); fp32 rounding is
+    // symmetric in sign, so every later value is sh times the one computed
+    // without it (up to the sign of exact zeros, which no code or scale
+    // sees), and sh is folded into the exact scale sinv = sh / sqrt(D).
+    const float sinv = (h & 1) ? -inv : inv;
     float xk[E], xv[E];
 #pragma unroll
-    for (int k = 0; k < E; ++k) {
-        const float sg = (k & 1) ? -sh : sh;
-        xk[k] = h2f(kr[k]) * sg;
-        xv[k] = h2f(vr[k]) * sg;
+    for (int k = 0; k < E; k += 2) {
+        const float ka = h2f(kr[k]), kb = h2f(kr[k + 1]);
+        const float va = h2f(vr[k]), vb = h2f(vr[k + 1]);
+        xk[k] = ka - kb;
+        xk[k + 1] = ka + kb;
+        xv[k] = va - vb;
+        xv[k + 1] = va + vb;
     }
-    wht_wide<E>(xk, j);
-    wht_wide<E>(xv, j);
+    wht_wide<E, 2>(xk, j);
+    wht_wide<E, 2>(xv, j);
     uint32_t kcode = 0, vcode = 0;
     float krms, vrms, rms_e = 0.0f;
     if constexpr (PROD) {
         float r[E];
 #pragma unroll
         for (int k = 0; k < E; ++k) {
-            xk[k] *= inv;
-            xv[k] *= inv;
+            xk[k] *= sinv;
+            xv[k] *= sinv;
             r[k] = xk[k] * xk[k];
         }
         krms = sqrtf(tree_wide<E>(r) / (float)D);
@@ -178,23 +187,30 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
         const float ky = 1.0f / krms, vy = 1.0f / vrms;
 #pragma unroll
         for (int k = 0; k < E; ++k) {
-            const float kn = clamp_ref(div_by(xk[k], krms, ky), -2.5f, 2.5f);
-            const float vn = clamp_ref(div_by(xv[k], vrms, vy), -2.75f, 2.75f);
-            const uint32_t c4 = search_x4<3>(kn, tab + kTabK3T);
-            e[k] = kn - *reinterpret_cast<const float*>(reinterpret_cast<const char*>(tab + kTabK3) + c4);
-            kcode |= (((e[k] >= 0.0f) ? 8u : 0u) | (c4 >> 2)) << (4 * k);
-            vcode |= (search_x4<4>(vn, tab + kTabV4T) >> 2) << (4 * k);
+            // fmin/fmax clamp a NaN to the low bound, whose codes (0) are the
+            // reference's for NaN; its residual is made NaN below.
+            const float kn = fminf(fmaxf(div_by(xk[k], krms, ky), -2.5f), 2.5f);
+            const float vn = fminf(fmaxf(div_by(xv[k], vrms, vy), -2.75f), 2.75f);
+            float level;
+            const uint32_t c = k3_code(kn, tab, level);
+            e[k] = kn - level;
+            kcode |= (((e[k] >= 0.0f) ? 8u : 0u) | c) << (4 * k);
+            vcode |= v4_code(vn, tab) << (4 * k);
             r[k] = e[k] * e[k];
         }
         rms_e = sqrtf(tree_wide<E>(r) / (float)D);
         if (rms_e < kMinRMS) rms_e = kMinRMS;
+        // The rotation spreads a non-finite input over the whole row: then
+        // every K/rms is NaN, the reference's residual RMS is NaN, and the
+        // codes above are its codes for NaN (index 0, sign 0).
+        if (!(krms <= 3.402823466e38f)) rms_e = __builtin_nanf("");
     } else {
         // Pair sums fmaf(x0, x0, x1 * x1) (tq_turbo_mse_kernels.cu:108, contracted).
         float rk[E / 2], rv[E / 2];
 #pragma unroll
         for (int k = 0; k < E; ++k) {
-            xk[k] *= inv;
-            xv[k] *= inv;
+            xk[k] *= sinv;
+            xv[k] *= sinv;
         }
 #pragma unroll
         for (int p = 0; p < E / 2; ++p) {
@@ -208,10 +224,8 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
         const float ky = 1.0f / krms, vy = 1.0f / vrms;
 #pragma unroll
         for (int k = 0; k < E; ++k) {
-            kcode |= (search_x4<4>(clamp_ref(div_by(xk[k], krms, ky), -2.75f, 2.75f), tab + kTabV4T)
-                      >> 2) << (4 * k);
-            vcode |= (search_x4<4>(clamp_ref(div_by(xv[k], vrms, vy), -2.75f, 2.75f), tab + kTabV4T)
-                      >> 2) << (4 * k);
+            kcode |= v4_code(fminf(fmaxf(div_by(xk[k], krms, ky), -2.75f), 2.75f), tab) << (4 * k);
+            vcode |= v4_code(fminf(fmaxf(div_by(xv[k], vrms, vy), -2.75f), 2.75f), tab) << (4 * k);
         }
     }
     if (!valid) return;

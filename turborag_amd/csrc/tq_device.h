@@ -288,26 +288,70 @@ __device__ constexpr thr::Table<16> kV4T = thr::thresholds(kV4);
 static_assert(thr::well_formed(kK3, kK3T) && thr::well_formed(kV4, kV4T),
               "codebook thresholds");
 
-// The 32-float LDS table of the wide pack: [0, 16) V4 thresholds, [16, 24)
-// K3 thresholds, [24, 32) K3 levels (index 0 of each threshold run unused).
-constexpr int kTabV4T = 0, kTabK3T = 16, kTabK3 = 24, kTabFloats = 32;
-__device__ __forceinline__ float pack_table_entry(int i) {
-    return i < kTabK3T ? kV4T.t[i] : (i < kTabK3 ? kK3T.t[i - kTabK3T] : kK3[i - kTabK3]);
-}
-
-// 4 * #{1 <= i < 2^BITS : x >= T[i]}: the nearest level's index times 4 (its
-// byte offset in a float table), by binary search over the thresholds T in
-// LDS.  Equal to 4 * nearest_*_count(x) for clamped x; NaN gives 0.
-template <int BITS>
-__device__ __forceinline__ uint32_t search_x4(float x, const float* T) {
-    uint32_t b = 0;
-#pragma unroll
-    for (int s = 1 << (BITS - 1); s >= 1; s >>= 1) {
-        const float t = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(T) + b +
-                                                        4 * s);
-        b += (x >= t) ? 4u * s : 0u;
+// Grid form of the search for clamped x (|x| <= 2.5 for K3, 2.75 for V4):
+// the cell g = (int)RN(8x + off) (8x is exact, so fma and mul-then-add agree;
+// g >= 0 on the clamped domain) holds at most one threshold, so with
+// first[g] = #{i : cell(T_i) < g} = the count at the cell's smallest float,
+// the count at x is first[g] + (x >= T[first[g] + 1]).
+constexpr float kK3Off = 20.0f, kV4Off = 22.0f;
+constexpr int kK3Cells = 41, kV4Cells = 45;
+struct alignas(16) PackTables {
+    uint8_t v4_first[48];  // [g], g < kV4Cells
+    uint8_t k3_first[48];  // [g], g < kK3Cells
+    float v4_t[20];        // [i] = T_i for 1 <= i < 16, [16] = +inf
+    float k3_q[8][4];      // [l] = {T_(l+1) (+inf for l = 7), level l, level l+1, 0}
+};
+namespace thr {
+constexpr int cell(float x, float off) { return (int)(x * 8.0f + off); }
+template <int N>
+constexpr bool one_per_cell(const Table<N>& T, float off, int cells) {
+    for (int i = 1; i < N; ++i) {
+        if (cell(T.t[i], off) < 0 || cell(T.t[i], off) >= cells) return false;
+        if (i > 1 && !(cell(T.t[i], off) > cell(T.t[i - 1], off))) return false;
     }
-    return b;
+    return true;
+}
+template <int N>
+constexpr uint8_t first_in_cell(const Table<N>& T, float off, int g) {
+    int n = 0;
+    for (int i = 1; i < N; ++i) n += cell(T.t[i], off) < g ? 1 : 0;
+    return (uint8_t)n;
+}
+constexpr PackTables pack_tables() {
+    PackTables p{};
+    for (int g = 0; g < kV4Cells; ++g) p.v4_first[g] = first_in_cell(kV4T, kV4Off, g);
+    for (int g = 0; g < kK3Cells; ++g) p.k3_first[g] = first_in_cell(kK3T, kK3Off, g);
+    for (int i = 1; i < 16; ++i) p.v4_t[i] = kV4T.t[i];
+    p.v4_t[16] = __builtin_huge_valf();
+    for (int l = 0; l < 8; ++l) {
+        p.k3_q[l][0] = l < 7 ? kK3T.t[l + 1] : __builtin_huge_valf();
+        p.k3_q[l][1] = kK3[l];
+        p.k3_q[l][2] = l < 7 ? kK3[l + 1] : kK3[l];
+    }
+    return p;
+}
+}  // namespace thr
+static_assert(thr::one_per_cell(kK3T, kK3Off, kK3Cells) &&
+                  thr::one_per_cell(kV4T, kV4Off, kV4Cells) &&
+                  thr::cell(-2.5f, kK3Off) == 0 && thr::cell(2.5f, kK3Off) == kK3Cells - 1 &&
+                  thr::cell(-2.75f, kV4Off) == 0 && thr::cell(2.75f, kV4Off) == kV4Cells - 1,
+              "search grid");
+__device__ constexpr PackTables kPackTables = thr::pack_tables();
+constexpr int kPackTableWords = sizeof(PackTables) / 4;
+static_assert(sizeof(PackTables) % 16 == 0, "LDS table of whole dwords, float4 rows aligned");
+
+// Nearest V4 index of a clamped x (the reference's first-minimum scan).
+__device__ __forceinline__ uint32_t v4_code(float x, const PackTables& T) {
+    const uint32_t l = T.v4_first[(int)__builtin_fmaf(x, 8.0f, kV4Off)];
+    return l + (x >= T.v4_t[l + 1] ? 1u : 0u);
+}
+// Nearest K3 index of a clamped x, and its level.
+__device__ __forceinline__ uint32_t k3_code(float x, const PackTables& T, float& level) {
+    const uint32_t l = T.k3_first[(int)__builtin_fmaf(x, 8.0f, kK3Off)];
+    const float4 q = *reinterpret_cast<const float4*>(T.k3_q[l]);
+    const bool up = x >= q.x;
+    level = up ? q.z : q.y;
+    return l + (up ? 1u : 0u);
 }
 
 // a / b rounded correctly, given y = RN(1/b) (Markstein's FMA division:
