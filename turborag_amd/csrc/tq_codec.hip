@@ -79,53 +79,74 @@ __global__ __launch_bounds__(kBlock) void prod_pack_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Pack, wide form (D = 64, 128): 16 lanes per (token, head) row, lane j owns
-// the E = D/16 contiguous elements E*j .. E*j + E-1, so four rows share a
-// wave.  The reference's butterfly stage len pairs elements i and i + len:
-// in-lane for len < E, lanes j and j ^ (len/E) otherwise; its halving trees
-// (r[i] += r[i + s], s = n/2 .. 1) likewise cross lanes for s >= E and end
-// in-lane.  Operation order per element is the reference's, so codes and
-// scales are bit-identical to the one-row-per-wave form above; codes leave as
-// one dword (K) and one dword (V) per lane (E = 8).
+// Pack, wide form (D = 64, 128): 16 lanes per (token, head) row, four rows
+// per wave.  Lane j owns the element pairs (32c + 2j, 32c + 2j + 1) of the
+// C = D/32 chunks c, in registers k = 2c and 2c + 1.  The reference's
+// butterfly stage len pairs elements i and i + len: in-lane for len = 1 and
+// len >= 32 (chunks c and c ^ (len/32)), lanes j and j ^ (len/2) for
+// len = 2 .. 16.  Its halving trees (r[i] += r[i + s], s = n/2 .. 1) run
+// in-lane over chunks first (s >= 32), then across lanes (s = 16 .. 2, one or
+// two values per lane), and end in-lane (s = 1): most of the adds stay in
+// registers.  Operation order per element is the reference's, so codes and
+// scales are bit-identical to the one-row-per-wave form above.  Code byte
+// 16c + j of a cell is the lane's chunk c.
 // ---------------------------------------------------------------------------
-template <int E, int FROM = 1>
-__device__ __forceinline__ void wht_wide(float (&x)[E], int j) {
-#pragma unroll
-    for (int len = FROM; len < E; len <<= 1)
-#pragma unroll
-        for (int k = 0; k < E; ++k)
-            if ((k & len) == 0) {
-                const float a = x[k], b = x[k + len];
-                x[k] = a + b;
-                x[k + len] = a - b;
-            }
-    // Cross-lane stages: partner + (+-mine), the signed copies made for all
-    // E values first so that no DPP add waits on the VALU op just before it.
+template <int C>
+__device__ __forceinline__ void wht_chunks(float (&x)[2 * C], int j) {
+    // len = 1 is done by the caller (it carries the sign flip).
+    // Cross-lane stages len = 2 .. 16: partner + (+-mine), the signed copies
+    // made for all values first so that no DPP add waits on the op before it.
 #pragma unroll
     for (int m = 1; m < 16; m <<= 1) {
         const bool lower = (j & m) == 0;
-        float t[E];
+        float t[2 * C];
 #pragma unroll
-        for (int k = 0; k < E; ++k) t[k] = lower ? x[k] : -x[k];
+        for (int k = 0; k < 2 * C; ++k) t[k] = lower ? x[k] : -x[k];
 #pragma unroll
-        for (int k = 0; k < E; ++k) x[k] = xor_lane(x[k], m) + t[k];
+        for (int k = 0; k < 2 * C; ++k) x[k] = xor_lane(x[k], m) + t[k];
     }
+    // len = 32, 64: chunks c and c + len/32.
+#pragma unroll
+    for (int d = 1; d < C; d <<= 1)
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+            if ((c & d) == 0)
+#pragma unroll
+                for (int b = 0; b < 2; ++b) {
+                    const float u = x[2 * c + b], w = x[2 * (c + d) + b];
+                    x[2 * c + b] = u + w;
+                    x[2 * (c + d) + b] = u - w;
+                }
 }
 
-// Halving-tree sum of the row's N = 16 * n values, n per lane (contiguous):
-// stages s >= n cross lanes (xor s/n, largest first), then in-lane.  Every
-// lane of the row ends with the total.
-template <int n>
-__device__ __forceinline__ float tree_wide(float (&r)[n]) {
+// Halving tree over the row's 32*C values r[2c + b] (element 32c + 2j + b):
+// s = 16C .. 32 in-lane over chunks, s = 16 .. 2 across lanes j ^ s/2, s = 1
+// in-lane.  Every lane ends with the total.
+template <int C>
+__device__ __forceinline__ float tree_chunks(float (&r)[2 * C]) {
 #pragma unroll
-    for (int m = 8; m >= 1; m >>= 1)
+    for (int d = C / 2; d >= 1; d >>= 1)
 #pragma unroll
-        for (int k = 0; k < n; ++k) r[k] += xor_lane(r[k], m);
+        for (int k = 0; k < 2 * d; ++k) r[k] += r[k + 2 * d];
 #pragma unroll
-    for (int s = n / 2; s >= 1; s >>= 1)
+    for (int m = 8; m >= 1; m >>= 1) {
+        r[0] += xor_lane(r[0], m);
+        r[1] += xor_lane(r[1], m);
+    }
+    return r[0] + r[1];
+}
+
+// Halving tree over the row's 16*C pair sums q[c] (pair 16c + j): s = 8C ..
+// 16 in-lane over chunks, s = 8 .. 1 across lanes.
+template <int C>
+__device__ __forceinline__ float tree_chunk_pairs(float (&q)[C]) {
 #pragma unroll
-        for (int k = 0; k < s; ++k) r[k] += r[k + s];
-    return r[0];
+    for (int d = C / 2; d >= 1; d >>= 1)
+#pragma unroll
+        for (int c = 0; c < d; ++c) q[c] += q[c + d];
+#pragma unroll
+    for (int m = 8; m >= 1; m >>= 1) q[0] += xor_lane(q[0], m);
+    return q[0];
 }
 
 template <int D, bool PROD>
@@ -133,9 +154,8 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
     const uint16_t* __restrict__ key, const uint16_t* __restrict__ value,
     const int32_t* __restrict__ slots, uint8_t* __restrict__ pool, PageGeom g, int num_rows,
     float inv) {
-    constexpr int E = D / 16;
-    static_assert(E == 4 || E == 8, "D = 64 or 128");
-    typedef uint16_t h4 __attribute__((ext_vector_type(E)));
+    constexpr int C = D / 32, E = 2 * C;
+    static_assert(C == 2 || C == 4, "D = 64 or 128");
     __shared__ PackTables tab;
     if (threadIdx.x < kPackTableWords)
         reinterpret_cast<uint32_t*>(&tab)[threadIdx.x] =
@@ -146,28 +166,33 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
     const bool valid = row < num_rows;
     const int rr = valid ? row : num_rows - 1;
     const int t = rr / g.H, h = rr % g.H;
-    const size_t off = (size_t)rr * D + E * j;
-    const h4 kr = *reinterpret_cast<const h4*>(key + off);
-    const h4 vr = *reinterpret_cast<const h4*>(value + off);
-    // s(i, h) = (-1)^(i + h) = sh * (-1)^k (E*j is even).  The first butterfly
-    // stage on (sh*a, -sh*b) gives (sh*(a - b), sh*(a + b)); fp32 rounding is
-    // symmetric in sign, so every later value is sh times the one computed
-    // without it (up to the sign of exact zeros, which no code or scale
-    // sees), and sh is folded into the exact scale sinv = sh / sqrt(D).
+    const uint32_t* kr = reinterpret_cast<const uint32_t*>(key + (size_t)rr * D) + j;
+    const uint32_t* vr = reinterpret_cast<const uint32_t*>(value + (size_t)rr * D) + j;
+    uint32_t kw[C], vw[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        kw[c] = kr[16 * c];
+        vw[c] = vr[16 * c];
+    }
+    // s(i, h) = (-1)^(i + h) = sh * (-1)^b for element i = 32c + 2j + b.  The
+    // first butterfly stage on (sh*a, -sh*b) gives (sh*(a - b), sh*(a + b));
+    // fp32 rounding is symmetric in sign, so every later value is sh times
+    // the one computed without it (up to the sign of exact zeros, which no
+    // code or scale sees), and sh is folded into the exact scale sh/sqrt(D).
     const float sinv = (h & 1) ? -inv : inv;
     float xk[E], xv[E];
 #pragma unroll
-    for (int k = 0; k < E; k += 2) {
-        const float ka = h2f(kr[k]), kb = h2f(kr[k + 1]);
-        const float va = h2f(vr[k]), vb = h2f(vr[k + 1]);
-        xk[k] = ka - kb;
-        xk[k + 1] = ka + kb;
-        xv[k] = va - vb;
-        xv[k + 1] = va + vb;
+    for (int c = 0; c < C; ++c) {
+        const float ka = h2f((uint16_t)kw[c]), kb = h2f((uint16_t)(kw[c] >> 16));
+        const float va = h2f((uint16_t)vw[c]), vb = h2f((uint16_t)(vw[c] >> 16));
+        xk[2 * c] = ka - kb;
+        xk[2 * c + 1] = ka + kb;
+        xv[2 * c] = va - vb;
+        xv[2 * c + 1] = va + vb;
     }
-    wht_wide<E, 2>(xk, j);
-    wht_wide<E, 2>(xv, j);
-    uint32_t kcode = 0, vcode = 0;
+    wht_chunks<C>(xk, j);
+    wht_chunks<C>(xv, j);
+    uint32_t kbyte[C], vbyte[C];
     float krms, vrms, rms_e = 0.0f;
     if constexpr (PROD) {
         float r[E];
@@ -177,14 +202,14 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
             xv[k] *= sinv;
             r[k] = xk[k] * xk[k];
         }
-        krms = sqrtf(tree_wide<E>(r) / (float)D);
+        krms = sqrtf(tree_chunks<C>(r) / (float)D);
         if (krms < kMinRMS) krms = kMinRMS;
 #pragma unroll
         for (int k = 0; k < E; ++k) r[k] = xv[k] * xv[k];
-        vrms = sqrtf(tree_wide<E>(r) / (float)D);
+        vrms = sqrtf(tree_chunks<C>(r) / (float)D);
         if (vrms < kMinRMS) vrms = kMinRMS;
-        float e[E];
         const float ky = 1.0f / krms, vy = 1.0f / vrms;
+        uint32_t kn4[E], vn4[E];
 #pragma unroll
         for (int k = 0; k < E; ++k) {
             // fmin/fmax clamp a NaN to the low bound, whose codes (0) are the
@@ -193,12 +218,17 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
             const float vn = fminf(fmaxf(div_by(xv[k], vrms, vy), -2.75f), 2.75f);
             float level;
             const uint32_t c = k3_code(kn, tab, level);
-            e[k] = kn - level;
-            kcode |= (((e[k] >= 0.0f) ? 8u : 0u) | c) << (4 * k);
-            vcode |= v4_code(vn, tab) << (4 * k);
-            r[k] = e[k] * e[k];
+            const float e = kn - level;
+            kn4[k] = ((e >= 0.0f) ? 8u : 0u) | c;
+            vn4[k] = v4_code(vn, tab);
+            r[k] = e * e;
         }
-        rms_e = sqrtf(tree_wide<E>(r) / (float)D);
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            kbyte[c] = kn4[2 * c] | (kn4[2 * c + 1] << 4);
+            vbyte[c] = vn4[2 * c] | (vn4[2 * c + 1] << 4);
+        }
+        rms_e = sqrtf(tree_chunks<C>(r) / (float)D);
         if (rms_e < kMinRMS) rms_e = kMinRMS;
         // The rotation spreads a non-finite input over the whole row: then
         // every K/rms is NaN, the reference's residual RMS is NaN, and the
@@ -206,26 +236,32 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
         if (!(krms <= 3.402823466e38f)) rms_e = __builtin_nanf("");
     } else {
         // Pair sums fmaf(x0, x0, x1 * x1) (tq_turbo_mse_kernels.cu:108, contracted).
-        float rk[E / 2], rv[E / 2];
+        float qk[C], qv[C];
 #pragma unroll
         for (int k = 0; k < E; ++k) {
             xk[k] *= sinv;
             xv[k] *= sinv;
         }
 #pragma unroll
-        for (int p = 0; p < E / 2; ++p) {
-            rk[p] = fmaf(xk[2 * p], xk[2 * p], xk[2 * p + 1] * xk[2 * p + 1]);
-            rv[p] = fmaf(xv[2 * p], xv[2 * p], xv[2 * p + 1] * xv[2 * p + 1]);
+        for (int c = 0; c < C; ++c) {
+            qk[c] = fmaf(xk[2 * c], xk[2 * c], xk[2 * c + 1] * xk[2 * c + 1]);
+            qv[c] = fmaf(xv[2 * c], xv[2 * c], xv[2 * c + 1] * xv[2 * c + 1]);
         }
-        krms = sqrtf(tree_wide<E / 2>(rk) / (float)D);
+        krms = sqrtf(tree_chunk_pairs<C>(qk) / (float)D);
         if (krms < kMinRMS) krms = kMinRMS;
-        vrms = sqrtf(tree_wide<E / 2>(rv) / (float)D);
+        vrms = sqrtf(tree_chunk_pairs<C>(qv) / (float)D);
         if (vrms < kMinRMS) vrms = kMinRMS;
         const float ky = 1.0f / krms, vy = 1.0f / vrms;
+        uint32_t kn4[E], vn4[E];
 #pragma unroll
         for (int k = 0; k < E; ++k) {
-            kcode |= v4_code(fminf(fmaxf(div_by(xk[k], krms, ky), -2.75f), 2.75f), tab) << (4 * k);
-            vcode |= v4_code(fminf(fmaxf(div_by(xv[k], vrms, vy), -2.75f), 2.75f), tab) << (4 * k);
+            kn4[k] = v4_code(fminf(fmaxf(div_by(xk[k], krms, ky), -2.75f), 2.75f), tab);
+            vn4[k] = v4_code(fminf(fmaxf(div_by(xv[k], vrms, vy), -2.75f), 2.75f), tab);
+        }
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            kbyte[c] = kn4[2 * c] | (kn4[2 * c + 1] << 4);
+            vbyte[c] = vn4[2 * c] | (vn4[2 * c + 1] << 4);
         }
     }
     if (!valid) return;
@@ -235,14 +271,14 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
     split_slot(slot, g, page, tib);
     const size_t cell = (size_t)(tib * g.H + h);
     uint8_t* base = pool + (size_t)page * g.page_size;
-    // Element pair (2b, 2b+1) is byte b (low nibble even); the lane's E/2
-    // bytes are contiguous at byte E*j/2 of the cell.
-    if constexpr (E == 8) {
-        *reinterpret_cast<uint32_t*>(base + g.kc_off + cell * g.code_stride + 4 * j) = kcode;
-        *reinterpret_cast<uint32_t*>(base + g.vc_off + cell * g.code_stride + 4 * j) = vcode;
-    } else {
-        *reinterpret_cast<uint16_t*>(base + g.kc_off + cell * g.code_stride + 2 * j) = (uint16_t)kcode;
-        *reinterpret_cast<uint16_t*>(base + g.vc_off + cell * g.code_stride + 2 * j) = (uint16_t)vcode;
+    // Element pair (2b, 2b+1) is byte b (low nibble even): chunk c of lane j
+    // is byte 16c + j.
+    uint8_t* kc = base + g.kc_off + cell * g.code_stride + j;
+    uint8_t* vc = base + g.vc_off + cell * g.code_stride + j;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        kc[16 * c] = (uint8_t)kbyte[c];
+        vc[16 * c] = (uint8_t)vbyte[c];
     }
     if (j == 0) {
         *reinterpret_cast<uint16_t*>(base + g.ks_off + cell * g.scale_stride) = f2h(krms);
