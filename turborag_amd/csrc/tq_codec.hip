@@ -18,6 +18,9 @@ namespace {
 using namespace dev;
 
 constexpr int kBlock = 256;
+// Lanes per row of the wide pack: 8 rows per wave share every per-row
+// instruction (RMS, reciprocal, square roots); 16 lanes ran 15% slower.
+constexpr int kPackLanes = 8;
 
 // ---------------------------------------------------------------------------
 // turbo_prod pack — src/cuda/tq_turbo_prod_kernels.cu:110-260
@@ -79,25 +82,25 @@ __global__ __launch_bounds__(kBlock) void prod_pack_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Pack, wide form (D = 64, 128): 16 lanes per (token, head) row, four rows
-// per wave.  Lane j owns the element pairs (32c + 2j, 32c + 2j + 1) of the
-// C = D/32 chunks c, in registers k = 2c and 2c + 1.  The reference's
+// Pack, wide form (D = 64, 128): R lanes per (token, head) row, 64/R rows
+// per wave.  Lane j owns the element pairs (2Rc + 2j, 2Rc + 2j + 1) of the
+// C = D/2R chunks c, in registers k = 2c and 2c + 1.  The reference's
 // butterfly stage len pairs elements i and i + len: in-lane for len = 1 and
-// len >= 32 (chunks c and c ^ (len/32)), lanes j and j ^ (len/2) for
-// len = 2 .. 16.  Its halving trees (r[i] += r[i + s], s = n/2 .. 1) run
-// in-lane over chunks first (s >= 32), then across lanes (s = 16 .. 2, one or
+// len >= 2R (chunks c and c ^ (len/2R)), lanes j and j ^ (len/2) for
+// len = 2 .. R.  Its halving trees (r[i] += r[i + s], s = n/2 .. 1) run
+// in-lane over chunks first (s >= 2R), then across lanes (s = R .. 2, one or
 // two values per lane), and end in-lane (s = 1): most of the adds stay in
 // registers.  Operation order per element is the reference's, so codes and
 // scales are bit-identical to the one-row-per-wave form above.  Code byte
-// 16c + j of a cell is the lane's chunk c.
+// Rc + j of a cell is the lane's chunk c.
 // ---------------------------------------------------------------------------
-template <int C>
+template <int C, int R>
 __device__ __forceinline__ void wht_chunks(float (&x)[2 * C], int j) {
     // len = 1 is done by the caller (it carries the sign flip).
-    // Cross-lane stages len = 2 .. 16: partner + (+-mine), the signed copies
+    // Cross-lane stages len = 2 .. R: partner + (+-mine), the signed copies
     // made for all values first so that no DPP add waits on the op before it.
 #pragma unroll
-    for (int m = 1; m < 16; m <<= 1) {
+    for (int m = 1; m < R; m <<= 1) {
         const bool lower = (j & m) == 0;
         float t[2 * C];
 #pragma unroll
@@ -119,50 +122,50 @@ __device__ __forceinline__ void wht_chunks(float (&x)[2 * C], int j) {
                 }
 }
 
-// Halving tree over the row's 32*C values r[2c + b] (element 32c + 2j + b):
-// s = 16C .. 32 in-lane over chunks, s = 16 .. 2 across lanes j ^ s/2, s = 1
+// Halving tree over the row's 2RC values r[2c + b] (element 2Rc + 2j + b):
+// s = RC .. 2R in-lane over chunks, s = R .. 2 across lanes j ^ s/2, s = 1
 // in-lane.  Every lane ends with the total.
-template <int C>
+template <int C, int R>
 __device__ __forceinline__ float tree_chunks(float (&r)[2 * C]) {
 #pragma unroll
     for (int d = C / 2; d >= 1; d >>= 1)
 #pragma unroll
         for (int k = 0; k < 2 * d; ++k) r[k] += r[k + 2 * d];
 #pragma unroll
-    for (int m = 8; m >= 1; m >>= 1) {
+    for (int m = R / 2; m >= 1; m >>= 1) {
         r[0] += xor_lane(r[0], m);
         r[1] += xor_lane(r[1], m);
     }
     return r[0] + r[1];
 }
 
-// Halving tree over the row's 16*C pair sums q[c] (pair 16c + j): s = 8C ..
-// 16 in-lane over chunks, s = 8 .. 1 across lanes.
-template <int C>
+// Halving tree over the row's RC pair sums q[c] (pair Rc + j): s = RC/2 ..
+// R in-lane over chunks, s = R/2 .. 1 across lanes.
+template <int C, int R>
 __device__ __forceinline__ float tree_chunk_pairs(float (&q)[C]) {
 #pragma unroll
     for (int d = C / 2; d >= 1; d >>= 1)
 #pragma unroll
         for (int c = 0; c < d; ++c) q[c] += q[c + d];
 #pragma unroll
-    for (int m = 8; m >= 1; m >>= 1) q[0] += xor_lane(q[0], m);
+    for (int m = R / 2; m >= 1; m >>= 1) q[0] += xor_lane(q[0], m);
     return q[0];
 }
 
-template <int D, bool PROD>
+template <int D, bool PROD, int R>
 __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
     const uint16_t* __restrict__ key, const uint16_t* __restrict__ value,
     const int32_t* __restrict__ slots, uint8_t* __restrict__ pool, PageGeom g, int num_rows,
     float inv) {
-    constexpr int C = D / 32, E = 2 * C;
-    static_assert(C == 2 || C == 4, "D = 64 or 128");
+    constexpr int C = D / (2 * R), E = 2 * C;
+    static_assert((R == 8 || R == 16) && C >= 2 && (C & (C - 1)) == 0, "R lanes per row");
     __shared__ PackTables tab;
     if (threadIdx.x < kPackTableWords)
         reinterpret_cast<uint32_t*>(&tab)[threadIdx.x] =
             reinterpret_cast<const uint32_t*>(&kPackTables)[threadIdx.x];
     __syncthreads();
-    const int j = threadIdx.x & 15;
-    const int row = blockIdx.x * (kBlock / 16) + (threadIdx.x >> 4);
+    const int j = threadIdx.x & (R - 1);
+    const int row = blockIdx.x * (kBlock / R) + threadIdx.x / R;
     const bool valid = row < num_rows;
     const int rr = valid ? row : num_rows - 1;
     const int t = rr / g.H, h = rr % g.H;
@@ -171,10 +174,10 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
     uint32_t kw[C], vw[C];
 #pragma unroll
     for (int c = 0; c < C; ++c) {
-        kw[c] = kr[16 * c];
-        vw[c] = vr[16 * c];
+        kw[c] = kr[R * c];
+        vw[c] = vr[R * c];
     }
-    // s(i, h) = (-1)^(i + h) = sh * (-1)^b for element i = 32c + 2j + b.  The
+    // s(i, h) = (-1)^(i + h) = sh * (-1)^b for element i = 2Rc + 2j + b.  The
     // first butterfly stage on (sh*a, -sh*b) gives (sh*(a - b), sh*(a + b));
     // fp32 rounding is symmetric in sign, so every later value is sh times
     // the one computed without it (up to the sign of exact zeros, which no
@@ -190,8 +193,8 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
         xv[2 * c] = va - vb;
         xv[2 * c + 1] = va + vb;
     }
-    wht_chunks<C>(xk, j);
-    wht_chunks<C>(xv, j);
+    wht_chunks<C, R>(xk, j);
+    wht_chunks<C, R>(xv, j);
     uint32_t kbyte[C], vbyte[C];
     float krms, vrms, rms_e = 0.0f;
     if constexpr (PROD) {
@@ -202,11 +205,11 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
             xv[k] *= sinv;
             r[k] = xk[k] * xk[k];
         }
-        krms = sqrtf(tree_chunks<C>(r) / (float)D);
+        krms = sqrtf(tree_chunks<C, R>(r) / (float)D);
         if (krms < kMinRMS) krms = kMinRMS;
 #pragma unroll
         for (int k = 0; k < E; ++k) r[k] = xv[k] * xv[k];
-        vrms = sqrtf(tree_chunks<C>(r) / (float)D);
+        vrms = sqrtf(tree_chunks<C, R>(r) / (float)D);
         if (vrms < kMinRMS) vrms = kMinRMS;
         const float ky = 1.0f / krms, vy = 1.0f / vrms;
         uint32_t kn4[E], vn4[E];
@@ -228,7 +231,7 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
             kbyte[c] = kn4[2 * c] | (kn4[2 * c + 1] << 4);
             vbyte[c] = vn4[2 * c] | (vn4[2 * c + 1] << 4);
         }
-        rms_e = sqrtf(tree_chunks<C>(r) / (float)D);
+        rms_e = sqrtf(tree_chunks<C, R>(r) / (float)D);
         if (rms_e < kMinRMS) rms_e = kMinRMS;
         // The rotation spreads a non-finite input over the whole row: then
         // every K/rms is NaN, the reference's residual RMS is NaN, and the
@@ -247,9 +250,9 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
             qk[c] = fmaf(xk[2 * c], xk[2 * c], xk[2 * c + 1] * xk[2 * c + 1]);
             qv[c] = fmaf(xv[2 * c], xv[2 * c], xv[2 * c + 1] * xv[2 * c + 1]);
         }
-        krms = sqrtf(tree_chunk_pairs<C>(qk) / (float)D);
+        krms = sqrtf(tree_chunk_pairs<C, R>(qk) / (float)D);
         if (krms < kMinRMS) krms = kMinRMS;
-        vrms = sqrtf(tree_chunk_pairs<C>(qv) / (float)D);
+        vrms = sqrtf(tree_chunk_pairs<C, R>(qv) / (float)D);
         if (vrms < kMinRMS) vrms = kMinRMS;
         const float ky = 1.0f / krms, vy = 1.0f / vrms;
         uint32_t kn4[E], vn4[E];
@@ -272,13 +275,13 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
     const size_t cell = (size_t)(tib * g.H + h);
     uint8_t* base = pool + (size_t)page * g.page_size;
     // Element pair (2b, 2b+1) is byte b (low nibble even): chunk c of lane j
-    // is byte 16c + j.
+    // is byte Rc + j.
     uint8_t* kc = base + g.kc_off + cell * g.code_stride + j;
     uint8_t* vc = base + g.vc_off + cell * g.code_stride + j;
 #pragma unroll
     for (int c = 0; c < C; ++c) {
-        kc[16 * c] = (uint8_t)kbyte[c];
-        vc[16 * c] = (uint8_t)vbyte[c];
+        kc[R * c] = (uint8_t)kbyte[c];
+        vc[R * c] = (uint8_t)vbyte[c];
     }
     if (j == 0) {
         *reinterpret_cast<uint16_t*>(base + g.ks_off + cell * g.scale_stride) = f2h(krms);
@@ -666,16 +669,17 @@ void launch_pack(Scheme s, const uint16_t* key, const uint16_t* value, const int
     const float inv = inv_sqrt_d(g.D);
     const auto al = [](uint64_t v, uint64_t a) { return (v & (a - 1)) == 0; };
     if ((g.D == 64 || g.D == 128) && al(g.kc_off, 4) && al(g.vc_off, 4) && al(g.page_size, 4) &&
-        al(reinterpret_cast<uintptr_t>(pool), 4) && al(reinterpret_cast<uintptr_t>(key), 16) &&
-        al(reinterpret_cast<uintptr_t>(value), 16)) {
-        const dim3 wgrid((rows + kBlock / 16 - 1) / (kBlock / 16));
+        al(reinterpret_cast<uintptr_t>(pool), 4) && al(reinterpret_cast<uintptr_t>(key), 4) &&
+        al(reinterpret_cast<uintptr_t>(value), 4)) {
+        constexpr int R = kPackLanes;
+        const dim3 wgrid((rows + kBlock / R - 1) / (kBlock / R));
         const bool prod = s == Scheme::Prod;
         auto go = [&](auto kernel) {
             hipLaunchKernelGGL(kernel, wgrid, dim3(kBlock), 0, stream, key, value, slots, pool, g,
                                rows, inv);
         };
-        if (g.D == 128) prod ? go(pack_wide_kernel<128, true>) : go(pack_wide_kernel<128, false>);
-        else prod ? go(pack_wide_kernel<64, true>) : go(pack_wide_kernel<64, false>);
+        if (g.D == 128) prod ? go(pack_wide_kernel<128, true, R>) : go(pack_wide_kernel<128, false, R>);
+        else prod ? go(pack_wide_kernel<64, true, R>) : go(pack_wide_kernel<64, false, R>);
         check_launch(prod ? "turbo_prod_pack_kv_kernel" : "turbo_mse_pack_kv_kernel");
         return;
     }
