@@ -19,7 +19,8 @@ using namespace dev;
 
 constexpr int kBlock = 256;
 // Lanes per row of the wide pack: 8 rows per wave share every per-row
-// instruction (RMS, reciprocal, square roots); 16 lanes ran 15% slower.
+// instruction (RMS, reciprocal, square roots); 16 lanes ran 15% slower, and
+// 4 lanes (200 VGPRs, two waves per SIMD) 43% slower.
 constexpr int kPackLanes = 8;
 
 // ---------------------------------------------------------------------------
