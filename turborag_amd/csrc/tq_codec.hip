@@ -95,21 +95,78 @@ __global__ __launch_bounds__(kBlock) void prod_pack_kernel(
 // scales are bit-identical to the one-row-per-wave form above.  Code byte
 // Rc + j of a cell is the lane's chunk c.
 // ---------------------------------------------------------------------------
-template <int C, int R>
+// Lane order of a pack row: physical lane p (of 8) holds logical lane
+// j = p for p < 4 and j = p ^ 3 for p >= 4.  Then logical j ^ 1 and j ^ 2
+// are physical p ^ 1 and p ^ 2 (quad_perm), and logical j ^ 4 is physical
+// 7 - p (row_half_mirror): every partner exchange is one DPP operand.
+__device__ __forceinline__ int pack_lane(int p) { return (p & 4) ? p ^ 3 : p; }
+
+template <int M>
+__device__ __forceinline__ float row8_xor(float v) {
+    constexpr int ctrl = M == 1 ? 0xB1 : (M == 2 ? 0x4E : 0x141);
+    static_assert(M == 1 || M == 2 || M == 4, "row of 8 lanes");
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), ctrl, 0xF, 0xF, true));
+}
+
+// y[k] = y[k] + c * (partner's y[k]) for 8 values, the partner read by DPP
+// (v_fmac_f32_dpp).  The s_nop gives the two wait states a DPP read needs
+// after the VALU write of its source.
+#define TQ_FMAC8(CTRL)                                                                     \
+    "s_nop 1\n\t"                                                                          \
+    "v_fmac_f32_dpp %0, %0, %8 " CTRL " row_mask:0xf bank_mask:0xf\n\t"                     \
+    "v_fmac_f32_dpp %1, %1, %8 " CTRL " row_mask:0xf bank_mask:0xf\n\t"                     \
+    "v_fmac_f32_dpp %2, %2, %8 " CTRL " row_mask:0xf bank_mask:0xf\n\t"                     \
+    "v_fmac_f32_dpp %3, %3, %8 " CTRL " row_mask:0xf bank_mask:0xf\n\t"                     \
+    "v_fmac_f32_dpp %4, %4, %8 " CTRL " row_mask:0xf bank_mask:0xf\n\t"                     \
+    "v_fmac_f32_dpp %5, %5, %8 " CTRL " row_mask:0xf bank_mask:0xf\n\t"                     \
+    "v_fmac_f32_dpp %6, %6, %8 " CTRL " row_mask:0xf bank_mask:0xf\n\t"                     \
+    "v_fmac_f32_dpp %7, %7, %8 " CTRL " row_mask:0xf bank_mask:0xf"
+
+template <int M>
+__device__ __forceinline__ void fmac_partner8(float* y, float c) {
+    if constexpr (M == 1)
+        asm(TQ_FMAC8("quad_perm:[1,0,3,2]")
+            : "+v"(y[0]), "+v"(y[1]), "+v"(y[2]), "+v"(y[3]), "+v"(y[4]), "+v"(y[5]),
+              "+v"(y[6]), "+v"(y[7])
+            : "v"(c));
+    else if constexpr (M == 2)
+        asm(TQ_FMAC8("quad_perm:[2,3,0,1]")
+            : "+v"(y[0]), "+v"(y[1]), "+v"(y[2]), "+v"(y[3]), "+v"(y[4]), "+v"(y[5]),
+              "+v"(y[6]), "+v"(y[7])
+            : "v"(c));
+    else
+        asm(TQ_FMAC8("row_half_mirror")
+            : "+v"(y[0]), "+v"(y[1]), "+v"(y[2]), "+v"(y[3]), "+v"(y[4]), "+v"(y[5]),
+              "+v"(y[6]), "+v"(y[7])
+            : "v"(c));
+}
+#undef TQ_FMAC8
+
+// Butterfly stages len = 2 .. 64 of a row held as chunks (len = 1 is done by
+// the caller: it carries the sign flip).  The cross-lane stages len = 2, 4, 8
+// pair logical lanes j and j ^ m (m = len/2): the lower lane needs
+// x + partner, the upper partner - x.  Each lane instead keeps
+// y = sigma_j * x and applies y += c * partner_y with c = +1 (lower) or -1
+// (upper), one fused DPP op: both lanes of a pair carry the same sigma, so
+// the lower gets sigma * (x + x'), the upper -sigma * (x' - x) exactly
+// (fp32 rounding is symmetric in sign), and sigma flips on upper lanes.
+// After the three stages sigma_j = (-1)^popcount(j); the caller folds it
+// into the exact scale.  The in-lane chunk stages len = 16 .. 64 are linear,
+// so sigma passes through them.
+template <int C>
 __device__ __forceinline__ void wht_chunks(float (&x)[2 * C], int j) {
-    // len = 1 is done by the caller (it carries the sign flip).
-    // Cross-lane stages len = 2 .. R: partner + (+-mine), the signed copies
-    // made for all values first so that no DPP add waits on the op before it.
+    static_assert((2 * C) % 8 == 0, "blocks of 8 values");
 #pragma unroll
-    for (int m = 1; m < R; m <<= 1) {
-        const bool lower = (j & m) == 0;
-        float t[2 * C];
+    for (int m = 1; m < 8; m <<= 1) {
+        const float c = (j & m) ? -1.0f : 1.0f;
 #pragma unroll
-        for (int k = 0; k < 2 * C; ++k) t[k] = lower ? x[k] : -x[k];
-#pragma unroll
-        for (int k = 0; k < 2 * C; ++k) x[k] = xor_lane(x[k], m) + t[k];
+        for (int k = 0; k < 2 * C; k += 8) {
+            if (m == 1) fmac_partner8<1>(x + k, c);
+            else if (m == 2) fmac_partner8<2>(x + k, c);
+            else fmac_partner8<4>(x + k, c);
+        }
     }
-    // len = 32, 64: chunks c and c + len/32.
+    // len = 16 .. 64: chunks c and c + len/16.
 #pragma unroll
     for (int d = 1; d < C; d <<= 1)
 #pragma unroll
@@ -123,49 +180,51 @@ __device__ __forceinline__ void wht_chunks(float (&x)[2 * C], int j) {
                 }
 }
 
-// Halving tree over the row's 2RC values r[2c + b] (element 2Rc + 2j + b):
-// s = RC .. 2R in-lane over chunks, s = R .. 2 across lanes j ^ s/2, s = 1
-// in-lane.  Every lane ends with the total.
-template <int C, int R>
+// Halving tree over the row's 16C values r[2c + b] (element 16c + 2j + b):
+// s = 8C .. 16 in-lane over chunks, s = 8 .. 2 across logical lanes j ^ s/2,
+// s = 1 in-lane.  Every lane ends with the total.
+template <int C>
 __device__ __forceinline__ float tree_chunks(float (&r)[2 * C]) {
 #pragma unroll
     for (int d = C / 2; d >= 1; d >>= 1)
 #pragma unroll
         for (int k = 0; k < 2 * d; ++k) r[k] += r[k + 2 * d];
-#pragma unroll
-    for (int m = R / 2; m >= 1; m >>= 1) {
-        r[0] += xor_lane(r[0], m);
-        r[1] += xor_lane(r[1], m);
-    }
+    r[0] += row8_xor<4>(r[0]);
+    r[1] += row8_xor<4>(r[1]);
+    r[0] += row8_xor<2>(r[0]);
+    r[1] += row8_xor<2>(r[1]);
+    r[0] += row8_xor<1>(r[0]);
+    r[1] += row8_xor<1>(r[1]);
     return r[0] + r[1];
 }
 
-// Halving tree over the row's RC pair sums q[c] (pair Rc + j): s = RC/2 ..
-// R in-lane over chunks, s = R/2 .. 1 across lanes.
-template <int C, int R>
+// Halving tree over the row's 8C pair sums q[c] (pair 8c + j): s = 4C .. 8
+// in-lane over chunks, s = 4 .. 1 across logical lanes.
+template <int C>
 __device__ __forceinline__ float tree_chunk_pairs(float (&q)[C]) {
 #pragma unroll
     for (int d = C / 2; d >= 1; d >>= 1)
 #pragma unroll
         for (int c = 0; c < d; ++c) q[c] += q[c + d];
-#pragma unroll
-    for (int m = R / 2; m >= 1; m >>= 1) q[0] += xor_lane(q[0], m);
+    q[0] += row8_xor<4>(q[0]);
+    q[0] += row8_xor<2>(q[0]);
+    q[0] += row8_xor<1>(q[0]);
     return q[0];
 }
 
-template <int D, bool PROD, int R>
+template <int D, bool PROD>
 __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
     const uint16_t* __restrict__ key, const uint16_t* __restrict__ value,
     const int32_t* __restrict__ slots, uint8_t* __restrict__ pool, PageGeom g, int num_rows,
     float inv) {
-    constexpr int C = D / (2 * R), E = 2 * C;
-    static_assert((R == 8 || R == 16) && C >= 2 && (C & (C - 1)) == 0, "R lanes per row");
+    constexpr int R = kPackLanes, C = D / (2 * R), E = 2 * C;
+    static_assert(C == 4 || C == 8, "D = 64 or 128");
     __shared__ PackTables tab;
     if (threadIdx.x < kPackTableWords)
         reinterpret_cast<uint32_t*>(&tab)[threadIdx.x] =
             reinterpret_cast<const uint32_t*>(&kPackTables)[threadIdx.x];
     __syncthreads();
-    const int j = threadIdx.x & (R - 1);
+    const int j = pack_lane(threadIdx.x & (R - 1));
     const int row = blockIdx.x * (kBlock / R) + threadIdx.x / R;
     const bool valid = row < num_rows;
     const int rr = valid ? row : num_rows - 1;
@@ -182,8 +241,9 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
     // first butterfly stage on (sh*a, -sh*b) gives (sh*(a - b), sh*(a + b));
     // fp32 rounding is symmetric in sign, so every later value is sh times
     // the one computed without it (up to the sign of exact zeros, which no
-    // code or scale sees), and sh is folded into the exact scale sh/sqrt(D).
-    const float sinv = (h & 1) ? -inv : inv;
+    // code or scale sees).  sh and the lane sign of wht_chunks are folded
+    // into the exact scale +-1/sqrt(D).
+    const float sinv = ((h ^ __popc(j)) & 1) ? -inv : inv;
     float xk[E], xv[E];
 #pragma unroll
     for (int c = 0; c < C; ++c) {
@@ -194,8 +254,8 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
         xv[2 * c] = va - vb;
         xv[2 * c + 1] = va + vb;
     }
-    wht_chunks<C, R>(xk, j);
-    wht_chunks<C, R>(xv, j);
+    wht_chunks<C>(xk, j);
+    wht_chunks<C>(xv, j);
     uint32_t kbyte[C], vbyte[C];
     float krms, vrms, rms_e = 0.0f;
     if constexpr (PROD) {
@@ -206,11 +266,11 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
             xv[k] *= sinv;
             r[k] = xk[k] * xk[k];
         }
-        krms = sqrtf(tree_chunks<C, R>(r) / (float)D);
+        krms = sqrtf(tree_chunks<C>(r) / (float)D);
         if (krms < kMinRMS) krms = kMinRMS;
 #pragma unroll
         for (int k = 0; k < E; ++k) r[k] = xv[k] * xv[k];
-        vrms = sqrtf(tree_chunks<C, R>(r) / (float)D);
+        vrms = sqrtf(tree_chunks<C>(r) / (float)D);
         if (vrms < kMinRMS) vrms = kMinRMS;
         const float ky = 1.0f / krms, vy = 1.0f / vrms;
         uint32_t kn4[E], vn4[E];
@@ -232,7 +292,7 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
             kbyte[c] = kn4[2 * c] | (kn4[2 * c + 1] << 4);
             vbyte[c] = vn4[2 * c] | (vn4[2 * c + 1] << 4);
         }
-        rms_e = sqrtf(tree_chunks<C, R>(r) / (float)D);
+        rms_e = sqrtf(tree_chunks<C>(r) / (float)D);
         if (rms_e < kMinRMS) rms_e = kMinRMS;
         // The rotation spreads a non-finite input over the whole row: then
         // every K/rms is NaN, the reference's residual RMS is NaN, and the
@@ -251,9 +311,9 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
             qk[c] = fmaf(xk[2 * c], xk[2 * c], xk[2 * c + 1] * xk[2 * c + 1]);
             qv[c] = fmaf(xv[2 * c], xv[2 * c], xv[2 * c + 1] * xv[2 * c + 1]);
         }
-        krms = sqrtf(tree_chunk_pairs<C, R>(qk) / (float)D);
+        krms = sqrtf(tree_chunk_pairs<C>(qk) / (float)D);
         if (krms < kMinRMS) krms = kMinRMS;
-        vrms = sqrtf(tree_chunk_pairs<C, R>(qv) / (float)D);
+        vrms = sqrtf(tree_chunk_pairs<C>(qv) / (float)D);
         if (vrms < kMinRMS) vrms = kMinRMS;
         const float ky = 1.0f / krms, vy = 1.0f / vrms;
         uint32_t kn4[E], vn4[E];
@@ -679,8 +739,8 @@ void launch_pack(Scheme s, const uint16_t* key, const uint16_t* value, const int
             hipLaunchKernelGGL(kernel, wgrid, dim3(kBlock), 0, stream, key, value, slots, pool, g,
                                rows, inv);
         };
-        if (g.D == 128) prod ? go(pack_wide_kernel<128, true, R>) : go(pack_wide_kernel<128, false, R>);
-        else prod ? go(pack_wide_kernel<64, true, R>) : go(pack_wide_kernel<64, false, R>);
+        if (g.D == 128) prod ? go(pack_wide_kernel<128, true>) : go(pack_wide_kernel<128, false>);
+        else prod ? go(pack_wide_kernel<64, true>) : go(pack_wide_kernel<64, false>);
         check_launch(prod ? "turbo_prod_pack_kv_kernel" : "turbo_mse_pack_kv_kernel");
         return;
     }
