@@ -118,10 +118,11 @@ def test_compiled_tables_match(oracle, tmp_path):
         "  constexpr PackTables p = thr::pack_tables();\n"
         '  for (int i = 1; i < 8; ++i) printf("%a\\n", a.t[i]);\n'
         '  for (int i = 1; i < 16; ++i) printf("%a\\n", b.t[i]);\n'
-        '  for (int g = 0; g < kV4Cells; ++g) printf("%d\\n", p.v4_first[g]);\n'
-        '  for (int g = 0; g < kK3Cells; ++g) printf("%d\\n", p.k3_first[g]);\n'
-        '  for (int i = 1; i < 17; ++i) printf("%a\\n", p.v4_t[i]);\n'
-        '  for (int l = 0; l < 8; ++l) printf("%a %a %a\\n", p.k3_q[l][0], p.k3_q[l][1], p.k3_q[l][2]);\n'
+        '  for (int g = 0; g < kV4Cells; ++g) printf("%d\\n", p.v4_row[g] / 8);\n'
+        '  for (int g = 0; g < kK3Cells; ++g) printf("%d\\n", p.k3_row[g] / 16);\n'
+        '  for (int l = 0; l < 16; ++l) printf("%a %u\\n", p.v4[l].t, p.v4[l].code);\n'
+        '  for (int l = 0; l < 8; ++l)\n'
+        '    printf("%a %a %a %u\\n", p.k3[l].t, p.k3[l].lo, p.k3[l].hi, p.k3[l].code);\n'
         "}\n")
     exe = tmp_path / "thr"
     subprocess.run([hipcc, "-std=c++17", "-O1", "--offload-arch=gfx950",
@@ -138,9 +139,12 @@ def test_compiled_tables_match(oracle, tmp_path):
     n += 45
     assert [int(v) for v in out[n:n + 41]] == list(_grid(T3, 20.0, 41))
     n += 41
-    assert np.array_equal(fl(out[n:n + 16]), np.append(T4[1:], f32(np.inf)))
-    n += 16
-    q = fl(out[n:n + 24]).reshape(8, 3)
-    assert np.array_equal(q[:, 0], np.append(T3[1:], f32(np.inf)))
-    assert np.array_equal(q[:, 1], oracle.k3)
-    assert np.array_equal(q[:, 2], np.append(oracle.k3[1:], oracle.k3[7]))
+    v4 = out[n:n + 32]
+    assert np.array_equal(fl(v4[0::2]), np.append(T4[1:], f32(np.inf)))
+    assert [int(c) for c in v4[1::2]] == list(range(16))
+    n += 32
+    k3 = out[n:n + 32]
+    assert np.array_equal(fl(k3[0::4]), np.append(T3[1:], f32(np.inf)))
+    assert np.array_equal(fl(k3[1::4]), oracle.k3)
+    assert np.array_equal(fl(k3[2::4]), np.append(oracle.k3[1:], oracle.k3[7]))
+    assert [int(c) for c in k3[3::4]] == list(range(8))

@@ -247,12 +247,8 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
     float xk[E], xv[E];
 #pragma unroll
     for (int c = 0; c < C; ++c) {
-        const float ka = h2f((uint16_t)kw[c]), kb = h2f((uint16_t)(kw[c] >> 16));
-        const float va = h2f((uint16_t)vw[c]), vb = h2f((uint16_t)(vw[c] >> 16));
-        xk[2 * c] = ka - kb;
-        xk[2 * c + 1] = ka + kb;
-        xv[2 * c] = va - vb;
-        xv[2 * c + 1] = va + vb;
+        half_pair_diff_sum(kw[c], xk[2 * c], xk[2 * c + 1]);
+        half_pair_diff_sum(vw[c], xv[2 * c], xv[2 * c + 1]);
     }
     wht_chunks<C>(xk, j);
     wht_chunks<C>(xv, j);

@@ -295,11 +295,21 @@ static_assert(thr::well_formed(kK3, kK3T) && thr::well_formed(kV4, kV4T),
 // the count at x is first[g] + (x >= T[first[g] + 1]).
 constexpr float kK3Off = 20.0f, kV4Off = 22.0f;
 constexpr int kK3Cells = 41, kV4Cells = 45;
+// One row per possible first[g]: the next threshold (+inf past the last
+// level), the levels on either side of it for the K residual, and the index.
+struct V4Row {
+    float t;
+    uint32_t code;
+};
+struct alignas(16) K3Row {
+    float t, lo, hi;
+    uint32_t code;
+};
 struct alignas(16) PackTables {
-    uint8_t v4_first[48];  // [g], g < kV4Cells
-    uint8_t k3_first[48];  // [g], g < kK3Cells
-    float v4_t[20];        // [i] = T_i for 1 <= i < 16, [16] = +inf
-    float k3_q[8][4];      // [l] = {T_(l+1) (+inf for l = 7), level l, level l+1, 0}
+    uint8_t v4_row[48];  // [g] = byte offset of V4Row first[g], g < kV4Cells
+    uint8_t k3_row[48];  // [g] = byte offset of K3Row first[g], g < kK3Cells
+    V4Row v4[16];
+    K3Row k3[8];
 };
 namespace thr {
 constexpr int cell(float x, float off) { return (int)(x * 8.0f + off); }
@@ -312,22 +322,21 @@ constexpr bool one_per_cell(const Table<N>& T, float off, int cells) {
     return true;
 }
 template <int N>
-constexpr uint8_t first_in_cell(const Table<N>& T, float off, int g) {
+constexpr int first_in_cell(const Table<N>& T, float off, int g) {
     int n = 0;
     for (int i = 1; i < N; ++i) n += cell(T.t[i], off) < g ? 1 : 0;
-    return (uint8_t)n;
+    return n;
 }
 constexpr PackTables pack_tables() {
     PackTables p{};
-    for (int g = 0; g < kV4Cells; ++g) p.v4_first[g] = first_in_cell(kV4T, kV4Off, g);
-    for (int g = 0; g < kK3Cells; ++g) p.k3_first[g] = first_in_cell(kK3T, kK3Off, g);
-    for (int i = 1; i < 16; ++i) p.v4_t[i] = kV4T.t[i];
-    p.v4_t[16] = __builtin_huge_valf();
-    for (int l = 0; l < 8; ++l) {
-        p.k3_q[l][0] = l < 7 ? kK3T.t[l + 1] : __builtin_huge_valf();
-        p.k3_q[l][1] = kK3[l];
-        p.k3_q[l][2] = l < 7 ? kK3[l + 1] : kK3[l];
-    }
+    for (int g = 0; g < kV4Cells; ++g)
+        p.v4_row[g] = (uint8_t)(sizeof(V4Row) * first_in_cell(kV4T, kV4Off, g));
+    for (int g = 0; g < kK3Cells; ++g)
+        p.k3_row[g] = (uint8_t)(sizeof(K3Row) * first_in_cell(kK3T, kK3Off, g));
+    for (int l = 0; l < 16; ++l) p.v4[l] = {l < 15 ? kV4T.t[l + 1] : __builtin_huge_valf(), (uint32_t)l};
+    for (int l = 0; l < 8; ++l)
+        p.k3[l] = {l < 7 ? kK3T.t[l + 1] : __builtin_huge_valf(), kK3[l], l < 7 ? kK3[l + 1] : kK3[l],
+                   (uint32_t)l};
     return p;
 }
 }  // namespace thr
@@ -336,22 +345,35 @@ static_assert(thr::one_per_cell(kK3T, kK3Off, kK3Cells) &&
                   thr::cell(-2.5f, kK3Off) == 0 && thr::cell(2.5f, kK3Off) == kK3Cells - 1 &&
                   thr::cell(-2.75f, kV4Off) == 0 && thr::cell(2.75f, kV4Off) == kV4Cells - 1,
               "search grid");
+static_assert(sizeof(V4Row) == 8 && sizeof(K3Row) == 16 && sizeof(PackTables) % 16 == 0,
+              "LDS table of whole dwords, rows aligned");
 __device__ constexpr PackTables kPackTables = thr::pack_tables();
 constexpr int kPackTableWords = sizeof(PackTables) / 4;
-static_assert(sizeof(PackTables) % 16 == 0, "LDS table of whole dwords, float4 rows aligned");
 
 // Nearest V4 index of a clamped x (the reference's first-minimum scan).
 __device__ __forceinline__ uint32_t v4_code(float x, const PackTables& T) {
-    const uint32_t l = T.v4_first[(int)__builtin_fmaf(x, 8.0f, kV4Off)];
-    return l + (x >= T.v4_t[l + 1] ? 1u : 0u);
+    const V4Row r = *reinterpret_cast<const V4Row*>(
+        reinterpret_cast<const char*>(T.v4) + T.v4_row[(int)__builtin_fmaf(x, 8.0f, kV4Off)]);
+    return r.code + (x >= r.t ? 1u : 0u);
 }
 // Nearest K3 index of a clamped x, and its level.
 __device__ __forceinline__ uint32_t k3_code(float x, const PackTables& T, float& level) {
-    const uint32_t l = T.k3_first[(int)__builtin_fmaf(x, 8.0f, kK3Off)];
-    const float4 q = *reinterpret_cast<const float4*>(T.k3_q[l]);
-    const bool up = x >= q.x;
-    level = up ? q.z : q.y;
-    return l + (up ? 1u : 0u);
+    const K3Row r = *reinterpret_cast<const K3Row*>(
+        reinterpret_cast<const char*>(T.k3) + T.k3_row[(int)__builtin_fmaf(x, 8.0f, kK3Off)]);
+    const bool up = x >= r.t;
+    level = up ? r.hi : r.lo;
+    return r.code + (up ? 1u : 0u);
+}
+
+// For the fp16 pair w = (a low, b high): d = fp32(a) - fp32(b) and
+// s = fp32(a) + fp32(b), each rounded once, read straight from the halves
+// (v_fma_mix_f32 computes a * 1.0 +- b in fp32 with one rounding; the fp16
+// operands widen exactly).
+__device__ __forceinline__ void half_pair_diff_sum(uint32_t w, float& d, float& s) {
+    asm("v_fma_mix_f32 %0, %2, 1.0, -%2 op_sel:[0,0,1] op_sel_hi:[1,0,1]\n\t"
+        "v_fma_mix_f32 %1, %2, 1.0, %2 op_sel:[0,0,1] op_sel_hi:[1,0,1]"
+        : "=&v"(d), "=v"(s)
+        : "v"(w));
 }
 
 // a / b rounded correctly, given y = RN(1/b) (Markstein's FMA division:
