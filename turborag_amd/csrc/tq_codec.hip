@@ -212,12 +212,69 @@ __device__ __forceinline__ float tree_chunk_pairs(float (&q)[C]) {
     return q[0];
 }
 
+// One tensor's row, held as chunks: rotation (the first stage from the fp16
+// pairs), RMS, codes packed two per byte.  kCodesK3: 3-bit K code + residual
+// sign and the residual RMS (turbo_prod K); kCodesV4: 4-bit code, RMS of the
+// squares (turbo_prod V); kCodesV4Pairs: 4-bit code, RMS of the pair sums
+// fmaf(x0, x0, x1 * x1) (turbo_mse, tq_turbo_mse_kernels.cu:108, contracted).
+constexpr int kCodesK3 = 0, kCodesV4 = 1, kCodesV4Pairs = 2;
+template <int C, int MODE>
+__device__ __forceinline__ void quantize_chunks(const uint32_t (&w)[C], int j, float sinv,
+                                                const PackTables& tab, uint32_t (&bytes)[C],
+                                                float& rms, float& rms_e) {
+    constexpr int E = 2 * C, D = 16 * C;
+    float x[E];
+#pragma unroll
+    for (int c = 0; c < C; ++c) half_pair_diff_sum(w[c], x[2 * c], x[2 * c + 1]);
+    wht_chunks<C>(x, j);
+#pragma unroll
+    for (int k = 0; k < E; ++k) x[k] *= sinv;
+    if constexpr (MODE == kCodesV4Pairs) {
+        float q[C];
+#pragma unroll
+        for (int c = 0; c < C; ++c) q[c] = fmaf(x[2 * c], x[2 * c], x[2 * c + 1] * x[2 * c + 1]);
+        rms = sqrtf(tree_chunk_pairs<C>(q) / (float)D);
+    } else {
+        float r[E];
+#pragma unroll
+        for (int k = 0; k < E; ++k) r[k] = x[k] * x[k];
+        rms = sqrtf(tree_chunks<C>(r) / (float)D);
+    }
+    if (rms < kMinRMS) rms = kMinRMS;
+    const float y = 1.0f / rms;
+    uint32_t n4[E];
+    if constexpr (MODE == kCodesK3) {
+        float r[E];
+#pragma unroll
+        for (int k = 0; k < E; ++k) {
+            // fmin/fmax clamp a NaN to the low bound, whose codes (0) are the
+            // reference's for NaN; its residual is made NaN below.
+            const float kn = fminf(fmaxf(div_by(x[k], rms, y), -2.5f), 2.5f);
+            float level;
+            n4[k] = k3_nibble(kn, tab, level);
+            const float e = kn - level;
+            r[k] = e * e;
+        }
+        rms_e = sqrtf(tree_chunks<C>(r) / (float)D);
+        if (rms_e < kMinRMS) rms_e = kMinRMS;
+        // The rotation spreads a non-finite input over the whole row: then
+        // every K/rms is NaN, the reference's residual RMS is NaN, and the
+        // codes above are its codes for NaN (index 0, sign 0).
+        if (!(rms <= 3.402823466e38f)) rms_e = __builtin_nanf("");
+    } else {
+#pragma unroll
+        for (int k = 0; k < E; ++k) n4[k] = v4_code(div_by(x[k], rms, y), tab);
+    }
+#pragma unroll
+    for (int c = 0; c < C; ++c) bytes[c] = n4[2 * c] | (n4[2 * c + 1] << 4);
+}
+
 template <int D, bool PROD>
 __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
     const uint16_t* __restrict__ key, const uint16_t* __restrict__ value,
     const int32_t* __restrict__ slots, uint8_t* __restrict__ pool, PageGeom g, int num_rows,
     float inv) {
-    constexpr int R = kPackLanes, C = D / (2 * R), E = 2 * C;
+    constexpr int R = kPackLanes, C = D / (2 * R);
     static_assert(C == 4 || C == 8, "D = 64 or 128");
     __shared__ PackTables tab;
     if (threadIdx.x < kPackTableWords)
@@ -228,7 +285,8 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
     const int row = blockIdx.x * (kBlock / R) + threadIdx.x / R;
     const bool valid = row < num_rows;
     const int rr = valid ? row : num_rows - 1;
-    const int t = rr / g.H, h = rr % g.H;
+    const int t = g.h_shift >= 0 ? rr >> g.h_shift : rr / g.H;
+    const int h = rr - t * g.H;
     const uint32_t* kr = reinterpret_cast<const uint32_t*>(key + (size_t)rr * D) + j;
     const uint32_t* vr = reinterpret_cast<const uint32_t*>(value + (size_t)rr * D) + j;
     uint32_t kw[C], vw[C];
@@ -244,86 +302,12 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
     // code or scale sees).  sh and the lane sign of wht_chunks are folded
     // into the exact scale +-1/sqrt(D).
     const float sinv = ((h ^ __popc(j)) & 1) ? -inv : inv;
-    float xk[E], xv[E];
-#pragma unroll
-    for (int c = 0; c < C; ++c) {
-        half_pair_diff_sum(kw[c], xk[2 * c], xk[2 * c + 1]);
-        half_pair_diff_sum(vw[c], xv[2 * c], xv[2 * c + 1]);
-    }
-    wht_chunks<C>(xk, j);
-    wht_chunks<C>(xv, j);
+    // K, then V: one tensor's values live at a time.
     uint32_t kbyte[C], vbyte[C];
-    float krms, vrms, rms_e = 0.0f;
-    if constexpr (PROD) {
-        float r[E];
-#pragma unroll
-        for (int k = 0; k < E; ++k) {
-            xk[k] *= sinv;
-            xv[k] *= sinv;
-            r[k] = xk[k] * xk[k];
-        }
-        krms = sqrtf(tree_chunks<C>(r) / (float)D);
-        if (krms < kMinRMS) krms = kMinRMS;
-#pragma unroll
-        for (int k = 0; k < E; ++k) r[k] = xv[k] * xv[k];
-        vrms = sqrtf(tree_chunks<C>(r) / (float)D);
-        if (vrms < kMinRMS) vrms = kMinRMS;
-        const float ky = 1.0f / krms, vy = 1.0f / vrms;
-        uint32_t kn4[E], vn4[E];
-#pragma unroll
-        for (int k = 0; k < E; ++k) {
-            // fmin/fmax clamp a NaN to the low bound, whose codes (0) are the
-            // reference's for NaN; its residual is made NaN below.
-            const float kn = fminf(fmaxf(div_by(xk[k], krms, ky), -2.5f), 2.5f);
-            const float vn = fminf(fmaxf(div_by(xv[k], vrms, vy), -2.75f), 2.75f);
-            float level;
-            const uint32_t c = k3_code(kn, tab, level);
-            const float e = kn - level;
-            kn4[k] = ((e >= 0.0f) ? 8u : 0u) | c;
-            vn4[k] = v4_code(vn, tab);
-            r[k] = e * e;
-        }
-#pragma unroll
-        for (int c = 0; c < C; ++c) {
-            kbyte[c] = kn4[2 * c] | (kn4[2 * c + 1] << 4);
-            vbyte[c] = vn4[2 * c] | (vn4[2 * c + 1] << 4);
-        }
-        rms_e = sqrtf(tree_chunks<C>(r) / (float)D);
-        if (rms_e < kMinRMS) rms_e = kMinRMS;
-        // The rotation spreads a non-finite input over the whole row: then
-        // every K/rms is NaN, the reference's residual RMS is NaN, and the
-        // codes above are its codes for NaN (index 0, sign 0).
-        if (!(krms <= 3.402823466e38f)) rms_e = __builtin_nanf("");
-    } else {
-        // Pair sums fmaf(x0, x0, x1 * x1) (tq_turbo_mse_kernels.cu:108, contracted).
-        float qk[C], qv[C];
-#pragma unroll
-        for (int k = 0; k < E; ++k) {
-            xk[k] *= sinv;
-            xv[k] *= sinv;
-        }
-#pragma unroll
-        for (int c = 0; c < C; ++c) {
-            qk[c] = fmaf(xk[2 * c], xk[2 * c], xk[2 * c + 1] * xk[2 * c + 1]);
-            qv[c] = fmaf(xv[2 * c], xv[2 * c], xv[2 * c + 1] * xv[2 * c + 1]);
-        }
-        krms = sqrtf(tree_chunk_pairs<C>(qk) / (float)D);
-        if (krms < kMinRMS) krms = kMinRMS;
-        vrms = sqrtf(tree_chunk_pairs<C>(qv) / (float)D);
-        if (vrms < kMinRMS) vrms = kMinRMS;
-        const float ky = 1.0f / krms, vy = 1.0f / vrms;
-        uint32_t kn4[E], vn4[E];
-#pragma unroll
-        for (int k = 0; k < E; ++k) {
-            kn4[k] = v4_code(fminf(fmaxf(div_by(xk[k], krms, ky), -2.75f), 2.75f), tab);
-            vn4[k] = v4_code(fminf(fmaxf(div_by(xv[k], vrms, vy), -2.75f), 2.75f), tab);
-        }
-#pragma unroll
-        for (int c = 0; c < C; ++c) {
-            kbyte[c] = kn4[2 * c] | (kn4[2 * c + 1] << 4);
-            vbyte[c] = vn4[2 * c] | (vn4[2 * c + 1] << 4);
-        }
-    }
+    float krms, vrms, rms_e = 0.0f, unused;
+    quantize_chunks<C, PROD ? kCodesK3 : kCodesV4Pairs>(kw, j, sinv, tab, kbyte, krms, rms_e);
+    __builtin_amdgcn_sched_barrier(0);
+    quantize_chunks<C, PROD ? kCodesV4 : kCodesV4Pairs>(vw, j, sinv, tab, vbyte, vrms, unused);
     if (!valid) return;
     const int slot = slots[t];
     if (slot < 0) return;

@@ -288,81 +288,118 @@ __device__ constexpr thr::Table<16> kV4T = thr::thresholds(kV4);
 static_assert(thr::well_formed(kK3, kK3T) && thr::well_formed(kV4, kV4T),
               "codebook thresholds");
 
-// Grid form of the search for clamped x (|x| <= 2.5 for K3, 2.75 for V4):
-// the cell g = (int)RN(8x + off) (8x is exact, so fma and mul-then-add agree;
-// g >= 0 on the clamped domain) holds at most one threshold, so with
-// first[g] = #{i : cell(T_i) < g} = the count at the cell's smallest float,
-// the count at x is first[g] + (x >= T[first[g] + 1]).
-constexpr float kK3Off = 20.0f, kV4Off = 22.0f;
-constexpr int kK3Cells = 41, kV4Cells = 45;
-// One row per possible first[g]: the next threshold (+inf past the last
-// level), the levels on either side of it for the K residual, and the index.
+// Grid form of the searches.  A cell g = (int)RN(8x + off) (8x is exact, so
+// fma and mul-then-add agree; g >= 0 on the domain) holds at most one
+// breakpoint, so with first[g] = #{i : cell(B_i) < g} = the count at the
+// cell's smallest float, the count at x is first[g] + (x >= B[first[g] + 1]).
+//
+// V4: breakpoints T_1 .. T_15, domain |x| <= 12 without a clamp: the codes of
+// a clamp to +-2.75 are those of the unclamped x (no threshold lies beyond),
+// and |x / rms| <= sqrt(D) <= 11.32 for D <= 128 (rms >= |x_i| / sqrt(D), and
+// the 1e-8 floor only lowers the ratio); NaN converts to cell 0, code 0.
+// K3 (turbo_prod K, x clamped to +-2.5): the nibble (sign << 3 | code) and the
+// level of the residual e = x - level form a step function over the 15
+// breakpoints L_0 < T_1 < L_1 < ... < T_7 < L_7: past T_c the code is c,
+// past L_c the sign is 1 (e >= 0 exactly when x >= L_c).  State
+// m = #{breakpoints <= x} has code m >> 1, sign m & 1.
+constexpr float kK3Off = 20.0f, kV4Off = 96.0f;
+constexpr int kK3Cells = 41, kV4Cells = 193;
 struct V4Row {
-    float t;
+    float t;  // next threshold (+inf past the last)
     uint32_t code;
 };
 struct alignas(16) K3Row {
-    float t, lo, hi;
-    uint32_t code;
+    float b, lo, hi, pad0;  // next breakpoint (+inf past the last); levels of states m, m + 1
+    uint32_t nlo, nhi;      // nibbles of states m, m + 1
+    uint32_t pad1, pad2;
 };
 struct alignas(16) PackTables {
-    uint8_t v4_row[48];  // [g] = byte offset of V4Row first[g], g < kV4Cells
-    uint8_t k3_row[48];  // [g] = byte offset of K3Row first[g], g < kK3Cells
+    uint8_t v4_row[208];   // [g] = byte offset of V4Row first[g], g < kV4Cells
+    uint16_t k3_row[48];   // [g] = byte offset of K3Row first[g], g < kK3Cells
     V4Row v4[16];
-    K3Row k3[8];
+    K3Row k3[16];
 };
 namespace thr {
 constexpr int cell(float x, float off) { return (int)(x * 8.0f + off); }
 template <int N>
-constexpr bool one_per_cell(const Table<N>& T, float off, int cells) {
-    for (int i = 1; i < N; ++i) {
-        if (cell(T.t[i], off) < 0 || cell(T.t[i], off) >= cells) return false;
-        if (i > 1 && !(cell(T.t[i], off) > cell(T.t[i - 1], off))) return false;
+struct Points {
+    float b[N + 1];  // b[1..N] sorted breakpoints
+};
+template <int N>
+constexpr bool one_per_cell(const Points<N>& P, float off, int cells) {
+    for (int i = 1; i <= N; ++i) {
+        if (cell(P.b[i], off) < 0 || cell(P.b[i], off) >= cells) return false;
+        if (i > 1 && !(cell(P.b[i], off) > cell(P.b[i - 1], off))) return false;
     }
     return true;
 }
 template <int N>
-constexpr int first_in_cell(const Table<N>& T, float off, int g) {
+constexpr int first_in_cell(const Points<N>& P, float off, int g) {
     int n = 0;
-    for (int i = 1; i < N; ++i) n += cell(T.t[i], off) < g ? 1 : 0;
+    for (int i = 1; i <= N; ++i) n += cell(P.b[i], off) < g ? 1 : 0;
     return n;
 }
-constexpr PackTables pack_tables() {
-    PackTables p{};
-    for (int g = 0; g < kV4Cells; ++g)
-        p.v4_row[g] = (uint8_t)(sizeof(V4Row) * first_in_cell(kV4T, kV4Off, g));
-    for (int g = 0; g < kK3Cells; ++g)
-        p.k3_row[g] = (uint8_t)(sizeof(K3Row) * first_in_cell(kK3T, kK3Off, g));
-    for (int l = 0; l < 16; ++l) p.v4[l] = {l < 15 ? kV4T.t[l + 1] : __builtin_huge_valf(), (uint32_t)l};
-    for (int l = 0; l < 8; ++l)
-        p.k3[l] = {l < 7 ? kK3T.t[l + 1] : __builtin_huge_valf(), kK3[l], l < 7 ? kK3[l + 1] : kK3[l],
-                   (uint32_t)l};
+constexpr Points<15> v4_points() {
+    Points<15> p{};
+    for (int i = 1; i < 16; ++i) p.b[i] = kV4T.t[i];
     return p;
 }
+constexpr Points<15> k3_points() {
+    Points<15> p{};
+    for (int i = 1; i <= 15; ++i) p.b[i] = (i & 1) ? kK3[(i - 1) / 2] : kK3T.t[i / 2];
+    return p;
+}
+constexpr uint32_t k3_nibble(int m) { return (uint32_t)((m >> 1) | ((m & 1) << 3)); }
+constexpr PackTables pack_tables() {
+    PackTables p{};
+    constexpr Points<15> v4p = v4_points(), k3p = k3_points();
+    for (int g = 0; g < kV4Cells; ++g)
+        p.v4_row[g] = (uint8_t)(sizeof(V4Row) * first_in_cell(v4p, kV4Off, g));
+    for (int g = 0; g < kK3Cells; ++g)
+        p.k3_row[g] = (uint16_t)(sizeof(K3Row) * first_in_cell(k3p, kK3Off, g));
+    for (int l = 0; l < 16; ++l) p.v4[l] = {l < 15 ? v4p.b[l + 1] : __builtin_huge_valf(), (uint32_t)l};
+    for (int m = 0; m < 16; ++m)
+        p.k3[m] = {m < 15 ? k3p.b[m + 1] : __builtin_huge_valf(), kK3[m >> 1],
+                   kK3[(m < 15 ? m + 1 : m) >> 1], 0.0f, k3_nibble(m),
+                   k3_nibble(m < 15 ? m + 1 : m), 0u, 0u};
+    return p;
+}
+constexpr bool sorted(const Points<15>& P) {
+    for (int i = 2; i <= 15; ++i)
+        if (!(P.b[i] > P.b[i - 1])) return false;
+    return true;
+}
 }  // namespace thr
-static_assert(thr::one_per_cell(kK3T, kK3Off, kK3Cells) &&
-                  thr::one_per_cell(kV4T, kV4Off, kV4Cells) &&
+static_assert(thr::sorted(thr::v4_points()) && thr::sorted(thr::k3_points()) &&
+                  thr::one_per_cell(thr::v4_points(), kV4Off, kV4Cells) &&
+                  thr::one_per_cell(thr::k3_points(), kK3Off, kK3Cells) &&
                   thr::cell(-2.5f, kK3Off) == 0 && thr::cell(2.5f, kK3Off) == kK3Cells - 1 &&
-                  thr::cell(-2.75f, kV4Off) == 0 && thr::cell(2.75f, kV4Off) == kV4Cells - 1,
-              "search grid");
-static_assert(sizeof(V4Row) == 8 && sizeof(K3Row) == 16 && sizeof(PackTables) % 16 == 0,
-              "LDS table of whole dwords, rows aligned");
+                  thr::cell(-12.0f, kV4Off) == 0 && thr::cell(12.0f, kV4Off) == kV4Cells - 1,
+              "search grids");
+static_assert(sizeof(V4Row) == 8 && sizeof(K3Row) == 32 && sizeof(PackTables) % 16 == 0 &&
+                  sizeof(PackTables) / 4 <= 256,
+              "LDS table of whole dwords, rows aligned, one dword per thread of a block");
 __device__ constexpr PackTables kPackTables = thr::pack_tables();
 constexpr int kPackTableWords = sizeof(PackTables) / 4;
 
-// Nearest V4 index of a clamped x (the reference's first-minimum scan).
+// Nearest V4 index of x (the reference's first-minimum scan of x clamped to
+// +-2.75), for |x| <= 12 or NaN.
 __device__ __forceinline__ uint32_t v4_code(float x, const PackTables& T) {
-    const V4Row r = *reinterpret_cast<const V4Row*>(
-        reinterpret_cast<const char*>(T.v4) + T.v4_row[(int)__builtin_fmaf(x, 8.0f, kV4Off)]);
-    return r.code + (x >= r.t ? 1u : 0u);
+    const char* row =
+        reinterpret_cast<const char*>(T.v4) + T.v4_row[(int)__builtin_fmaf(x, 8.0f, kV4Off)];
+    const float t = *reinterpret_cast<const float*>(row);
+    return *reinterpret_cast<const uint32_t*>(row + 4) + (x >= t ? 1u : 0u);
 }
-// Nearest K3 index of a clamped x, and its level.
-__device__ __forceinline__ uint32_t k3_code(float x, const PackTables& T, float& level) {
-    const K3Row r = *reinterpret_cast<const K3Row*>(
-        reinterpret_cast<const char*>(T.k3) + T.k3_row[(int)__builtin_fmaf(x, 8.0f, kK3Off)]);
-    const bool up = x >= r.t;
-    level = up ? r.hi : r.lo;
-    return r.code + (up ? 1u : 0u);
+// turbo_prod K nibble (residual sign << 3 | nearest K3 index) of a clamped x,
+// and the level of its residual.
+__device__ __forceinline__ uint32_t k3_nibble(float x, const PackTables& T, float& level) {
+    const char* row =
+        reinterpret_cast<const char*>(T.k3) + T.k3_row[(int)__builtin_fmaf(x, 8.0f, kK3Off)];
+    const float4 blh = *reinterpret_cast<const float4*>(row);
+    const uint2 n = *reinterpret_cast<const uint2*>(row + 16);
+    const bool up = x >= blh.x;
+    level = up ? blh.z : blh.y;
+    return up ? n.y : n.x;
 }
 
 // For the fp16 pair w = (a low, b high): d = fp32(a) - fp32(b) and
