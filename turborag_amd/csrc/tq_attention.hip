@@ -269,9 +269,15 @@ __device__ __forceinline__ _Float16 hi_lo(float x, bool lo) {
 }  // namespace mfma
 
 // CH = tokens per wave iteration (32: two QK tiles, one PV step; 64: four and
-// two); NW = waves per workgroup; NP = row groups per workgroup (2: two new
-// tokens of one paged sequence share every decoded K/V chunk, each with its
-// own MFMA columns, softmax state and accumulators).
+// two); NW = waves per workgroup; NP = row groups per workgroup.
+// NP = 1: the 16 MFMA columns are the group's 8 query rows as fp16 hi and lo
+// parts (columns 2r, 2r + 1), summed after each product.
+// NP = 2 (paged rows): two new tokens of one sequence share every decoded K/V
+// chunk; the 16 columns are (position, row) = (i / 8, i % 8) and the hi and lo
+// parts are stacked along the reduction instead (QK: k-steps s and s + 4 take
+// the same decoded K against the hi and the lo query; PV: the hi and the lo P
+// against the same decoded V), so each lane's column is one query row and its
+// softmax runs once.
 template <bool PROD, int CH, int NW, bool PAGED, int NP = 1>
 __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     const uint16_t* __restrict__ query, const uint8_t* __restrict__ pool,
@@ -349,6 +355,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     // per position: this lane's column row length, the group's longest and
     // shortest row
     int rowlen[NP] = {}, gend[NP] = {}, gmin[NP] = {};
+    // NP = 2: this lane's column row length and the shortest live row
+    int rl_col = 0, gmin_live = 0x7fffffff;
     if constexpr (PAGED) {
         kv_end = 0;
 #pragma unroll
@@ -356,6 +364,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
             const int rr = (rg + p) * kRows + (lane & 7);
             const int lv = p < npos && rr < num_queries ? pr.row_kv_len[rr] : 0;
             rowlen[p] = __shfl(lv, i >> 1);
+            const int lc = __shfl(lv, i & 7);
+            if ((i >> 3) == p) rl_col = lc;
             int m = max(lv, __shfl_xor(lv, 1)), n = min(lv, __shfl_xor(lv, 1));
             m = max(m, __shfl_xor(m, 2));
             n = min(n, __shfl_xor(n, 2));
@@ -364,6 +374,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
             gend[p] = __builtin_amdgcn_readfirstlane(m);
             gmin[p] = __builtin_amdgcn_readfirstlane(n);
             kv_end = max(kv_end, gend[p]);
+            if (p < npos) gmin_live = min(gmin_live, gmin[p]);
         }
         seq = __builtin_amdgcn_readfirstlane(pr.row_seq[rg * kRows]);
         if (t_begin >= kv_end) return;  // uniform over the workgroup, before any barrier
@@ -496,12 +507,17 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     // B operand of QK, built once per workgroup: column i = row i/2, hi (i
     // even) or lo (i odd) part; k-index 8*gq + e of step s is d = 32*gq + 8*s + e.
     const bool lo_col = (i & 1) != 0;
-    for (int ps = w; ps < 4 * NP; ps += kWaves) {  // (position, k-step) of the B operand
+    for (int ps = w; ps < 4 * NP; ps += kWaves) {
         const int p = ps >> 2, s = ps & 3;
         half8 b;
+        if constexpr (NP == 2) {  // part p (0 hi, 1 lo) of column i's row, k-step s
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-            b[e] = hi_lo(qs[p * kRows + (i >> 1)][32 * gq + 8 * s + e], lo_col);
+            for (int e = 0; e < 8; ++e) b[e] = hi_lo(qs[i][32 * gq + 8 * s + e], p == 1);
+        } else {  // position p, k-step s; column parity picks hi or lo
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                b[e] = hi_lo(qs[p * kRows + (i >> 1)][32 * gq + 8 * s + e], lo_col);
+        }
         bqs[p][s][lane] = __builtin_bit_cast(uint4, b);
     }
     lds_barrier();
@@ -675,31 +691,171 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
             first = false;
         }
     };
-    if (NP == 2 && npos == 2)
-        chunk_loop(std::integral_constant<int, NP>{});
+    // NP = 2: one softmax state per lane (its column's row), hi and lo stacked
+    // along the reductions.  A unit with one position runs the same loop; the
+    // second position's columns compute on zero queries and are dropped.
+    float m_col = kInitMax, l_col = 0.0f;
+    f32x4 acc_col[8];
+#pragma unroll
+    for (int v = 0; v < 8; ++v) acc_col[v] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    auto stacked_loop = [&]() {
+        while (t0 < t_end) {  // wave-uniform
+            const uint4* kw = cur.kw;
+            const uint32_t(*vw)[8] = cur.vw;
+            {
+                const float ks = h2f(cur.ks), vs = h2f(cur.vs), re = PROD ? h2f(cur.re) : 0.0f;
+                tsc[w][lane & (kChunk - 1)] = cur.valid ? make_float4(ks * ck, ks * re * cr, vs, 0.0f)
+                                                        : make_float4(0.f, 0.f, 0.f, -INFINITY);
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            Chunk nxt;
+            const int t1 = t0 + kWaves * kChunk;
+            if (t1 < t_end) {  // codes of the next chunk, slots of the one after
+                fetch(t1, slot_nx, nxt);
+                slot_nx = load_slot(t1 + kWaves * kChunk);
+            }
+            // QK: each decoded A operand against the hi and the lo query
+            f32x4 cb[kTiles], cs[kTiles];
+#pragma unroll
+            for (int tau = 0; tau < kTiles; ++tau) {
+                cb[tau] = (f32x4){0.f, 0.f, 0.f, 0.f};
+                cs[tau] = cb[tau];
+                const uint32_t wd[4] = {kw[tau].x, kw[tau].y, kw[tau].z, kw[tau].w};
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const half8 a = as_h8(lookup(wd[s], 0, 0), lookup(wd[s], 1, 0),
+                                          lookup(wd[s], 2, 0), lookup(wd[s], 3, 0));
+                    cb[tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[0][s], cb[tau], 0, 0, 0);
+                    cb[tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[1][s], cb[tau], 0, 0, 0);
+                    if (PROD) {
+                        const uint32_t he = ((wd[s] << 4) & 0x80808080u) ^ 0xBCBCBCBCu;  // even d
+                        const uint32_t ho = (wd[s] & 0x80808080u) ^ 0xBCBCBCBCu;         // odd d
+                        const half8 sa = as_h8(__builtin_amdgcn_perm(ho, he, 0x040C000Cu),
+                                               __builtin_amdgcn_perm(ho, he, 0x050C010Cu),
+                                               __builtin_amdgcn_perm(ho, he, 0x060C020Cu),
+                                               __builtin_amdgcn_perm(ho, he, 0x070C030Cu));
+                        cs[tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sa, bq[0][s], cs[tau], 0, 0, 0);
+                        cs[tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sa, bq[1][s], cs[tau], 0, 0, 0);
+                    }
+                }
+            }
+            // Logits (base 2) of tokens 16*tau + 4*gq + e for this lane's column.
+            const bool masked = t0 + kChunk > gmin_live;
+            float lg[kTiles][4];
+            float mloc = -INFINITY;
+#pragma unroll
+            for (int tau = 0; tau < kTiles; ++tau)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float4 sc = tsc[w][16 * tau + 4 * gq + e];
+                    lg[tau][e] = fmaf(cb[tau][e], sc.x, fmaf(cs[tau][e], sc.y, sc.w));
+                    if (masked)
+                        if (t0 + 16 * tau + 4 * gq + e >= rl_col) lg[tau][e] = -INFINITY;
+                    mloc = fmaxf(mloc, lg[tau][e]);
+                }
+            mloc = fmaxf(mloc, lane_xor<16>(mloc));
+            mloc = fmaxf(mloc, lane_xor<32>(mloc));
+            const float m_new = fmaxf(m_col, mloc);
+            const float alpha = first ? 0.0f : __builtin_amdgcn_exp2f(m_col - m_new);
+            m_col = m_new;
+            float lsum = 0.0f;
+#pragma unroll
+            for (int tau = 0; tau < kTiles; ++tau)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    lg[tau][e] = __builtin_amdgcn_exp2f(lg[tau][e] - m_new);
+                    lsum += lg[tau][e];
+                }
+            l_col = l_col * alpha + lsum;
+            if (!first && __any(alpha != 1.0f)) {
+                // acc lane (d, gq) holds rows 4gq .. 4gq + 3 (columns of lanes 4gq + e)
+                float a[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) a[e] = __shfl(alpha, 4 * gq + e);
+#pragma unroll
+                for (int v = 0; v < 8; ++v)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc_col[v][e] *= a[e];
+            }
+            // PV: the hi and the lo P against each decoded B operand
+#pragma unroll
+            for (int st = 0; st < kSteps; ++st) {
+                half8 ah, al;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int tau = 2 * st + (e >> 2), ee = e & 3;
+                    const float x = lg[tau][ee] * tsc[w][16 * tau + 4 * gq + ee].z;
+                    ah[e] = hi_lo(x, false);
+                    al[e] = hi_lo(x, true);
+                }
+                uint32_t bv[8][4];  // [N-tile v = d - 8i][token pair]
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const uint32_t we = vw[st][2 * q], wo = vw[st][2 * q + 1];
+                    const uint32_t lob = (we & 0x0F0F0F0Fu) | ((wo & 0x0F0F0F0Fu) << 4);
+                    const uint32_t hib = ((we >> 4) & 0x0F0F0F0Fu) | (wo & 0xF0F0F0F0u);
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) {
+                        bv[2 * b][q] = lookup(lob, b, 1);
+                        bv[2 * b + 1][q] = lookup(hib, b, 1);
+                    }
+                }
+#pragma unroll
+                for (int v = 0; v < 8; ++v) {
+                    const half8 bvv = as_h8(bv[v][0], bv[v][1], bv[v][2], bv[v][3]);
+                    acc_col[v] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bvv, acc_col[v], 0, 0, 0);
+                    acc_col[v] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bvv, acc_col[v], 0, 0, 0);
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            cur = nxt;
+            t0 = t1;
+            first = false;
+        }
+    };
+    if constexpr (NP == 2)
+        stacked_loop();
     else
         chunk_loop(std::integral_constant<int, 1>{});
 
-    // Wave results: l summed over the g lanes of each column; o rows from the
-    // hi + lo columns, the V codebook scale divided out.
-#pragma unroll
-    for (int p = 0; p < NP; ++p) {
-        float l_tot = l_run[p] + lane_xor<16>(l_run[p]);
+    // Wave results: l summed over the g lanes of each column; o rows (NP = 1:
+    // from the hi + lo columns), the V codebook scale divided out.
+    if constexpr (NP == 2) {
+        float l_tot = l_col + lane_xor<16>(l_col);
         l_tot += lane_xor<32>(l_tot);
-        if (gq == 0 && !lo_col) {
-            mm[w][p * kRows + (i >> 1)] = m_run[p];
-            ml[w][p * kRows + (i >> 1)] = l_tot;
+        if (gq == 0) {
+            mm[w][i] = m_col;
+            ml[w][i] = l_tot;
+        }
+    } else {
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            float l_tot = l_run[p] + lane_xor<16>(l_run[p]);
+            l_tot += lane_xor<32>(l_tot);
+            if (gq == 0 && !lo_col) {
+                mm[w][p * kRows + (i >> 1)] = m_run[p];
+                ml[w][p * kRows + (i >> 1)] = l_tot;
+            }
         }
     }
     __syncthreads();  // every wave is done with the tables that mo overwrites
     const float iav = 1.0f / kAlphaV;
+    if constexpr (NP == 2) {
 #pragma unroll
-    for (int p = 0; p < NP; ++p)
+        for (int v = 0; v < 8; ++v)
 #pragma unroll
-        for (int v = 0; v < 8; ++v) {
-            mo[w][p * kRows + 2 * gq][8 * i + v] = (acc[p][v][0] + acc[p][v][1]) * iav;
-            mo[w][p * kRows + 2 * gq + 1][8 * i + v] = (acc[p][v][2] + acc[p][v][3]) * iav;
-        }
+            for (int e = 0; e < 4; ++e) mo[w][4 * gq + e][8 * i + v] = acc_col[v][e] * iav;
+    } else {
+#pragma unroll
+        for (int p = 0; p < NP; ++p)
+#pragma unroll
+            for (int v = 0; v < 8; ++v) {
+                mo[w][p * kRows + 2 * gq][8 * i + v] = (acc[p][v][0] + acc[p][v][1]) * iav;
+                mo[w][p * kRows + 2 * gq + 1][8 * i + v] = (acc[p][v][2] + acc[p][v][3]) * iav;
+            }
+    }
     __syncthreads();
 
     // Merge the waves; inverse WHT and sign flip; partial to the workspace.
