@@ -230,6 +230,10 @@ constexpr float kAlphaK = 1.2918981f;
 constexpr float kAlphaV = 1.5982153f;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kRows = 8;     // query rows per workgroup (16 MFMA columns, hi/lo)
+// Page schemes of the split kernel: turbo_mse, turbo_prod, and the
+// reference's unexported QJL-1b page (K = +-1 signs times one fp16 scale per
+// (token, head); src/cuda/tq_qjl_kernels.cu).
+constexpr int kSchMse = 0, kSchProd = 1, kSchQjl = 2;
 constexpr int kPartStride = 128 + 4;  // floats per partial row: o[128], m, l, pad (16-B rows)
 
 __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
@@ -278,7 +282,11 @@ __device__ __forceinline__ _Float16 hi_lo(float x, bool lo) {
 // the same decoded K against the hi and the lo query; PV: the hi and the lo P
 // against the same decoded V), so each lane's column is one query row and its
 // softmax runs once.
-template <bool PROD, int CH, int NW, bool PAGED, int NP = 1>
+// SCH = page scheme (kSch*).  QJL: the A operand of QK is the +-1 sign
+// matrix, read as fp16 octets from an LDS table indexed by sign byte; the
+// logit is ks * <qrot, signs> (no 1/sqrt(D) beyond the rotation's, :254);
+// the rotation's sign flip has no head term.
+template <int SCH, int CH, int NW, bool PAGED, int NP = 1>
 __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     const uint16_t* __restrict__ query, const uint8_t* __restrict__ pool,
     const int32_t* __restrict__ slots, float* __restrict__ ws, PageGeom g, int num_queries,
@@ -289,6 +297,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     static_assert(CH == 32 || CH == 64, "chunk of 32 or 64 tokens");
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
     static_assert(NP == 1 || (NP == 2 && PAGED), "two positions: paged rows only");
+    constexpr bool PROD = SCH == kSchProd, QJL = SCH == kSchQjl;
+    static_assert(!QJL || (!PAGED && NP == 1), "QJL: slot-mapped rows, one position");
     constexpr int kR = kRows * NP;  // query rows of the workgroup
     // Decode tables indexed by a code byte (low nibble = even d), fp16 pairs:
     // table 0 = K (prod: aK*K3, mse: aV*V4), table 1 = V (aV*V4), 32 copies
@@ -422,13 +432,21 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
         c.vs = ld_u16(pool + (c.valid ? so + g.vs_off : dummy_off + 2));
         c.re = PROD ? ld_u16(pool + (c.valid ? so + g.kres_off : dummy_off + 4)) : (uint16_t)0;
         // (with 32-token chunks lanes l and l + 32 hold the same token)
-        tko[w][lane & (kChunk - 1)] = c.valid ? pb + g.kc_off + cell * g.code_stride : dummy_off;
+        // K row: code_stride bytes, or QJL's D/8 = 16 sign bytes
+        const uint64_t kstride = QJL ? 16u : (uint64_t)g.code_stride;
+        tko[w][lane & (kChunk - 1)] = c.valid ? pb + g.kc_off + cell * kstride : dummy_off;
         tvo[w][lane & (kChunk - 1)] = c.valid ? pb + g.vc_off + cell * g.code_stride : dummy_off;
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-        for (int tau = 0; tau < kTiles; ++tau)
-            c.kw[tau] = *reinterpret_cast<const uint4*>(pool + (tko[w][16 * tau + i] + 16 * gq));
+        for (int tau = 0; tau < kTiles; ++tau) {
+            if constexpr (QJL)  // sign bytes 4gq .. 4gq + 3: k-steps 0 .. 3
+                c.kw[tau] = make_uint4(
+                    *reinterpret_cast<const uint32_t*>(pool + (tko[w][16 * tau + i] + 4 * gq)), 0u,
+                    0u, 0u);
+            else
+                c.kw[tau] = *reinterpret_cast<const uint4*>(pool + (tko[w][16 * tau + i] + 16 * gq));
+        }
         // k-step p covers tiles 2p, 2p+1; k-index 8gq + e is token
         // 32p + 4gq + e (e < 4) or 32p + 16 + 4gq + (e - 4).
 #pragma unroll
@@ -471,7 +489,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     // issued, so waiting for them never waits for the codes.
     float qf[kQPerWave][2];
     {
-        const float sh = (h & 1) ? -1.0f : 1.0f;
+        const float sh = (!QJL && (h & 1)) ? -1.0f : 1.0f;
 #pragma unroll
         for (int k = 0; k < kQPerWave; ++k) {
             qf[k][0] = h2f(qraw[k] & 0xffff) * sh;
@@ -500,8 +518,24 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
 #pragma unroll
         for (int k = 0; k < kRowsPerWave; k += 4) {
             const int e = w * kRowsPerWave + k + (lane >> 4);
-            const uint32_t v = (lane & 8) ? vstage[e] : kstage[e];  // words 32..63: V
-            *reinterpret_cast<uint4*>(&lut[e][4 * (lane & 15)]) = make_uint4(v, v, v, v);
+            if constexpr (QJL) {  // K half: 8 copies of the fp16 +-1 octet of sign byte e
+                uint4 v4;
+                if (lane & 8) {
+                    const uint32_t v = vstage[e];
+                    v4 = make_uint4(v, v, v, v);
+                } else {
+                    uint32_t wd[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        wd[q] = ((e >> (2 * q)) & 1 ? 0x3C00u : 0xBC00u) |
+                                ((e >> (2 * q + 1)) & 1 ? 0x3C000000u : 0xBC000000u);
+                    v4 = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+                }
+                *reinterpret_cast<uint4*>(&lut[e][4 * (lane & 15)]) = v4;
+            } else {
+                const uint32_t v = (lane & 8) ? vstage[e] : kstage[e];  // words 32..63: V
+                *reinterpret_cast<uint4*>(&lut[e][4 * (lane & 15)]) = make_uint4(v, v, v, v);
+            }
         }
     }
     // B operand of QK, built once per workgroup: column i = row i/2, hi (i
@@ -536,6 +570,15 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
         const uint32_t a = __builtin_amdgcn_perm(word, base, 0x03020000u | ((4u + b) << 8)) + lut_hi;
         return *reinterpret_cast<const lds_u32*>(a);
     };
+    // QJL: the fp16 +-1 octet of sign byte b of word (copy lane % 8).
+    const uint32_t lutq =
+        (uint32_t)reinterpret_cast<uintptr_t>((lds_u32*)&lut[0][4 * (lane & 7)]);
+    auto signs = [&](uint32_t word, int b) -> half8 {
+        const uint32_t a =
+            __builtin_amdgcn_perm(word, lutq, 0x03020000u | ((4u + b) << 8)) + (lutq & 0xFF00u);
+        typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+        return __builtin_bit_cast(half8, *reinterpret_cast<const lds_u32x4*>(a));
+    };
 
     float m_run[NP], l_run[NP];
     f32x4 acc[NP][8];
@@ -558,8 +601,9 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
             const uint32_t(*vw)[8] = cur.vw;
             {
                 const float ks = h2f(cur.ks), vs = h2f(cur.vs), re = PROD ? h2f(cur.re) : 0.0f;
-                tsc[w][lane & (kChunk - 1)] = cur.valid ? make_float4(ks * ck, ks * re * cr, vs, 0.0f)
-                                                        : make_float4(0.f, 0.f, 0.f, -INFINITY);
+                const float4 sc = QJL ? make_float4(0.0f, ks * kLog2e, vs, 0.0f)
+                                      : make_float4(ks * ck, ks * re * cr, vs, 0.0f);
+                tsc[w][lane & (kChunk - 1)] = cur.valid ? sc : make_float4(0.f, 0.f, 0.f, -INFINITY);
             }
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -582,6 +626,14 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                 const uint32_t wd[4] = {kw[tau].x, kw[tau].y, kw[tau].z, kw[tau].w};
     #pragma unroll
                 for (int s = 0; s < 4; ++s) {
+                    if constexpr (QJL) {  // sign byte s of the lane's word
+                        const half8 sa = signs(wd[0], s);
+    #pragma unroll
+                        for (int p = 0; p < NPA; ++p)
+                            cs[p][tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sa, bq[p][s],
+                                                                                cs[p][tau], 0, 0, 0);
+                        continue;
+                    }
                     const half8 a = as_h8(lookup(wd[s], 0, 0), lookup(wd[s], 1, 0),
                                           lookup(wd[s], 2, 0), lookup(wd[s], 3, 0));
     #pragma unroll
@@ -616,9 +668,15 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const float4 sc = tsc[w][16 * tau + 4 * gq + e];
-                        const float sb = cb[p][tau][e] + quad_xor<1>(cb[p][tau][e]);
-                        const float sr = PROD ? cs[p][tau][e] + quad_xor<1>(cs[p][tau][e]) : 0.0f;
-                        lg[p][tau][e] = fmaf(sb, sc.x, fmaf(sr, sc.y, sc.w));
+                        if constexpr (QJL) {
+                            const float sr = cs[p][tau][e] + quad_xor<1>(cs[p][tau][e]);
+                            lg[p][tau][e] = fmaf(sr, sc.y, sc.w);
+                        } else {
+                            const float sb = cb[p][tau][e] + quad_xor<1>(cb[p][tau][e]);
+                            const float sr =
+                                PROD ? cs[p][tau][e] + quad_xor<1>(cs[p][tau][e]) : 0.0f;
+                            lg[p][tau][e] = fmaf(sb, sc.x, fmaf(sr, sc.y, sc.w));
+                        }
                         if (masked)  // causal limit of this column's row
                             if (t0 + 16 * tau + 4 * gq + e >= rowlen[p]) lg[p][tau][e] = -INFINITY;
                         mloc = fmaxf(mloc, lg[p][tau][e]);
@@ -698,7 +756,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     f32x4 acc_col[8];
 #pragma unroll
     for (int v = 0; v < 8; ++v) acc_col[v] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    auto stacked_loop = [&]() {
+    if constexpr (NP == 2) {
         while (t0 < t_end) {  // wave-uniform
             const uint4* kw = cur.kw;
             const uint32_t(*vw)[8] = cur.vw;
@@ -814,11 +872,9 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
             t0 = t1;
             first = false;
         }
-    };
-    if constexpr (NP == 2)
-        stacked_loop();
-    else
+    } else {
         chunk_loop(std::integral_constant<int, 1>{});
+    }
 
     // Wave results: l summed over the g lanes of each column; o rows (NP = 1:
     // from the hi + lo columns), the V codebook scale divided out.
@@ -878,7 +934,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
             o1 += mo[u][r][2 * lane + 1] * wt;
         }
         wht_pair<64>(o0, o1, lane);
-        const float s0 = (h & 1) ? -inv : inv;
+        const float s0 = (!QJL && (h & 1)) ? -inv : inv;
         float* part = ws + ((pid + (size_t)num_splits * g.H * p) * kRows + r % kRows) * kPartStride;
         part[2 * lane] = o0 * s0;
         part[2 * lane + 1] = o1 * -s0;
@@ -1099,6 +1155,49 @@ bool mfma_attention_ok(const PageGeom& g, const void* pool) {
         default: throw Error("head_dim must be a power of two in [2, 128]");     \
     }
 
+namespace {
+// The MFMA split-K attention over slot-mapped tokens: split + combine launches.
+template <int SCH>
+void launch_mfma_attention(const uint16_t* query, const uint8_t* pool, const int32_t* slots,
+                           uint16_t* output, const PageGeom& g, int num_queries,
+                           int num_kv_tokens, float inv, hipStream_t stream, const char* split_name,
+                           const char* combine_name) {
+    using namespace mfma;
+    const int rows = num_queries * g.H;
+    const int row_groups = (num_queries + kRows - 1) / kRows;
+    const int heads = g.H * row_groups;
+    // One 256-token split per workgroup, or longer splits once there are
+    // more than ~2 workgroups per CU.
+    const int max_splits = std::max(1, (num_kv_tokens + kSplitMinTokens - 1) / kSplitMinTokens);
+    const int want = std::max(1, (kSplitBlocksPerCU * num_cus() + heads - 1) / heads);
+    int splits = std::min(std::min(max_splits, want), 1024);
+    const int tps = num_kv_tokens > 0 ? (num_kv_tokens + splits - 1) / splits : 0;
+    if (tps > 0) splits = (num_kv_tokens + tps - 1) / tps;
+    const size_t blocks = (size_t)splits * heads;
+    float* ws =
+        static_cast<float*>(workspace(stream, blocks * kRows * kPartStride * sizeof(float)));
+    constexpr int kCH = kSplitChunk, kNW = kSplitWaves;
+    const PagedRows none{};
+    if (num_kv_tokens == 0) {  // no partials: the combine writes the zero output
+        hipLaunchKernelGGL(attn_mfma_combine_kernel<false>, dim3(4 * rows), dim3(256), 0, stream,
+                           ws, output, g.H, 0, num_queries, 1, none);
+        check_launch(combine_name);
+        return;
+    }
+    hipLaunchKernelGGL((attn_mfma_split_kernel<SCH, kCH, kNW, false>), dim3(blocks),
+                       dim3(64 * kNW), 0, stream, query, pool, slots, ws, g, num_queries,
+                       num_kv_tokens, tps, splits, inv, none);
+    check_launch(split_name);
+    if (splits <= kItemCombineMaxSplits)
+        hipLaunchKernelGGL(attn_mfma_combine_items_kernel<false>, dim3(heads), dim3(256), 0,
+                           stream, ws, output, g.H, splits, num_queries, tps, none);
+    else
+        hipLaunchKernelGGL(attn_mfma_combine_kernel<false>, dim3(4 * rows), dim3(256), 0, stream,
+                           ws, output, g.H, splits, num_queries, tps, none);
+    check_launch(combine_name);
+}
+}  // namespace
+
 void launch_attention(Scheme s, const uint16_t* query, const uint8_t* pool, const int32_t* slots,
                       uint16_t* output, const PageGeom& g, int num_queries, int num_kv_tokens,
                       hipStream_t stream) {
@@ -1106,45 +1205,16 @@ void launch_attention(Scheme s, const uint16_t* query, const uint8_t* pool, cons
     if (rows <= 0) return;
     const float inv = inv_sqrt_d(g.D);
     if (mfma_attention_ok(g, pool)) {
-        using namespace mfma;
-        const int row_groups = (num_queries + kRows - 1) / kRows;
-        const int heads = g.H * row_groups;
-        // One 256-token split per workgroup, or longer splits once there are
-        // more than ~2 workgroups per CU.
-        const int max_splits =
-            std::max(1, (num_kv_tokens + kSplitMinTokens - 1) / kSplitMinTokens);
-        const int want = std::max(1, (kSplitBlocksPerCU * num_cus() + heads - 1) / heads);
-        int splits = std::min(std::min(max_splits, want), 1024);
-        const int tps = num_kv_tokens > 0 ? (num_kv_tokens + splits - 1) / splits : 0;
-        if (tps > 0) splits = (num_kv_tokens + tps - 1) / tps;
-        const size_t blocks = (size_t)splits * heads;
-        float* ws = static_cast<float*>(
-            workspace(stream, blocks * kRows * kPartStride * sizeof(float)));
-        const bool prod = s == Scheme::Prod;
-        constexpr int kCH = kSplitChunk, kNW = kSplitWaves;
-        const PagedRows none{};
-        if (num_kv_tokens == 0) {  // no partials: the combine writes the zero output
-            hipLaunchKernelGGL(attn_mfma_combine_kernel<false>, dim3(4 * rows), dim3(256), 0,
-                               stream, ws, output, g.H, 0, num_queries, 1, none);
-            check_launch(prod ? "turbo_prod_fused_attn_combine" : "turbo_mse_fused_attn_combine");
-            return;
-        }
-        if (prod)
-            hipLaunchKernelGGL((attn_mfma_split_kernel<true, kCH, kNW, false>), dim3(blocks),
-                               dim3(64 * kNW), 0, stream, query, pool, slots, ws, g, num_queries,
-                               num_kv_tokens, tps, splits, inv, none);
+        if (s == Scheme::Prod)
+            launch_mfma_attention<mfma::kSchProd>(query, pool, slots, output, g, num_queries,
+                                                  num_kv_tokens, inv, stream,
+                                                  "turbo_prod_fused_attn_split",
+                                                  "turbo_prod_fused_attn_combine");
         else
-            hipLaunchKernelGGL((attn_mfma_split_kernel<false, kCH, kNW, false>), dim3(blocks),
-                               dim3(64 * kNW), 0, stream, query, pool, slots, ws, g, num_queries,
-                               num_kv_tokens, tps, splits, inv, none);
-        check_launch(prod ? "turbo_prod_fused_attn_split" : "turbo_mse_fused_attn_split");
-        if (splits <= kItemCombineMaxSplits)
-            hipLaunchKernelGGL(attn_mfma_combine_items_kernel<false>, dim3(heads), dim3(256), 0,
-                               stream, ws, output, g.H, splits, num_queries, tps, none);
-        else
-            hipLaunchKernelGGL(attn_mfma_combine_kernel<false>, dim3(4 * rows), dim3(256), 0,
-                               stream, ws, output, g.H, splits, num_queries, tps, none);
-        check_launch(prod ? "turbo_prod_fused_attn_combine" : "turbo_mse_fused_attn_combine");
+            launch_mfma_attention<mfma::kSchMse>(query, pool, slots, output, g, num_queries,
+                                                 num_kv_tokens, inv, stream,
+                                                 "turbo_mse_fused_attn_split",
+                                                 "turbo_mse_fused_attn_combine");
         return;
     }
     // Enough waves to cover the chip several times, at least 32 tokens each.
@@ -1215,11 +1285,11 @@ void launch_paged_attention(Scheme s, const uint16_t* query, const uint8_t* pool
         check_launch(prod ? "turbo_prod_paged_attn_pairs" : "turbo_mse_paged_attn_pairs");
         // The grid covers every row group as a unit; units past the pair count exit.
         if (prod)
-            hipLaunchKernelGGL((attn_mfma_split_kernel<true, kCH, kNW, true, 2>), dim3(blocks),
+            hipLaunchKernelGGL((attn_mfma_split_kernel<kSchProd, kCH, kNW, true, 2>), dim3(blocks),
                                dim3(64 * kNW), 0, stream, query, pool, nullptr, ws, g, num_rows,
                                max_kv_len, tps, splits, inv, pr);
         else
-            hipLaunchKernelGGL((attn_mfma_split_kernel<false, kCH, kNW, true, 2>), dim3(blocks),
+            hipLaunchKernelGGL((attn_mfma_split_kernel<kSchMse, kCH, kNW, true, 2>), dim3(blocks),
                                dim3(64 * kNW), 0, stream, query, pool, nullptr, ws, g, num_rows,
                                max_kv_len, tps, splits, inv, pr);
         check_launch(prod ? "turbo_prod_paged_attn_split" : "turbo_mse_paged_attn_split");
@@ -1232,6 +1302,33 @@ void launch_paged_attention(Scheme s, const uint16_t* query, const uint8_t* pool
         hipLaunchKernelGGL(attn_mfma_combine_kernel<true>, dim3(4 * rows), dim3(256), 0, stream,
                            ws, output, g.H, max_kv_len > 0 ? splits : 0, num_rows, tps, pr);
     check_launch(prod ? "turbo_prod_paged_attn_combine" : "turbo_mse_paged_attn_combine");
+}
+
+bool launch_qjl_mfma_attention(const uint16_t* query, const uint8_t* pool, const int32_t* slots,
+                               uint16_t* output, const QjlGeom& q, int num_queries,
+                               int num_kv_tokens, hipStream_t stream) {
+    const auto al = [](uint64_t v, uint64_t a) { return (v & (a - 1)) == 0; };
+    if (!(q.D == 128 && q.k1_bytes == 16 && q.v4_bytes == 64 && al(q.page_size, 4) &&
+          al(q.k1_off, 4) && al(q.v4_off, 4) && al(q.ks_off, 2) && al(q.vs_off, 2) &&
+          al(reinterpret_cast<uintptr_t>(pool), 16)))
+        return false;
+    PageGeom g{};
+    g.page_size = q.page_size;
+    g.kc_off = q.k1_off;
+    g.vc_off = q.v4_off;
+    g.ks_off = q.ks_off;
+    g.vs_off = q.vs_off;
+    g.code_stride = q.v4_bytes;  // V rows; the K sign rows are D/8 = 16 bytes
+    g.scale_stride = 2;
+    g.H = q.H;
+    g.D = q.D;
+    g.block_size = q.block_size;
+    g.bs_shift = (q.block_size & (q.block_size - 1)) == 0 ? __builtin_ctz(q.block_size) : -1;
+    g.h_shift = (q.H & (q.H - 1)) == 0 ? __builtin_ctz(q.H) : -1;
+    launch_mfma_attention<mfma::kSchQjl>(query, pool, slots, output, g, num_queries,
+                                         num_kv_tokens, inv_sqrt_d(q.D), stream,
+                                         "qjl_fused_attn_split", "qjl_fused_attn_combine");
+    return true;
 }
 
 void launch_logits(const uint16_t* query, const uint8_t* pool, const int32_t* slots,

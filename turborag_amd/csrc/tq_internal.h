@@ -123,6 +123,11 @@ void launch_qjl_dequant(const uint8_t* pool, const int32_t* slots, uint16_t* out
 void launch_qjl_attention(const uint16_t* query, const uint8_t* pool, const int32_t* slots,
                           uint16_t* output, const QjlGeom& g, int num_queries, int num_kv_tokens,
                           hipStream_t stream);
+// The MFMA split-K form of launch_qjl_attention (D = 128, 4-byte aligned
+// fields, 16-byte aligned pool); false (nothing launched) when not eligible.
+bool launch_qjl_mfma_attention(const uint16_t* query, const uint8_t* pool, const int32_t* slots,
+                               uint16_t* output, const QjlGeom& g, int num_queries,
+                               int num_kv_tokens, hipStream_t stream);
 void launch_int4_pack(const uint16_t* key, const uint16_t* value, const int32_t* slots,
                       uint8_t* pool, const Int4Geom& g, int num_tokens, hipStream_t stream);
 void launch_int4_dequant(const uint8_t* pool, const int32_t* slots, uint16_t* out_key,

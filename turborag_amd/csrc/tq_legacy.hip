@@ -432,6 +432,9 @@ void launch_qjl_attention(const uint16_t* query, const uint8_t* pool, const int3
                           hipStream_t stream) {
     const int rows = num_queries * g.H;
     if (rows <= 0) return;
+    if (launch_qjl_mfma_attention(query, pool, slots, output, g, num_queries, num_kv_tokens,
+                                  stream))
+        return;
     const float inv = inv_sqrt_d(g.D);
     // Enough waves to cover the chip several times, at least 32 tokens each.
     int splits = (2048 + rows - 1) / rows;
