@@ -146,11 +146,11 @@ def test_compiled_tables_match(oracle, tmp_path):
         '  for (int i = 1; i < 8; ++i) printf("%a\\n", a.t[i]);\n'
         '  for (int i = 1; i < 16; ++i) printf("%a\\n", b.t[i]);\n'
         '  for (int g = 0; g < kV4Cells; ++g) printf("%d\\n", p.v4_row[g] / 8);\n'
-        '  for (int g = 0; g < kK3Cells; ++g) printf("%d\\n", p.k3_row[g] / 32);\n'
+        '  for (int g = 0; g < kK3Cells; ++g) printf("%d\\n", p.k3_row[g] / 8);\n'
         '  for (int l = 0; l < 16; ++l) printf("%a %u\\n", p.v4[l].t, p.v4[l].code);\n'
         "  for (int m = 0; m < 16; ++m)\n"
-        '    printf("%a %a %a %u %u\\n", p.k3[m].b, p.k3[m].lo, p.k3[m].hi, p.k3[m].nlo,'
-        " p.k3[m].nhi);\n"
+        '    printf("%a %a %a %u %u\\n", p.k3a[m].b, p.k3a[m].lo, p.k3b[m].hi, p.k3b[m].nlo,'
+        " p.k3c[m].nhi);\n"
         "}\n")
     exe = tmp_path / "thr"
     r = subprocess.run([hipcc, "-std=c++17", "-O1", "--offload-arch=gfx950",

@@ -308,16 +308,26 @@ struct V4Row {
     float t;  // next threshold (+inf past the last)
     uint32_t code;
 };
-struct alignas(16) K3Row {
-    float b, lo, hi, pad0;  // next breakpoint (+inf past the last); levels of states m, m + 1
-    uint32_t nlo, nhi;      // nibbles of states m, m + 1
-    uint32_t pad1, pad2;
+// K3 state m as three 8-byte rows, one array each (16 rows x 8 B = 128 B:
+// every row of an array in its own pair of LDS banks, so random lookups by
+// the lanes of a wave do not conflict).
+struct K3RowA {
+    float b, lo;  // next breakpoint (+inf past the last); level of state m
+};
+struct K3RowB {
+    float hi;      // level of state m + 1
+    uint32_t nlo;  // nibble of state m
+};
+struct K3RowC {
+    uint32_t nhi, pad;  // nibble of state m + 1
 };
 struct alignas(16) PackTables {
-    uint8_t v4_row[208];   // [g] = byte offset of V4Row first[g], g < kV4Cells
-    uint16_t k3_row[48];   // [g] = byte offset of K3Row first[g], g < kK3Cells
+    uint8_t v4_row[208];  // [g] = 8 * first[g] (byte offset of the V4 row), g < kV4Cells
+    uint8_t k3_row[48];   // [g] = 8 * first[g] (byte offset in each K3 array), g < kK3Cells
     V4Row v4[16];
-    K3Row k3[16];
+    K3RowA k3a[16];
+    K3RowB k3b[16];
+    K3RowC k3c[16];
 };
 namespace thr {
 constexpr int cell(float x, float off) { return (int)(x * 8.0f + off); }
@@ -356,12 +366,14 @@ constexpr PackTables pack_tables() {
     for (int g = 0; g < kV4Cells; ++g)
         p.v4_row[g] = (uint8_t)(sizeof(V4Row) * first_in_cell(v4p, kV4Off, g));
     for (int g = 0; g < kK3Cells; ++g)
-        p.k3_row[g] = (uint16_t)(sizeof(K3Row) * first_in_cell(k3p, kK3Off, g));
+        p.k3_row[g] = (uint8_t)(8 * first_in_cell(k3p, kK3Off, g));
     for (int l = 0; l < 16; ++l) p.v4[l] = {l < 15 ? v4p.b[l + 1] : __builtin_huge_valf(), (uint32_t)l};
-    for (int m = 0; m < 16; ++m)
-        p.k3[m] = {m < 15 ? k3p.b[m + 1] : __builtin_huge_valf(), kK3[m >> 1],
-                   kK3[(m < 15 ? m + 1 : m) >> 1], 0.0f, k3_nibble(m),
-                   k3_nibble(m < 15 ? m + 1 : m), 0u, 0u};
+    for (int m = 0; m < 16; ++m) {
+        const int m1 = m < 15 ? m + 1 : m;
+        p.k3a[m] = {m < 15 ? k3p.b[m + 1] : __builtin_huge_valf(), kK3[m >> 1]};
+        p.k3b[m] = {kK3[m1 >> 1], k3_nibble(m)};
+        p.k3c[m] = {k3_nibble(m1), 0u};
+    }
     return p;
 }
 constexpr bool sorted(const Points<15>& P) {
@@ -376,7 +388,8 @@ static_assert(thr::sorted(thr::v4_points()) && thr::sorted(thr::k3_points()) &&
                   thr::cell(-2.5f, kK3Off) == 0 && thr::cell(2.5f, kK3Off) == kK3Cells - 1 &&
                   thr::cell(-12.0f, kV4Off) == 0 && thr::cell(12.0f, kV4Off) == kV4Cells - 1,
               "search grids");
-static_assert(sizeof(V4Row) == 8 && sizeof(K3Row) == 32 && sizeof(PackTables) % 16 == 0 &&
+static_assert(sizeof(V4Row) == 8 && sizeof(K3RowA) == 8 && sizeof(K3RowB) == 8 &&
+                  sizeof(K3RowC) == 8 && sizeof(PackTables) % 16 == 0 &&
                   sizeof(PackTables) / 4 <= 256,
               "LDS table of whole dwords, rows aligned, one dword per thread of a block");
 __device__ constexpr PackTables kPackTables = thr::pack_tables();
@@ -393,13 +406,13 @@ __device__ __forceinline__ uint32_t v4_code(float x, const PackTables& T) {
 // turbo_prod K nibble (residual sign << 3 | nearest K3 index) of a clamped x,
 // and the level of its residual.
 __device__ __forceinline__ uint32_t k3_nibble(float x, const PackTables& T, float& level) {
-    const char* row =
-        reinterpret_cast<const char*>(T.k3) + T.k3_row[(int)__builtin_fmaf(x, 8.0f, kK3Off)];
-    const float4 blh = *reinterpret_cast<const float4*>(row);
-    const uint2 n = *reinterpret_cast<const uint2*>(row + 16);
-    const bool up = x >= blh.x;
-    level = up ? blh.z : blh.y;
-    return up ? n.y : n.x;
+    const uint32_t off = T.k3_row[(int)__builtin_fmaf(x, 8.0f, kK3Off)];
+    const K3RowA a = *reinterpret_cast<const K3RowA*>(reinterpret_cast<const char*>(T.k3a) + off);
+    const K3RowB b = *reinterpret_cast<const K3RowB*>(reinterpret_cast<const char*>(T.k3b) + off);
+    const uint32_t nhi = reinterpret_cast<const K3RowC*>(reinterpret_cast<const char*>(T.k3c) + off)->nhi;
+    const bool up = x >= a.b;
+    level = up ? b.hi : a.lo;
+    return up ? nhi : b.nlo;
 }
 
 // For the fp16 pair w = (a low, b high): d = fp32(a) - fp32(b) and
