@@ -251,8 +251,8 @@ struct PagedRows {
     const int32_t* row_seq;
     const int32_t* row_kv_len;
     int max_blocks;
-    // Two-position form: pair k covers row groups pair_first[k] and, when
-    // pair_count[k] == 2, the next group of the same sequence.
+    // Multi-position form: unit k covers the pair_count[k] row groups from
+    // pair_first[k] on, all of one sequence (num_pairs[0] units).
     const int32_t* pair_first;
     const int32_t* pair_count;
     const int32_t* num_pairs;
@@ -296,10 +296,13 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     constexpr int kTiles = CH / 16, kSteps = CH / 32;
     static_assert(CH == 32 || CH == 64, "chunk of 32 or 64 tokens");
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
-    static_assert(NP == 1 || (NP == 2 && PAGED), "two positions: paged rows only");
+    static_assert(NP == 1 || ((NP == 2 || NP == 4) && PAGED), "2 or 4 positions: paged rows");
     constexpr bool PROD = SCH == kSchProd, QJL = SCH == kSchQjl;
     static_assert(!QJL || (!PAGED && NP == 1), "QJL: slot-mapped rows, one position");
     constexpr int kR = kRows * NP;  // query rows of the workgroup
+    // NP >= 2: NT tiles of 16 MFMA columns, (position 2t + i / 8, row i % 8)
+    constexpr int NT = NP >= 2 ? NP / 2 : 1;
+    constexpr int kMoRows = NP >= 2 ? 16 : kR;  // rows merged per pass (one tile)
     // Decode tables indexed by a code byte (low nibble = even d), fp16 pairs:
     // table 0 = K (prod: aK*K3, mse: aV*V4), table 1 = V (aV*V4), 32 copies
     // each.  Entry e of table t, copy c is word e*64 + 32t + c and lane l
@@ -313,8 +316,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     __shared__ float4 tsc[kWaves][kChunk];  // per token: K scale a, residual scale b, vs, bias
     __shared__ float mm[kWaves][kR], ml[kWaves][kR];
     __shared__ uint32_t kstage[256], vstage[256];
-    static_assert(sizeof(float) * kWaves * kR * 128 <= sizeof(lut), "merge space");
-    float(*mo)[kR][128] = reinterpret_cast<float(*)[kR][128]>(&lut[0][0]);
+    static_assert(sizeof(float) * kWaves * kMoRows * 128 <= sizeof(lut), "merge space");
+    float(*mo)[kMoRows][128] = reinterpret_cast<float(*)[kMoRows][128]>(&lut[0][0]);
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
@@ -333,7 +336,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
         constexpr int kRun = 8;
         // work units: row groups, or pairs of them (NP = 2; the grid is sized
         // for one unit per group, the items past the pair count exit)
-        const int units = NP == 2 ? __builtin_amdgcn_readfirstlane(pr.num_pairs[0])
+        const int units = NP >= 2 ? __builtin_amdgcn_readfirstlane(pr.num_pairs[0])
                                   : (num_queries + kRows - 1) / kRows;
         const int items = num_splits * g.H * units;
         const int x = blockIdx.x & 7, li = blockIdx.x >> 3;
@@ -342,7 +345,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
         const int unit = v % units;
         h = (v / units) % g.H;
         split = v / (units * g.H);
-        if constexpr (NP == 2) {
+        if constexpr (NP >= 2) {
             rg = __builtin_amdgcn_readfirstlane(pr.pair_first[unit]);
             npos = __builtin_amdgcn_readfirstlane(pr.pair_count[unit]);
         } else {
@@ -365,8 +368,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     // per position: this lane's column row length, the group's longest and
     // shortest row
     int rowlen[NP] = {}, gend[NP] = {}, gmin[NP] = {};
-    // NP = 2: this lane's column row length and the shortest live row
-    int rl_col = 0, gmin_live = 0x7fffffff;
+    // NP >= 2: this lane's column row length per tile and the shortest live row
+    int rl_col[NT] = {}, gmin_live = 0x7fffffff;
     if constexpr (PAGED) {
         kv_end = 0;
 #pragma unroll
@@ -375,7 +378,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
             const int lv = p < npos && rr < num_queries ? pr.row_kv_len[rr] : 0;
             rowlen[p] = __shfl(lv, i >> 1);
             const int lc = __shfl(lv, i & 7);
-            if ((i >> 3) == p) rl_col = lc;
+            if (NP >= 2 && (i >> 3) == (p & 1)) rl_col[p >> 1] = lc;
             int m = max(lv, __shfl_xor(lv, 1)), n = min(lv, __shfl_xor(lv, 1));
             m = max(m, __shfl_xor(m, 2));
             n = min(n, __shfl_xor(n, 2));
@@ -390,6 +393,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
         if (t_begin >= kv_end) return;  // uniform over the workgroup, before any barrier
     }
     const int t_end = min(kv_end, t_begin + tokens_per_split);
+    const int ntile = (npos + 1) >> 1;  // NP >= 2: tiles of 16 columns in use
 
     // A chunk's codes and per-token scales, loaded ahead of its compute.
     struct Chunk {
@@ -504,6 +508,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
 #pragma unroll
     for (int k = 0; k < kQPerWave; ++k) {
         const int r = w + k * kWaves;
+        if (NP >= 2 && r / kRows >= 2 * ntile) continue;  // an unused tile (wave-uniform)
         float q0 = qf[k][0], q1 = qf[k][1];
         wht_pair<64>(q0, q1, lane);
         const bool live = r / kRows < npos && rg * kRows + r < num_queries;
@@ -543,10 +548,12 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     const bool lo_col = (i & 1) != 0;
     for (int ps = w; ps < 4 * NP; ps += kWaves) {
         const int p = ps >> 2, s = ps & 3;
+        if (NP >= 2 && (p >> 1) >= ntile) break;  // unused tiles (never read)
         half8 b;
-        if constexpr (NP == 2) {  // part p (0 hi, 1 lo) of column i's row, k-step s
+        if constexpr (NP >= 2) {  // tile p / 2, part p % 2 (hi, lo) of column i's row, k-step s
 #pragma unroll
-            for (int e = 0; e < 8; ++e) b[e] = hi_lo(qs[i][32 * gq + 8 * s + e], p == 1);
+            for (int e = 0; e < 8; ++e)
+                b[e] = hi_lo(qs[16 * (p >> 1) + i][32 * gq + 8 * s + e], (p & 1) != 0);
         } else {  // position p, k-step s; column parity picks hi or lo
 #pragma unroll
             for (int e = 0; e < 8; ++e)
@@ -749,14 +756,21 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
             first = false;
         }
     };
-    // NP = 2: one softmax state per lane (its column's row), hi and lo stacked
-    // along the reductions.  A unit with one position runs the same loop; the
-    // second position's columns compute on zero queries and are dropped.
-    float m_col = kInitMax, l_col = 0.0f;
-    f32x4 acc_col[8];
+    // NP >= 2: one softmax state per lane and tile (its column's row), hi and
+    // lo stacked along the reductions.  A unit with fewer positions runs the
+    // loop over the tiles it needs; a tile's unused columns compute on zero
+    // queries and are dropped.
+    float m_col[NT], l_col[NT];
+    f32x4 acc_col[NT][8];
 #pragma unroll
-    for (int v = 0; v < 8; ++v) acc_col[v] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    if constexpr (NP == 2) {
+    for (int t = 0; t < NT; ++t) {
+        m_col[t] = kInitMax;
+        l_col[t] = 0.0f;
+#pragma unroll
+        for (int v = 0; v < 8; ++v) acc_col[t][v] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    }
+    auto stacked_loop = [&](auto nta) {
+        constexpr int NTA = decltype(nta)::value;
         while (t0 < t_end) {  // wave-uniform
             const uint4* kw = cur.kw;
             const uint32_t(*vw)[8] = cur.vw;
@@ -773,19 +787,27 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                 fetch(t1, slot_nx, nxt);
                 slot_nx = load_slot(t1 + kWaves * kChunk);
             }
-            // QK: each decoded A operand against the hi and the lo query
-            f32x4 cb[kTiles], cs[kTiles];
+            // QK: each decoded A operand against every tile's hi and lo query
+            f32x4 cb[NTA][kTiles], cs[NTA][kTiles];
 #pragma unroll
             for (int tau = 0; tau < kTiles; ++tau) {
-                cb[tau] = (f32x4){0.f, 0.f, 0.f, 0.f};
-                cs[tau] = cb[tau];
+#pragma unroll
+                for (int t = 0; t < NTA; ++t) {
+                    cb[t][tau] = (f32x4){0.f, 0.f, 0.f, 0.f};
+                    cs[t][tau] = cb[t][tau];
+                }
                 const uint32_t wd[4] = {kw[tau].x, kw[tau].y, kw[tau].z, kw[tau].w};
 #pragma unroll
                 for (int s = 0; s < 4; ++s) {
                     const half8 a = as_h8(lookup(wd[s], 0, 0), lookup(wd[s], 1, 0),
                                           lookup(wd[s], 2, 0), lookup(wd[s], 3, 0));
-                    cb[tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[0][s], cb[tau], 0, 0, 0);
-                    cb[tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[1][s], cb[tau], 0, 0, 0);
+#pragma unroll
+                    for (int t = 0; t < NTA; ++t) {
+                        cb[t][tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[2 * t][s],
+                                                                            cb[t][tau], 0, 0, 0);
+                        cb[t][tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[2 * t + 1][s],
+                                                                            cb[t][tau], 0, 0, 0);
+                    }
                     if (PROD) {
                         const uint32_t he = ((wd[s] << 4) & 0x80808080u) ^ 0xBCBCBCBCu;  // even d
                         const uint32_t ho = (wd[s] & 0x80808080u) ^ 0xBCBCBCBCu;         // odd d
@@ -793,60 +815,70 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                                                __builtin_amdgcn_perm(ho, he, 0x050C010Cu),
                                                __builtin_amdgcn_perm(ho, he, 0x060C020Cu),
                                                __builtin_amdgcn_perm(ho, he, 0x070C030Cu));
-                        cs[tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sa, bq[0][s], cs[tau], 0, 0, 0);
-                        cs[tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sa, bq[1][s], cs[tau], 0, 0, 0);
+#pragma unroll
+                        for (int t = 0; t < NTA; ++t) {
+                            cs[t][tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                sa, bq[2 * t][s], cs[t][tau], 0, 0, 0);
+                            cs[t][tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                sa, bq[2 * t + 1][s], cs[t][tau], 0, 0, 0);
+                        }
                     }
                 }
             }
-            // Logits (base 2) of tokens 16*tau + 4*gq + e for this lane's column.
             const bool masked = t0 + kChunk > gmin_live;
-            float lg[kTiles][4];
-            float mloc = -INFINITY;
+            float lg[NTA][kTiles][4];
 #pragma unroll
-            for (int tau = 0; tau < kTiles; ++tau)
+            for (int t = 0; t < NTA; ++t) {
+                // Logits (base 2) of tokens 16*tau + 4*gq + e for this lane's column.
+                float mloc = -INFINITY;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float4 sc = tsc[w][16 * tau + 4 * gq + e];
-                    lg[tau][e] = fmaf(cb[tau][e], sc.x, fmaf(cs[tau][e], sc.y, sc.w));
-                    if (masked)
-                        if (t0 + 16 * tau + 4 * gq + e >= rl_col) lg[tau][e] = -INFINITY;
-                    mloc = fmaxf(mloc, lg[tau][e]);
+                for (int tau = 0; tau < kTiles; ++tau)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float4 sc = tsc[w][16 * tau + 4 * gq + e];
+                        lg[t][tau][e] = fmaf(cb[t][tau][e], sc.x, fmaf(cs[t][tau][e], sc.y, sc.w));
+                        if (masked)
+                            if (t0 + 16 * tau + 4 * gq + e >= rl_col[t]) lg[t][tau][e] = -INFINITY;
+                        mloc = fmaxf(mloc, lg[t][tau][e]);
+                    }
+                mloc = fmaxf(mloc, lane_xor<16>(mloc));
+                mloc = fmaxf(mloc, lane_xor<32>(mloc));
+                const float m_new = fmaxf(m_col[t], mloc);
+                const float alpha = first ? 0.0f : __builtin_amdgcn_exp2f(m_col[t] - m_new);
+                m_col[t] = m_new;
+                float lsum = 0.0f;
+#pragma unroll
+                for (int tau = 0; tau < kTiles; ++tau)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        lg[t][tau][e] = __builtin_amdgcn_exp2f(lg[t][tau][e] - m_new);
+                        lsum += lg[t][tau][e];
+                    }
+                l_col[t] = l_col[t] * alpha + lsum;
+                if (!first && __any(alpha != 1.0f)) {
+                    // acc lane (d, gq) holds rows 4gq .. 4gq + 3 (columns of lanes 4gq + e)
+                    float a[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) a[e] = __shfl(alpha, 4 * gq + e);
+#pragma unroll
+                    for (int v = 0; v < 8; ++v)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) acc_col[t][v][e] *= a[e];
                 }
-            mloc = fmaxf(mloc, lane_xor<16>(mloc));
-            mloc = fmaxf(mloc, lane_xor<32>(mloc));
-            const float m_new = fmaxf(m_col, mloc);
-            const float alpha = first ? 0.0f : __builtin_amdgcn_exp2f(m_col - m_new);
-            m_col = m_new;
-            float lsum = 0.0f;
-#pragma unroll
-            for (int tau = 0; tau < kTiles; ++tau)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    lg[tau][e] = __builtin_amdgcn_exp2f(lg[tau][e] - m_new);
-                    lsum += lg[tau][e];
-                }
-            l_col = l_col * alpha + lsum;
-            if (!first && __any(alpha != 1.0f)) {
-                // acc lane (d, gq) holds rows 4gq .. 4gq + 3 (columns of lanes 4gq + e)
-                float a[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) a[e] = __shfl(alpha, 4 * gq + e);
-#pragma unroll
-                for (int v = 0; v < 8; ++v)
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) acc_col[v][e] *= a[e];
             }
-            // PV: the hi and the lo P against each decoded B operand
+            // PV: every tile's hi and lo P against each decoded B operand
 #pragma unroll
             for (int st = 0; st < kSteps; ++st) {
-                half8 ah, al;
+                half8 ah[NTA], al[NTA];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const int tau = 2 * st + (e >> 2), ee = e & 3;
-                    const float x = lg[tau][ee] * tsc[w][16 * tau + 4 * gq + ee].z;
-                    ah[e] = hi_lo(x, false);
-                    al[e] = hi_lo(x, true);
-                }
+                for (int t = 0; t < NTA; ++t)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const int tau = 2 * st + (e >> 2), ee = e & 3;
+                        const float x = lg[t][tau][ee] * tsc[w][16 * tau + 4 * gq + ee].z;
+                        ah[t][e] = hi_lo(x, false);
+                        al[t][e] = hi_lo(x, true);
+                    }
                 uint32_t bv[8][4];  // [N-tile v = d - 8i][token pair]
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
@@ -862,8 +894,13 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
 #pragma unroll
                 for (int v = 0; v < 8; ++v) {
                     const half8 bvv = as_h8(bv[v][0], bv[v][1], bv[v][2], bv[v][3]);
-                    acc_col[v] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bvv, acc_col[v], 0, 0, 0);
-                    acc_col[v] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bvv, acc_col[v], 0, 0, 0);
+#pragma unroll
+                    for (int t = 0; t < NTA; ++t) {
+                        acc_col[t][v] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[t], bvv,
+                                                                               acc_col[t][v], 0, 0, 0);
+                        acc_col[t][v] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[t], bvv,
+                                                                               acc_col[t][v], 0, 0, 0);
+                    }
                 }
             }
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -872,18 +909,32 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
             t0 = t1;
             first = false;
         }
+    };
+    if constexpr (NP >= 2) {
+        if (NT == 2 && ntile == 2)
+            stacked_loop(std::integral_constant<int, NT>{});
+        else
+            stacked_loop(std::integral_constant<int, 1>{});
     } else {
         chunk_loop(std::integral_constant<int, 1>{});
     }
 
     // Wave results: l summed over the g lanes of each column; o rows (NP = 1:
-    // from the hi + lo columns), the V codebook scale divided out.
-    if constexpr (NP == 2) {
-        float l_tot = l_col + lane_xor<16>(l_col);
-        l_tot += lane_xor<32>(l_tot);
-        if (gq == 0) {
-            mm[w][i] = m_col;
-            ml[w][i] = l_tot;
+    // from the hi + lo columns), the V codebook scale divided out.  Then the
+    // waves are merged per row, the inverse WHT and sign flip applied, and the
+    // partial written to the workspace (NP >= 2: one tile of 16 rows per pass
+    // through the merge space).  A position whose rows all end before this
+    // split has no partial (its combine reads only the splits below its
+    // longest row).
+    if constexpr (NP >= 2) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            float l_tot = l_col[t] + lane_xor<16>(l_col[t]);
+            l_tot += lane_xor<32>(l_tot);
+            if (gq == 0) {
+                mm[w][16 * t + i] = m_col[t];
+                ml[w][16 * t + i] = l_tot;
+            }
         }
     } else {
 #pragma unroll
@@ -896,51 +947,53 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
             }
         }
     }
-    __syncthreads();  // every wave is done with the tables that mo overwrites
     const float iav = 1.0f / kAlphaV;
-    if constexpr (NP == 2) {
+    const float s0 = (!QJL && (h & 1)) ? -inv : inv;
 #pragma unroll
-        for (int v = 0; v < 8; ++v)
+    for (int t = 0; t < NT; ++t) {
+        if (NP >= 2 && t >= ntile) break;  // wave- and workgroup-uniform
+        __syncthreads();  // every wave is done with the tables (or the last pass) mo overwrites
+        if constexpr (NP >= 2) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) mo[w][4 * gq + e][8 * i + v] = acc_col[v][e] * iav;
-    } else {
+            for (int v = 0; v < 8; ++v)
 #pragma unroll
-        for (int p = 0; p < NP; ++p)
+                for (int e = 0; e < 4; ++e) mo[w][4 * gq + e][8 * i + v] = acc_col[t][v][e] * iav;
+        } else {
 #pragma unroll
-            for (int v = 0; v < 8; ++v) {
-                mo[w][p * kRows + 2 * gq][8 * i + v] = (acc[p][v][0] + acc[p][v][1]) * iav;
-                mo[w][p * kRows + 2 * gq + 1][8 * i + v] = (acc[p][v][2] + acc[p][v][3]) * iav;
-            }
-    }
-    __syncthreads();
-
-    // Merge the waves; inverse WHT and sign flip; partial to the workspace.
-    // A group whose rows all end before this split has no partial (its
-    // combine reads only the splits below its longest row).
-    for (int r = w; r < kR; r += kWaves) {
-        const int p = r / kRows;
-        bool keep = p < npos;
-        if constexpr (PAGED) keep = keep && t_begin < gend[p];
-        if (!keep) continue;  // wave-uniform
-        float M = mm[0][r];
+            for (int p = 0; p < NP; ++p)
 #pragma unroll
-        for (int u = 1; u < kWaves; ++u) M = fmaxf(M, mm[u][r]);
-        float L = 0.f, o0 = 0.f, o1 = 0.f;
-#pragma unroll
-        for (int u = 0; u < kWaves; ++u) {
-            const float wt = exp2f(mm[u][r] - M);
-            L += ml[u][r] * wt;
-            o0 += mo[u][r][2 * lane] * wt;
-            o1 += mo[u][r][2 * lane + 1] * wt;
+                for (int v = 0; v < 8; ++v) {
+                    mo[w][p * kRows + 2 * gq][8 * i + v] = (acc[p][v][0] + acc[p][v][1]) * iav;
+                    mo[w][p * kRows + 2 * gq + 1][8 * i + v] = (acc[p][v][2] + acc[p][v][3]) * iav;
+                }
         }
-        wht_pair<64>(o0, o1, lane);
-        const float s0 = (!QJL && (h & 1)) ? -inv : inv;
-        float* part = ws + ((pid + (size_t)num_splits * g.H * p) * kRows + r % kRows) * kPartStride;
-        part[2 * lane] = o0 * s0;
-        part[2 * lane + 1] = o1 * -s0;
-        if (lane == 0) {
-            part[128] = M;
-            part[129] = L;
+        __syncthreads();
+        for (int rr = w; rr < kMoRows; rr += kWaves) {
+            const int r = kMoRows * t + rr;  // row of the workgroup
+            const int p = r / kRows;
+            bool keep = p < npos;
+            if constexpr (PAGED) keep = keep && t_begin < gend[p];
+            if (!keep) continue;  // wave-uniform
+            float M = mm[0][r];
+#pragma unroll
+            for (int u = 1; u < kWaves; ++u) M = fmaxf(M, mm[u][r]);
+            float L = 0.f, o0 = 0.f, o1 = 0.f;
+#pragma unroll
+            for (int u = 0; u < kWaves; ++u) {
+                const float wt = exp2f(mm[u][r] - M);
+                L += ml[u][r] * wt;
+                o0 += mo[u][rr][2 * lane] * wt;
+                o1 += mo[u][rr][2 * lane + 1] * wt;
+            }
+            wht_pair<64>(o0, o1, lane);
+            float* part =
+                ws + ((pid + (size_t)num_splits * g.H * p) * kRows + r % kRows) * kPartStride;
+            part[2 * lane] = o0 * s0;
+            part[2 * lane + 1] = o1 * -s0;
+            if (lane == 0) {
+                part[128] = M;
+                part[129] = L;
+            }
         }
     }
 }
@@ -1083,16 +1136,18 @@ __global__ __launch_bounds__(256) void attn_mfma_combine_items_kernel(
         make_uint2(fin(acc.x) | (fin(acc.y) << 16), fin(acc.z) | (fin(acc.w) << 16));
 }
 
-// Pairs of row groups for the two-position paged kernel, from row_seq (rows
-// in aligned groups of 8 share a sequence): each run of consecutive groups of
-// one sequence is cut into pairs from its start, the last one single when the
-// run is odd.  One wave walks the groups 64 at a time: a group starts a run
-// when its sequence differs from the previous group's, and starts a pair when
-// its distance from its run's start is even.
-__global__ __launch_bounds__(64) void pair_groups_kernel(const int32_t* __restrict__ row_seq,
+// Units of up to U row groups for the multi-position paged kernel, from
+// row_seq (rows in aligned groups of 8 share a sequence): each run of
+// consecutive groups of one sequence is cut into units of U from its start,
+// the last one shorter.  One wave walks the groups 64 at a time: a group
+// starts a run when its sequence differs from the previous group's, and
+// starts a unit when its distance from its run's start is a multiple of U.
+template <int U>
+__global__ __launch_bounds__(64) void unit_groups_kernel(const int32_t* __restrict__ row_seq,
                                                          int groups, int32_t* __restrict__ first,
                                                          int32_t* __restrict__ count,
-                                                         int32_t* __restrict__ num_pairs) {
+                                                         int32_t* __restrict__ num_units) {
+    static_assert(U >= 2 && (U & (U - 1)) == 0, "power-of-two unit");
     using mfma::kRows;
     const int lane = threadIdx.x;
     int run_start = 0, out = 0;
@@ -1101,23 +1156,32 @@ __global__ __launch_bounds__(64) void pair_groups_kernel(const int32_t* __restri
         const bool in = gi < groups;
         const int sq = in ? row_seq[(size_t)gi * kRows] : 0;
         const int before = in && gi > 0 ? row_seq[(size_t)(gi - 1) * kRows] : 0;
-        const int after = gi + 1 < groups ? row_seq[(size_t)(gi + 1) * kRows] : 0;
         const bool new_run = in && (gi == 0 || sq != before);
         const uint64_t runs = __ballot(new_run);
         const uint64_t upto = runs & (lane == 63 ? ~0ull : ((2ull << lane) - 1));
         const int rs = upto ? g0 + 63 - __builtin_clzll(upto) : run_start;
-        const bool start = in && ((gi - rs) & 1) == 0;
+        const bool start = in && ((gi - rs) & (U - 1)) == 0;
         const uint64_t starts = __ballot(start);
         if (start) {
-            const int k = out + __builtin_popcountll(starts & ((1ull << lane) - 1));
-            first[k] = gi;
-            count[k] = gi + 1 < groups && after == sq ? 2 : 1;
+            int c = 1;  // the run's groups from gi on, at most U
+#pragma unroll
+            for (int k = 1; k < U; ++k)
+                if (c == k && gi + k < groups && row_seq[(size_t)(gi + k) * kRows] == sq) ++c;
+            const int o = out + __builtin_popcountll(starts & ((1ull << lane) - 1));
+            first[o] = gi;
+            count[o] = c;
         }
         out += __builtin_popcountll(starts);
         run_start = __shfl(rs, 63);
     }
-    if (lane == 0) num_pairs[0] = out;
+    if (lane == 0) num_units[0] = out;
 }
+
+// New-token positions (row groups of one sequence) per paged workgroup.
+#ifndef TQ_PAGED_POSITIONS
+#define TQ_PAGED_POSITIONS 4
+#endif
+constexpr int kPagedPositions = TQ_PAGED_POSITIONS;
 
 // Split kernel shape: tokens per wave iteration and waves per workgroup.
 #ifndef TQ_SPLIT_CHUNK
@@ -1280,18 +1344,18 @@ void launch_paged_attention(Scheme s, const uint16_t* query, const uint8_t* pool
     const bool prod = s == Scheme::Prod;
     constexpr int kCH = kSplitChunk, kNW = kSplitWaves;
     if (max_kv_len > 0) {
-        hipLaunchKernelGGL(pair_groups_kernel, dim3(1), dim3(64), 0, stream, row_seq, row_groups,
-                           pair_first, pair_count, num_pairs);
-        check_launch(prod ? "turbo_prod_paged_attn_pairs" : "turbo_mse_paged_attn_pairs");
-        // The grid covers every row group as a unit; units past the pair count exit.
+        hipLaunchKernelGGL(unit_groups_kernel<kPagedPositions>, dim3(1), dim3(64), 0, stream,
+                           row_seq, row_groups, pair_first, pair_count, num_pairs);
+        check_launch(prod ? "turbo_prod_paged_attn_units" : "turbo_mse_paged_attn_units");
+        // The grid covers every row group as a unit; items past the unit count exit.
         if (prod)
-            hipLaunchKernelGGL((attn_mfma_split_kernel<kSchProd, kCH, kNW, true, 2>), dim3(blocks),
-                               dim3(64 * kNW), 0, stream, query, pool, nullptr, ws, g, num_rows,
-                               max_kv_len, tps, splits, inv, pr);
+            hipLaunchKernelGGL((attn_mfma_split_kernel<kSchProd, kCH, kNW, true, kPagedPositions>),
+                               dim3(blocks), dim3(64 * kNW), 0, stream, query, pool, nullptr, ws,
+                               g, num_rows, max_kv_len, tps, splits, inv, pr);
         else
-            hipLaunchKernelGGL((attn_mfma_split_kernel<kSchMse, kCH, kNW, true, 2>), dim3(blocks),
-                               dim3(64 * kNW), 0, stream, query, pool, nullptr, ws, g, num_rows,
-                               max_kv_len, tps, splits, inv, pr);
+            hipLaunchKernelGGL((attn_mfma_split_kernel<kSchMse, kCH, kNW, true, kPagedPositions>),
+                               dim3(blocks), dim3(64 * kNW), 0, stream, query, pool, nullptr, ws,
+                               g, num_rows, max_kv_len, tps, splits, inv, pr);
         check_launch(prod ? "turbo_prod_paged_attn_split" : "turbo_mse_paged_attn_split");
     }
     if (splits <= kItemCombineMaxSplits)
