@@ -202,43 +202,16 @@ __device__ __forceinline__ int nearest_v4(float x) {
     return best;
 }
 
-// Counting forms of nearest_k3 / nearest_v4 for clamped inputs (|x| <= 2.5,
-// 2.75).  The codebooks are sorted and their levels at least 0.25 apart, far
-// above the fp32 spacing of the distances, so the fp32 distances |x - c_i|
-// fall strictly up to the first minimum and rise strictly after it: the
-// index of the first minimum (the reference's strict '<' scan) is the number
-// of strict decreases of consecutive distances.  NaN compares false in both.
-__device__ __forceinline__ int nearest_k3_count(float x) {
-    float prev = fabsf(x - kK3[0]);
-    int n = 0;
-#pragma unroll
-    for (int i = 1; i < 8; ++i) {
-        const float d = fabsf(x - kK3[i]);
-        n += d < prev ? 1 : 0;
-        prev = d;
-    }
-    return n;
-}
-
-__device__ __forceinline__ int nearest_v4_count(float x) {
-    float prev = fabsf(x - kV4[0]);
-    int n = 0;
-#pragma unroll
-    for (int i = 1; i < 16; ++i) {
-        const float d = fabsf(x - kV4[i]);
-        n += d < prev ? 1 : 0;
-        prev = d;
-    }
-    return n;
-}
-
 // Decision thresholds of the nearest-level scans.  For neighbouring levels
 // a < b, closer(x) = fp32 |x - b| < fp32 |x - a| is false up to a and true
 // from b on, and monotone in between (fp32 subtraction rounds monotonically),
 // so on the clamped domain it is x >= T for T = the smallest float with
-// closer(T).  The strict-decrease count above is then #{i : x >= T_i}: a
-// branchless binary search over the sorted T_i.  The T_i are computed here at
-// compile time by bisection over floats with the same fp32 operations.
+// closer(T).  The levels are sorted and at least 0.25 apart, far above the
+// fp32 spacing of the distances, so the distances fall strictly up to the
+// first minimum and rise after it: the index the reference's strict '<' scan
+// returns is the number of strict decreases, #{i : x >= T_i}.  The T_i are
+// computed here at compile time by bisection over floats with the same fp32
+// operations.
 namespace thr {
 constexpr float cabs(float v) { return v < 0.0f ? -v : v; }
 constexpr bool closer(float x, float a, float b) { return cabs(x - b) < cabs(x - a); }
