@@ -463,11 +463,17 @@ __global__ __launch_bounds__(kBlock) void dequant_kernel(
 // ---------------------------------------------------------------------------
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-template <int D, bool PROD>
+// SCH: 0 turbo_mse, 1 turbo_prod, 2 the reference's unexported QJL-1b page
+// (tq_qjl_kernels.cu:189-245): K = +-ks per sign bit, fed through the same
+// per-row table as 0/1 "nibbles" (the sign byte's bits spread one per
+// nibble), and the rotation's sign flip (-1)^i has no head term.
+template <int D, int SCH>
 __global__ __launch_bounds__(kBlock) void dequant_stream_kernel(
     const uint8_t* __restrict__ pool, const int32_t* __restrict__ slots,
     uint16_t* __restrict__ out_key, uint16_t* __restrict__ out_value, PageGeom g, int num_rows,
     float inv, OutLayout ol) {
+    constexpr bool PROD = SCH == 1, QJL = SCH == 2;
+    static_assert(!QJL || D == 128, "QJL: D = 128");
     constexpr int E = 32;           // elements per lane
     constexpr int LPR = D / E;      // lanes per row
     constexpr int RPW = 64 / LPR;   // rows per wave group
@@ -533,7 +539,19 @@ __global__ __launch_bounds__(kBlock) void dequant_stream_kernel(
                 reinterpret_cast<const uint32_t*>(base + g.kc_off + cell * g.code_stride) + j;
             const uint32_t* vp =
                 reinterpret_cast<const uint32_t*>(base + g.vc_off + cell * g.code_stride) + j;
-            it.kw = make_uint4(kp[0], kp[LPR], kp[2 * LPR], kp[3 * LPR]);
+            if constexpr (QJL) {
+                // sign byte j + 4m (elements 8(j + 4m) .. + 7) spread to one
+                // bit per nibble: nibble i = bit i
+                const uint8_t* kb = base + g.kc_off + cell * (D / 8) + j;
+                const auto spread = [](uint32_t b) {
+                    b = (b | (b << 12)) & 0x000F000Fu;
+                    b = (b | (b << 6)) & 0x03030303u;
+                    return (b | (b << 3)) & 0x11111111u;
+                };
+                it.kw = make_uint4(spread(kb[0]), spread(kb[4]), spread(kb[8]), spread(kb[12]));
+            } else {
+                it.kw = make_uint4(kp[0], kp[LPR], kp[2 * LPR], kp[3 * LPR]);
+            }
             it.vw = make_uint4(vp[0], vp[LPR], vp[2 * LPR], vp[3 * LPR]);
             it.ks = h2f(ld_u16(base + g.ks_off + cell * g.scale_stride));
             it.vs = h2f(ld_u16(base + g.vs_off + cell * g.scale_stride));
@@ -597,8 +615,8 @@ __global__ __launch_bounds__(kBlock) void dequant_stream_kernel(
         // ... and the two largest (chunk m ^ 1, m ^ 2) are in the lane again.
         reg_stage(8);
         reg_stage(16);
-        // Element 8*(j + LPR*m) + i has sign (-1)^(i + h).
-        const float se = (it.h & 1) ? -inv : inv;
+        // Element 8*(j + LPR*m) + i has sign (-1)^(i + h) ((-1)^i for QJL).
+        const float se = (!QJL && (it.h & 1)) ? -inv : inv;
         u32x4 v[4];
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
@@ -658,8 +676,9 @@ __global__ __launch_bounds__(kBlock) void dequant_stream_kernel(
 #pragma unroll
             for (int n = 0; n < 16; ++n) {
                 const float kv =
-                    PROD ? (kK3[n & 7] + cur.re * ((n & 8) ? 1.0f : -1.0f)) * cur.ks
-                         : kV4[n] * cur.ks;
+                    QJL ? ((n & 1) ? cur.ks : -cur.ks)
+                    : PROD ? (kK3[n & 7] + cur.re * ((n & 8) ? 1.0f : -1.0f)) * cur.ks
+                           : kV4[n] * cur.ks;
                 myK[n * kWaves * 64] = kv;
                 myV[n * kWaves * 64] = kV4[n] * cur.vs;
             }
@@ -735,6 +754,42 @@ void launch_pack(Scheme s, const uint16_t* key, const uint16_t* value, const int
     }
 }
 
+bool launch_qjl_stream_dequant(const uint8_t* pool, const int32_t* slots, uint16_t* out_key,
+                               uint16_t* out_value, const QjlGeom& q, int num_tokens,
+                               hipStream_t stream) {
+    const auto al = [](uint64_t v, uint64_t a) { return (v & (a - 1)) == 0; };
+    if (!(q.D == 128 && q.k1_bytes == 16 && q.v4_bytes == 64 && al(q.page_size, 4) &&
+          al(q.v4_off, 4) && al(q.ks_off, 2) && al(q.vs_off, 2) &&
+          al(reinterpret_cast<uintptr_t>(pool), 4) && al(reinterpret_cast<uintptr_t>(out_key), 16) &&
+          al(reinterpret_cast<uintptr_t>(out_value), 16)))
+        return false;
+    const int rows = num_tokens * q.H;
+    if (rows <= 0) return true;
+    PageGeom g{};
+    g.page_size = q.page_size;
+    g.kc_off = q.k1_off;
+    g.vc_off = q.v4_off;
+    g.ks_off = q.ks_off;
+    g.vs_off = q.vs_off;
+    g.code_stride = q.v4_bytes;  // V rows; the K sign rows are D/8 = 16 bytes
+    g.scale_stride = 2;
+    g.H = q.H;
+    g.D = q.D;
+    g.block_size = q.block_size;
+    g.bs_shift = (q.block_size & (q.block_size - 1)) == 0 ? __builtin_ctz(q.block_size) : -1;
+    g.h_shift = (q.H & (q.H - 1)) == 0 ? __builtin_ctz(q.H) : -1;
+    OutLayout ol;
+    ol.tok = (uint64_t)g.H * g.D;
+    ol.head = (uint64_t)g.D;
+    const int rows_per_block = kBlock / (g.D / 32);
+    const int blocks_needed = (rows + rows_per_block - 1) / rows_per_block;
+    const dim3 grid(std::max(1, std::min(blocks_needed, 4 * num_cus())));
+    hipLaunchKernelGGL((dequant_stream_kernel<128, 2>), grid, dim3(kBlock), 0, stream, pool, slots,
+                       out_key, out_value, g, rows, inv_sqrt_d(g.D), ol);
+    check_launch("qjl_dequant_kv_kernel");
+    return true;
+}
+
 void launch_dequant(Scheme s, const uint8_t* pool, const int32_t* slots, uint16_t* out_key,
                     uint16_t* out_value, const PageGeom& g, int num_tokens, hipStream_t stream,
                     bool head_major) {
@@ -756,9 +811,9 @@ void launch_dequant(Scheme s, const uint8_t* pool, const int32_t* slots, uint16_
             hipLaunchKernelGGL(kernel, grid, dim3(kBlock), 0, stream, pool, slots, out_key,
                                out_value, g, rows, inv, ol);
         };
-        if (g.D == 128) prod ? go(dequant_stream_kernel<128, true>) : go(dequant_stream_kernel<128, false>);
-        else if (g.D == 64) prod ? go(dequant_stream_kernel<64, true>) : go(dequant_stream_kernel<64, false>);
-        else prod ? go(dequant_stream_kernel<32, true>) : go(dequant_stream_kernel<32, false>);
+        if (g.D == 128) prod ? go(dequant_stream_kernel<128, 1>) : go(dequant_stream_kernel<128, 0>);
+        else if (g.D == 64) prod ? go(dequant_stream_kernel<64, 1>) : go(dequant_stream_kernel<64, 0>);
+        else prod ? go(dequant_stream_kernel<32, 1>) : go(dequant_stream_kernel<32, 0>);
         check_launch(prod ? "turbo_prod_dequant_kv_kernel" : "turbo_mse_dequant_kv_kernel");
         return;
     }

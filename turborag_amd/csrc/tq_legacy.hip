@@ -288,6 +288,46 @@ __global__ __launch_bounds__(kBlock) void int4_dequant_kernel(
     *reinterpret_cast<uint32_t*>(out_value + off) = f2h2(s4(vb & 0xF) * vs, s4(vb >> 4) * vs);
 }
 
+// The same for D = 128, streaming: 16 lanes per (token, head) row, four rows
+// per wave.  Lane j decodes code dword j (elements 8j .. 8j + 7: a nibble
+// sign-extends with one bit-field extract) and writes 16 bytes, so each
+// tensor's row of 256 bytes leaves as two whole 128-byte lines in one
+// non-temporal store instruction.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(kBlock) void int4_dequant_wide_kernel(
+    const uint8_t* __restrict__ pool, const int32_t* __restrict__ slots,
+    uint16_t* __restrict__ out_key, uint16_t* __restrict__ out_value, Int4Geom g,
+    int num_rows) {
+    constexpr int D = 128;
+    const int j = threadIdx.x & 15;
+    const int row = blockIdx.x * (kBlock / 16) + (threadIdx.x >> 4);
+    if (row >= num_rows) return;
+    const int t = row / g.H, h = row - t * g.H;
+    const int slot = slots[t];
+    if (slot < 0) return;
+    int page, tib;
+    page_of(slot, g.block_size, page, tib);
+    const size_t cell = (size_t)tib * g.H + h;
+    const uint8_t* base = pool + (size_t)page * g.page_size;
+    const uint32_t kw = reinterpret_cast<const uint32_t*>(base + g.kc_off + cell * g.code_bytes)[j];
+    const uint32_t vw = reinterpret_cast<const uint32_t*>(base + g.vc_off + cell * g.code_bytes)[j];
+    const float ks = h2f(ld_u16(base + g.ks_off + cell * g.scale_bytes));
+    const float vs = h2f(ld_u16(base + g.vs_off + cell * g.scale_bytes));
+    const auto decode = [](uint32_t w, float sc) {
+        uint32_t o[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float a = (float)(int)__builtin_amdgcn_sbfe((int)w, 8 * q, 4);
+            const float b = (float)(int)__builtin_amdgcn_sbfe((int)w, 8 * q + 4, 4);
+            o[q] = f2h2(a * sc, b * sc);
+        }
+        return u32x4{o[0], o[1], o[2], o[3]};
+    };
+    const size_t off = (size_t)row * D + 8 * j;
+    __builtin_nontemporal_store(decode(kw, ks), reinterpret_cast<u32x4*>(out_key + off));
+    __builtin_nontemporal_store(decode(vw, vs), reinterpret_cast<u32x4*>(out_value + off));
+}
+
 // ---------------------------------------------------------------------------
 // Dense fp16 page (tq_dense_kernels.cu): a copy of each (token, head) row of
 // D halves between [N, H, D] and the page cell, one dword per thread.
@@ -420,6 +460,7 @@ void launch_qjl_dequant(const uint8_t* pool, const int32_t* slots, uint16_t* out
                         hipStream_t stream) {
     const long long rows = (long long)num_tokens * g.H;
     if (rows <= 0) return;
+    if (launch_qjl_stream_dequant(pool, slots, out_key, out_value, g, num_tokens, stream)) return;
     const float inv = inv_sqrt_d(g.D);
     TQ_DISPATCH_D(g.D, hipLaunchKernelGGL(qjl_dequant_kernel<kD>, dim3(row_blocks(rows, kD)),
                                           dim3(kBlock), 0, stream, pool, slots, out_key,
@@ -468,6 +509,15 @@ void launch_int4_dequant(const uint8_t* pool, const int32_t* slots, uint16_t* ou
                          hipStream_t stream) {
     const long long rows = (long long)num_tokens * g.H;
     if (rows <= 0) return;
+    const auto al = [](uint64_t v, uint64_t a) { return (v & (a - 1)) == 0; };
+    if (g.D == 128 && g.code_bytes == 64 && al(g.page_size, 4) && al(g.kc_off, 4) &&
+        al(g.vc_off, 4) && al(reinterpret_cast<uintptr_t>(pool), 4) &&
+        al(reinterpret_cast<uintptr_t>(out_key), 16) && al(reinterpret_cast<uintptr_t>(out_value), 16)) {
+        hipLaunchKernelGGL(int4_dequant_wide_kernel, dim3((unsigned)((rows + 15) / 16)),
+                           dim3(kBlock), 0, stream, pool, slots, out_key, out_value, g, (int)rows);
+        check_launch("tq_dequant_kv_kernel");
+        return;
+    }
     TQ_DISPATCH_D(g.D, hipLaunchKernelGGL(int4_dequant_kernel<kD>, dim3(row_blocks(rows, kD)),
                                           dim3(kBlock), 0, stream, pool, slots, out_key,
                                           out_value, g, (int)rows));
