@@ -217,7 +217,9 @@ __device__ __forceinline__ float tree_chunk_pairs(float (&q)[C]) {
 // sign and the residual RMS (turbo_prod K); kCodesV4: 4-bit code, RMS of the
 // squares (turbo_prod V); kCodesV4Pairs: 4-bit code, RMS of the pair sums
 // fmaf(x0, x0, x1 * x1) (turbo_mse, tq_turbo_mse_kernels.cu:108, contracted).
-constexpr int kCodesK3 = 0, kCodesV4 = 1, kCodesV4Pairs = 2;
+// kCodesSigns: the QJL-1b K sign bits (x / rms >= 0) of the element pair,
+// two bits per chunk, and the RMS of the squares.
+constexpr int kCodesK3 = 0, kCodesV4 = 1, kCodesV4Pairs = 2, kCodesSigns = 3;
 template <int C, int MODE>
 __device__ __forceinline__ void quantize_chunks(const uint32_t (&w)[C], int j, float sinv,
                                                 const PackTables& tab, uint32_t (&bytes)[C],
@@ -261,6 +263,15 @@ __device__ __forceinline__ void quantize_chunks(const uint32_t (&w)[C], int j, f
         // every K/rms is NaN, the reference's residual RMS is NaN, and the
         // codes above are its codes for NaN (index 0, sign 0).
         if (!(rms <= 3.402823466e38f)) rms_e = __builtin_nanf("");
+    } else if constexpr (MODE == kCodesSigns) {
+        // x / rms >= 0 is x >= 0 for a finite rms >= 1e-8 (no quotient of a
+        // sum of fp16 values that is not zero underflows); a non-finite rms
+        // means a non-finite row, every quotient NaN: bit 0.
+        const bool fin = rms <= 3.402823466e38f;
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+            bytes[c] = (fin && x[2 * c] >= 0.0f ? 1u : 0u) | (fin && x[2 * c + 1] >= 0.0f ? 2u : 0u);
+        return;
     } else {
 #pragma unroll
         for (int k = 0; k < E; ++k) n4[k] = v4_code(div_by(x[k], rms, y), tab);
@@ -269,13 +280,17 @@ __device__ __forceinline__ void quantize_chunks(const uint32_t (&w)[C], int j, f
     for (int c = 0; c < C; ++c) bytes[c] = n4[2 * c] | (n4[2 * c + 1] << 4);
 }
 
-template <int D, bool PROD>
+// SCH: 0 turbo_mse, 1 turbo_prod, 2 the reference's unexported QJL-1b page
+// (tq_qjl_kernels.cu:72-181: K sign bits, V 4-bit codes, sign flip (-1)^i
+// without the head term).
+template <int D, int SCH>
 __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
     const uint16_t* __restrict__ key, const uint16_t* __restrict__ value,
     const int32_t* __restrict__ slots, uint8_t* __restrict__ pool, PageGeom g, int num_rows,
     float inv) {
     constexpr int R = kPackLanes, C = D / (2 * R);
     static_assert(C == 4 || C == 8, "D = 64 or 128");
+    constexpr bool PROD = SCH == 1, QJL = SCH == 2;
     __shared__ PackTables tab;
     if (threadIdx.x < kPackTableWords)
         reinterpret_cast<uint32_t*>(&tab)[threadIdx.x] =
@@ -301,13 +316,28 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
     // the one computed without it (up to the sign of exact zeros, which no
     // code or scale sees).  sh and the lane sign of wht_chunks are folded
     // into the exact scale +-1/sqrt(D).
-    const float sinv = ((h ^ __popc(j)) & 1) ? -inv : inv;
+    const float sinv = (((QJL ? 0 : h) ^ __popc(j)) & 1) ? -inv : inv;
     // K, then V: one tensor's values live at a time.
     uint32_t kbyte[C], vbyte[C];
     float krms, vrms, rms_e = 0.0f, unused;
-    quantize_chunks<C, PROD ? kCodesK3 : kCodesV4Pairs>(kw, j, sinv, tab, kbyte, krms, rms_e);
+    quantize_chunks<C, QJL ? kCodesSigns : PROD ? kCodesK3 : kCodesV4Pairs>(kw, j, sinv, tab, kbyte,
+                                                                           krms, rms_e);
     __builtin_amdgcn_sched_barrier(0);
-    quantize_chunks<C, PROD ? kCodesV4 : kCodesV4Pairs>(vw, j, sinv, tab, vbyte, vrms, unused);
+    quantize_chunks<C, QJL || PROD ? kCodesV4 : kCodesV4Pairs>(vw, j, sinv, tab, vbyte, vrms,
+                                                               unused);
+    // QJL: the sign byte of elements 8b .. 8b + 7 gathers two bits from each
+    // of four lanes (logical j ^ 1, j ^ 2: quad DPP); chunk c gives bytes 2c
+    // (lanes 0-3) and 2c + 1 (lanes 4-7), bits 2(j % 4), 2(j % 4) + 1.
+    uint32_t kbits[C / 4] = {};
+    if constexpr (QJL) {
+#pragma unroll
+        for (int c = 0; c < C; ++c) kbits[c >> 2] |= kbyte[c] << (8 * (c & 3) + 2 * (j & 3));
+#pragma unroll
+        for (int q = 0; q < C / 4; ++q) {
+            kbits[q] |= __float_as_uint(row8_xor<1>(__uint_as_float(kbits[q])));
+            kbits[q] |= __float_as_uint(row8_xor<2>(__uint_as_float(kbits[q])));
+        }
+    }
     if (!valid) return;
     const int slot = slots[t];
     if (slot < 0) return;
@@ -317,13 +347,20 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(
     uint8_t* base = pool + (size_t)page * g.page_size;
     // Element pair (2b, 2b+1) is byte b (low nibble even): chunk c of lane j
     // is byte Rc + j.
-    uint8_t* kc = base + g.kc_off + cell * g.code_stride + j;
     uint8_t* vc = base + g.vc_off + cell * g.code_stride + j;
+    if constexpr (QJL) {
+        if ((j & 3) == 0) {
+            uint8_t* kb = base + g.kc_off + cell * (D / 8) + (j >> 2);
 #pragma unroll
-    for (int c = 0; c < C; ++c) {
-        kc[R * c] = (uint8_t)kbyte[c];
-        vc[R * c] = (uint8_t)vbyte[c];
+            for (int c = 0; c < C; ++c) kb[2 * c] = (uint8_t)(kbits[c >> 2] >> (8 * (c & 3)));
+        }
+    } else {
+        uint8_t* kc = base + g.kc_off + cell * g.code_stride + j;
+#pragma unroll
+        for (int c = 0; c < C; ++c) kc[R * c] = (uint8_t)kbyte[c];
     }
+#pragma unroll
+    for (int c = 0; c < C; ++c) vc[R * c] = (uint8_t)vbyte[c];
     if (j == 0) {
         *reinterpret_cast<uint16_t*>(base + g.ks_off + cell * g.scale_stride) = f2h(krms);
         if (PROD)
@@ -738,8 +775,8 @@ void launch_pack(Scheme s, const uint16_t* key, const uint16_t* value, const int
             hipLaunchKernelGGL(kernel, wgrid, dim3(kBlock), 0, stream, key, value, slots, pool, g,
                                rows, inv);
         };
-        if (g.D == 128) prod ? go(pack_wide_kernel<128, true>) : go(pack_wide_kernel<128, false>);
-        else prod ? go(pack_wide_kernel<64, true>) : go(pack_wide_kernel<64, false>);
+        if (g.D == 128) prod ? go(pack_wide_kernel<128, 1>) : go(pack_wide_kernel<128, 0>);
+        else prod ? go(pack_wide_kernel<64, 1>) : go(pack_wide_kernel<64, 0>);
         check_launch(prod ? "turbo_prod_pack_kv_kernel" : "turbo_mse_pack_kv_kernel");
         return;
     }
@@ -752,6 +789,40 @@ void launch_pack(Scheme s, const uint16_t* key, const uint16_t* value, const int
                                               key, value, slots, pool, g, rows, inv));
         check_launch("turbo_mse_pack_kv_kernel");
     }
+}
+
+bool launch_qjl_wide_pack(const uint16_t* key, const uint16_t* value, const int32_t* slots,
+                          uint8_t* pool, const QjlGeom& q, int num_tokens, hipStream_t stream) {
+    const auto al = [](uint64_t v, uint64_t a) { return (v & (a - 1)) == 0; };
+    if (!((q.D == 64 || q.D == 128) && q.k1_bytes == q.D / 8 && q.v4_bytes == q.D / 2 &&
+          al(q.ks_off, 2) && al(q.vs_off, 2) && al(q.page_size, 2) &&
+          al(reinterpret_cast<uintptr_t>(key), 4) && al(reinterpret_cast<uintptr_t>(value), 4)))
+        return false;
+    const int rows = num_tokens * q.H;
+    if (rows <= 0) return true;
+    PageGeom g{};
+    g.page_size = q.page_size;
+    g.kc_off = q.k1_off;
+    g.vc_off = q.v4_off;
+    g.ks_off = q.ks_off;
+    g.vs_off = q.vs_off;
+    g.code_stride = q.v4_bytes;  // V rows; the K sign rows are D/8 bytes
+    g.scale_stride = 2;
+    g.H = q.H;
+    g.D = q.D;
+    g.block_size = q.block_size;
+    g.bs_shift = (q.block_size & (q.block_size - 1)) == 0 ? __builtin_ctz(q.block_size) : -1;
+    g.h_shift = (q.H & (q.H - 1)) == 0 ? __builtin_ctz(q.H) : -1;
+    const dim3 grid((rows + kBlock / kPackLanes - 1) / (kBlock / kPackLanes));
+    const float inv = inv_sqrt_d(g.D);
+    if (g.D == 128)
+        hipLaunchKernelGGL((pack_wide_kernel<128, 2>), grid, dim3(kBlock), 0, stream, key, value,
+                           slots, pool, g, rows, inv);
+    else
+        hipLaunchKernelGGL((pack_wide_kernel<64, 2>), grid, dim3(kBlock), 0, stream, key, value,
+                           slots, pool, g, rows, inv);
+    check_launch("qjl_pack_kv_kernel");
+    return true;
 }
 
 bool launch_qjl_stream_dequant(const uint8_t* pool, const int32_t* slots, uint16_t* out_key,

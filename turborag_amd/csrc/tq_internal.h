@@ -123,6 +123,9 @@ void launch_qjl_dequant(const uint8_t* pool, const int32_t* slots, uint16_t* out
 void launch_qjl_attention(const uint16_t* query, const uint8_t* pool, const int32_t* slots,
                           uint16_t* output, const QjlGeom& g, int num_queries, int num_kv_tokens,
                           hipStream_t stream);
+// The wide form of launch_qjl_pack (D = 64, 128); false when not eligible.
+bool launch_qjl_wide_pack(const uint16_t* key, const uint16_t* value, const int32_t* slots,
+                          uint8_t* pool, const QjlGeom& g, int num_tokens, hipStream_t stream);
 // The streaming form of launch_qjl_dequant (D = 128, aligned fields and
 // outputs); false (nothing launched) when not eligible.
 bool launch_qjl_stream_dequant(const uint8_t* pool, const int32_t* slots, uint16_t* out_key,

@@ -446,6 +446,7 @@ static unsigned row_blocks(long long rows, int D) {
 
 void launch_qjl_pack(const uint16_t* key, const uint16_t* value, const int32_t* slots,
                      uint8_t* pool, const QjlGeom& g, int num_tokens, hipStream_t stream) {
+    if (launch_qjl_wide_pack(key, value, slots, pool, g, num_tokens, stream)) return;
     const long long rows = (long long)num_tokens * g.H;
     if (rows <= 0) return;
     const float inv = inv_sqrt_d(g.D);
