@@ -261,6 +261,72 @@ __global__ __launch_bounds__(kBlock) void int4_pack_kernel(
     }
 }
 
+// The same for D = 128, wide: 16 lanes per (token, head) row, lane j owns
+// elements 8j .. 8j + 7 (one 16-byte load, one code dword).  The row's scale
+// is one correctly rounded division; x / scale is Markstein's FMA-corrected
+// product with its reciprocal (div_by: correctly rounded for these ranges,
+// quotients of |x| <= 65504 by scale >= 1e-8, or zero), then rounded half to
+// even, NaN to 0, clamped to [-8, 7].
+__device__ __forceinline__ uint32_t q_int4_pair(float x0, float x1, float scale, float y) {
+    auto q = [&](float x) {
+        float r = __builtin_rintf(div_by(x, scale, y));
+        r = r == r ? r : 0.0f;  // NaN (a non-finite x or scale) converts to 0
+        return (uint32_t)(int)fminf(fmaxf(r, -8.0f), 7.0f) & 0xFu;
+    };
+    return q(x0) | (q(x1) << 4);
+}
+
+typedef uint16_t h8v __attribute__((ext_vector_type(8)));
+__global__ __launch_bounds__(kBlock) void int4_pack_wide_kernel(
+    const uint16_t* __restrict__ key, const uint16_t* __restrict__ value,
+    const int32_t* __restrict__ slots, uint8_t* __restrict__ pool, Int4Geom g, int num_rows) {
+    constexpr int D = 128;
+    const int j = threadIdx.x & 15;
+    const int row = blockIdx.x * (kBlock / 16) + (threadIdx.x >> 4);
+    const bool valid = row < num_rows;
+    const int rr = valid ? row : num_rows - 1;
+    const int t = rr / g.H, h = rr - t * g.H;
+    const size_t off = (size_t)rr * D + 8 * j;
+    const h8v kr = *reinterpret_cast<const h8v*>(key + off);
+    const h8v vr = *reinterpret_cast<const h8v*>(value + off);
+    float k[8], v[8];
+    // absmax over the row (fmaxf from 0 ignores NaN, as block_max does)
+    float ka = 0.0f, va = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        k[e] = h2f(kr[e]);
+        v[e] = h2f(vr[e]);
+        ka = fmaxf(ka, fabsf(k[e]));
+        va = fmaxf(va, fabsf(v[e]));
+    }
+#pragma unroll
+    for (int m = 8; m >= 1; m >>= 1) {
+        ka = fmaxf(ka, xor_lane(ka, m));
+        va = fmaxf(va, xor_lane(va, m));
+    }
+    const float kscale = fmaxf(ka / 7.0f, 1e-8f), vscale = fmaxf(va / 7.0f, 1e-8f);
+    const float ky = 1.0f / kscale, vy = 1.0f / vscale;
+    uint32_t kw = 0, vw = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        kw |= q_int4_pair(k[2 * b], k[2 * b + 1], kscale, ky) << (8 * b);
+        vw |= q_int4_pair(v[2 * b], v[2 * b + 1], vscale, vy) << (8 * b);
+    }
+    if (!valid) return;
+    const int slot = slots[t];
+    if (slot < 0) return;
+    int page, tib;
+    page_of(slot, g.block_size, page, tib);
+    const size_t cell = (size_t)tib * g.H + h;
+    uint8_t* base = pool + (size_t)page * g.page_size;
+    reinterpret_cast<uint32_t*>(base + g.kc_off + cell * g.code_bytes)[j] = kw;
+    reinterpret_cast<uint32_t*>(base + g.vc_off + cell * g.code_bytes)[j] = vw;
+    if (j == 0) {
+        put_u16(base + g.ks_off + cell * g.scale_bytes, f2h(kscale));
+        put_u16(base + g.vs_off + cell * g.scale_bytes, f2h(vscale));
+    }
+}
+
 // tq_dequant_kv_kernel, tq_dequant_kernels.cu:6-55: fp16(code * fp32(scale)).
 template <int D>
 __global__ __launch_bounds__(kBlock) void int4_dequant_kernel(
@@ -499,6 +565,15 @@ void launch_int4_pack(const uint16_t* key, const uint16_t* value, const int32_t*
                       uint8_t* pool, const Int4Geom& g, int num_tokens, hipStream_t stream) {
     const long long rows = (long long)num_tokens * g.H;
     if (rows <= 0) return;
+    const auto al = [](uint64_t v, uint64_t a) { return (v & (a - 1)) == 0; };
+    if (g.D == 128 && g.code_bytes == 64 && al(g.page_size, 4) && al(g.kc_off, 4) &&
+        al(g.vc_off, 4) && al(reinterpret_cast<uintptr_t>(pool), 4) &&
+        al(reinterpret_cast<uintptr_t>(key), 16) && al(reinterpret_cast<uintptr_t>(value), 16)) {
+        hipLaunchKernelGGL(int4_pack_wide_kernel, dim3((unsigned)((rows + 15) / 16)),
+                           dim3(kBlock), 0, stream, key, value, slots, pool, g, (int)rows);
+        check_launch("tq_pack_kv_kernel");
+        return;
+    }
     TQ_DISPATCH_D(g.D, hipLaunchKernelGGL(int4_pack_kernel<kD>, dim3(row_blocks(rows, kD)),
                                           dim3(kBlock), 0, stream, key, value, slots, pool, g,
                                           (int)rows));
