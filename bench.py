@@ -170,19 +170,24 @@ def event_time_us(run, reps):
 
 
 def launch_pass(w: Workload, reps: int) -> None:
-    """Eager launches only: dequant and attention of every layer, then a plain
-    device copy of the dequant's byte count (the calibration kernel for the
-    FETCH_SIZE / WRITE_SIZE counters)."""
+    """Eager launches only: dequant and attention of every layer, one step of
+    the batched paged decode (append + attention), then a plain device copy of
+    the dequant's byte count (the calibration kernel for the FETCH_SIZE /
+    WRITE_SIZE counters)."""
     import torch
     half = w.deq_bytes // 4  # fp16 elements copied: deq_bytes / 2 read, / 2 written
     src = torch.empty(half, dtype=torch.float16, device=w.dev).fill_(1.0)
     dst = torch.empty_like(src)
+    bt = batched_setup(w)
     for _ in range(reps):
         w.all_dequant()
         w.all_attention()
+        bt["batch"].repack()
+        bt["batch"].attention(bt["query"], bt["row_seq"], bt["row_len"], bt["tables"], bt["out"])
         for _ in range(4):
             dst.copy_(src)
     torch.cuda.synchronize()
+    bt["batch"].close()
     log(f"[bench] launch pass: {reps} x {w.NL} layers; copy calibration kernel moves "
         f"{half * 2} B read + {half * 2} B written")
 
@@ -301,6 +306,9 @@ def main() -> int:
     log(f"[bench] pack (36 layers x 8192 tokens): turbo_prod {pack['turbo_prod_us_per_layer']:.1f} "
         f"us/layer, turbo_mse {pack['turbo_mse_us_per_layer']:.1f} us/layer")
 
+    logits = measure_logits(w)
+    log(f"[bench] turbo_prod logits @32K: {logits['us']:.1f} us ({logits['GBps']:.0f} GB/s)")
+
     legacy = measure_legacy(w)
     log(f"[bench] unexported kernels @32K: qjl dequant {legacy['qjl_dequant_us']:.1f} us, "
         f"qjl attention {legacy['qjl_attention_us']:.1f} us, int4 dequant "
@@ -357,6 +365,7 @@ def main() -> int:
         "loader": loader,
         "store": store,
         "pack": pack,
+        "logits": logits,
         "unexported_kernels": legacy,
         "batched_decode": batched,
         "step_ms_events": round(ev_ms_per_step, 4),
@@ -517,6 +526,20 @@ def measure_pack(w: Workload, reps: int = 5) -> dict:
     return out
 
 
+def measure_logits(w: Workload, reps: int = 10) -> dict:
+    """The turbo_prod logits entry on one layer of the step (GQA 16/2 rows,
+    32K tokens): fp32 logits [8, 2, 32768] written.  Algorithmic bytes: pool +
+    slots + query read, logits written."""
+    import torch
+    lg = torch.empty(w.rows * w.H * w.N, dtype=torch.float32, device=w.dev)
+    us = event_time_us(lambda: w.tq.fused_attn_logits(w.qa, w.pools[0], w.slots, lg, w.lp, w.cfg,
+                                                      w.rows, w.N, stream=w._stream()), reps)
+    alg = w.pools[0].numel() + w.N * 4 + w.qa.numel() * 2 + lg.numel() * 4
+    del lg
+    return {"us": round(us, 2), "algorithmic_bytes": alg, "GBps": round(alg / us / 1e3, 1),
+            "shape": "8 GQA rows x 2 kv heads x 32768 tokens, fp32"}
+
+
 def measure_legacy(w: Workload, reps: int = 10) -> dict:
     """The kernels the reference compiles but does not export, on one layer
     of the step's shape (32K tokens, H = 2, D = 128, the step's shuffled
@@ -558,11 +581,9 @@ def measure_legacy(w: Workload, reps: int = 10) -> dict:
     return t
 
 
-def measure_batched(w: Workload, reps: int = 10) -> dict:
-    """One serving step of a batch of paged sequences (32 sequences, lengths
-    U[1024, 32768], 1-8 new tokens each, pages scattered by the allocator):
-    one pack launch appending every new token, then one paged-attention
-    launch for 8 GQA rows per new token (causal over the new tokens)."""
+def batched_setup(w: Workload) -> dict:
+    """The batch of the batched-decode step: 32 turbo_prod sequences, lengths
+    U[1024, 32768] (seed 500), 1-8 new tokens each (seed 501), appended."""
     import numpy as np
     import torch
 
@@ -572,8 +593,21 @@ def measure_batched(w: Workload, reps: int = 10) -> dict:
     b = PagedBatch(w.tq, "turbo_prod", lens, widths, seed=500, device=w.dev)
     b.append_new_tokens(seed=503)
     query, row_seq, row_len = b.decode_rows(seed=504)
-    bt = b.block_tables()
-    out = torch.empty_like(query)
+    return {"batch": b, "query": query, "row_seq": row_seq, "row_len": row_len,
+            "tables": b.block_tables(), "out": torch.empty_like(query), "lens": lens,
+            "widths": widths}
+
+
+def measure_batched(w: Workload, reps: int = 10) -> dict:
+    """One serving step of a batch of paged sequences (32 sequences, lengths
+    U[1024, 32768], 1-8 new tokens each, pages scattered by the allocator):
+    one pack launch appending every new token, then one paged-attention
+    launch for 8 GQA rows per new token (causal over the new tokens)."""
+    import torch
+
+    st = batched_setup(w)
+    b, query, row_seq, row_len = st["batch"], st["query"], st["row_seq"], st["row_len"]
+    bt, out, lens, widths = st["tables"], st["out"], st["lens"], st["widths"]
     torch.cuda.synchronize()
     att_us = event_time_us(lambda: b.attention(query, row_seq, row_len, bt, out), reps)
     app_us = event_time_us(b.repack, reps)
