@@ -11,6 +11,10 @@
         the factor that maps the same counter of a plain device copy of
         <copy-bytes> read and written onto those bytes.
 
+    python -m turborag_amd.rocprof_summary counters <prefix> "<command>"
+        Mean of every counter of a ``--pmc`` run (derived metrics included,
+        e.g. MfmaUtil, VALUBusy, OccupancyPercent) per library kernel.
+
 <prefix> is the path rocprofv3 wrote to minus the ``_kernel_trace.csv`` /
 ``_counter_collection.csv`` suffix.
 """
@@ -98,9 +102,30 @@ def traffic(fetch_prefix: str, write_prefix: str, copy_bytes: int) -> dict:
     return res
 
 
+def counters_md(prefix: str, command: str) -> str:
+    """Kernel x counter table of per-dispatch means (library kernels)."""
+    d: dict[str, dict[str, list[float]]] = defaultdict(lambda: defaultdict(list))
+    with open(f"{prefix}_counter_collection.csv", newline="") as f:
+        for r in csv.DictReader(f):
+            if "tq::" in r["Kernel_Name"]:
+                d[short_name(r["Kernel_Name"])][r["Counter_Name"]].append(float(r["Counter_Value"]))
+    names = sorted({c for v in d.values() for c in v})
+    out = [f"Command (repo root, MI355X):\n\n```\n{command}\n```\n",
+           "| kernel | dispatches | " + " | ".join(names) + " |",
+           "|---|---:|" + "---:|" * len(names)]
+    for k, v in d.items():
+        n = max(len(x) for x in v.values())
+        cells = [f"{statistics.mean(v[c]):.2f}" if c in v else "" for c in names]
+        out.append(f"| `{k}` | {n} | " + " | ".join(cells) + " |")
+    return "\n".join(out) + "\n"
+
+
 def main(argv: list[str]) -> int:
     if len(argv) >= 3 and argv[0] == "kernels":
         print(kernels_md(argv[1], argv[2]))
+        return 0
+    if len(argv) >= 3 and argv[0] == "counters":
+        print(counters_md(argv[1], argv[2]))
         return 0
     if len(argv) >= 6 and argv[0] == "traffic":
         res = traffic(argv[1], argv[2], int(argv[3]))
