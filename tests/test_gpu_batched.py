@@ -116,3 +116,37 @@ def test_paged_many_sequences_against_slot_map_attention(tq, cuda):
     print(f"    worst rel diff {worst:.3e}", flush=True)
     assert worst < 2e-3
     b.close()
+
+
+def test_paged_over_a_thousand_row_groups(tq, cuda):
+    """More than 1024 row groups: the plan is built 1024 groups at a time, so
+    runs of a sequence's positions and units of four positions straddle the
+    window ends.  Every row group equals the reference-ABI
+    fused_attention_output over its sequence's slot map."""
+    rng = np.random.default_rng(550)
+    lens = rng.integers(16, 300, size=300)
+    widths = rng.integers(1, 9, size=300)
+    groups = int(widths.sum())
+    print(f"[batched >1024 groups] groups={groups}", flush=True)
+    assert groups > 1100
+    b = PagedBatch(tq, "turbo_prod", lens, widths, seed=551, device=cuda)
+    b.append_new_tokens(seed=908)
+    query, row_seq, row_len = b.decode_rows(seed=909)
+    out = torch.zeros_like(query)
+    b.attention(query, row_seq, row_len, b.block_tables(), out)
+    ref = torch.zeros_like(query)
+    r = 0
+    for s, (L, w) in enumerate(zip(lens, widths)):
+        for j in range(w):
+            n = int(L) + j + 1
+            slots = torch.from_numpy(b.slots_of(s, n)).to(cuda)
+            tq.fused_attn_output(query[r:r + 8].contiguous(), b.pool, slots, ref[r:r + 8], b.layout,
+                                 b.cfg, 8, n)
+            r += 8
+    torch.cuda.synchronize()
+    o = out.float().reshape(-1, 8 * out.shape[1] * out.shape[2])
+    e = ref.float().reshape(-1, 8 * out.shape[1] * out.shape[2])
+    err = ((o - e).abs().amax(dim=1) / e.abs().amax(dim=1)).max().item()
+    print(f"    worst rel diff {err:.3e}", flush=True)
+    assert err < 2e-3
+    b.close()

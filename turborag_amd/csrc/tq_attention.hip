@@ -246,17 +246,38 @@ __device__ __forceinline__ half8 as_h8(uint32_t a, uint32_t b, uint32_t c, uint3
 // row_seq[r] (the 8 rows of an aligned group share one) and attends its
 // first row_kv_len[r] tokens; token t of sequence s is in page
 // block_tables[s * max_blocks + t / B].
+// A unit: the npos consecutive row groups (new-token positions) of one
+// sequence from row group `first` on, computed together.  It has one item
+// per kv head; each item is n passes (workgroup-wide chunk steps of kPass
+// tokens) over the unit's first kv_end tokens, a pass weighing w work units,
+// and item h takes work positions [start + h*w*n, start + (h+1)*w*n) of the
+// step's total work.
+struct PagedUnit {
+    int32_t first, npos, kv_end, start, n, w, pad0, pad1;
+};
 struct PagedRows {
     const int32_t* block_tables;
     const int32_t* row_seq;
     const int32_t* row_kv_len;
     int max_blocks;
-    // Multi-position form: unit k covers the pair_count[k] row groups from
-    // pair_first[k] on, all of one sequence (num_pairs[0] units).
-    const int32_t* pair_first;
-    const int32_t* pair_count;
-    const int32_t* num_pairs;
+    // The step's plan (paged_plan_kernel): plan[0] units, then a sentinel
+    // whose start is the total work plan[1]; the unit of each row group.
+    const PagedUnit* units;
+    const int32_t* unit_of_group;
+    const int32_t* plan;
 };
+// Workgroup s of G takes the work positions [bound(s), bound(s + 1)); a pass
+// belongs to the segment holding its first work position.
+__device__ __forceinline__ int seg_bound(int s, int total, int G) {
+    return (int)(((long long)s * total) / G);
+}
+// Passes [x0, x1) of an item (start S, n passes of weight w) that begin in
+// the work range [b0, b1).
+__device__ __forceinline__ void item_passes(int S, int n, int w, int b0, int b1, int& x0,
+                                            int& x1) {
+    x0 = S >= b0 ? 0 : (b0 - S + w - 1) / w;
+    x1 = S >= b1 ? 0 : min(n, (b1 - S + w - 1) / w);
+}
 
 // Workgroup barrier for LDS traffic only: waits for this wave's LDS accesses,
 // not for its outstanding global loads (which __syncthreads() would drain).
@@ -319,682 +340,722 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     static_assert(sizeof(float) * kWaves * kMoRows * 128 <= sizeof(lut), "merge space");
     float(*mo)[kMoRows][128] = reinterpret_cast<float(*)[kMoRows][128]>(&lut[0][0]);
 
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
-    const int i = lane & 15, gq = lane >> 4;
-    // Work item of this workgroup.  Paged rows: items are ordered row group
-    // fastest (the row groups of one sequence's new tokens are adjacent and
-    // read the same pages), cut into runs of kRun items, and the runs are dealt
-    // to the 8 XCDs round robin (workgroup b runs on XCD b % 8): a run's
-    // workgroups share one XCD and start together, so its L2 serves the
-    // repeated page reads, and every XCD gets an even share of the splits.
-    // The partial's slot in the workspace (pid) keeps the split-fastest
-    // order the combine reads.
-    int split, h, rg, npos = 1;
-    size_t pid = blockIdx.x;
-    if constexpr (PAGED) {
-        constexpr int kRun = 8;
-        // work units: row groups, or pairs of them (NP = 2; the grid is sized
-        // for one unit per group, the items past the pair count exit)
-        const int units = NP >= 2 ? __builtin_amdgcn_readfirstlane(pr.num_pairs[0])
-                                  : (num_queries + kRows - 1) / kRows;
-        const int items = num_splits * g.H * units;
-        const int x = blockIdx.x & 7, li = blockIdx.x >> 3;
-        const int v = (((li / kRun) * 8 + x) * kRun) + li % kRun;
-        if (v >= items) return;
-        const int unit = v % units;
-        h = (v / units) % g.H;
-        split = v / (units * g.H);
-        if constexpr (NP >= 2) {
-            rg = __builtin_amdgcn_readfirstlane(pr.pair_first[unit]);
-            npos = __builtin_amdgcn_readfirstlane(pr.pair_count[unit]);
-        } else {
-            rg = unit;
-        }
-        pid = (size_t)split + (size_t)num_splits * (h + (size_t)g.H * rg);
-    } else {
-        split = blockIdx.x % num_splits;
-        const int hr = blockIdx.x / num_splits;
-        h = hr % g.H;
-        rg = hr / g.H;
-    }
     const float ck = inv * kLog2e / (PROD ? kAlphaK : kAlphaV);  // logit scale per unit ks
     const float cr = inv * kLog2e;                                 // residual: ks * re
-    const int t_begin = split * tokens_per_split;
-    // Paged rows: the group's sequence and per-row kv lengths (causal limit);
-    // rowlen is that of this lane's MFMA column row.  A split past every row's
-    // length has no partial (the combine does not read it).
-    int kv_end = num_kv_tokens, seq = 0;
-    // per position: this lane's column row length, the group's longest and
-    // shortest row
-    int rowlen[NP] = {}, gend[NP] = {}, gmin[NP] = {};
-    // NP >= 2: this lane's column row length per tile and the shortest live row
-    int rl_col[NT] = {}, gmin_live = 0x7fffffff;
-    if constexpr (PAGED) {
-        kv_end = 0;
+    // One work item: kv head h, row groups rg .. rg + npos - 1, tokens
+    // [t_begin, t_cap) (paged: and below each row's length), partial slot pid.
+    // (tid is a parameter so that a caller looping over items can keep the
+    // per-thread values derived from it from being hoisted out of the loop
+    // and held across the token loop.)
+    auto item = [&](const int tid, const int h, const int rg, const int npos, const int t_begin,
+                    const int t_cap, const size_t pid) {
+        const int lane = tid & 63;
+        const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
+        const int i = lane & 15, gq = lane >> 4;
+        // Paged rows: the group's sequence and per-row kv lengths (causal limit);
+        // rowlen is that of this lane's MFMA column row.  A piece past every row's
+        // length has no partial (the combine does not read it).
+        int kv_end = num_kv_tokens, seq = 0;
+        // per position: this lane's column row length, the group's longest and
+        // shortest row
+        int rowlen[NP] = {}, gend[NP] = {}, gmin[NP] = {};
+        // NP >= 2: this lane's column row length per tile and the shortest live row
+        int rl_col[NT] = {}, gmin_live = 0x7fffffff;
+        if constexpr (PAGED) {
+            kv_end = 0;
 #pragma unroll
-        for (int p = 0; p < NP; ++p) {
-            const int rr = (rg + p) * kRows + (lane & 7);
-            const int lv = p < npos && rr < num_queries ? pr.row_kv_len[rr] : 0;
-            rowlen[p] = __shfl(lv, i >> 1);
-            const int lc = __shfl(lv, i & 7);
-            if (NP >= 2 && (i >> 3) == (p & 1)) rl_col[p >> 1] = lc;
-            int m = max(lv, __shfl_xor(lv, 1)), n = min(lv, __shfl_xor(lv, 1));
-            m = max(m, __shfl_xor(m, 2));
-            n = min(n, __shfl_xor(n, 2));
-            m = max(m, __shfl_xor(m, 4));
-            n = min(n, __shfl_xor(n, 4));
-            gend[p] = __builtin_amdgcn_readfirstlane(m);
-            gmin[p] = __builtin_amdgcn_readfirstlane(n);
-            kv_end = max(kv_end, gend[p]);
-            if (p < npos) gmin_live = min(gmin_live, gmin[p]);
-        }
-        seq = __builtin_amdgcn_readfirstlane(pr.row_seq[rg * kRows]);
-        if (t_begin >= kv_end) return;  // uniform over the workgroup, before any barrier
-    }
-    const int t_end = min(kv_end, t_begin + tokens_per_split);
-    const int ntile = (npos + 1) >> 1;  // NP >= 2: tiles of 16 columns in use
-
-    // A chunk's codes and per-token scales, loaded ahead of its compute.
-    struct Chunk {
-        uint4 kw[kTiles];        // K: tile tau, token 16*tau + i, bytes [16gq, 16gq + 16)
-        uint32_t vw[kSteps][8];  // V: step p, k-index 8gq + e (token below), dword i
-        uint16_t ks, re, vs;  // this lane's token's fp16 scales (raw: still in flight)
-        bool valid;
-    };
-    // Token of this lane in the chunk at t0 and its slot (the load is issued
-    // here and consumed by fetch, so other work can run in between).  Lanes
-    // past the range re-read the last token of the range.
-    auto load_slot = [&](int t0) -> int {
-        const int t = max(min(t0 + (lane & (kChunk - 1)), t_end - 1), 0);
-        if constexpr (PAGED) {  // token t of sequence seq: page table entry t / B
-            const int blk = min(g.bs_shift >= 0 ? t >> g.bs_shift : t / g.block_size,
-                                pr.max_blocks - 1);
-            const int page = pr.block_tables[(size_t)seq * pr.max_blocks + blk];
-            return page < 0 ? -1 : page * g.block_size + (t - blk * g.block_size);
-        } else {
-            return slots[t];
-        }
-    };
-    // slot -> cell offsets (exchanged through LDS) -> scale and code loads,
-    // issued for every lane.  Tokens past the range or with a negative slot
-    // read the first bytes of the query instead (always valid memory: the
-    // offset of the query from the pool) and get bias -inf.  The loads stay in
-    // flight until the chunk is computed.
-    const uint64_t dummy_off =
-        (uint64_t)(reinterpret_cast<uintptr_t>(query) - reinterpret_cast<uintptr_t>(pool));
-    auto fetch = [&](int t0, int slot, Chunk& c) {
-        c.valid = t0 + (lane & (kChunk - 1)) < t_end && slot >= 0;
-        int page, tib;
-        split_slot(c.valid ? slot : 0, g, page, tib);
-        const uint64_t cell = (uint64_t)(tib * g.H + h);
-        const uint64_t pb = (uint64_t)page * g.page_size;
-        // Byte offsets from pool (integer selects: no branches around loads).
-        // (distinct dummy bytes per field, so the three loads stay separate)
-        const uint64_t so = pb + cell * g.scale_stride;
-        c.ks = ld_u16(pool + (c.valid ? so + g.ks_off : dummy_off));
-        c.vs = ld_u16(pool + (c.valid ? so + g.vs_off : dummy_off + 2));
-        c.re = PROD ? ld_u16(pool + (c.valid ? so + g.kres_off : dummy_off + 4)) : (uint16_t)0;
-        // (with 32-token chunks lanes l and l + 32 hold the same token)
-        // K row: code_stride bytes, or QJL's D/8 = 16 sign bytes
-        const uint64_t kstride = QJL ? 16u : (uint64_t)g.code_stride;
-        tko[w][lane & (kChunk - 1)] = c.valid ? pb + g.kc_off + cell * kstride : dummy_off;
-        tvo[w][lane & (kChunk - 1)] = c.valid ? pb + g.vc_off + cell * g.code_stride : dummy_off;
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-        for (int tau = 0; tau < kTiles; ++tau) {
-            if constexpr (QJL)  // sign bytes 4gq .. 4gq + 3: k-steps 0 .. 3
-                c.kw[tau] = make_uint4(
-                    *reinterpret_cast<const uint32_t*>(pool + (tko[w][16 * tau + i] + 4 * gq)), 0u,
-                    0u, 0u);
-            else
-                c.kw[tau] = *reinterpret_cast<const uint4*>(pool + (tko[w][16 * tau + i] + 16 * gq));
-        }
-        // k-step p covers tiles 2p, 2p+1; k-index 8gq + e is token
-        // 32p + 4gq + e (e < 4) or 32p + 16 + 4gq + (e - 4).
-#pragma unroll
-        for (int p = 0; p < kSteps; ++p)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int tok = 32 * p + (e < 4 ? 4 * gq + e : 16 + 4 * gq + (e - 4));
-                c.vw[p][e] = *reinterpret_cast<const uint32_t*>(pool + (tvo[w][tok] + 4 * i));
+            for (int p = 0; p < NP; ++p) {
+                const int rr = (rg + p) * kRows + (lane & 7);
+                const int lv = p < npos && rr < num_queries ? pr.row_kv_len[rr] : 0;
+                rowlen[p] = __shfl(lv, i >> 1);
+                const int lc = __shfl(lv, i & 7);
+                if (NP >= 2 && (i >> 3) == (p & 1)) rl_col[p >> 1] = lc;
+                int m = max(lv, __shfl_xor(lv, 1)), n = min(lv, __shfl_xor(lv, 1));
+                m = max(m, __shfl_xor(m, 2));
+                n = min(n, __shfl_xor(n, 2));
+                m = max(m, __shfl_xor(m, 4));
+                n = min(n, __shfl_xor(n, 4));
+                gend[p] = __builtin_amdgcn_readfirstlane(m);
+                gmin[p] = __builtin_amdgcn_readfirstlane(n);
+                kv_end = max(kv_end, gend[p]);
+                if (p < npos) gmin_live = min(gmin_live, gmin[p]);
             }
-    };
+            seq = __builtin_amdgcn_readfirstlane(pr.row_seq[rg * kRows]);
+            if (t_begin >= kv_end) return;  // uniform over the workgroup, before any barrier
+        }
+        const int t_end = min(kv_end, t_cap);
+        const int ntile = (npos + 1) >> 1;  // NP >= 2: tiles of 16 columns in use
 
-    // Issue order matters (the vector-memory counter is in order): query
-    // rows first, then the first chunk's slots; the decode tables are built
-    // while they are in flight.
-    constexpr int kQPerWave = kR / kWaves;
-    static_assert(kR % kWaves == 0, "rows per wave");
-    // Row r of the workgroup is row r % 8 of group rg + r / 8 (consecutive
-    // groups: rows rg * 8 + r).
-    uint32_t qraw[kQPerWave];
+        // A chunk's codes and per-token scales, loaded ahead of its compute.
+        struct Chunk {
+            uint4 kw[kTiles];        // K: tile tau, token 16*tau + i, bytes [16gq, 16gq + 16)
+            uint32_t vw[kSteps][8];  // V: step p, k-index 8gq + e (token below), dword i
+            uint16_t ks, re, vs;  // this lane's token's fp16 scales (raw: still in flight)
+            bool valid;
+        };
+        // Token of this lane in the chunk at t0 and its slot (the load is issued
+        // here and consumed by fetch, so other work can run in between).  Lanes
+        // past the range re-read the last token of the range.
+        auto load_slot = [&](int t0) -> int {
+            const int t = max(min(t0 + (lane & (kChunk - 1)), t_end - 1), 0);
+            if constexpr (PAGED) {  // token t of sequence seq: page table entry t / B
+                const int blk = min(g.bs_shift >= 0 ? t >> g.bs_shift : t / g.block_size,
+                                    pr.max_blocks - 1);
+                const int page = pr.block_tables[(size_t)seq * pr.max_blocks + blk];
+                return page < 0 ? -1 : page * g.block_size + (t - blk * g.block_size);
+            } else {
+                return slots[t];
+            }
+        };
+        // slot -> cell offsets (exchanged through LDS) -> scale and code loads,
+        // issued for every lane.  Tokens past the range or with a negative slot
+        // read the first bytes of the query instead (always valid memory: the
+        // offset of the query from the pool) and get bias -inf.  The loads stay in
+        // flight until the chunk is computed.
+        const uint64_t dummy_off =
+            (uint64_t)(reinterpret_cast<uintptr_t>(query) - reinterpret_cast<uintptr_t>(pool));
+        auto fetch = [&](int t0, int slot, Chunk& c) {
+            c.valid = t0 + (lane & (kChunk - 1)) < t_end && slot >= 0;
+            int page, tib;
+            split_slot(c.valid ? slot : 0, g, page, tib);
+            const uint64_t cell = (uint64_t)(tib * g.H + h);
+            const uint64_t pb = (uint64_t)page * g.page_size;
+            // Byte offsets from pool (integer selects: no branches around loads).
+            // (distinct dummy bytes per field, so the three loads stay separate)
+            const uint64_t so = pb + cell * g.scale_stride;
+            c.ks = ld_u16(pool + (c.valid ? so + g.ks_off : dummy_off));
+            c.vs = ld_u16(pool + (c.valid ? so + g.vs_off : dummy_off + 2));
+            c.re = PROD ? ld_u16(pool + (c.valid ? so + g.kres_off : dummy_off + 4)) : (uint16_t)0;
+            // (with 32-token chunks lanes l and l + 32 hold the same token)
+            // K row: code_stride bytes, or QJL's D/8 = 16 sign bytes
+            const uint64_t kstride = QJL ? 16u : (uint64_t)g.code_stride;
+            tko[w][lane & (kChunk - 1)] = c.valid ? pb + g.kc_off + cell * kstride : dummy_off;
+            tvo[w][lane & (kChunk - 1)] = c.valid ? pb + g.vc_off + cell * g.code_stride : dummy_off;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-    for (int k = 0; k < kQPerWave; ++k) {
-        const int qi = min(rg * kRows + w + k * kWaves, num_queries - 1);
-        qraw[k] = *reinterpret_cast<const uint32_t*>(query + ((size_t)qi * g.H + h) * 128 +
-                                                      2 * lane);
-    }
-    int t0 = t_begin + w * kChunk;
-    const int slot0 = load_slot(t0);
+            for (int tau = 0; tau < kTiles; ++tau) {
+                if constexpr (QJL)  // sign bytes 4gq .. 4gq + 3: k-steps 0 .. 3
+                    c.kw[tau] = make_uint4(
+                        *reinterpret_cast<const uint32_t*>(pool + (tko[w][16 * tau + i] + 4 * gq)), 0u,
+                        0u, 0u);
+                else
+                    c.kw[tau] = *reinterpret_cast<const uint4*>(pool + (tko[w][16 * tau + i] + 16 * gq));
+            }
+            // k-step p covers tiles 2p, 2p+1; k-index 8gq + e is token
+            // 32p + 4gq + e (e < 4) or 32p + 16 + 4gq + (e - 4).
+#pragma unroll
+            for (int p = 0; p < kSteps; ++p)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int tok = 32 * p + (e < 4 ? 4 * gq + e : 16 + 4 * gq + (e - 4));
+                    c.vw[p][e] = *reinterpret_cast<const uint32_t*>(pool + (tvo[w][tok] + 4 * i));
+                }
+        };
 
-    // Decode tables: one entry per thread into a staging row (waves 0-3).
-    if (w < 4) {
-        const int lo = tid & 15, hi = tid >> 4;
-        const float vlo = pick(kV4, lo), vhi = pick(kV4, hi);
-        const uint32_t vv = pack_h2(kAlphaV * vlo, kAlphaV * vhi);
-        const uint32_t kv =
-            PROD ? pack_h2(kAlphaK * pick(kK3, lo & 7), kAlphaK * pick(kK3, hi & 7)) : vv;
-        kstage[tid] = kv;
-        vstage[tid] = vv;
-    }
-    // Query halves to fp32 (times the sign flip) before the code loads are
-    // issued, so waiting for them never waits for the codes.
-    float qf[kQPerWave][2];
-    {
-        const float sh = (!QJL && (h & 1)) ? -1.0f : 1.0f;
+        // Issue order matters (the vector-memory counter is in order): query
+        // rows first, then the first chunk's slots; the decode tables are built
+        // while they are in flight.
+        constexpr int kQPerWave = kR / kWaves;
+        static_assert(kR % kWaves == 0, "rows per wave");
+        // Row r of the workgroup is row r % 8 of group rg + r / 8 (consecutive
+        // groups: rows rg * 8 + r).
+        uint32_t qraw[kQPerWave];
 #pragma unroll
         for (int k = 0; k < kQPerWave; ++k) {
-            qf[k][0] = h2f(qraw[k] & 0xffff) * sh;
-            qf[k][1] = h2f(qraw[k] >> 16) * (-sh);
+            const int qi = min(rg * kRows + w + k * kWaves, num_queries - 1);
+            qraw[k] = *reinterpret_cast<const uint32_t*>(query + ((size_t)qi * g.H + h) * 128 +
+                                                          2 * lane);
         }
-    }
-    Chunk cur;
-    fetch(t0, slot0, cur);  // in flight during the setup below (empty waves: all invalid)
+        int t0 = t_begin + w * kChunk;
+        const int slot0 = load_slot(t0);
 
-    // Rotated query rows of this group (wave w: rows w, w + NW, ...):
-    // qrot = WHT(q * s) * inv.
+        // Decode tables: one entry per thread into a staging row (waves 0-3).
+        if (w < 4) {
+            const int lo = tid & 15, hi = tid >> 4;
+            const float vlo = pick(kV4, lo), vhi = pick(kV4, hi);
+            const uint32_t vv = pack_h2(kAlphaV * vlo, kAlphaV * vhi);
+            const uint32_t kv =
+                PROD ? pack_h2(kAlphaK * pick(kK3, lo & 7), kAlphaK * pick(kK3, hi & 7)) : vv;
+            kstage[tid] = kv;
+            vstage[tid] = vv;
+        }
+        // Query halves to fp32 (times the sign flip) before the code loads are
+        // issued, so waiting for them never waits for the codes.
+        float qf[kQPerWave][2];
+        {
+            const float sh = (!QJL && (h & 1)) ? -1.0f : 1.0f;
 #pragma unroll
-    for (int k = 0; k < kQPerWave; ++k) {
-        const int r = w + k * kWaves;
-        if (NP >= 2 && r / kRows >= 2 * ntile) continue;  // an unused tile (wave-uniform)
-        float q0 = qf[k][0], q1 = qf[k][1];
-        wht_pair<64>(q0, q1, lane);
-        const bool live = r / kRows < npos && rg * kRows + r < num_queries;
-        qs[r][2 * lane] = live ? q0 * inv : 0.0f;
-        qs[r][2 * lane + 1] = live ? q1 * inv : 0.0f;
-    }
-    lds_barrier();  // staged table rows and rotated queries visible
+            for (int k = 0; k < kQPerWave; ++k) {
+                qf[k][0] = h2f(qraw[k] & 0xffff) * sh;
+                qf[k][1] = h2f(qraw[k] >> 16) * (-sh);
+            }
+        }
+        Chunk cur;
+        fetch(t0, slot0, cur);  // in flight during the setup below (empty waves: all invalid)
 
-    // Every wave replicates staged rows with conflict-free 1 KB stores.
-    {
-        constexpr int kRowsPerWave = 256 / kWaves;
+        // Rotated query rows of this group (wave w: rows w, w + NW, ...):
+        // qrot = WHT(q * s) * inv.
 #pragma unroll
-        for (int k = 0; k < kRowsPerWave; k += 4) {
-            const int e = w * kRowsPerWave + k + (lane >> 4);
-            if constexpr (QJL) {  // K half: 8 copies of the fp16 +-1 octet of sign byte e
-                uint4 v4;
-                if (lane & 8) {
-                    const uint32_t v = vstage[e];
-                    v4 = make_uint4(v, v, v, v);
+        for (int k = 0; k < kQPerWave; ++k) {
+            const int r = w + k * kWaves;
+            if (NP >= 2 && r / kRows >= 2 * ntile) continue;  // an unused tile (wave-uniform)
+            float q0 = qf[k][0], q1 = qf[k][1];
+            wht_pair<64>(q0, q1, lane);
+            const bool live = r / kRows < npos && rg * kRows + r < num_queries;
+            qs[r][2 * lane] = live ? q0 * inv : 0.0f;
+            qs[r][2 * lane + 1] = live ? q1 * inv : 0.0f;
+        }
+        lds_barrier();  // staged table rows and rotated queries visible
+
+        // Every wave replicates staged rows with conflict-free 1 KB stores.
+        {
+            constexpr int kRowsPerWave = 256 / kWaves;
+#pragma unroll
+            for (int k = 0; k < kRowsPerWave; k += 4) {
+                const int e = w * kRowsPerWave + k + (lane >> 4);
+                if constexpr (QJL) {  // K half: 8 copies of the fp16 +-1 octet of sign byte e
+                    uint4 v4;
+                    if (lane & 8) {
+                        const uint32_t v = vstage[e];
+                        v4 = make_uint4(v, v, v, v);
+                    } else {
+                        uint32_t wd[4];
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            wd[q] = ((e >> (2 * q)) & 1 ? 0x3C00u : 0xBC00u) |
+                                    ((e >> (2 * q + 1)) & 1 ? 0x3C000000u : 0xBC000000u);
+                        v4 = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+                    }
+                    *reinterpret_cast<uint4*>(&lut[e][4 * (lane & 15)]) = v4;
                 } else {
-                    uint32_t wd[4];
-#pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        wd[q] = ((e >> (2 * q)) & 1 ? 0x3C00u : 0xBC00u) |
-                                ((e >> (2 * q + 1)) & 1 ? 0x3C000000u : 0xBC000000u);
-                    v4 = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+                    const uint32_t v = (lane & 8) ? vstage[e] : kstage[e];  // words 32..63: V
+                    *reinterpret_cast<uint4*>(&lut[e][4 * (lane & 15)]) = make_uint4(v, v, v, v);
                 }
-                *reinterpret_cast<uint4*>(&lut[e][4 * (lane & 15)]) = v4;
-            } else {
-                const uint32_t v = (lane & 8) ? vstage[e] : kstage[e];  // words 32..63: V
-                *reinterpret_cast<uint4*>(&lut[e][4 * (lane & 15)]) = make_uint4(v, v, v, v);
             }
         }
-    }
-    // B operand of QK, built once per workgroup: column i = row i/2, hi (i
-    // even) or lo (i odd) part; k-index 8*gq + e of step s is d = 32*gq + 8*s + e.
-    const bool lo_col = (i & 1) != 0;
-    for (int ps = w; ps < 4 * NP; ps += kWaves) {
-        const int p = ps >> 2, s = ps & 3;
-        if (NP >= 2 && (p >> 1) >= ntile) break;  // unused tiles (never read)
-        half8 b;
-        if constexpr (NP >= 2) {  // tile p / 2, part p % 2 (hi, lo) of column i's row, k-step s
+        // B operand of QK, built once per workgroup: column i = row i/2, hi (i
+        // even) or lo (i odd) part; k-index 8*gq + e of step s is d = 32*gq + 8*s + e.
+        const bool lo_col = (i & 1) != 0;
+        for (int ps = w; ps < 4 * NP; ps += kWaves) {
+            const int p = ps >> 2, s = ps & 3;
+            if (NP >= 2 && (p >> 1) >= ntile) break;  // unused tiles (never read)
+            half8 b;
+            if constexpr (NP >= 2) {  // tile p / 2, part p % 2 (hi, lo) of column i's row, k-step s
 #pragma unroll
-            for (int e = 0; e < 8; ++e)
-                b[e] = hi_lo(qs[16 * (p >> 1) + i][32 * gq + 8 * s + e], (p & 1) != 0);
-        } else {  // position p, k-step s; column parity picks hi or lo
+                for (int e = 0; e < 8; ++e)
+                    b[e] = hi_lo(qs[16 * (p >> 1) + i][32 * gq + 8 * s + e], (p & 1) != 0);
+            } else {  // position p, k-step s; column parity picks hi or lo
 #pragma unroll
-            for (int e = 0; e < 8; ++e)
-                b[e] = hi_lo(qs[p * kRows + (i >> 1)][32 * gq + 8 * s + e], lo_col);
+                for (int e = 0; e < 8; ++e)
+                    b[e] = hi_lo(qs[p * kRows + (i >> 1)][32 * gq + 8 * s + e], lo_col);
+            }
+            bqs[p][s][lane] = __builtin_bit_cast(uint4, b);
         }
-        bqs[p][s][lane] = __builtin_bit_cast(uint4, b);
-    }
-    lds_barrier();
-    half8 bq[NP][4];
+        lds_barrier();
+        // NP = 1: the B operands in registers; NP >= 2 reads them from LDS per
+        // k-step (64 registers fewer in the two-tile loop).
+        half8 bq[1][4];
+        if constexpr (NP == 1) {
 #pragma unroll
-    for (int p = 0; p < NP; ++p)
-#pragma unroll
-        for (int s = 0; s < 4; ++s) bq[p][s] = __builtin_bit_cast(half8, bqs[p][s][lane]);
-    // Byte address of this lane's copy of entry 0 of each table; a lookup
-    // puts the code byte into byte 1 (entry stride 256 B) with one v_perm.
-    const uint32_t lutk = (uint32_t)reinterpret_cast<uintptr_t>((lds_u32*)&lut[0][lane & 31]);
-    const uint32_t lutv = lutk + 128u;
-    const uint32_t lut_hi = lutk & 0xFF00u;  // byte 1 of the base, re-added after the perm
-    auto lookup = [&](uint32_t word, int b, int table) -> uint32_t {
-        const uint32_t base = table ? lutv : lutk;
-        const uint32_t a = __builtin_amdgcn_perm(word, base, 0x03020000u | ((4u + b) << 8)) + lut_hi;
-        return *reinterpret_cast<const lds_u32*>(a);
-    };
-    // QJL: the fp16 +-1 octet of sign byte b of word (copy lane % 8).
-    const uint32_t lutq =
-        (uint32_t)reinterpret_cast<uintptr_t>((lds_u32*)&lut[0][4 * (lane & 7)]);
-    auto signs = [&](uint32_t word, int b) -> half8 {
-        const uint32_t a =
-            __builtin_amdgcn_perm(word, lutq, 0x03020000u | ((4u + b) << 8)) + (lutq & 0xFF00u);
-        typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
-        return __builtin_bit_cast(half8, *reinterpret_cast<const lds_u32x4*>(a));
-    };
+            for (int s = 0; s < 4; ++s) bq[0][s] = __builtin_bit_cast(half8, bqs[0][s][lane]);
+        }
+        // Byte address of this lane's copy of entry 0 of each table; a lookup
+        // puts the code byte into byte 1 (entry stride 256 B) with one v_perm.
+        const uint32_t lutk = (uint32_t)reinterpret_cast<uintptr_t>((lds_u32*)&lut[0][lane & 31]);
+        const uint32_t lutv = lutk + 128u;
+        const uint32_t lut_hi = lutk & 0xFF00u;  // byte 1 of the base, re-added after the perm
+        auto lookup = [&](uint32_t word, int b, int table) -> uint32_t {
+            const uint32_t base = table ? lutv : lutk;
+            const uint32_t a = __builtin_amdgcn_perm(word, base, 0x03020000u | ((4u + b) << 8)) + lut_hi;
+            return *reinterpret_cast<const lds_u32*>(a);
+        };
+        // QJL: the fp16 +-1 octet of sign byte b of word (copy lane % 8).
+        const uint32_t lutq =
+            (uint32_t)reinterpret_cast<uintptr_t>((lds_u32*)&lut[0][4 * (lane & 7)]);
+        auto signs = [&](uint32_t word, int b) -> half8 {
+            const uint32_t a =
+                __builtin_amdgcn_perm(word, lutq, 0x03020000u | ((4u + b) << 8)) + (lutq & 0xFF00u);
+            typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+            return __builtin_bit_cast(half8, *reinterpret_cast<const lds_u32x4*>(a));
+        };
 
-    float m_run[NP], l_run[NP];
-    f32x4 acc[NP][8];
-#pragma unroll
-    for (int p = 0; p < NP; ++p) {
-        m_run[p] = kInitMax;
-        l_run[p] = 0.0f;
-#pragma unroll
-        for (int v = 0; v < 8; ++v) acc[p][v] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    }
-    bool first = true;
-    int slot_nx = load_slot(t0 + kWaves * kChunk);
-
-    // The chunk loop, for the positions the workgroup has (a pair unit of a
-    // single group runs the one-position loop).
-    auto chunk_loop = [&](auto npa) {
-        constexpr int NPA = decltype(npa)::value;
-        while (t0 < t_end) {  // wave-uniform
-            const uint4* kw = cur.kw;
-            const uint32_t(*vw)[8] = cur.vw;
-            {
-                const float ks = h2f(cur.ks), vs = h2f(cur.vs), re = PROD ? h2f(cur.re) : 0.0f;
-                const float4 sc = QJL ? make_float4(0.0f, ks * kLog2e, vs, 0.0f)
-                                      : make_float4(ks * ck, ks * re * cr, vs, 0.0f);
-                tsc[w][lane & (kChunk - 1)] = cur.valid ? sc : make_float4(0.f, 0.f, 0.f, -INFINITY);
-            }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            Chunk nxt;
-            const int t1 = t0 + kWaves * kChunk;
-            if (t1 < t_end) {  // codes of the next chunk, slots of the one after
-                fetch(t1, slot_nx, nxt);
-                slot_nx = load_slot(t1 + kWaves * kChunk);
-            }
-
-            // QK: one decoded A operand per k-step, an MFMA per position
-            f32x4 cb[NPA][kTiles], cs[NPA][kTiles];
-    #pragma unroll
-            for (int tau = 0; tau < kTiles; ++tau) {
-    #pragma unroll
-                for (int p = 0; p < NPA; ++p) {
-                    cb[p][tau] = (f32x4){0.f, 0.f, 0.f, 0.f};
-                    cs[p][tau] = cb[p][tau];
-                }
-                const uint32_t wd[4] = {kw[tau].x, kw[tau].y, kw[tau].z, kw[tau].w};
-    #pragma unroll
-                for (int s = 0; s < 4; ++s) {
-                    if constexpr (QJL) {  // sign byte s of the lane's word
-                        const half8 sa = signs(wd[0], s);
-    #pragma unroll
-                        for (int p = 0; p < NPA; ++p)
-                            cs[p][tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sa, bq[p][s],
-                                                                                cs[p][tau], 0, 0, 0);
-                        continue;
-                    }
-                    const half8 a = as_h8(lookup(wd[s], 0, 0), lookup(wd[s], 1, 0),
-                                          lookup(wd[s], 2, 0), lookup(wd[s], 3, 0));
-    #pragma unroll
-                    for (int p = 0; p < NPA; ++p)
-                        cb[p][tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[p][s], cb[p][tau],
-                                                                            0, 0, 0);
-                    if (PROD) {
-                        // Residual signs (nibble bit 3: 1 -> +1) as fp16 pairs in
-                        // registers: high bytes 0x3C / 0xBC, low bytes 0.
-                        const uint32_t he = ((wd[s] << 4) & 0x80808080u) ^ 0xBCBCBCBCu;  // even d
-                        const uint32_t ho = (wd[s] & 0x80808080u) ^ 0xBCBCBCBCu;         // odd d
-                        const half8 sa = as_h8(__builtin_amdgcn_perm(ho, he, 0x040C000Cu),
-                                               __builtin_amdgcn_perm(ho, he, 0x050C010Cu),
-                                               __builtin_amdgcn_perm(ho, he, 0x060C020Cu),
-                                               __builtin_amdgcn_perm(ho, he, 0x070C030Cu));
-    #pragma unroll
-                        for (int p = 0; p < NPA; ++p)
-                            cs[p][tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sa, bq[p][s],
-                                                                                cs[p][tau], 0, 0, 0);
-                    }
-                }
-            }
-            // Logits (base 2) of tokens 16*tau + 4*gq + e; hi + lo columns summed.
-            float lg[NPA][kTiles][4];
-    #pragma unroll
-            for (int p = 0; p < NPA; ++p) {
-                // rows shorter than the chunk's end need the causal mask
-                const bool masked = PAGED && t0 + kChunk > gmin[p];
-                float mloc = -INFINITY;
-    #pragma unroll
-                for (int tau = 0; tau < kTiles; ++tau)
-    #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float4 sc = tsc[w][16 * tau + 4 * gq + e];
-                        if constexpr (QJL) {
-                            const float sr = cs[p][tau][e] + quad_xor<1>(cs[p][tau][e]);
-                            lg[p][tau][e] = fmaf(sr, sc.y, sc.w);
-                        } else {
-                            const float sb = cb[p][tau][e] + quad_xor<1>(cb[p][tau][e]);
-                            const float sr =
-                                PROD ? cs[p][tau][e] + quad_xor<1>(cs[p][tau][e]) : 0.0f;
-                            lg[p][tau][e] = fmaf(sb, sc.x, fmaf(sr, sc.y, sc.w));
-                        }
-                        if (masked)  // causal limit of this column's row
-                            if (t0 + 16 * tau + 4 * gq + e >= rowlen[p]) lg[p][tau][e] = -INFINITY;
-                        mloc = fmaxf(mloc, lg[p][tau][e]);
-                    }
-                mloc = fmaxf(mloc, lane_xor<16>(mloc));
-                mloc = fmaxf(mloc, lane_xor<32>(mloc));
-                // v_exp_f32 without denormal handling: arguments are <= 0 and a
-                // weight below 2^-126 of the running maximum is negligible.
-                const float m_new = fmaxf(m_run[p], mloc);
-                const float alpha = first ? 0.0f : __builtin_amdgcn_exp2f(m_run[p] - m_new);
-                m_run[p] = m_new;
-                float lsum = 0.0f;
-    #pragma unroll
-                for (int tau = 0; tau < kTiles; ++tau)
-    #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        lg[p][tau][e] = __builtin_amdgcn_exp2f(lg[p][tau][e] - m_new);
-                        lsum += lg[p][tau][e];
-                    }
-                l_run[p] = l_run[p] * alpha + lsum;
-                if (!first && __any(alpha != 1.0f)) {
-                    // acc lane (d, gq) holds columns 4gq..4gq+3 = rows 2gq, 2gq+1.
-                    const float a0 = __shfl(alpha, 4 * gq), a1 = __shfl(alpha, 4 * gq + 2);
-    #pragma unroll
-                    for (int v = 0; v < 8; ++v) {
-                        acc[p][v][0] *= a0;
-                        acc[p][v][1] *= a0;
-                        acc[p][v][2] *= a1;
-                        acc[p][v][3] *= a1;
-                    }
-                }
-            }
-            // PV: one decoded B operand per N-tile, an MFMA per position
-    #pragma unroll
-            for (int st = 0; st < kSteps; ++st) {
-                half8 ap[NPA];
-    #pragma unroll
-                for (int p = 0; p < NPA; ++p)
-    #pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const int tau = 2 * st + (e >> 2), ee = e & 3;
-                        const float vs = tsc[w][16 * tau + 4 * gq + ee].z;
-                        ap[p][e] = hi_lo(lg[p][tau][ee] * vs, lo_col);
-                    }
-                uint32_t bv[8][4];  // [N-tile v = d - 8i][token pair]
-    #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const uint32_t we = vw[st][2 * q], wo = vw[st][2 * q + 1];
-                    const uint32_t lob = (we & 0x0F0F0F0Fu) | ((wo & 0x0F0F0F0Fu) << 4);
-                    const uint32_t hib = ((we >> 4) & 0x0F0F0F0Fu) | (wo & 0xF0F0F0F0u);
-    #pragma unroll
-                    for (int b = 0; b < 4; ++b) {
-                        bv[2 * b][q] = lookup(lob, b, 1);
-                        bv[2 * b + 1][q] = lookup(hib, b, 1);
-                    }
-                }
-    #pragma unroll
-                for (int v = 0; v < 8; ++v) {
-                    const half8 bvv = as_h8(bv[v][0], bv[v][1], bv[v][2], bv[v][3]);
-    #pragma unroll
-                    for (int p = 0; p < NPA; ++p)
-                        acc[p][v] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ap[p], bvv, acc[p][v], 0, 0,
-                                                                           0);
-                }
-            }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            cur = nxt;
-            t0 = t1;
-            first = false;
-        }
-    };
-    // NP >= 2: one softmax state per lane and tile (its column's row), hi and
-    // lo stacked along the reductions.  A unit with fewer positions runs the
-    // loop over the tiles it needs; a tile's unused columns compute on zero
-    // queries and are dropped.
-    float m_col[NT], l_col[NT];
-    f32x4 acc_col[NT][8];
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        m_col[t] = kInitMax;
-        l_col[t] = 0.0f;
-#pragma unroll
-        for (int v = 0; v < 8; ++v) acc_col[t][v] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    }
-    auto stacked_loop = [&](auto nta) {
-        constexpr int NTA = decltype(nta)::value;
-        while (t0 < t_end) {  // wave-uniform
-            const uint4* kw = cur.kw;
-            const uint32_t(*vw)[8] = cur.vw;
-            {
-                const float ks = h2f(cur.ks), vs = h2f(cur.vs), re = PROD ? h2f(cur.re) : 0.0f;
-                tsc[w][lane & (kChunk - 1)] = cur.valid ? make_float4(ks * ck, ks * re * cr, vs, 0.0f)
-                                                        : make_float4(0.f, 0.f, 0.f, -INFINITY);
-            }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            Chunk nxt;
-            const int t1 = t0 + kWaves * kChunk;
-            if (t1 < t_end) {  // codes of the next chunk, slots of the one after
-                fetch(t1, slot_nx, nxt);
-                slot_nx = load_slot(t1 + kWaves * kChunk);
-            }
-            // QK: each decoded A operand against every tile's hi and lo query
-            f32x4 cb[NTA][kTiles], cs[NTA][kTiles];
-#pragma unroll
-            for (int tau = 0; tau < kTiles; ++tau) {
-#pragma unroll
-                for (int t = 0; t < NTA; ++t) {
-                    cb[t][tau] = (f32x4){0.f, 0.f, 0.f, 0.f};
-                    cs[t][tau] = cb[t][tau];
-                }
-                const uint32_t wd[4] = {kw[tau].x, kw[tau].y, kw[tau].z, kw[tau].w};
-#pragma unroll
-                for (int s = 0; s < 4; ++s) {
-                    const half8 a = as_h8(lookup(wd[s], 0, 0), lookup(wd[s], 1, 0),
-                                          lookup(wd[s], 2, 0), lookup(wd[s], 3, 0));
-#pragma unroll
-                    for (int t = 0; t < NTA; ++t) {
-                        cb[t][tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[2 * t][s],
-                                                                            cb[t][tau], 0, 0, 0);
-                        cb[t][tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[2 * t + 1][s],
-                                                                            cb[t][tau], 0, 0, 0);
-                    }
-                    if (PROD) {
-                        const uint32_t he = ((wd[s] << 4) & 0x80808080u) ^ 0xBCBCBCBCu;  // even d
-                        const uint32_t ho = (wd[s] & 0x80808080u) ^ 0xBCBCBCBCu;         // odd d
-                        const half8 sa = as_h8(__builtin_amdgcn_perm(ho, he, 0x040C000Cu),
-                                               __builtin_amdgcn_perm(ho, he, 0x050C010Cu),
-                                               __builtin_amdgcn_perm(ho, he, 0x060C020Cu),
-                                               __builtin_amdgcn_perm(ho, he, 0x070C030Cu));
-#pragma unroll
-                        for (int t = 0; t < NTA; ++t) {
-                            cs[t][tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                                sa, bq[2 * t][s], cs[t][tau], 0, 0, 0);
-                            cs[t][tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                                sa, bq[2 * t + 1][s], cs[t][tau], 0, 0, 0);
-                        }
-                    }
-                }
-            }
-            const bool masked = t0 + kChunk > gmin_live;
-            float lg[NTA][kTiles][4];
-#pragma unroll
-            for (int t = 0; t < NTA; ++t) {
-                // Logits (base 2) of tokens 16*tau + 4*gq + e for this lane's column.
-                float mloc = -INFINITY;
-#pragma unroll
-                for (int tau = 0; tau < kTiles; ++tau)
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float4 sc = tsc[w][16 * tau + 4 * gq + e];
-                        lg[t][tau][e] = fmaf(cb[t][tau][e], sc.x, fmaf(cs[t][tau][e], sc.y, sc.w));
-                        if (masked)
-                            if (t0 + 16 * tau + 4 * gq + e >= rl_col[t]) lg[t][tau][e] = -INFINITY;
-                        mloc = fmaxf(mloc, lg[t][tau][e]);
-                    }
-                mloc = fmaxf(mloc, lane_xor<16>(mloc));
-                mloc = fmaxf(mloc, lane_xor<32>(mloc));
-                const float m_new = fmaxf(m_col[t], mloc);
-                const float alpha = first ? 0.0f : __builtin_amdgcn_exp2f(m_col[t] - m_new);
-                m_col[t] = m_new;
-                float lsum = 0.0f;
-#pragma unroll
-                for (int tau = 0; tau < kTiles; ++tau)
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        lg[t][tau][e] = __builtin_amdgcn_exp2f(lg[t][tau][e] - m_new);
-                        lsum += lg[t][tau][e];
-                    }
-                l_col[t] = l_col[t] * alpha + lsum;
-                if (!first && __any(alpha != 1.0f)) {
-                    // acc lane (d, gq) holds rows 4gq .. 4gq + 3 (columns of lanes 4gq + e)
-                    float a[4];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) a[e] = __shfl(alpha, 4 * gq + e);
-#pragma unroll
-                    for (int v = 0; v < 8; ++v)
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) acc_col[t][v][e] *= a[e];
-                }
-            }
-            // PV: every tile's hi and lo P against each decoded B operand
-#pragma unroll
-            for (int st = 0; st < kSteps; ++st) {
-                half8 ah[NTA], al[NTA];
-#pragma unroll
-                for (int t = 0; t < NTA; ++t)
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const int tau = 2 * st + (e >> 2), ee = e & 3;
-                        const float x = lg[t][tau][ee] * tsc[w][16 * tau + 4 * gq + ee].z;
-                        ah[t][e] = hi_lo(x, false);
-                        al[t][e] = hi_lo(x, true);
-                    }
-                uint32_t bv[8][4];  // [N-tile v = d - 8i][token pair]
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const uint32_t we = vw[st][2 * q], wo = vw[st][2 * q + 1];
-                    const uint32_t lob = (we & 0x0F0F0F0Fu) | ((wo & 0x0F0F0F0Fu) << 4);
-                    const uint32_t hib = ((we >> 4) & 0x0F0F0F0Fu) | (wo & 0xF0F0F0F0u);
-#pragma unroll
-                    for (int b = 0; b < 4; ++b) {
-                        bv[2 * b][q] = lookup(lob, b, 1);
-                        bv[2 * b + 1][q] = lookup(hib, b, 1);
-                    }
-                }
-#pragma unroll
-                for (int v = 0; v < 8; ++v) {
-                    const half8 bvv = as_h8(bv[v][0], bv[v][1], bv[v][2], bv[v][3]);
-#pragma unroll
-                    for (int t = 0; t < NTA; ++t) {
-                        acc_col[t][v] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[t], bvv,
-                                                                               acc_col[t][v], 0, 0, 0);
-                        acc_col[t][v] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[t], bvv,
-                                                                               acc_col[t][v], 0, 0, 0);
-                    }
-                }
-            }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            cur = nxt;
-            t0 = t1;
-            first = false;
-        }
-    };
-    if constexpr (NP >= 2) {
-        if (NT == 2 && ntile == 2)
-            stacked_loop(std::integral_constant<int, NT>{});
-        else
-            stacked_loop(std::integral_constant<int, 1>{});
-    } else {
-        chunk_loop(std::integral_constant<int, 1>{});
-    }
-
-    // Wave results: l summed over the g lanes of each column; o rows (NP = 1:
-    // from the hi + lo columns), the V codebook scale divided out.  Then the
-    // waves are merged per row, the inverse WHT and sign flip applied, and the
-    // partial written to the workspace (NP >= 2: one tile of 16 rows per pass
-    // through the merge space).  A position whose rows all end before this
-    // split has no partial (its combine reads only the splits below its
-    // longest row).
-    if constexpr (NP >= 2) {
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            float l_tot = l_col[t] + lane_xor<16>(l_col[t]);
-            l_tot += lane_xor<32>(l_tot);
-            if (gq == 0) {
-                mm[w][16 * t + i] = m_col[t];
-                ml[w][16 * t + i] = l_tot;
-            }
-        }
-    } else {
+        float m_run[NP], l_run[NP];
+        f32x4 acc[NP][8];
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
-            float l_tot = l_run[p] + lane_xor<16>(l_run[p]);
-            l_tot += lane_xor<32>(l_tot);
-            if (gq == 0 && !lo_col) {
-                mm[w][p * kRows + (i >> 1)] = m_run[p];
-                ml[w][p * kRows + (i >> 1)] = l_tot;
-            }
-        }
-    }
-    const float iav = 1.0f / kAlphaV;
-    const float s0 = (!QJL && (h & 1)) ? -inv : inv;
+            m_run[p] = kInitMax;
+            l_run[p] = 0.0f;
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        if (NP >= 2 && t >= ntile) break;  // wave- and workgroup-uniform
-        __syncthreads();  // every wave is done with the tables (or the last pass) mo overwrites
+            for (int v = 0; v < 8; ++v) acc[p][v] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        }
+        bool first = true;
+        int slot_nx = load_slot(t0 + kWaves * kChunk);
+
+        // The chunk loop, for the positions the workgroup has (a pair unit of a
+        // single group runs the one-position loop).
+        auto chunk_loop = [&](auto npa) {
+            constexpr int NPA = decltype(npa)::value;
+            while (t0 < t_end) {  // wave-uniform
+                const uint4* kw = cur.kw;
+                const uint32_t(*vw)[8] = cur.vw;
+                {
+                    const float ks = h2f(cur.ks), vs = h2f(cur.vs), re = PROD ? h2f(cur.re) : 0.0f;
+                    const float4 sc = QJL ? make_float4(0.0f, ks * kLog2e, vs, 0.0f)
+                                          : make_float4(ks * ck, ks * re * cr, vs, 0.0f);
+                    tsc[w][lane & (kChunk - 1)] = cur.valid ? sc : make_float4(0.f, 0.f, 0.f, -INFINITY);
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                Chunk nxt;
+                const int t1 = t0 + kWaves * kChunk;
+                if (t1 < t_end) {  // codes of the next chunk, slots of the one after
+                    fetch(t1, slot_nx, nxt);
+                    slot_nx = load_slot(t1 + kWaves * kChunk);
+                }
+
+                // QK: one decoded A operand per k-step, an MFMA per position
+                f32x4 cb[NPA][kTiles], cs[NPA][kTiles];
+        #pragma unroll
+                for (int tau = 0; tau < kTiles; ++tau) {
+        #pragma unroll
+                    for (int p = 0; p < NPA; ++p) {
+                        cb[p][tau] = (f32x4){0.f, 0.f, 0.f, 0.f};
+                        cs[p][tau] = cb[p][tau];
+                    }
+                    const uint32_t wd[4] = {kw[tau].x, kw[tau].y, kw[tau].z, kw[tau].w};
+        #pragma unroll
+                    for (int s = 0; s < 4; ++s) {
+                        if constexpr (QJL) {  // sign byte s of the lane's word
+                            const half8 sa = signs(wd[0], s);
+        #pragma unroll
+                            for (int p = 0; p < NPA; ++p)
+                                cs[p][tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sa, bq[p][s],
+                                                                                    cs[p][tau], 0, 0, 0);
+                            continue;
+                        }
+                        const half8 a = as_h8(lookup(wd[s], 0, 0), lookup(wd[s], 1, 0),
+                                              lookup(wd[s], 2, 0), lookup(wd[s], 3, 0));
+        #pragma unroll
+                        for (int p = 0; p < NPA; ++p)
+                            cb[p][tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[p][s], cb[p][tau],
+                                                                                0, 0, 0);
+                        if (PROD) {
+                            // Residual signs (nibble bit 3: 1 -> +1) as fp16 pairs in
+                            // registers: high bytes 0x3C / 0xBC, low bytes 0.
+                            const uint32_t he = ((wd[s] << 4) & 0x80808080u) ^ 0xBCBCBCBCu;  // even d
+                            const uint32_t ho = (wd[s] & 0x80808080u) ^ 0xBCBCBCBCu;         // odd d
+                            const half8 sa = as_h8(__builtin_amdgcn_perm(ho, he, 0x040C000Cu),
+                                                   __builtin_amdgcn_perm(ho, he, 0x050C010Cu),
+                                                   __builtin_amdgcn_perm(ho, he, 0x060C020Cu),
+                                                   __builtin_amdgcn_perm(ho, he, 0x070C030Cu));
+        #pragma unroll
+                            for (int p = 0; p < NPA; ++p)
+                                cs[p][tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sa, bq[p][s],
+                                                                                    cs[p][tau], 0, 0, 0);
+                        }
+                    }
+                }
+                // Logits (base 2) of tokens 16*tau + 4*gq + e; hi + lo columns summed.
+                float lg[NPA][kTiles][4];
+        #pragma unroll
+                for (int p = 0; p < NPA; ++p) {
+                    // rows shorter than the chunk's end need the causal mask
+                    const bool masked = PAGED && t0 + kChunk > gmin[p];
+                    float mloc = -INFINITY;
+        #pragma unroll
+                    for (int tau = 0; tau < kTiles; ++tau)
+        #pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const float4 sc = tsc[w][16 * tau + 4 * gq + e];
+                            if constexpr (QJL) {
+                                const float sr = cs[p][tau][e] + quad_xor<1>(cs[p][tau][e]);
+                                lg[p][tau][e] = fmaf(sr, sc.y, sc.w);
+                            } else {
+                                const float sb = cb[p][tau][e] + quad_xor<1>(cb[p][tau][e]);
+                                const float sr =
+                                    PROD ? cs[p][tau][e] + quad_xor<1>(cs[p][tau][e]) : 0.0f;
+                                lg[p][tau][e] = fmaf(sb, sc.x, fmaf(sr, sc.y, sc.w));
+                            }
+                            if (masked)  // causal limit of this column's row
+                                if (t0 + 16 * tau + 4 * gq + e >= rowlen[p]) lg[p][tau][e] = -INFINITY;
+                            mloc = fmaxf(mloc, lg[p][tau][e]);
+                        }
+                    mloc = fmaxf(mloc, lane_xor<16>(mloc));
+                    mloc = fmaxf(mloc, lane_xor<32>(mloc));
+                    // v_exp_f32 without denormal handling: arguments are <= 0 and a
+                    // weight below 2^-126 of the running maximum is negligible.
+                    const float m_new = fmaxf(m_run[p], mloc);
+                    const float alpha = first ? 0.0f : __builtin_amdgcn_exp2f(m_run[p] - m_new);
+                    m_run[p] = m_new;
+                    float lsum = 0.0f;
+        #pragma unroll
+                    for (int tau = 0; tau < kTiles; ++tau)
+        #pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            lg[p][tau][e] = __builtin_amdgcn_exp2f(lg[p][tau][e] - m_new);
+                            lsum += lg[p][tau][e];
+                        }
+                    l_run[p] = l_run[p] * alpha + lsum;
+                    if (!first && __any(alpha != 1.0f)) {
+                        // acc lane (d, gq) holds columns 4gq..4gq+3 = rows 2gq, 2gq+1.
+                        const float a0 = __shfl(alpha, 4 * gq), a1 = __shfl(alpha, 4 * gq + 2);
+        #pragma unroll
+                        for (int v = 0; v < 8; ++v) {
+                            acc[p][v][0] *= a0;
+                            acc[p][v][1] *= a0;
+                            acc[p][v][2] *= a1;
+                            acc[p][v][3] *= a1;
+                        }
+                    }
+                }
+                // PV: one decoded B operand per N-tile, an MFMA per position
+        #pragma unroll
+                for (int st = 0; st < kSteps; ++st) {
+                    half8 ap[NPA];
+        #pragma unroll
+                    for (int p = 0; p < NPA; ++p)
+        #pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            const int tau = 2 * st + (e >> 2), ee = e & 3;
+                            const float vs = tsc[w][16 * tau + 4 * gq + ee].z;
+                            ap[p][e] = hi_lo(lg[p][tau][ee] * vs, lo_col);
+                        }
+                    uint32_t bv[8][4];  // [N-tile v = d - 8i][token pair]
+        #pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const uint32_t we = vw[st][2 * q], wo = vw[st][2 * q + 1];
+                        const uint32_t lob = (we & 0x0F0F0F0Fu) | ((wo & 0x0F0F0F0Fu) << 4);
+                        const uint32_t hib = ((we >> 4) & 0x0F0F0F0Fu) | (wo & 0xF0F0F0F0u);
+        #pragma unroll
+                        for (int b = 0; b < 4; ++b) {
+                            bv[2 * b][q] = lookup(lob, b, 1);
+                            bv[2 * b + 1][q] = lookup(hib, b, 1);
+                        }
+                    }
+        #pragma unroll
+                    for (int v = 0; v < 8; ++v) {
+                        const half8 bvv = as_h8(bv[v][0], bv[v][1], bv[v][2], bv[v][3]);
+        #pragma unroll
+                        for (int p = 0; p < NPA; ++p)
+                            acc[p][v] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ap[p], bvv, acc[p][v], 0, 0,
+                                                                               0);
+                    }
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                cur = nxt;
+                t0 = t1;
+                first = false;
+            }
+        };
+        // NP >= 2: one softmax state per lane and tile (its column's row), hi and
+        // lo stacked along the reductions.  A unit with fewer positions runs the
+        // loop over the tiles it needs; a tile's unused columns compute on zero
+        // queries and are dropped.
+        float m_col[NT], l_col[NT];
+        f32x4 acc_col[NT][8];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            m_col[t] = kInitMax;
+            l_col[t] = 0.0f;
+#pragma unroll
+            for (int v = 0; v < 8; ++v) acc_col[t][v] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        }
+        auto stacked_loop = [&](auto nta) {
+            constexpr int NTA = decltype(nta)::value;
+            while (t0 < t_end) {  // wave-uniform
+                const uint4* kw = cur.kw;
+                const uint32_t(*vw)[8] = cur.vw;
+                {
+                    const float ks = h2f(cur.ks), vs = h2f(cur.vs), re = PROD ? h2f(cur.re) : 0.0f;
+                    tsc[w][lane & (kChunk - 1)] = cur.valid ? make_float4(ks * ck, ks * re * cr, vs, 0.0f)
+                                                            : make_float4(0.f, 0.f, 0.f, -INFINITY);
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                Chunk nxt;
+                const int t1 = t0 + kWaves * kChunk;
+                if (t1 < t_end) {  // codes of the next chunk, slots of the one after
+                    fetch(t1, slot_nx, nxt);
+                    slot_nx = load_slot(t1 + kWaves * kChunk);
+                }
+                // QK: each decoded A operand against every tile's hi and lo query
+                f32x4 cb[NTA][kTiles], cs[NTA][kTiles];
+#pragma unroll
+                for (int tau = 0; tau < kTiles; ++tau)
+#pragma unroll
+                    for (int t = 0; t < NTA; ++t) {
+                        cb[t][tau] = (f32x4){0.f, 0.f, 0.f, 0.f};
+                        cs[t][tau] = cb[t][tau];
+                    }
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    half8 bk[2 * NTA];  // k-step s of each tile's hi and lo query
+#pragma unroll
+                    for (int pp = 0; pp < 2 * NTA; ++pp)
+                        bk[pp] = __builtin_bit_cast(half8, bqs[pp][s][lane]);
+#pragma unroll
+                    for (int tau = 0; tau < kTiles; ++tau) {
+                        const uint32_t wd = s == 0   ? kw[tau].x
+                                            : s == 1 ? kw[tau].y
+                                            : s == 2 ? kw[tau].z
+                                                     : kw[tau].w;
+                        const half8 a = as_h8(lookup(wd, 0, 0), lookup(wd, 1, 0), lookup(wd, 2, 0),
+                                              lookup(wd, 3, 0));
+#pragma unroll
+                        for (int t = 0; t < NTA; ++t) {
+                            cb[t][tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bk[2 * t],
+                                                                                cb[t][tau], 0, 0, 0);
+                            cb[t][tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bk[2 * t + 1],
+                                                                                cb[t][tau], 0, 0, 0);
+                        }
+                        if (PROD) {
+                            const uint32_t he = ((wd << 4) & 0x80808080u) ^ 0xBCBCBCBCu;  // even d
+                            const uint32_t ho = (wd & 0x80808080u) ^ 0xBCBCBCBCu;         // odd d
+                            const half8 sa = as_h8(__builtin_amdgcn_perm(ho, he, 0x040C000Cu),
+                                                   __builtin_amdgcn_perm(ho, he, 0x050C010Cu),
+                                                   __builtin_amdgcn_perm(ho, he, 0x060C020Cu),
+                                                   __builtin_amdgcn_perm(ho, he, 0x070C030Cu));
+#pragma unroll
+                            for (int t = 0; t < NTA; ++t) {
+                                cs[t][tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                    sa, bk[2 * t], cs[t][tau], 0, 0, 0);
+                                cs[t][tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                    sa, bk[2 * t + 1], cs[t][tau], 0, 0, 0);
+                            }
+                        }
+                    }
+                }
+                const bool masked = t0 + kChunk > gmin_live;
+                float lg[NTA][kTiles][4];
+#pragma unroll
+                for (int t = 0; t < NTA; ++t) {
+                    // Logits (base 2) of tokens 16*tau + 4*gq + e for this lane's column.
+                    float mloc = -INFINITY;
+#pragma unroll
+                    for (int tau = 0; tau < kTiles; ++tau)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const float4 sc = tsc[w][16 * tau + 4 * gq + e];
+                            lg[t][tau][e] = fmaf(cb[t][tau][e], sc.x, fmaf(cs[t][tau][e], sc.y, sc.w));
+                            if (masked)
+                                if (t0 + 16 * tau + 4 * gq + e >= rl_col[t]) lg[t][tau][e] = -INFINITY;
+                            mloc = fmaxf(mloc, lg[t][tau][e]);
+                        }
+                    mloc = fmaxf(mloc, lane_xor<16>(mloc));
+                    mloc = fmaxf(mloc, lane_xor<32>(mloc));
+                    const float m_new = fmaxf(m_col[t], mloc);
+                    const float alpha = first ? 0.0f : __builtin_amdgcn_exp2f(m_col[t] - m_new);
+                    m_col[t] = m_new;
+                    float lsum = 0.0f;
+#pragma unroll
+                    for (int tau = 0; tau < kTiles; ++tau)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            lg[t][tau][e] = __builtin_amdgcn_exp2f(lg[t][tau][e] - m_new);
+                            lsum += lg[t][tau][e];
+                        }
+                    l_col[t] = l_col[t] * alpha + lsum;
+                    if (!first && __any(alpha != 1.0f)) {
+                        // acc lane (d, gq) holds rows 4gq .. 4gq + 3 (columns of lanes 4gq + e)
+                        float a[4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) a[e] = __shfl(alpha, 4 * gq + e);
+#pragma unroll
+                        for (int v = 0; v < 8; ++v)
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) acc_col[t][v][e] *= a[e];
+                    }
+                }
+                // PV: every tile's hi and lo P against each decoded B operand
+#pragma unroll
+                for (int st = 0; st < kSteps; ++st) {
+                    half8 ah[NTA], al[NTA];
+#pragma unroll
+                    for (int t = 0; t < NTA; ++t)
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            const int tau = 2 * st + (e >> 2), ee = e & 3;
+                            const float x = lg[t][tau][ee] * tsc[w][16 * tau + 4 * gq + ee].z;
+                            ah[t][e] = hi_lo(x, false);
+                            al[t][e] = hi_lo(x, true);
+                        }
+                    uint32_t bv[8][4];  // [N-tile v = d - 8i][token pair]
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const uint32_t we = vw[st][2 * q], wo = vw[st][2 * q + 1];
+                        const uint32_t lob = (we & 0x0F0F0F0Fu) | ((wo & 0x0F0F0F0Fu) << 4);
+                        const uint32_t hib = ((we >> 4) & 0x0F0F0F0Fu) | (wo & 0xF0F0F0F0u);
+#pragma unroll
+                        for (int b = 0; b < 4; ++b) {
+                            bv[2 * b][q] = lookup(lob, b, 1);
+                            bv[2 * b + 1][q] = lookup(hib, b, 1);
+                        }
+                    }
+#pragma unroll
+                    for (int v = 0; v < 8; ++v) {
+                        const half8 bvv = as_h8(bv[v][0], bv[v][1], bv[v][2], bv[v][3]);
+#pragma unroll
+                        for (int t = 0; t < NTA; ++t) {
+                            acc_col[t][v] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[t], bvv,
+                                                                                   acc_col[t][v], 0, 0, 0);
+                            acc_col[t][v] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[t], bvv,
+                                                                                   acc_col[t][v], 0, 0, 0);
+                        }
+                    }
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                cur = nxt;
+                t0 = t1;
+                first = false;
+            }
+        };
+        if constexpr (NP >= 2) {
+            if (NT == 2 && ntile == 2)
+                stacked_loop(std::integral_constant<int, NT>{});
+            else
+                stacked_loop(std::integral_constant<int, 1>{});
+        } else {
+            chunk_loop(std::integral_constant<int, 1>{});
+        }
+
+        // Wave results: l summed over the g lanes of each column; o rows (NP = 1:
+        // from the hi + lo columns), the V codebook scale divided out.  Then the
+        // waves are merged per row, the inverse WHT and sign flip applied, and the
+        // partial written to the workspace (NP >= 2: one tile of 16 rows per pass
+        // through the merge space).  A position whose rows all end before this
+        // piece has no partial (its combine reads only the pieces below its
+        // longest row).
         if constexpr (NP >= 2) {
 #pragma unroll
-            for (int v = 0; v < 8; ++v)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) mo[w][4 * gq + e][8 * i + v] = acc_col[t][v][e] * iav;
+            for (int t = 0; t < NT; ++t) {
+                float l_tot = l_col[t] + lane_xor<16>(l_col[t]);
+                l_tot += lane_xor<32>(l_tot);
+                if (gq == 0) {
+                    mm[w][16 * t + i] = m_col[t];
+                    ml[w][16 * t + i] = l_tot;
+                }
+            }
         } else {
 #pragma unroll
-            for (int p = 0; p < NP; ++p)
-#pragma unroll
-                for (int v = 0; v < 8; ++v) {
-                    mo[w][p * kRows + 2 * gq][8 * i + v] = (acc[p][v][0] + acc[p][v][1]) * iav;
-                    mo[w][p * kRows + 2 * gq + 1][8 * i + v] = (acc[p][v][2] + acc[p][v][3]) * iav;
+            for (int p = 0; p < NP; ++p) {
+                float l_tot = l_run[p] + lane_xor<16>(l_run[p]);
+                l_tot += lane_xor<32>(l_tot);
+                if (gq == 0 && !lo_col) {
+                    mm[w][p * kRows + (i >> 1)] = m_run[p];
+                    ml[w][p * kRows + (i >> 1)] = l_tot;
                 }
+            }
         }
+        const float iav = 1.0f / kAlphaV;
+        const float s0 = (!QJL && (h & 1)) ? -inv : inv;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            if (NP >= 2 && t >= ntile) break;  // wave- and workgroup-uniform
+            __syncthreads();  // every wave is done with the tables (or the last pass) mo overwrites
+            if constexpr (NP >= 2) {
+#pragma unroll
+                for (int v = 0; v < 8; ++v)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) mo[w][4 * gq + e][8 * i + v] = acc_col[t][v][e] * iav;
+            } else {
+#pragma unroll
+                for (int p = 0; p < NP; ++p)
+#pragma unroll
+                    for (int v = 0; v < 8; ++v) {
+                        mo[w][p * kRows + 2 * gq][8 * i + v] = (acc[p][v][0] + acc[p][v][1]) * iav;
+                        mo[w][p * kRows + 2 * gq + 1][8 * i + v] = (acc[p][v][2] + acc[p][v][3]) * iav;
+                    }
+            }
+            __syncthreads();
+            for (int rr = w; rr < kMoRows; rr += kWaves) {
+                const int r = kMoRows * t + rr;  // row of the workgroup
+                const int p = r / kRows;
+                bool keep = p < npos;
+                if constexpr (PAGED) keep = keep && t_begin < gend[p];
+                if (!keep) continue;  // wave-uniform
+                float M = mm[0][r];
+#pragma unroll
+                for (int u = 1; u < kWaves; ++u) M = fmaxf(M, mm[u][r]);
+                float L = 0.f, o0 = 0.f, o1 = 0.f;
+#pragma unroll
+                for (int u = 0; u < kWaves; ++u) {
+                    const float wt = exp2f(mm[u][r] - M);
+                    L += ml[u][r] * wt;
+                    o0 += mo[u][rr][2 * lane] * wt;
+                    o1 += mo[u][rr][2 * lane + 1] * wt;
+                }
+                wht_pair<64>(o0, o1, lane);
+                float* part = ws + ((pid * NP + p) * kRows + r % kRows) * kPartStride;
+                part[2 * lane] = o0 * s0;
+                part[2 * lane + 1] = o1 * -s0;
+                if (lane == 0) {
+                    part[128] = M;
+                    part[129] = L;
+                }
+            }
+        }
+    };  // item
+
+    if constexpr (PAGED) {
+        // This workgroup's segment of the step's work.  Workgroup b runs on
+        // XCD b % 8 and the segments of one XCD are consecutive, so the items
+        // that read the same pages (the heads and positions of a sequence)
+        // mostly share an L2.
+        constexpr int kPass = kChunk * kWaves;
+        const int G = gridDim.x;
+        const int seg = (G & 7) == 0 ? (int)(blockIdx.x & 7) * (G >> 3) + (int)(blockIdx.x >> 3)
+                                     : (int)blockIdx.x;
+        const int nu = __builtin_amdgcn_readfirstlane(pr.plan[0]);
+        const int total = __builtin_amdgcn_readfirstlane(pr.plan[1]);
+        const int b0 = seg_bound(seg, total, G), b1 = seg_bound(seg + 1, total, G);
+        if (b0 >= b1) return;  // an empty segment (less work than workgroups)
+        // The unit holding work position b0 (exactly one: the units' work
+        // ranges partition [0, total)).
+        __shared__ int s_unit;
+        for (int u = threadIdx.x; u < nu; u += 64 * kWaves)
+            if (pr.units[u].start <= b0 && b0 < pr.units[u + 1].start) s_unit = u;
         __syncthreads();
-        for (int rr = w; rr < kMoRows; rr += kWaves) {
-            const int r = kMoRows * t + rr;  // row of the workgroup
-            const int p = r / kRows;
-            bool keep = p < npos;
-            if constexpr (PAGED) keep = keep && t_begin < gend[p];
-            if (!keep) continue;  // wave-uniform
-            float M = mm[0][r];
-#pragma unroll
-            for (int u = 1; u < kWaves; ++u) M = fmaxf(M, mm[u][r]);
-            float L = 0.f, o0 = 0.f, o1 = 0.f;
-#pragma unroll
-            for (int u = 0; u < kWaves; ++u) {
-                const float wt = exp2f(mm[u][r] - M);
-                L += ml[u][r] * wt;
-                o0 += mo[u][rr][2 * lane] * wt;
-                o1 += mo[u][rr][2 * lane + 1] * wt;
-            }
-            wht_pair<64>(o0, o1, lane);
-            float* part =
-                ws + ((pid + (size_t)num_splits * g.H * p) * kRows + r % kRows) * kPartStride;
-            part[2 * lane] = o0 * s0;
-            part[2 * lane + 1] = o1 * -s0;
-            if (lane == 0) {
-                part[128] = M;
-                part[129] = L;
+        // The walk over the items overlapping the segment, in work order.  Its
+        // position (unit, head) lives in LDS (one copy per wave, volatile
+        // accesses), so no walk state is held in registers across an item.
+        __shared__ int s_walk[kWaves][2];
+        const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        volatile int* walk = s_walk[wv];
+        {
+            const int u = __builtin_amdgcn_readfirstlane(s_unit);
+            const PagedUnit un = pr.units[u];
+            if ((threadIdx.x & 63) == 0) {
+                walk[0] = u;
+                walk[1] = (b0 - un.start) / (un.w * un.n);
             }
         }
+        for (;;) {
+            const int u = __builtin_amdgcn_readfirstlane(walk[0]);
+            const int hh = __builtin_amdgcn_readfirstlane(walk[1]);
+            if (u >= nu) break;
+            const PagedUnit un = pr.units[u];
+            const int S = un.start + hh * un.w * un.n;
+            if (S >= b1) break;
+            if ((threadIdx.x & 63) == 0) {
+                walk[0] = hh + 1 == g.H ? u + 1 : u;
+                walk[1] = hh + 1 == g.H ? 0 : hh + 1;
+            }
+            int x0, x1;
+            item_passes(S, un.n, un.w, b0, b1, x0, x1);
+            if (x0 < x1) {
+                int tid = threadIdx.x;
+                asm volatile("" : "+v"(tid));  // opaque per item (see item)
+                item(tid, hh, un.first, un.npos, x0 * kPass, min(x1 * kPass, un.kv_end),
+                     (size_t)(u * g.H + hh + seg));
+            }
+        }
+    } else {
+        const int split = blockIdx.x % num_splits, hr = blockIdx.x / num_splits;
+        const int t_begin = split * tokens_per_split;
+        item(threadIdx.x, hr % g.H, hr / g.H, 1, t_begin, t_begin + tokens_per_split, blockIdx.x);
     }
 }
 // Sum of the split partials of one output row (q, h): o = sum_s 2^(m_s - M)
@@ -1002,12 +1063,9 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
 // threads = 8 groups x 32 d.  Group g takes splits g, g + 8, ...: it loads up
 // to 16 partials' (m, l, o[d]) in one round, merges them with a running
 // maximum, and the 8 groups are merged in LDS.
-// PAGED: the group's splits stop at its longest row (later splits wrote no
-// partial); num_queries and tokens_per_split are only used then.
-template <bool PAGED>
-__global__ __launch_bounds__(256) void attn_mfma_combine_kernel(
-    const float* __restrict__ ws, uint16_t* __restrict__ output, int H, int num_splits,
-    int num_queries, int tokens_per_split, mfma::PagedRows pr) {
+__global__ __launch_bounds__(256) void attn_mfma_combine_kernel(const float* __restrict__ ws,
+                                                                uint16_t* __restrict__ output,
+                                                                int H, int num_splits) {
     using namespace mfma;
     constexpr int kBatch = 16;
     __shared__ float red_m[8], red_l[8];
@@ -1019,14 +1077,7 @@ __global__ __launch_bounds__(256) void attn_mfma_combine_kernel(
     const int d = 32 * dq + dd;
     const size_t base_bid = (size_t)(rg * H + h) * num_splits;
     auto part = [&](int s) { return ws + ((base_bid + s) * kRows + r) * kPartStride; };
-    int S = num_splits;
-    if constexpr (PAGED) {
-        int kv = 0;
-#pragma unroll
-        for (int k = 0; k < kRows; ++k)
-            kv = max(kv, rg * kRows + k < num_queries ? pr.row_kv_len[rg * kRows + k] : 0);
-        S = min(num_splits, (kv + tokens_per_split - 1) / tokens_per_split);
-    }
+    const int S = num_splits;
 
     float M = kInitMax, L = 0.f, acc = 0.f;
     for (int base = sg; base < S; base += 8 * kBatch) {
@@ -1079,22 +1130,14 @@ __global__ __launch_bounds__(256) void attn_mfma_combine_kernel(
 // (8 in flight).  One block per item instead of 4 per row: for the many short
 // items of a batched decode step the block count, not the bytes, is the cost.
 constexpr int kItemCombineMaxSplits = 32;
-template <bool PAGED>
 __global__ __launch_bounds__(256) void attn_mfma_combine_items_kernel(
     const float* __restrict__ ws, uint16_t* __restrict__ output, int H, int num_splits,
-    int num_queries, int tokens_per_split, mfma::PagedRows pr) {
+    int num_queries) {
     using namespace mfma;
     const int item = blockIdx.x;  // h + H * rg
     const int h = item % H, rg = item / H;
     const int t = threadIdx.x, r = t >> 5, d0 = 4 * (t & 31);
-    int S = num_splits;
-    if constexpr (PAGED) {
-        int kv = 0;
-#pragma unroll
-        for (int k = 0; k < kRows; ++k)
-            kv = max(kv, rg * kRows + k < num_queries ? pr.row_kv_len[rg * kRows + k] : 0);
-        S = min(num_splits, (kv + tokens_per_split - 1) / tokens_per_split);
-    }
+    const int S = num_splits;
     const float* base = ws + ((size_t)item * num_splits * kRows + r) * kPartStride;
     float M = kInitMax, L = 0.f;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1136,45 +1179,180 @@ __global__ __launch_bounds__(256) void attn_mfma_combine_items_kernel(
         make_uint2(fin(acc.x) | (fin(acc.y) << 16), fin(acc.z) | (fin(acc.w) << 16));
 }
 
-// Units of up to U row groups for the multi-position paged kernel, from
-// row_seq (rows in aligned groups of 8 share a sequence): each run of
-// consecutive groups of one sequence is cut into units of U from its start,
-// the last one shorter.  One wave walks the groups 64 at a time: a group
-// starts a run when its sequence differs from the previous group's, and
-// starts a unit when its distance from its run's start is a multiple of U.
+// Merge of a paged step's partials: one block per (row group, kv head), laid
+// out as in attn_mfma_combine_items_kernel.  The row group is position p of
+// unit u; its item's passes were cut at segment bounds into pieces, one
+// partial per segment they start in (slot item + segment, position p), and
+// a piece starting at or past the group's longest row wrote none.
+__global__ __launch_bounds__(256) void attn_paged_combine_kernel(
+    const float* __restrict__ ws, uint16_t* __restrict__ output, int H, int num_queries,
+    int num_segments, int positions, int pass, mfma::PagedRows pr) {
+    using namespace mfma;
+    const int item = blockIdx.x;  // h + H * rg
+    const int h = item % H, rg = item / H;
+    const int t = threadIdx.x, r = t >> 5, d0 = 4 * (t & 31);
+    const int u = pr.unit_of_group[rg];
+    const PagedUnit un = pr.units[u];
+    const int total = pr.plan[1], G = num_segments;
+    const int p = rg - un.first;
+    int kv = 0;
+#pragma unroll
+    for (int k = 0; k < kRows; ++k)
+        kv = max(kv, rg * kRows + k < num_queries ? pr.row_kv_len[rg * kRows + k] : 0);
+    const int S = un.start + h * un.w * un.n;
+    // segments holding the item's first and last pass starts
+    int g_lo = 0, g_hi = -1;
+    if (un.n > 0 && kv > 0) {
+        g_lo = (int)(((long long)(S + 1) * G - 1) / total);
+        g_hi = (int)(((long long)(S + un.w * (un.n - 1) + 1) * G - 1) / total);
+    }
+    const size_t slot0 = (size_t)u * H + h;
+    float M = kInitMax, L = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int b = g_lo; b <= g_hi; b += 8) {
+        float pm[8], pl[8];
+        float4 po[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int gs = min(b + k, g_hi);
+            int x0, x1;
+            item_passes(S, un.n, un.w, seg_bound(gs, total, G), seg_bound(gs + 1, total, G), x0,
+                        x1);
+            const bool ok = b + k <= g_hi && x0 < x1 && x0 * pass < kv;
+            const float* pp =
+                ws + (((slot0 + gs) * positions + p) * kRows + r) * kPartStride;
+            pm[k] = ok ? pp[128] : kInitMax;
+            pl[k] = ok ? pp[129] : 0.f;
+            po[k] = ok ? *reinterpret_cast<const float4*>(pp + d0) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        float mb = M;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) mb = fmaxf(mb, pm[k]);
+        const float sc = exp2f(M - mb);
+        L *= sc;
+        acc.x *= sc;
+        acc.y *= sc;
+        acc.z *= sc;
+        acc.w *= sc;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float wt = exp2f(pm[k] - mb);
+            L += pl[k] * wt;
+            acc.x += po[k].x * wt;
+            acc.y += po[k].y * wt;
+            acc.z += po[k].z * wt;
+            acc.w += po[k].w * wt;
+        }
+        M = mb;
+    }
+    const int q = rg * kRows + r;
+    if (q >= num_queries) return;
+    const auto fin = [&](float o) { return (uint32_t)f2h(L > 0.f ? o / L : o); };
+    *reinterpret_cast<uint2*>(output + ((size_t)q * H + h) * 128 + d0) =
+        make_uint2(fin(acc.x) | (fin(acc.y) << 16), fin(acc.z) | (fin(acc.w) << 16));
+}
+
+// Inclusive scan over the 1024 threads of a block (16 waves) with an
+// associative op: within each wave by shuffles, then over the wave totals.
+template <typename Op>
+__device__ int block_scan_1024(int v, int ident, int* s_tot, Op op) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int o = __shfl_up(v, d);
+        if (lane >= d) v = op(v, o);
+    }
+    if (lane == 63) s_tot[wv] = v;
+    __syncthreads();
+    int pre = ident;
+    for (int k = 0; k < wv; ++k) pre = op(pre, s_tot[k]);
+    __syncthreads();  // s_tot is reused by the next scan
+    return op(pre, v);
+}
+
+// The plan of a paged step, one block of 1024 threads.  Row groups (8 rows
+// of one sequence) form units: each run of consecutive groups of one
+// sequence is cut into units of U groups from its start, the last one
+// shorter.  A unit's items (one per kv head) are n = ceil(kv_end / pass)
+// passes over its longest row (at most max_kv_len), a pass weighing w: with
+// U = 4, 4 for a unit of more than two positions (the two-tile loop) and 3
+// otherwise, about their measured cost ratio.  Work positions are given out
+// in unit order.  The groups are taken 1024 at a time, carrying the run
+// start, the unit count and the work total from window to window.
 template <int U>
-__global__ __launch_bounds__(64) void unit_groups_kernel(const int32_t* __restrict__ row_seq,
-                                                         int groups, int32_t* __restrict__ first,
-                                                         int32_t* __restrict__ count,
-                                                         int32_t* __restrict__ num_units) {
-    static_assert(U >= 2 && (U & (U - 1)) == 0, "power-of-two unit");
+__global__ __launch_bounds__(1024) void paged_plan_kernel(
+    const int32_t* __restrict__ row_seq, const int32_t* __restrict__ row_kv_len, int num_rows,
+    int groups, int H, int pass, int max_kv_len, mfma::PagedUnit* __restrict__ units,
+    int32_t* __restrict__ unit_of_group, int32_t* __restrict__ plan) {
+    static_assert(U >= 1 && U <= 4 && (U & (U - 1)) == 0, "1, 2 or 4 groups per unit");
     using mfma::kRows;
-    const int lane = threadIdx.x;
-    int run_start = 0, out = 0;
-    for (int g0 = 0; g0 < groups; g0 += 64) {
-        const int gi = g0 + lane;
+    constexpr int kWin = 1024;
+    __shared__ int s_sq[kWin + U], s_gk[kWin + U], s_tot[16], s_carry[4];
+    const int j = threadIdx.x;
+    auto group_kv = [&](int gi) {  // the group's longest row (rows past num_rows: 0)
+        int m = 0;
+#pragma unroll
+        for (int k = 0; k < kRows; ++k) {
+            const int rr = gi * kRows + k;
+            if (rr < num_rows) m = max(m, row_kv_len[rr]);
+        }
+        return min(m, max_kv_len);
+    };
+    const auto add = [](int a, int b) { return a + b; };
+    const auto mx = [](int a, int b) { return max(a, b); };
+    int c_units = 0, c_work = 0, c_rs = 0, c_sq = 0;
+    for (int base = 0; base < groups; base += kWin) {
+        const int gi = base + j;
         const bool in = gi < groups;
         const int sq = in ? row_seq[(size_t)gi * kRows] : 0;
-        const int before = in && gi > 0 ? row_seq[(size_t)(gi - 1) * kRows] : 0;
-        const bool new_run = in && (gi == 0 || sq != before);
-        const uint64_t runs = __ballot(new_run);
-        const uint64_t upto = runs & (lane == 63 ? ~0ull : ((2ull << lane) - 1));
-        const int rs = upto ? g0 + 63 - __builtin_clzll(upto) : run_start;
-        const bool start = in && ((gi - rs) & (U - 1)) == 0;
-        const uint64_t starts = __ballot(start);
-        if (start) {
-            int c = 1;  // the run's groups from gi on, at most U
-#pragma unroll
-            for (int k = 1; k < U; ++k)
-                if (c == k && gi + k < groups && row_seq[(size_t)(gi + k) * kRows] == sq) ++c;
-            const int o = out + __builtin_popcountll(starts & ((1ull << lane) - 1));
-            first[o] = gi;
-            count[o] = c;
+        s_sq[j] = sq;
+        s_gk[j] = in ? group_kv(gi) : 0;
+        if (j < U - 1) {  // look-ahead for units that straddle the window's end
+            const int gx = base + kWin + j;
+            s_sq[kWin + j] = gx < groups ? row_seq[(size_t)gx * kRows] : 0;
+            s_gk[kWin + j] = gx < groups ? group_kv(gx) : 0;
         }
-        out += __builtin_popcountll(starts);
-        run_start = __shfl(rs, 63);
+        __syncthreads();
+        const int prev = j > 0 ? s_sq[j - 1] : c_sq;
+        const bool new_run = in && (gi == 0 || sq != prev);
+        int rs = block_scan_1024(new_run ? gi : -1, -1, s_tot, mx);
+        if (rs < 0) rs = c_rs;
+        const bool start = in && ((gi - rs) & (U - 1)) == 0;
+        int c = 1, kv = s_gk[j];
+#pragma unroll
+        for (int k = 1; k < U; ++k)
+            if (c == k && gi + k < groups && s_sq[j + k] == sq) {
+                ++c;
+                kv = max(kv, s_gk[j + k]);
+            }
+        const int w = U > 2 ? (c > 2 ? 4 : 3) : 1;
+        const int n = (kv + pass - 1) / pass;
+        const int work = start ? H * w * n : 0;
+        const int ui = block_scan_1024(start ? 1 : 0, 0, s_tot, add);
+        const int wi = block_scan_1024(work, 0, s_tot, add);
+        if (start) {
+            const int o = c_units + ui - 1;
+            units[o] = mfma::PagedUnit{gi, c, kv, c_work + wi - work, n, w, 0, 0};
+            for (int k = 0; k < c; ++k) unit_of_group[gi + k] = o;
+        }
+        if (j == kWin - 1) {  // window totals (inclusive scans at the last thread)
+            s_carry[0] = ui;
+            s_carry[1] = wi;
+            s_carry[2] = rs;
+            s_carry[3] = s_sq[min(groups - base, kWin) - 1];
+        }
+        __syncthreads();
+        c_units += s_carry[0];
+        c_work += s_carry[1];
+        c_rs = s_carry[2];
+        c_sq = s_carry[3];
+        __syncthreads();  // before the next window rewrites s_sq and s_carry
     }
-    if (lane == 0) num_units[0] = out;
+    if (j == 0) {
+        units[c_units] = mfma::PagedUnit{0, 0, 0, c_work, 0, 1, 0, 0};  // sentinel
+        plan[0] = c_units;
+        plan[1] = c_work;
+    }
 }
 
 // New-token positions (row groups of one sequence) per paged workgroup.
@@ -1182,6 +1360,11 @@ __global__ __launch_bounds__(64) void unit_groups_kernel(const int32_t* __restri
 #define TQ_PAGED_POSITIONS 4
 #endif
 constexpr int kPagedPositions = TQ_PAGED_POSITIONS;
+// Paged steps: work segments (workgroups) per CU.
+#ifndef TQ_PAGED_SEGMENTS_PER_CU
+#define TQ_PAGED_SEGMENTS_PER_CU 1
+#endif
+constexpr int kPagedSegmentsPerCU = TQ_PAGED_SEGMENTS_PER_CU;
 
 // Split kernel shape: tokens per wave iteration and waves per workgroup.
 #ifndef TQ_SPLIT_CHUNK
@@ -1243,8 +1426,8 @@ void launch_mfma_attention(const uint16_t* query, const uint8_t* pool, const int
     constexpr int kCH = kSplitChunk, kNW = kSplitWaves;
     const PagedRows none{};
     if (num_kv_tokens == 0) {  // no partials: the combine writes the zero output
-        hipLaunchKernelGGL(attn_mfma_combine_kernel<false>, dim3(4 * rows), dim3(256), 0, stream,
-                           ws, output, g.H, 0, num_queries, 1, none);
+        hipLaunchKernelGGL(attn_mfma_combine_kernel, dim3(4 * rows), dim3(256), 0, stream, ws,
+                           output, g.H, 0);
         check_launch(combine_name);
         return;
     }
@@ -1253,11 +1436,11 @@ void launch_mfma_attention(const uint16_t* query, const uint8_t* pool, const int
                        num_kv_tokens, tps, splits, inv, none);
     check_launch(split_name);
     if (splits <= kItemCombineMaxSplits)
-        hipLaunchKernelGGL(attn_mfma_combine_items_kernel<false>, dim3(heads), dim3(256), 0,
-                           stream, ws, output, g.H, splits, num_queries, tps, none);
+        hipLaunchKernelGGL(attn_mfma_combine_items_kernel, dim3(heads), dim3(256), 0, stream,
+                           ws, output, g.H, splits, num_queries);
     else
-        hipLaunchKernelGGL(attn_mfma_combine_kernel<false>, dim3(4 * rows), dim3(256), 0, stream,
-                           ws, output, g.H, splits, num_queries, tps, none);
+        hipLaunchKernelGGL(attn_mfma_combine_kernel, dim3(4 * rows), dim3(256), 0, stream, ws,
+                           output, g.H, splits);
     check_launch(combine_name);
 }
 }  // namespace
@@ -1319,52 +1502,42 @@ void launch_paged_attention(Scheme s, const uint16_t* query, const uint8_t* pool
     const float inv = inv_sqrt_d(g.D);
     const int row_groups = (num_rows + kRows - 1) / kRows;
     const int heads = g.H * row_groups;
-    // Split length: a multiple of one workgroup pass (waves x chunk) sized so
-    // that the longest group would yield about 8 workgroups per CU in total
-    // (pairs of groups then take about half that: the per-workgroup setup is
-    // amortised over as many passes as with one group per workgroup).
+    // The plan splits the step's work (every unit's passes over its kv
+    // length, for every kv head) into G equal segments, one workgroup each:
+    // G a multiple of 8 (the kernel's XCD mapping).
     constexpr int kPass = kSplitChunk * kSplitWaves;
-    const long long want_tokens =
-        ((long long)std::max(max_kv_len, 1) * heads + 8LL * num_cus() - 1) / (8LL * num_cus());
-    const int tps = (int)std::max<long long>(
-        kPass, ((want_tokens + kPass - 1) / kPass) * kPass);
-    const int splits = std::max(1, (max_kv_len + tps - 1) / tps);
-    const size_t items = (size_t)splits * heads;  // partial slots: (split, head, group)
-    const size_t blocks = 64 * ((items + 63) / 64);  // runs of 8 dealt to 8 XCDs (see the kernel)
-    // Workspace: the partials, then the pair table of the row groups.
-    const size_t part_bytes = items * kRows * kPartStride * sizeof(float);
-    char* wsb = static_cast<char*>(
-        workspace(stream, part_bytes + (2 * (size_t)row_groups + 1) * sizeof(int32_t)));
+    const int G = 8 * ((kPagedSegmentsPerCU * num_cus() + 7) / 8);
+    // Workspace: the partials (slot item + segment: at most heads + G - 1
+    // slots of kPagedPositions positions), then the plan.
+    const size_t part_bytes =
+        ((size_t)heads + G) * kPagedPositions * kRows * kPartStride * sizeof(float);
+    const size_t unit_bytes = ((size_t)row_groups + 1) * sizeof(PagedUnit);
+    char* wsb = static_cast<char*>(workspace(
+        stream, part_bytes + unit_bytes + ((size_t)row_groups + 4) * sizeof(int32_t)));
     float* ws = reinterpret_cast<float*>(wsb);
-    int32_t* pair_first = reinterpret_cast<int32_t*>(wsb + part_bytes);
-    int32_t* pair_count = pair_first + row_groups;
-    int32_t* num_pairs = pair_count + row_groups;
-    const PagedRows pr{block_tables, row_seq, row_kv_len, max_blocks,
-                       pair_first, pair_count, num_pairs};
+    PagedUnit* units = reinterpret_cast<PagedUnit*>(wsb + part_bytes);
+    int32_t* plan = reinterpret_cast<int32_t*>(wsb + part_bytes + unit_bytes);
+    int32_t* unit_of_group = plan + 4;
+    const PagedRows pr{block_tables, row_seq, row_kv_len, max_blocks, units, unit_of_group, plan};
     const bool prod = s == Scheme::Prod;
     constexpr int kCH = kSplitChunk, kNW = kSplitWaves;
+    hipLaunchKernelGGL(paged_plan_kernel<kPagedPositions>, dim3(1), dim3(1024), 0, stream, row_seq,
+                       row_kv_len, num_rows, row_groups, g.H, kPass, std::max(max_kv_len, 0),
+                       units, unit_of_group, plan);
+    check_launch(prod ? "turbo_prod_paged_attn_plan" : "turbo_mse_paged_attn_plan");
     if (max_kv_len > 0) {
-        hipLaunchKernelGGL(unit_groups_kernel<kPagedPositions>, dim3(1), dim3(64), 0, stream,
-                           row_seq, row_groups, pair_first, pair_count, num_pairs);
-        check_launch(prod ? "turbo_prod_paged_attn_units" : "turbo_mse_paged_attn_units");
-        // The grid covers every row group as a unit; items past the unit count exit.
         if (prod)
             hipLaunchKernelGGL((attn_mfma_split_kernel<kSchProd, kCH, kNW, true, kPagedPositions>),
-                               dim3(blocks), dim3(64 * kNW), 0, stream, query, pool, nullptr, ws,
-                               g, num_rows, max_kv_len, tps, splits, inv, pr);
+                               dim3(G), dim3(64 * kNW), 0, stream, query, pool, nullptr, ws, g,
+                               num_rows, max_kv_len, 0, 0, inv, pr);
         else
             hipLaunchKernelGGL((attn_mfma_split_kernel<kSchMse, kCH, kNW, true, kPagedPositions>),
-                               dim3(blocks), dim3(64 * kNW), 0, stream, query, pool, nullptr, ws,
-                               g, num_rows, max_kv_len, tps, splits, inv, pr);
+                               dim3(G), dim3(64 * kNW), 0, stream, query, pool, nullptr, ws, g,
+                               num_rows, max_kv_len, 0, 0, inv, pr);
         check_launch(prod ? "turbo_prod_paged_attn_split" : "turbo_mse_paged_attn_split");
     }
-    if (splits <= kItemCombineMaxSplits)
-        hipLaunchKernelGGL(attn_mfma_combine_items_kernel<true>, dim3(heads), dim3(256), 0,
-                           stream, ws, output, g.H, max_kv_len > 0 ? splits : 0, num_rows, tps,
-                           pr);
-    else
-        hipLaunchKernelGGL(attn_mfma_combine_kernel<true>, dim3(4 * rows), dim3(256), 0, stream,
-                           ws, output, g.H, max_kv_len > 0 ? splits : 0, num_rows, tps, pr);
+    hipLaunchKernelGGL(attn_paged_combine_kernel, dim3(heads), dim3(256), 0, stream, ws, output,
+                       g.H, num_rows, G, kPagedPositions, kPass, pr);
     check_launch(prod ? "turbo_prod_paged_attn_combine" : "turbo_mse_paged_attn_combine");
 }
 
