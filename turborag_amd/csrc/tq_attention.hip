@@ -769,8 +769,9 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                 const uint32_t(*vw)[8] = cur.vw;
                 {
                     const float ks = h2f(cur.ks), vs = h2f(cur.vs), re = PROD ? h2f(cur.re) : 0.0f;
-                    tsc[w][lane & (kChunk - 1)] = cur.valid ? make_float4(ks * ck, ks * re * cr, vs, 0.0f)
-                                                            : make_float4(0.f, 0.f, 0.f, -INFINITY);
+                    tsc[w][lane & (kChunk - 1)] =
+                        cur.valid ? make_float4(ks * ck, ks * re * cr, 0.5f * vs, 0.0f)
+                                  : make_float4(0.f, 0.f, 0.f, -INFINITY);
                 }
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -828,36 +829,51 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                     }
                 }
                 const bool masked = t0 + kChunk > gmin_live;
+                // Logits (base 2) of tokens 16*tau + 4*gq + e for this lane's column.
                 float lg[NTA][kTiles][4];
 #pragma unroll
-                for (int t = 0; t < NTA; ++t) {
-                    // Logits (base 2) of tokens 16*tau + 4*gq + e for this lane's column.
-                    float mloc = -INFINITY;
+                for (int t = 0; t < NTA; ++t)
 #pragma unroll
                     for (int tau = 0; tau < kTiles; ++tau)
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             const float4 sc = tsc[w][16 * tau + 4 * gq + e];
                             lg[t][tau][e] = fmaf(cb[t][tau][e], sc.x, fmaf(cs[t][tau][e], sc.y, sc.w));
-                            if (masked)
-                                if (t0 + 16 * tau + 4 * gq + e >= rl_col[t]) lg[t][tau][e] = -INFINITY;
-                            mloc = fmaxf(mloc, lg[t][tau][e]);
                         }
-                    mloc = fmaxf(mloc, lane_xor<16>(mloc));
-                    mloc = fmaxf(mloc, lane_xor<32>(mloc));
-                    const float m_new = fmaxf(m_col[t], mloc);
-                    const float alpha = first ? 0.0f : __builtin_amdgcn_exp2f(m_col[t] - m_new);
-                    m_col[t] = m_new;
-                    float lsum = 0.0f;
+                if (masked) {  // a row of the unit ends in this chunk (wave-uniform)
+                    asm volatile("" ::: "memory");  // a branch: no selects on every chunk
+#pragma unroll
+                    for (int t = 0; t < NTA; ++t)
+#pragma unroll
+                        for (int tau = 0; tau < kTiles; ++tau)
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                if (t0 + 16 * tau + 4 * gq + e >= rl_col[t])
+                                    lg[t][tau][e] = -INFINITY;
+                }
+                // Online softmax with a lagging maximum: m_col moves (and the
+                // accumulators are rescaled) only when a logit passes it by more
+                // than 1, so the weights stay <= 2 (the PV operand is P * vs / 2).
+                float mloc[NTA];
+                bool grow = false;
+#pragma unroll
+                for (int t = 0; t < NTA; ++t) {
+                    float m = -INFINITY;
 #pragma unroll
                     for (int tau = 0; tau < kTiles; ++tau)
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            lg[t][tau][e] = __builtin_amdgcn_exp2f(lg[t][tau][e] - m_new);
-                            lsum += lg[t][tau][e];
-                        }
-                    l_col[t] = l_col[t] * alpha + lsum;
-                    if (!first && __any(alpha != 1.0f)) {
+                        for (int e = 0; e < 4; ++e) m = fmaxf(m, lg[t][tau][e]);
+                    m = fmaxf(m, lane_xor<16>(m));
+                    mloc[t] = fmaxf(m, lane_xor<32>(m));
+                    grow = grow || mloc[t] > m_col[t] + 1.0f;
+                }
+                if (__any(grow)) {  // wave-uniform
+#pragma unroll
+                    for (int t = 0; t < NTA; ++t) {
+                        const float m_new = fmaxf(m_col[t], mloc[t]);
+                        const float alpha = __builtin_amdgcn_exp2f(m_col[t] - m_new);
+                        m_col[t] = m_new;
+                        l_col[t] *= alpha;
                         // acc lane (d, gq) holds rows 4gq .. 4gq + 3 (columns of lanes 4gq + e)
                         float a[4];
 #pragma unroll
@@ -867,6 +883,18 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
 #pragma unroll
                             for (int e = 0; e < 4; ++e) acc_col[t][v][e] *= a[e];
                     }
+                }
+#pragma unroll
+                for (int t = 0; t < NTA; ++t) {
+                    float lsum = 0.0f;
+#pragma unroll
+                    for (int tau = 0; tau < kTiles; ++tau)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            lg[t][tau][e] = __builtin_amdgcn_exp2f(lg[t][tau][e] - m_col[t]);
+                            lsum += lg[t][tau][e];
+                        }
+                    l_col[t] += lsum;
                 }
                 // PV: every tile's hi and lo P against each decoded B operand
 #pragma unroll
@@ -959,7 +987,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
 #pragma unroll
                 for (int v = 0; v < 8; ++v)
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) mo[w][4 * gq + e][8 * i + v] = acc_col[t][v][e] * iav;
+                    for (int e = 0; e < 4; ++e)  // (x2: the PV operand was P * vs / 2)
+                        mo[w][4 * gq + e][8 * i + v] = acc_col[t][v][e] * (2.0f * iav);
             } else {
 #pragma unroll
                 for (int p = 0; p < NP; ++p)
