@@ -291,6 +291,17 @@ __device__ __forceinline__ _Float16 hi_lo(float x, bool lo) {
     const _Float16 h = (_Float16)x;
     return lo ? (_Float16)(x - (float)h) : h;
 }
+// The lo parts of (x0, x1) as an fp16 pair, given their hi parts h (fp16
+// pair, low half x0's): fp16(x - hi) with v_fma_mix (x * 1 - hi rounded once;
+// the difference is exact in fp32), one instruction per half.
+__device__ __forceinline__ uint32_t lo_pair(float x0, float x1, uint32_t h) {
+    uint32_t r;
+    asm("v_fma_mixlo_f16 %0, %1, 1.0, -%3 op_sel_hi:[0,0,1]\n\t"
+        "v_fma_mixhi_f16 %0, %2, 1.0, -%3 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
+        : "=&v"(r)
+        : "v"(x0), "v"(x1), "v"(h));
+    return r;
+}
 }  // namespace mfma
 
 // CH = tokens per wave iteration (32: two QK tiles, one PV step; 64: four and
@@ -901,14 +912,20 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                 for (int st = 0; st < kSteps; ++st) {
                     half8 ah[NTA], al[NTA];
 #pragma unroll
-                    for (int t = 0; t < NTA; ++t)
+                    for (int t = 0; t < NTA; ++t) {
+                        uint32_t hw[4], lw[4];
 #pragma unroll
-                        for (int e = 0; e < 8; ++e) {
+                        for (int e = 0; e < 8; e += 2) {
                             const int tau = 2 * st + (e >> 2), ee = e & 3;
-                            const float x = lg[t][tau][ee] * tsc[w][16 * tau + 4 * gq + ee].z;
-                            ah[t][e] = hi_lo(x, false);
-                            al[t][e] = hi_lo(x, true);
+                            const float x0 = lg[t][tau][ee] * tsc[w][16 * tau + 4 * gq + ee].z;
+                            const float x1 =
+                                lg[t][tau][ee + 1] * tsc[w][16 * tau + 4 * gq + ee + 1].z;
+                            hw[e >> 1] = pack_h2(x0, x1);
+                            lw[e >> 1] = lo_pair(x0, x1, hw[e >> 1]);
                         }
+                        ah[t] = as_h8(hw[0], hw[1], hw[2], hw[3]);
+                        al[t] = as_h8(lw[0], lw[1], lw[2], lw[3]);
+                    }
                     uint32_t bv[8][4];  // [N-tile v = d - 8i][token pair]
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
