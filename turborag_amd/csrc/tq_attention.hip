@@ -266,11 +266,24 @@ struct PagedRows {
     const int32_t* unit_of_group;
     const int32_t* plan;
 };
-// Workgroup s of G takes the work positions [bound(s), bound(s + 1)); a pass
-// belongs to the segment holding its first work position.
-__device__ __forceinline__ int seg_bound(int s, int total, int G) {
-    return (int)(((long long)s * total) / G);
-}
+// Workgroup s of G takes the work positions [bound(s), bound(s + 1)) with
+// bound(s) = floor(s * total / G) = q*s + floor(r*s / G) (q, r = total div, mod
+// G; r*s < G*G stays in 32 bits); a pass belongs to the segment holding its
+// first work position.
+struct Segments {
+    int q, r, G;
+    __device__ Segments(int total, int g) : q(total / g), r(total % g), G(g) {}
+    __device__ int bound(int s) const { return q * s + (int)((uint32_t)(r * s) / (uint32_t)G); }
+    // The segment holding work position x < total: an estimate within one of
+    // floor(((x + 1) G - 1) / total), then corrected.
+    __device__ int of(int x, int total) const {
+        int g = (int)(((double)x + 1.0) * G / total) - 1;
+        g = max(0, min(g, G - 1));
+        while (g + 1 < G && bound(g + 1) <= x) ++g;
+        while (g > 0 && bound(g) > x) --g;
+        return g;
+    }
+};
 // Passes [x0, x1) of an item (start S, n passes of weight w) that begin in
 // the work range [b0, b1).
 __device__ __forceinline__ void item_passes(int S, int n, int w, int b0, int b1, int& x0,
@@ -1056,7 +1069,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                                      : (int)blockIdx.x;
         const int nu = __builtin_amdgcn_readfirstlane(pr.plan[0]);
         const int total = __builtin_amdgcn_readfirstlane(pr.plan[1]);
-        const int b0 = seg_bound(seg, total, G), b1 = seg_bound(seg + 1, total, G);
+        const Segments sg(total, G);
+        const int b0 = sg.bound(seg), b1 = sg.bound(seg + 1);
         if (b0 >= b1) return;  // an empty segment (less work than workgroups)
         // The unit holding work position b0 (exactly one: the units' work
         // ranges partition [0, total)).
@@ -1248,9 +1262,10 @@ __global__ __launch_bounds__(256) void attn_paged_combine_kernel(
     const int S = un.start + h * un.w * un.n;
     // segments holding the item's first and last pass starts
     int g_lo = 0, g_hi = -1;
+    const Segments sg(max(total, 1), G);
     if (un.n > 0 && kv > 0) {
-        g_lo = (int)(((long long)(S + 1) * G - 1) / total);
-        g_hi = (int)(((long long)(S + un.w * (un.n - 1) + 1) * G - 1) / total);
+        g_lo = sg.of(S, total);
+        g_hi = sg.of(S + un.w * (un.n - 1), total);
     }
     const size_t slot0 = (size_t)u * H + h;
     float M = kInitMax, L = 0.f;
@@ -1262,8 +1277,7 @@ __global__ __launch_bounds__(256) void attn_paged_combine_kernel(
         for (int k = 0; k < 8; ++k) {
             const int gs = min(b + k, g_hi);
             int x0, x1;
-            item_passes(S, un.n, un.w, seg_bound(gs, total, G), seg_bound(gs + 1, total, G), x0,
-                        x1);
+            item_passes(S, un.n, un.w, sg.bound(gs), sg.bound(gs + 1), x0, x1);
             const bool ok = b + k <= g_hi && x0 < x1 && x0 * pass < kv;
             const float* pp =
                 ws + (((slot0 + gs) * positions + p) * kRows + r) * kPartStride;
