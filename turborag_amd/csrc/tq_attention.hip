@@ -239,6 +239,10 @@ constexpr int kPartStride = 128 + 4;  // floats per partial row: o[128], m, l, p
 __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
     return __builtin_bit_cast(uint32_t, (half2v){(_Float16)a, (_Float16)b});
 }
+// One 16x16x32 fp16 MFMA: c += a * b (fp32 accumulate).
+__device__ __forceinline__ f32x4 mma(half8 a, half8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
 __device__ __forceinline__ half8 as_h8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
     return __builtin_bit_cast(half8, (u32x4){a, b, c, d});
 }
@@ -454,17 +458,20 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
             // K row: code_stride bytes, or QJL's D/8 = 16 sign bytes
             const uint64_t kstride = QJL ? 16u : (uint64_t)g.code_stride;
             tko[w][lane & (kChunk - 1)] = c.valid ? pb + g.kc_off + cell * kstride : dummy_off;
-            tvo[w][lane & (kChunk - 1)] = c.valid ? pb + g.vc_off + cell * g.code_stride : dummy_off;
+            tvo[w][lane & (kChunk - 1)] =
+                c.valid ? pb + g.vc_off + cell * g.code_stride : dummy_off;
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
             for (int tau = 0; tau < kTiles; ++tau) {
                 if constexpr (QJL)  // sign bytes 4gq .. 4gq + 3: k-steps 0 .. 3
                     c.kw[tau] = make_uint4(
-                        *reinterpret_cast<const uint32_t*>(pool + (tko[w][16 * tau + i] + 4 * gq)), 0u,
+                        *reinterpret_cast<const uint32_t*>(pool + (tko[w][16 * tau + i] + 4 * gq)),
+                        0u,
                         0u, 0u);
                 else
-                    c.kw[tau] = *reinterpret_cast<const uint4*>(pool + (tko[w][16 * tau + i] + 16 * gq));
+                    c.kw[tau] =
+                        *reinterpret_cast<const uint4*>(pool + (tko[w][16 * tau + i] + 16 * gq));
             }
             // k-step p covers tiles 2p, 2p+1; k-index 8gq + e is token
             // 32p + 4gq + e (e < 4) or 32p + 16 + 4gq + (e - 4).
@@ -591,7 +598,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
         const uint32_t lut_hi = lutk & 0xFF00u;  // byte 1 of the base, re-added after the perm
         auto lookup = [&](uint32_t word, int b, int table) -> uint32_t {
             const uint32_t base = table ? lutv : lutk;
-            const uint32_t a = __builtin_amdgcn_perm(word, base, 0x03020000u | ((4u + b) << 8)) + lut_hi;
+            const uint32_t a =
+                __builtin_amdgcn_perm(word, base, 0x03020000u | ((4u + b) << 8)) + lut_hi;
             return *reinterpret_cast<const lds_u32*>(a);
         };
         // QJL: the fp16 +-1 octet of sign byte b of word (copy lane % 8).
@@ -627,7 +635,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                     const float ks = h2f(cur.ks), vs = h2f(cur.vs), re = PROD ? h2f(cur.re) : 0.0f;
                     const float4 sc = QJL ? make_float4(0.0f, ks * kLog2e, vs, 0.0f)
                                           : make_float4(ks * ck, ks * re * cr, vs, 0.0f);
-                    tsc[w][lane & (kChunk - 1)] = cur.valid ? sc : make_float4(0.f, 0.f, 0.f, -INFINITY);
+                    tsc[w][lane & (kChunk - 1)] =
+                        cur.valid ? sc : make_float4(0.f, 0.f, 0.f, -INFINITY);
                 }
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -654,29 +663,27 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                             const half8 sa = signs(wd[0], s);
         #pragma unroll
                             for (int p = 0; p < NPA; ++p)
-                                cs[p][tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sa, bq[p][s],
-                                                                                    cs[p][tau], 0, 0, 0);
+                                cs[p][tau] = mma(sa, bq[p][s], cs[p][tau]);
                             continue;
                         }
                         const half8 a = as_h8(lookup(wd[s], 0, 0), lookup(wd[s], 1, 0),
                                               lookup(wd[s], 2, 0), lookup(wd[s], 3, 0));
         #pragma unroll
                         for (int p = 0; p < NPA; ++p)
-                            cb[p][tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[p][s], cb[p][tau],
-                                                                                0, 0, 0);
+                            cb[p][tau] = mma(a, bq[p][s], cb[p][tau]);
                         if (PROD) {
                             // Residual signs (nibble bit 3: 1 -> +1) as fp16 pairs in
                             // registers: high bytes 0x3C / 0xBC, low bytes 0.
-                            const uint32_t he = ((wd[s] << 4) & 0x80808080u) ^ 0xBCBCBCBCu;  // even d
-                            const uint32_t ho = (wd[s] & 0x80808080u) ^ 0xBCBCBCBCu;         // odd d
+                            // even d, odd d
+                            const uint32_t he = ((wd[s] << 4) & 0x80808080u) ^ 0xBCBCBCBCu;
+                            const uint32_t ho = (wd[s] & 0x80808080u) ^ 0xBCBCBCBCu;
                             const half8 sa = as_h8(__builtin_amdgcn_perm(ho, he, 0x040C000Cu),
                                                    __builtin_amdgcn_perm(ho, he, 0x050C010Cu),
                                                    __builtin_amdgcn_perm(ho, he, 0x060C020Cu),
                                                    __builtin_amdgcn_perm(ho, he, 0x070C030Cu));
         #pragma unroll
                             for (int p = 0; p < NPA; ++p)
-                                cs[p][tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sa, bq[p][s],
-                                                                                    cs[p][tau], 0, 0, 0);
+                                cs[p][tau] = mma(sa, bq[p][s], cs[p][tau]);
                         }
                     }
                 }
@@ -702,7 +709,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                                 lg[p][tau][e] = fmaf(sb, sc.x, fmaf(sr, sc.y, sc.w));
                             }
                             if (masked)  // causal limit of this column's row
-                                if (t0 + 16 * tau + 4 * gq + e >= rowlen[p]) lg[p][tau][e] = -INFINITY;
+                                if (t0 + 16 * tau + 4 * gq + e >= rowlen[p])
+                                    lg[p][tau][e] = -INFINITY;
                             mloc = fmaxf(mloc, lg[p][tau][e]);
                         }
                     mloc = fmaxf(mloc, lane_xor<16>(mloc));
@@ -762,8 +770,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                         const half8 bvv = as_h8(bv[v][0], bv[v][1], bv[v][2], bv[v][3]);
         #pragma unroll
                         for (int p = 0; p < NPA; ++p)
-                            acc[p][v] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ap[p], bvv, acc[p][v], 0, 0,
-                                                                               0);
+                            acc[p][v] = mma(ap[p], bvv, acc[p][v]);
                     }
                 }
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -830,10 +837,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                                               lookup(wd, 3, 0));
 #pragma unroll
                         for (int t = 0; t < NTA; ++t) {
-                            cb[t][tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bk[2 * t],
-                                                                                cb[t][tau], 0, 0, 0);
-                            cb[t][tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bk[2 * t + 1],
-                                                                                cb[t][tau], 0, 0, 0);
+                            cb[t][tau] = mma(a, bk[2 * t], cb[t][tau]);
+                            cb[t][tau] = mma(a, bk[2 * t + 1], cb[t][tau]);
                         }
                         if (PROD) {
                             const uint32_t he = ((wd << 4) & 0x80808080u) ^ 0xBCBCBCBCu;  // even d
@@ -844,10 +849,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                                                    __builtin_amdgcn_perm(ho, he, 0x070C030Cu));
 #pragma unroll
                             for (int t = 0; t < NTA; ++t) {
-                                cs[t][tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                                    sa, bk[2 * t], cs[t][tau], 0, 0, 0);
-                                cs[t][tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                                    sa, bk[2 * t + 1], cs[t][tau], 0, 0, 0);
+                                cs[t][tau] = mma(sa, bk[2 * t], cs[t][tau]);
+                                cs[t][tau] = mma(sa, bk[2 * t + 1], cs[t][tau]);
                             }
                         }
                     }
@@ -862,7 +865,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             const float4 sc = tsc[w][16 * tau + 4 * gq + e];
-                            lg[t][tau][e] = fmaf(cb[t][tau][e], sc.x, fmaf(cs[t][tau][e], sc.y, sc.w));
+                            lg[t][tau][e] =
+                                fmaf(cb[t][tau][e], sc.x, fmaf(cs[t][tau][e], sc.y, sc.w));
                         }
                 if (masked) {  // a row of the unit ends in this chunk (wave-uniform)
                     asm volatile("" ::: "memory");  // a branch: no selects on every chunk
@@ -956,10 +960,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                         const half8 bvv = as_h8(bv[v][0], bv[v][1], bv[v][2], bv[v][3]);
 #pragma unroll
                         for (int t = 0; t < NTA; ++t) {
-                            acc_col[t][v] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[t], bvv,
-                                                                                   acc_col[t][v], 0, 0, 0);
-                            acc_col[t][v] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[t], bvv,
-                                                                                   acc_col[t][v], 0, 0, 0);
+                            acc_col[t][v] = mma(ah[t], bvv, acc_col[t][v]);
+                            acc_col[t][v] = mma(al[t], bvv, acc_col[t][v]);
                         }
                     }
                 }
@@ -1025,7 +1027,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
 #pragma unroll
                     for (int v = 0; v < 8; ++v) {
                         mo[w][p * kRows + 2 * gq][8 * i + v] = (acc[p][v][0] + acc[p][v][1]) * iav;
-                        mo[w][p * kRows + 2 * gq + 1][8 * i + v] = (acc[p][v][2] + acc[p][v][3]) * iav;
+                        mo[w][p * kRows + 2 * gq + 1][8 * i + v] =
+                            (acc[p][v][2] + acc[p][v][3]) * iav;
                     }
             }
             __syncthreads();
@@ -1283,7 +1286,8 @@ __global__ __launch_bounds__(256) void attn_paged_combine_kernel(
                 ws + (((slot0 + gs) * positions + p) * kRows + r) * kPartStride;
             pm[k] = ok ? pp[128] : kInitMax;
             pl[k] = ok ? pp[129] : 0.f;
-            po[k] = ok ? *reinterpret_cast<const float4*>(pp + d0) : make_float4(0.f, 0.f, 0.f, 0.f);
+            po[k] = ok ? *reinterpret_cast<const float4*>(pp + d0)
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
         }
         float mb = M;
 #pragma unroll
