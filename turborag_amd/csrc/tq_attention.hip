@@ -1571,6 +1571,11 @@ void launch_paged_attention(Scheme s, const uint16_t* query, const uint8_t* pool
     // G a multiple of 8 (the kernel's XCD mapping).
     constexpr int kPass = kSplitChunk * kSplitWaves;
     const int G = 8 * ((kPagedSegmentsPerCU * num_cus() + 7) / 8);
+    // The plan counts work in int32: at most H * 4 * ceil(max_kv_len / kPass)
+    // per row group.
+    if ((long long)row_groups * g.H * 4 * ((std::max(max_kv_len, 0) + kPass - 1) / kPass) >
+        INT32_MAX)
+        throw Error("paged attention: too many rows for this max_kv_len");
     // Workspace: the partials (slot item + segment: at most heads + G - 1
     // slots of kPagedPositions positions), then the plan.
     const size_t part_bytes =
