@@ -257,7 +257,7 @@ __device__ __forceinline__ half8 as_h8(uint32_t a, uint32_t b, uint32_t c, uint3
 // and item h takes work positions [start + h*w*n, start + (h+1)*w*n) of the
 // step's total work.
 struct PagedUnit {
-    int32_t first, npos, kv_end, start, n, w, pad0, pad1;
+    int32_t first, npos, kv_end, start, n, w, index, pad;  // index: the unit's number
 };
 struct PagedRows {
     const int32_t* block_tables;
@@ -265,9 +265,9 @@ struct PagedRows {
     const int32_t* row_kv_len;
     int max_blocks;
     // The step's plan (paged_plan_kernel): plan[0] units, then a sentinel
-    // whose start is the total work plan[1]; the unit of each row group.
+    // whose start is the total work plan[1]; a copy of each row group's unit.
     const PagedUnit* units;
-    const int32_t* unit_of_group;
+    const PagedUnit* group_unit;
     const int32_t* plan;
 };
 // Workgroup s of G takes the work positions [bound(s), bound(s + 1)) with
@@ -281,7 +281,7 @@ struct Segments {
     // The segment holding work position x < total: an estimate within one of
     // floor(((x + 1) G - 1) / total), then corrected.
     __device__ int of(int x, int total) const {
-        int g = (int)(((double)x + 1.0) * G / total) - 1;
+        int g = (int)(((float)x + 1.0f) * (float)G / (float)total) - 1;
         g = max(0, min(g, G - 1));
         while (g + 1 < G && bound(g + 1) <= x) ++g;
         while (g > 0 && bound(g) > x) --g;
@@ -1254,8 +1254,8 @@ __global__ __launch_bounds__(256) void attn_paged_combine_kernel(
     const int item = blockIdx.x;  // h + H * rg
     const int h = item % H, rg = item / H;
     const int t = threadIdx.x, r = t >> 5, d0 = 4 * (t & 31);
-    const int u = pr.unit_of_group[rg];
-    const PagedUnit un = pr.units[u];
+    const PagedUnit un = pr.group_unit[rg];
+    const int u = un.index;
     const int total = pr.plan[1], G = num_segments;
     const int p = rg - un.first;
     int kv = 0;
@@ -1347,7 +1347,7 @@ template <int U>
 __global__ __launch_bounds__(1024) void paged_plan_kernel(
     const int32_t* __restrict__ row_seq, const int32_t* __restrict__ row_kv_len, int num_rows,
     int groups, int H, int pass, int max_kv_len, mfma::PagedUnit* __restrict__ units,
-    int32_t* __restrict__ unit_of_group, int32_t* __restrict__ plan) {
+    mfma::PagedUnit* __restrict__ group_unit, int32_t* __restrict__ plan) {
     static_assert(U >= 1 && U <= 4 && (U & (U - 1)) == 0, "1, 2 or 4 groups per unit");
     using mfma::kRows;
     constexpr int kWin = 1024;
@@ -1396,8 +1396,9 @@ __global__ __launch_bounds__(1024) void paged_plan_kernel(
         const int wi = block_scan_1024(work, 0, s_tot, add);
         if (start) {
             const int o = c_units + ui - 1;
-            units[o] = mfma::PagedUnit{gi, c, kv, c_work + wi - work, n, w, 0, 0};
-            for (int k = 0; k < c; ++k) unit_of_group[gi + k] = o;
+            const mfma::PagedUnit rec{gi, c, kv, c_work + wi - work, n, w, o, 0};
+            units[o] = rec;
+            for (int k = 0; k < c; ++k) group_unit[gi + k] = rec;
         }
         if (j == kWin - 1) {  // window totals (inclusive scans at the last thread)
             s_carry[0] = ui;
@@ -1413,7 +1414,7 @@ __global__ __launch_bounds__(1024) void paged_plan_kernel(
         __syncthreads();  // before the next window rewrites s_sq and s_carry
     }
     if (j == 0) {
-        units[c_units] = mfma::PagedUnit{0, 0, 0, c_work, 0, 1, 0, 0};  // sentinel
+        units[c_units] = mfma::PagedUnit{0, 0, 0, c_work, 0, 1, c_units, 0};  // sentinel
         plan[0] = c_units;
         plan[1] = c_work;
     }
@@ -1577,22 +1578,22 @@ void launch_paged_attention(Scheme s, const uint16_t* query, const uint8_t* pool
         INT32_MAX)
         throw Error("paged attention: too many rows for this max_kv_len");
     // Workspace: the partials (slot item + segment: at most heads + G - 1
-    // slots of kPagedPositions positions), then the plan.
+    // slots of kPagedPositions positions), then the plan: the units and a
+    // sentinel, each row group's unit, the unit count and total work.
     const size_t part_bytes =
         ((size_t)heads + G) * kPagedPositions * kRows * kPartStride * sizeof(float);
-    const size_t unit_bytes = ((size_t)row_groups + 1) * sizeof(PagedUnit);
-    char* wsb = static_cast<char*>(workspace(
-        stream, part_bytes + unit_bytes + ((size_t)row_groups + 4) * sizeof(int32_t)));
+    const size_t unit_bytes = (2 * (size_t)row_groups + 1) * sizeof(PagedUnit);
+    char* wsb = static_cast<char*>(workspace(stream, part_bytes + unit_bytes + 4 * sizeof(int32_t)));
     float* ws = reinterpret_cast<float*>(wsb);
     PagedUnit* units = reinterpret_cast<PagedUnit*>(wsb + part_bytes);
+    PagedUnit* group_unit = units + row_groups + 1;
     int32_t* plan = reinterpret_cast<int32_t*>(wsb + part_bytes + unit_bytes);
-    int32_t* unit_of_group = plan + 4;
-    const PagedRows pr{block_tables, row_seq, row_kv_len, max_blocks, units, unit_of_group, plan};
+    const PagedRows pr{block_tables, row_seq, row_kv_len, max_blocks, units, group_unit, plan};
     const bool prod = s == Scheme::Prod;
     constexpr int kCH = kSplitChunk, kNW = kSplitWaves;
     hipLaunchKernelGGL(paged_plan_kernel<kPagedPositions>, dim3(1), dim3(1024), 0, stream, row_seq,
                        row_kv_len, num_rows, row_groups, g.H, kPass, std::max(max_kv_len, 0),
-                       units, unit_of_group, plan);
+                       units, group_unit, plan);
     check_launch(prod ? "turbo_prod_paged_attn_plan" : "turbo_mse_paged_attn_plan");
     if (max_kv_len > 0) {
         if (prod)
