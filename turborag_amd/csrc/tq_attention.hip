@@ -397,7 +397,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                 const int lv = p < npos && rr < num_queries ? pr.row_kv_len[rr] : 0;
                 rowlen[p] = __shfl(lv, i >> 1);
                 const int lc = __shfl(lv, i & 7);
-                if (NP >= 2 && (i >> 3) == (p & 1)) rl_col[p >> 1] = lc;
+                // (one position: both halves of the tile hold its rows, hi and lo)
+                if (NP >= 2 && (npos == 1 ? p == 0 : (i >> 3) == (p & 1))) rl_col[p >> 1] = lc;
                 int m = max(lv, __shfl_xor(lv, 1)), n = min(lv, __shfl_xor(lv, 1));
                 m = max(m, __shfl_xor(m, 2));
                 n = min(n, __shfl_xor(n, 2));
@@ -572,7 +573,12 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
             const int p = ps >> 2, s = ps & 3;
             if (NP >= 2 && (p >> 1) >= ntile) break;  // unused tiles (never read)
             half8 b;
-            if constexpr (NP >= 2) {  // tile p / 2, part p % 2 (hi, lo) of column i's row, k-step s
+            if (NP >= 2 && npos == 1) {  // one position: columns (part i / 8, row i % 8)
+                if (p != 0) continue;
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    b[e] = hi_lo(qs[i & 7][32 * gq + 8 * s + e], (i >> 3) != 0);
+            } else if constexpr (NP >= 2) {  // tile p / 2, part p % 2 (hi, lo) of column i's row
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
                     b[e] = hi_lo(qs[16 * (p >> 1) + i][32 * gq + 8 * s + e], (p & 1) != 0);
@@ -793,8 +799,14 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
 #pragma unroll
             for (int v = 0; v < 8; ++v) acc_col[t][v] = (f32x4){0.f, 0.f, 0.f, 0.f};
         }
-        auto stacked_loop = [&](auto nta) {
+        // COLS (a unit of one position): one tile whose columns are the
+        // position's rows as hi (columns 0-7) and lo (8-15) parts, as in the
+        // one-group kernel: one MFMA per product instead of two, and the two
+        // halves of a column pair summed (logits; outputs at the merge).
+        auto stacked_loop = [&](auto nta, auto cols) {
             constexpr int NTA = decltype(nta)::value;
+            constexpr bool COLS = decltype(cols)::value;
+            static_assert(!COLS || NTA == 1, "one tile");
             while (t0 < t_end) {  // wave-uniform
                 const uint4* kw = cur.kw;
                 const uint32_t(*vw)[8] = cur.vw;
@@ -825,7 +837,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                 for (int s = 0; s < 4; ++s) {
                     half8 bk[2 * NTA];  // k-step s of each tile's hi and lo query
 #pragma unroll
-                    for (int pp = 0; pp < 2 * NTA; ++pp)
+                    for (int pp = 0; pp < (COLS ? 1 : 2 * NTA); ++pp)
                         bk[pp] = __builtin_bit_cast(half8, bqs[pp][s][lane]);
 #pragma unroll
                     for (int tau = 0; tau < kTiles; ++tau) {
@@ -838,7 +850,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
 #pragma unroll
                         for (int t = 0; t < NTA; ++t) {
                             cb[t][tau] = mma(a, bk[2 * t], cb[t][tau]);
-                            cb[t][tau] = mma(a, bk[2 * t + 1], cb[t][tau]);
+                            if (!COLS) cb[t][tau] = mma(a, bk[2 * t + 1], cb[t][tau]);
                         }
                         if (PROD) {
                             const uint32_t he = ((wd << 4) & 0x80808080u) ^ 0xBCBCBCBCu;  // even d
@@ -850,7 +862,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
 #pragma unroll
                             for (int t = 0; t < NTA; ++t) {
                                 cs[t][tau] = mma(sa, bk[2 * t], cs[t][tau]);
-                                cs[t][tau] = mma(sa, bk[2 * t + 1], cs[t][tau]);
+                                if (!COLS) cs[t][tau] = mma(sa, bk[2 * t + 1], cs[t][tau]);
                             }
                         }
                     }
@@ -865,8 +877,12 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             const float4 sc = tsc[w][16 * tau + 4 * gq + e];
-                            lg[t][tau][e] =
-                                fmaf(cb[t][tau][e], sc.x, fmaf(cs[t][tau][e], sc.y, sc.w));
+                            float b = cb[t][tau][e], r = cs[t][tau][e];
+                            if constexpr (COLS) {  // + the partner column (lane ^ 8)
+                                b += lane_xor<8>(b);
+                                r += lane_xor<8>(r);
+                            }
+                            lg[t][tau][e] = fmaf(b, sc.x, fmaf(r, sc.y, sc.w));
                         }
                 if (masked) {  // a row of the unit ends in this chunk (wave-uniform)
                     asm volatile("" ::: "memory");  // a branch: no selects on every chunk
@@ -940,8 +956,14 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                             hw[e >> 1] = pack_h2(x0, x1);
                             lw[e >> 1] = lo_pair(x0, x1, hw[e >> 1]);
                         }
-                        ah[t] = as_h8(hw[0], hw[1], hw[2], hw[3]);
-                        al[t] = as_h8(lw[0], lw[1], lw[2], lw[3]);
+                        if constexpr (COLS) {  // column i < 8: hi; i >= 8: lo
+                            const bool lo = (i >> 3) != 0;
+                            ah[t] = as_h8(lo ? lw[0] : hw[0], lo ? lw[1] : hw[1], lo ? lw[2] : hw[2],
+                                          lo ? lw[3] : hw[3]);
+                        } else {
+                            ah[t] = as_h8(hw[0], hw[1], hw[2], hw[3]);
+                            al[t] = as_h8(lw[0], lw[1], lw[2], lw[3]);
+                        }
                     }
                     uint32_t bv[8][4];  // [N-tile v = d - 8i][token pair]
 #pragma unroll
@@ -961,7 +983,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
 #pragma unroll
                         for (int t = 0; t < NTA; ++t) {
                             acc_col[t][v] = mma(ah[t], bvv, acc_col[t][v]);
-                            acc_col[t][v] = mma(al[t], bvv, acc_col[t][v]);
+                            if (!COLS) acc_col[t][v] = mma(al[t], bvv, acc_col[t][v]);
                         }
                     }
                 }
@@ -974,9 +996,11 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
         };
         if constexpr (NP >= 2) {
             if (NT == 2 && ntile == 2)
-                stacked_loop(std::integral_constant<int, NT>{});
+                stacked_loop(std::integral_constant<int, NT>{}, std::false_type{});
+            else if (npos == 1)
+                stacked_loop(std::integral_constant<int, 1>{}, std::true_type{});
             else
-                stacked_loop(std::integral_constant<int, 1>{});
+                stacked_loop(std::integral_constant<int, 1>{}, std::false_type{});
         } else {
             chunk_loop(std::integral_constant<int, 1>{});
         }
@@ -1048,6 +1072,14 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                     L += ml[u][r] * wt;
                     o0 += mo[u][rr][2 * lane] * wt;
                     o1 += mo[u][rr][2 * lane + 1] * wt;
+                }
+                if (NP >= 2 && npos == 1) {  // one position: + its lo columns 8-15
+#pragma unroll
+                    for (int u = 0; u < kWaves; ++u) {
+                        const float wt = exp2f(mm[u][r] - M);
+                        o0 += mo[u][rr + kRows][2 * lane] * wt;
+                        o1 += mo[u][rr + kRows][2 * lane + 1] * wt;
+                    }
                 }
                 wht_pair<64>(o0, o1, lane);
                 float* part = ws + ((pid * NP + p) * kRows + r % kRows) * kPartStride;
