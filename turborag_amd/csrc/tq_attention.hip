@@ -325,12 +325,14 @@ __device__ __forceinline__ uint32_t lo_pair(float x0, float x1, uint32_t h) {
 // two); NW = waves per workgroup; NP = row groups per workgroup.
 // NP = 1: the 16 MFMA columns are the group's 8 query rows as fp16 hi and lo
 // parts (columns 2r, 2r + 1), summed after each product.
-// NP = 2 (paged rows): two new tokens of one sequence share every decoded K/V
-// chunk; the 16 columns are (position, row) = (i / 8, i % 8) and the hi and lo
-// parts are stacked along the reduction instead (QK: k-steps s and s + 4 take
-// the same decoded K against the hi and the lo query; PV: the hi and the lo P
-// against the same decoded V), so each lane's column is one query row and its
-// softmax runs once.
+// NP = 2 or 4 (paged rows): the new tokens (row groups) of one sequence in a
+// unit share every decoded K/V chunk; each tile of 16 columns is (position,
+// row) = (i / 8, i % 8) of two positions, and the hi and lo parts are stacked
+// along the reduction instead (QK: the same decoded K against the hi and the
+// lo query; PV: the hi and the lo P against the same decoded V), so each
+// lane's column is one query row and its softmax runs once.  A unit of one
+// position uses the one-group column layout in its tile.  PAGED: the grid is
+// one workgroup per work segment of the step's plan (paged_plan_kernel).
 // SCH = page scheme (kSch*).  QJL: the A operand of QK is the +-1 sign
 // matrix, read as fp16 octets from an LDS table indexed by sign byte; the
 // logit is ks * <qrot, signs> (no 1/sqrt(D) beyond the rotation's, :254);
@@ -630,8 +632,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
         bool first = true;
         int slot_nx = load_slot(t0 + kWaves * kChunk);
 
-        // The chunk loop, for the positions the workgroup has (a pair unit of a
-        // single group runs the one-position loop).
+        // The chunk loop of the one-group layout (NP = 1).
         auto chunk_loop = [&](auto npa) {
             constexpr int NPA = decltype(npa)::value;
             while (t0 < t_end) {  // wave-uniform
