@@ -212,6 +212,17 @@ int tq_launch_turbo_mse_paged_attention(const uint16_t* query, const uint8_t* pa
                                         const TQConfig* cfg, int num_rows, int max_kv_len,
                                         void* stream);
 
+/* No reference counterpart (its attention kernels need no scratch).  The
+ * split-K attention entries keep one device workspace per (device, stream);
+ * an outgrown one is freed once the stream's earlier kernels finished, and
+ * one handed out while its stream was captured into a graph is kept for that
+ * graph.  This synchronizes every device holding one and frees them all:
+ * for callers that cycle through many streams or free a stream handle that
+ * a new stream may reuse.  Graphs captured before it must not be replayed
+ * after it.  Not concurrent-safe with attention calls in flight on other
+ * host threads. */
+int tq_workspace_release(void);
+
 /* ---------------------------------------------------------------------- */
 /* Page allocator and block table (host bookkeeping).                       */
 /* Replaces TQAllocator (src/tq_allocator.cpp:5-31, include/tq_allocator.h) */

@@ -148,6 +148,137 @@ def test_meta_missing_file(sio, tmp_path):
         sio.read_meta(tmp_path / "nope.meta")
 
 
+# ── crafted archives: offsets and sizes from the file near 2^64 ──────── #
+
+def _records_of_valid_meta(n=7):
+    buf = io.BytesIO()
+    torch.save({"num_tokens": n, "slots": torch.arange(n, dtype=torch.int32)}, buf)
+    z = zipfile.ZipFile(io.BytesIO(buf.getvalue()))
+    return [(name, z.read(name)) for name in z.namelist()]
+
+
+def _hand_zip(records, patch=None):
+    """A stored zip written field by field (APPNOTE 4.3.7, 4.3.12, 4.3.16).
+    patch(name) may return {"lho": int, "usize": int, "csize": int,
+    "zip64": [u64, ...]}: 32-bit central-directory fields to write instead of
+    the true ones, and the values of a zip64 extra field (id 1)."""
+    import binascii
+    body, cd = b"", b""
+    for name, data in records:
+        nm = name.encode()
+        crc = binascii.crc32(data)
+        lho = len(body)
+        body += struct.pack("<IHHHHHIIIHH", 0x04034B50, 20, 0, 0, 0, 0x21, crc, len(data),
+                            len(data), len(nm), 0) + nm + data
+        p = (patch(name) if patch else None) or {}
+        extra = b""
+        if "zip64" in p:
+            vals = p["zip64"]
+            extra = struct.pack("<HH", 1, 8 * len(vals)) + b"".join(struct.pack("<Q", v) for v in vals)
+        cd += struct.pack("<IHHHHHHIIIHHHHHII", 0x02014B50, 20, 20, 0, 0, 0, 0x21, crc,
+                          p.get("csize", len(data)), p.get("usize", len(data)), len(nm), len(extra),
+                          0, 0, 0, 0, p.get("lho", lho)) + nm + extra
+    eocd = struct.pack("<IHHHHIIH", 0x06054B50, 0, 0, len(records), len(records), len(cd),
+                       len(body), 0)
+    return body + cd + eocd
+
+
+def test_hand_zip_helper_makes_a_readable_meta(sio, tmp_path):
+    p = tmp_path / "ok.meta"
+    p.write_bytes(_hand_zip(_records_of_valid_meta(7)))
+    n, s, _ = sio.read_meta(p)
+    assert n == 7 and torch.equal(s, torch.arange(7, dtype=torch.int32))
+
+
+@pytest.mark.parametrize("lho64", [0xFFFFFFFFFFFFFFFE, 0xFFFFFFFFFFFFFFFF, 1 << 63, 0x100000000])
+def test_meta_zip64_local_header_offset_past_the_file(sio, tmp_path, lho64):
+    # the data.pkl record's local-header offset comes from a zip64 extra
+    # field: rejected as beyond the file, not read before the buffer
+    recs = _records_of_valid_meta()
+    patch = lambda name: ({"lho": 0xFFFFFFFF, "zip64": [lho64]}
+                          if name.endswith("data.pkl") else None)
+    p = tmp_path / "lho.meta"
+    p.write_bytes(_hand_zip(recs, patch))
+    with pytest.raises(RuntimeError, match="beyond the file"):
+        sio.read_meta(p)
+
+
+@pytest.mark.parametrize("size64", [0xFFFFFFFFFFFFFF00, 0xFFFFFFFFFFFFFFFF, 1 << 40])
+def test_meta_zip64_record_size_past_the_file(sio, tmp_path, size64):
+    recs = _records_of_valid_meta()
+    patch = lambda name: ({"usize": 0xFFFFFFFF, "csize": 0xFFFFFFFF, "zip64": [size64, size64]}
+                          if name.endswith("data.pkl") else None)
+    p = tmp_path / "size.meta"
+    p.write_bytes(_hand_zip(recs, patch))
+    with pytest.raises(RuntimeError, match="beyond the file"):
+        sio.read_meta(p)
+
+
+def test_meta_short_zip64_extra_field(sio, tmp_path):
+    # the field claims the offset is in zip64 but carries no value for it
+    recs = _records_of_valid_meta()
+    patch = lambda name: {"lho": 0xFFFFFFFF, "zip64": []} if name.endswith("data.pkl") else None
+    p = tmp_path / "short.meta"
+    p.write_bytes(_hand_zip(recs, patch))
+    with pytest.raises(RuntimeError, match="short zip64"):
+        sio.read_meta(p)
+
+
+@pytest.mark.parametrize("n", [0xFFFFFFFFFFFFFFF0, 0xFFFFFFFFFFFFFFFF, 1 << 63])
+def test_pickle_binunicode8_huge_length(sio, tmp_path, n):
+    # BINUNICODE8 (0x8d) with a length near 2^64: "truncated", and the
+    # position never wraps back into the pickle
+    pkl = b"\x80\x04}\x8d" + struct.pack("<Q", n) + b"num_tokens" + b"K\x05s."
+    p = tmp_path / "u8.meta"
+    _zip_with_pickle(p, pkl)
+    with pytest.raises(RuntimeError, match="truncated"):
+        sio.read_meta(p)
+
+
+def _meta_pickle(shape, stride, offset=0, numel=4):
+    """{"num_tokens": 1, "slots": tensor} with the tensor's shape, stride and
+    storage offset as given (protocol 2, as torch.save emits it)."""
+    def ints(vals):
+        out = b"("
+        for v in vals:
+            out += b"\x8a\x08" + struct.pack("<q", v)
+        return out + b"t"
+    return (b"\x80\x02}(X\x0a\x00\x00\x00num_tokensK\x01X\x05\x00\x00\x00slots"
+            b"ctorch._utils\n_rebuild_tensor_v2\n(("
+            b"X\x07\x00\x00\x00storagectorch\nIntStorage\nX\x01\x00\x00\x000X\x03\x00\x00\x00cpu"
+            + b"\x8a\x08" + struct.pack("<q", numel) + b"tQ"
+            + b"\x8a\x08" + struct.pack("<q", offset) + ints(shape) + ints(stride)
+            + b"\x89ccollections\nOrderedDict\n)RtRu.")
+
+
+def _meta_with_tensor(path, shape, stride, offset=0, numel=4):
+    with zipfile.ZipFile(path, "w", compression=zipfile.ZIP_STORED) as z:
+        z.writestr("x/data.pkl", _meta_pickle(shape, stride, offset, numel))
+        z.writestr("x/data/0", np.arange(numel, dtype=np.int32).tobytes())
+
+
+def test_meta_tensor_pickle_helper_reads(sio, tmp_path):
+    p = tmp_path / "t.meta"
+    _meta_with_tensor(p, [3], [1], offset=1)
+    n, s, _ = sio.read_meta(p)
+    assert n == 1 and s.tolist() == [1, 2, 3]
+
+
+@pytest.mark.parametrize("shape,stride,offset,msg", [
+    ([1 << 62, 4], [4, 1], 0, "exceeds its storage"),         # element count overflows int64
+    ([1 << 32, 1 << 32], [1 << 32, 1], 0, "exceeds its storage"),
+    ([4], [1], 1 << 62, "exceeds its storage"),               # offset + n would wrap
+    ([4], [1], -1, "exceeds its storage"),
+    ([-4], [1], 0, "negative dimension"),
+    ([2, 2], [2], 0, "ranks differ"),                          # stride shorter than shape
+])
+def test_meta_tensor_geometry_from_the_file_is_checked(sio, tmp_path, shape, stride, offset, msg):
+    p = tmp_path / "g.meta"
+    _meta_with_tensor(p, shape, stride, offset)
+    with pytest.raises(RuntimeError, match=msg):
+        sio.read_meta(p)
+
+
 # ── fp16 scheme .bin ─────────────────────────────────────────────────── #
 
 def test_fp16_written_here_reads_with_torch(sio, tmp_path):

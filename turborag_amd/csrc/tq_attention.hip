@@ -228,6 +228,13 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 constexpr float kAlphaK = 1.2918981f;
 constexpr float kAlphaV = 1.5982153f;
+// turbo_mse K: the fp16 table of aV*V4 alone is exact only to 9.2e-5, which
+// logits of magnitude ~40 (outlier channels shared by q and k) turn into
+// ~1e-3 output errors.  A second table holds the fp16 residual
+// (aV*c - fp16(aV*c)) * 2^kLoShift per code, multiplied by the same query
+// operand in its own accumulator and scaled back by 2^-kLoShift.
+constexpr int kLoShift = 10;
+constexpr float kLoScale = 1.0f / (float)(1 << kLoShift);
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kRows = 8;     // query rows per workgroup (16 MFMA columns, hi/lo)
 // Page schemes of the split kernel: turbo_mse, turbo_prod, and the
@@ -238,6 +245,10 @@ constexpr int kPartStride = 128 + 4;  // floats per partial row: o[128], m, l, p
 
 __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
     return __builtin_bit_cast(uint32_t, (half2v){(_Float16)a, (_Float16)b});
+}
+// (x - fp16(x)) * 2^kLoShift (exact in fp32), rounded to fp16 by pack_h2.
+__device__ __forceinline__ float lo_part(float x) {
+    return (x - (float)(_Float16)x) * (float)(1 << kLoShift);
 }
 // One 16x16x32 fp16 MFMA: c += a * b (fp32 accumulate).
 __device__ __forceinline__ f32x4 mma(half8 a, half8 b, f32x4 c) {
@@ -355,7 +366,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     constexpr int NT = NP >= 2 ? NP / 2 : 1;
     constexpr int kMoRows = NP >= 2 ? 16 : kR;  // rows merged per pass (one tile)
     // Decode tables indexed by a code byte (low nibble = even d), fp16 pairs:
-    // table 0 = K (prod: aK*K3, mse: aV*V4), table 1 = V (aV*V4), 32 copies
+    // table 0 = K (prod: aK*K3, mse: the lo parts of aV*V4), table 1 = V (aV*V4,
+    // also mse's K hi parts), 32 copies
     // each.  Entry e of table t, copy c is word e*64 + 32t + c and lane l
     // reads copy l % 32, so a half-wave's 32 random lookups hit 32 distinct
     // banks.  After the token loop the space holds the per-wave results for
@@ -509,8 +521,10 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
             const int lo = tid & 15, hi = tid >> 4;
             const float vlo = pick(kV4, lo), vhi = pick(kV4, hi);
             const uint32_t vv = pack_h2(kAlphaV * vlo, kAlphaV * vhi);
+            // prod: aK * K3; mse: the lo parts of aV * V4 (its hi parts are the V table)
             const uint32_t kv =
-                PROD ? pack_h2(kAlphaK * pick(kK3, lo & 7), kAlphaK * pick(kK3, hi & 7)) : vv;
+                PROD ? pack_h2(kAlphaK * pick(kK3, lo & 7), kAlphaK * pick(kK3, hi & 7))
+                     : pack_h2(lo_part(kAlphaV * vlo), lo_part(kAlphaV * vhi));
             kstage[tid] = kv;
             vstage[tid] = vv;
         }
@@ -640,8 +654,9 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                 const uint32_t(*vw)[8] = cur.vw;
                 {
                     const float ks = h2f(cur.ks), vs = h2f(cur.vs), re = PROD ? h2f(cur.re) : 0.0f;
-                    const float4 sc = QJL ? make_float4(0.0f, ks * kLog2e, vs, 0.0f)
-                                          : make_float4(ks * ck, ks * re * cr, vs, 0.0f);
+                    const float4 sc = QJL    ? make_float4(0.0f, ks * kLog2e, vs, 0.0f)
+                                      : PROD ? make_float4(ks * ck, ks * re * cr, vs, 0.0f)
+                                             : make_float4(ks * ck, ks * ck * kLoScale, vs, 0.0f);
                     tsc[w][lane & (kChunk - 1)] =
                         cur.valid ? sc : make_float4(0.f, 0.f, 0.f, -INFINITY);
                 }
@@ -673,11 +688,20 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                                 cs[p][tau] = mma(sa, bq[p][s], cs[p][tau]);
                             continue;
                         }
-                        const half8 a = as_h8(lookup(wd[s], 0, 0), lookup(wd[s], 1, 0),
-                                              lookup(wd[s], 2, 0), lookup(wd[s], 3, 0));
+                        // prod: aK*K3 (table 0); mse: aV*V4 hi parts (table 1)
+                        const int kt = PROD ? 0 : 1;
+                        const half8 a = as_h8(lookup(wd[s], 0, kt), lookup(wd[s], 1, kt),
+                                              lookup(wd[s], 2, kt), lookup(wd[s], 3, kt));
         #pragma unroll
                         for (int p = 0; p < NPA; ++p)
                             cb[p][tau] = mma(a, bq[p][s], cb[p][tau]);
+                        if (!PROD) {  // mse: the lo parts (table 0) into cs
+                            const half8 al = as_h8(lookup(wd[s], 0, 0), lookup(wd[s], 1, 0),
+                                                   lookup(wd[s], 2, 0), lookup(wd[s], 3, 0));
+        #pragma unroll
+                            for (int p = 0; p < NPA; ++p)
+                                cs[p][tau] = mma(al, bq[p][s], cs[p][tau]);
+                        }
                         if (PROD) {
                             // Residual signs (nibble bit 3: 1 -> +1) as fp16 pairs in
                             // registers: high bytes 0x3C / 0xBC, low bytes 0.
@@ -711,8 +735,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                                 lg[p][tau][e] = fmaf(sr, sc.y, sc.w);
                             } else {
                                 const float sb = cb[p][tau][e] + quad_xor<1>(cb[p][tau][e]);
-                                const float sr =
-                                    PROD ? cs[p][tau][e] + quad_xor<1>(cs[p][tau][e]) : 0.0f;
+                                const float sr = cs[p][tau][e] + quad_xor<1>(cs[p][tau][e]);
                                 lg[p][tau][e] = fmaf(sb, sc.x, fmaf(sr, sc.y, sc.w));
                             }
                             if (masked)  // causal limit of this column's row
@@ -814,7 +837,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                 {
                     const float ks = h2f(cur.ks), vs = h2f(cur.vs), re = PROD ? h2f(cur.re) : 0.0f;
                     tsc[w][lane & (kChunk - 1)] =
-                        cur.valid ? make_float4(ks * ck, ks * re * cr, 0.5f * vs, 0.0f)
+                        cur.valid ? make_float4(ks * ck, PROD ? ks * re * cr : ks * ck * kLoScale,
+                                                0.5f * vs, 0.0f)
                                   : make_float4(0.f, 0.f, 0.f, -INFINITY);
                 }
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -846,12 +870,22 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                                             : s == 1 ? kw[tau].y
                                             : s == 2 ? kw[tau].z
                                                      : kw[tau].w;
-                        const half8 a = as_h8(lookup(wd, 0, 0), lookup(wd, 1, 0), lookup(wd, 2, 0),
-                                              lookup(wd, 3, 0));
+                        const int kt = PROD ? 0 : 1;  // mse: the hi parts are the V table
+                        const half8 a = as_h8(lookup(wd, 0, kt), lookup(wd, 1, kt),
+                                              lookup(wd, 2, kt), lookup(wd, 3, kt));
 #pragma unroll
                         for (int t = 0; t < NTA; ++t) {
                             cb[t][tau] = mma(a, bk[2 * t], cb[t][tau]);
                             if (!COLS) cb[t][tau] = mma(a, bk[2 * t + 1], cb[t][tau]);
+                        }
+                        if (!PROD) {  // mse: the lo parts (table 0) into cs
+                            const half8 al = as_h8(lookup(wd, 0, 0), lookup(wd, 1, 0),
+                                                   lookup(wd, 2, 0), lookup(wd, 3, 0));
+#pragma unroll
+                            for (int t = 0; t < NTA; ++t) {
+                                cs[t][tau] = mma(al, bk[2 * t], cs[t][tau]);
+                                if (!COLS) cs[t][tau] = mma(al, bk[2 * t + 1], cs[t][tau]);
+                            }
                         }
                         if (PROD) {
                             const uint32_t he = ((wd << 4) & 0x80808080u) ^ 0xBCBCBCBCu;  // even d

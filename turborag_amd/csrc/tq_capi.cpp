@@ -236,18 +236,110 @@ int num_cus() {
     return n;
 }
 
+// Split-K workspace for attention: one buffer per (device, stream).  Calls
+// on one stream run in order, so they can share it.  A call that needs more
+// replaces the buffer; the old one may still be read by kernels already
+// enqueued on the stream, so it is retired with an event recorded behind them
+// and freed once that event has completed (checked on later calls).  A
+// buffer handed out while its stream was being captured into a graph is
+// referenced by that graph, so it is never freed automatically, only by
+// tq_workspace_release().  More than kMaxStreams cached streams: the devices
+// are synchronized and the buffers no graph references are freed.
+namespace {
+struct WsBuf {
+    void* p = nullptr;
+    size_t n = 0;
+    bool captured = false;  // handed out during a stream capture
+};
+struct Retired {
+    void* p;
+    hipEvent_t ev;  // null: outgrown during capture, freed only on release
+    int dev;
+};
+std::mutex g_ws_mu;
+std::map<std::pair<int, hipStream_t>, WsBuf> g_ws;
+std::vector<Retired> g_retired;
+constexpr size_t kMaxStreams = 64;
+
+bool capturing(hipStream_t s) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &st) != hipSuccess) {
+        (void)hipGetLastError();
+        return true;  // unknown: treat as capturing (never record, never free)
+    }
+    return st != hipStreamCaptureStatusNone;
+}
+
+// Frees the retired buffers whose kernels have finished.  Lock held.
+void reap_retired() {
+    for (size_t k = 0; k < g_retired.size();) {
+        Retired& r = g_retired[k];
+        if (r.ev && hipEventQuery(r.ev) == hipSuccess) {
+            (void)hipFree(r.p);
+            (void)hipEventDestroy(r.ev);
+            g_retired[k] = g_retired.back();
+            g_retired.pop_back();
+        } else {
+            (void)hipGetLastError();  // hipErrorNotReady is not an error of the caller's
+            ++k;
+        }
+    }
+}
+
+// Synchronizes every device holding a cached buffer and frees them all
+// (with keep_captured, those a captured graph references stay).  Lock held.
+void release_all(bool keep_captured = false) {
+    std::vector<int> devs;
+    for (const auto& kv : g_ws) devs.push_back(kv.first.first);
+    for (const auto& r : g_retired) devs.push_back(r.dev);
+    std::sort(devs.begin(), devs.end());
+    devs.erase(std::unique(devs.begin(), devs.end()), devs.end());
+    int cur = 0;
+    (void)hipGetDevice(&cur);
+    for (int d : devs) {
+        if (hipSetDevice(d) == hipSuccess) (void)hipDeviceSynchronize();
+    }
+    for (auto it = g_ws.begin(); it != g_ws.end();) {
+        if (keep_captured && it->second.captured) {
+            ++it;
+            continue;
+        }
+        (void)hipSetDevice(it->first.first);
+        (void)hipFree(it->second.p);
+        it = g_ws.erase(it);
+    }
+    for (size_t k = 0; k < g_retired.size();) {
+        Retired& r = g_retired[k];
+        if (keep_captured && !r.ev) {  // retired during or after a capture: kept
+            ++k;
+            continue;
+        }
+        (void)hipSetDevice(r.dev);
+        (void)hipFree(r.p);
+        if (r.ev) (void)hipEventDestroy(r.ev);
+        g_retired[k] = g_retired.back();
+        g_retired.pop_back();
+    }
+    (void)hipSetDevice(cur);
+    (void)hipGetLastError();
+}
+}  // namespace
+
 void* workspace(hipStream_t stream, size_t bytes) {
-    // One buffer per (device, stream): calls on one stream are ordered, so
-    // reuse is safe; outgrown buffers are kept (a kernel may still use them).
-    static std::mutex mu;
-    struct Buf { void* p; size_t n; };
-    static std::map<std::pair<int, hipStream_t>, Buf> bufs;
-    static std::vector<void*> retired;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) throw Error("hipGetDevice failed");
-    std::lock_guard<std::mutex> lock(mu);
-    Buf& b = bufs[{dev, stream}];
-    if (b.n >= bytes && b.p) return b.p;
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    const bool cap = capturing(stream);
+    auto it = g_ws.find({dev, stream});
+    if (it != g_ws.end() && it->second.n >= bytes && it->second.p) {
+        it->second.captured = it->second.captured || cap;
+        return it->second.p;
+    }
+    if (!cap) {
+        reap_retired();
+        if (it == g_ws.end() && g_ws.size() >= kMaxStreams) release_all(/*keep_captured=*/true);
+    }
+    WsBuf& b = g_ws[{dev, stream}];
     size_t n = std::max<size_t>(bytes, 1 << 20);
     n = std::max(n, b.n * 2);
     void* p = nullptr;
@@ -255,10 +347,27 @@ void* workspace(hipStream_t stream, size_t bytes) {
         (void)hipGetLastError();
         throw Error("workspace hipMalloc failed");
     }
-    if (b.p) retired.push_back(b.p);
+    if (b.p) {
+        Retired r{b.p, nullptr, dev};
+        if (!cap && !b.captured) {
+            if (hipEventCreateWithFlags(&r.ev, hipEventDisableTiming) != hipSuccess ||
+                hipEventRecord(r.ev, stream) != hipSuccess) {
+                (void)hipGetLastError();
+                if (r.ev) (void)hipEventDestroy(r.ev);
+                r.ev = nullptr;
+            }
+        }
+        g_retired.push_back(r);
+    }
     b.p = p;
     b.n = n;
+    b.captured = cap;
     return p;
+}
+
+void release_workspaces() {
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    release_all();
 }
 
 }  // namespace tq
@@ -268,6 +377,10 @@ void* workspace(hipStream_t stream, size_t bytes) {
 // ---------------------------------------------------------------------------
 
 extern "C" const char* tq_last_error(void) { return g_last_error; }
+
+extern "C" int tq_workspace_release(void) {
+    return guarded([] { tq::release_workspaces(); });
+}
 
 extern "C" int tq_make_default_config(TQConfig* out) {
     if (!out) return -1;

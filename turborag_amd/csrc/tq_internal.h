@@ -63,8 +63,11 @@ float inv_sqrt_d(int D);
 // (the reference's TQ_CHECK_LAUNCH, include/tq_cuda_check.h:18-24).
 void check_launch(const char* what);
 
-// Per-(device, stream) scratch for split-K partials; grows, never shrinks.
+// Per-(device, stream) scratch for split-K partials.  Grows; an outgrown
+// buffer is freed once the stream's earlier kernels have finished.
 void* workspace(hipStream_t stream, size_t bytes);
+// Synchronizes the devices and frees every cached workspace (tq_workspace_release).
+void release_workspaces();
 
 // ---- launchers (tq_prod.hip, tq_mse.hip, tq_attention.hip) ---------------
 void launch_pack(Scheme s, const uint16_t* key, const uint16_t* value, const int32_t* slots,

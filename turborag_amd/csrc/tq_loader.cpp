@@ -9,6 +9,8 @@
 // compute stream waits for each layer's copy through an event.  With pinned
 // host pages (hipHostMalloc / torch pin_memory) the copies run at link rate
 // and overlap the dequant.
+#include <map>
+#include <memory>
 #include <mutex>
 #include <vector>
 
@@ -16,23 +18,23 @@
 
 namespace {
 
-// Per-device pool of reusable events (a stream wait captures the event's
-// state when it is enqueued, so an event may be re-recorded afterwards).
-std::vector<hipEvent_t>& device_events(int dev, size_t need) {
+// Per-device events of the loader.  A call holds its device's lock for its
+// whole enqueue loop, so two concurrent calls never record and wait on the
+// same event in between each other's record and wait (a stream wait takes
+// the event's state when it is enqueued, so the events can be re-recorded by
+// the next call).  The per-device records never move once created.
+struct DeviceEvents {
+    std::mutex mu;
+    std::vector<hipEvent_t> ev;
+};
+
+DeviceEvents& device_events(int dev) {
     static std::mutex mu;
-    static std::vector<std::vector<hipEvent_t>> pools;
+    static std::map<int, std::unique_ptr<DeviceEvents>> all;
     std::lock_guard<std::mutex> lock(mu);
-    if ((size_t)dev >= pools.size()) pools.resize(dev + 1);
-    auto& v = pools[dev];
-    while (v.size() < need) {
-        hipEvent_t e = nullptr;
-        if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
-            (void)hipGetLastError();
-            throw tq::Error("hipEventCreateWithFlags failed");
-        }
-        v.push_back(e);
-    }
-    return v;
+    auto& p = all[dev];
+    if (!p) p.reset(new DeviceEvents());
+    return *p;
 }
 
 void check(hipError_t e, const char* what) {
@@ -56,7 +58,14 @@ void load_layers(Scheme s, const uint8_t* const* host_pools, uint8_t* const* dev
             throw Error("load_layers: null pool or output pointer for a layer");
     int dev = 0;
     check(hipGetDevice(&dev), "hipGetDevice");
-    std::vector<hipEvent_t>& ev = device_events(dev, (size_t)num_layers + 1);
+    DeviceEvents& de = device_events(dev);
+    std::lock_guard<std::mutex> lock(de.mu);  // held until every layer is enqueued
+    std::vector<hipEvent_t>& ev = de.ev;
+    while (ev.size() < (size_t)num_layers + 1) {
+        hipEvent_t e = nullptr;
+        check(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreateWithFlags");
+        ev.push_back(e);
+    }
     const bool two = copy_stream != compute_stream;
     if (two) {
         // Copies must not overwrite pools that earlier compute work still reads.

@@ -226,20 +226,23 @@ void write_file_atomic(const std::string& path, const std::vector<std::pair<cons
 void put16(std::string& s, uint16_t v) { s.append(reinterpret_cast<const char*>(&v), 2); }
 void put32(std::string& s, uint32_t v) { s.append(reinterpret_cast<const char*>(&v), 4); }
 void put64(std::string& s, uint64_t v) { s.append(reinterpret_cast<const char*>(&v), 8); }
-uint16_t get16(const std::string& s, size_t o) {
-    if (o + 2 > s.size()) throw Error("zip: truncated");
+// True when [o, o + n) lies inside a buffer of `size` bytes.  Written without
+// o + n, which wraps for offsets read from a file.
+bool in_bounds(uint64_t o, uint64_t n, uint64_t size) { return o <= size && n <= size - o; }
+uint16_t get16(const std::string& s, uint64_t o) {
+    if (!in_bounds(o, 2, s.size())) throw Error("zip: truncated");
     uint16_t v;
     std::memcpy(&v, s.data() + o, 2);
     return v;
 }
-uint32_t get32(const std::string& s, size_t o) {
-    if (o + 4 > s.size()) throw Error("zip: truncated");
+uint32_t get32(const std::string& s, uint64_t o) {
+    if (!in_bounds(o, 4, s.size())) throw Error("zip: truncated");
     uint32_t v;
     std::memcpy(&v, s.data() + o, 4);
     return v;
 }
-uint64_t get64(const std::string& s, size_t o) {
-    if (o + 8 > s.size()) throw Error("zip: truncated");
+uint64_t get64(const std::string& s, uint64_t o) {
+    if (!in_bounds(o, 8, s.size())) throw Error("zip: truncated");
     uint64_t v;
     std::memcpy(&v, s.data() + o, 8);
     return v;
@@ -272,33 +275,51 @@ std::vector<ZipRecord> zip_records(const std::string& z) {
         count = get64(z, e64 + 32);
         cd_off = get64(z, e64 + 48);
     }
+    // Every offset and size below comes from the file: each is checked against
+    // the file's size before use (get16/32/64, in_bounds), never by a sum
+    // that could wrap.
+    if (cd_off > z.size()) throw Error("zip: central directory offset beyond the file");
     std::vector<ZipRecord> out;
-    size_t p = cd_off;
+    uint64_t p = cd_off;
     for (uint64_t k = 0; k < count; ++k) {
         if (get32(z, p) != 0x02014b50u) throw Error("zip: bad central directory entry");
         const uint16_t method = get16(z, p + 10);
         uint64_t csize = get32(z, p + 20), usize = get32(z, p + 24);
         const uint16_t nl = get16(z, p + 28), xl = get16(z, p + 30), cl = get16(z, p + 32);
         uint64_t lho = get32(z, p + 42);
-        if (p + 46 + nl > z.size()) throw Error("zip: truncated name");
+        // p + 46 <= size (get32 at p + 42 passed), so these sums cannot wrap
+        if (!in_bounds(p + 46, (uint64_t)nl + xl + cl, z.size()))
+            throw Error("zip: truncated central directory entry");
         std::string name = z.substr(p + 46, nl);
         // zip64 extended information (id 1): the 0xFFFFFFFF fields, in order
-        for (size_t x = p + 46 + nl; x + 4 <= p + 46 + nl + xl;) {
+        const uint64_t xend = p + 46 + nl + xl;
+        for (uint64_t x = p + 46 + nl; x + 4 <= xend;) {
             const uint16_t id = get16(z, x), len = get16(z, x + 2);
+            if (x + 4 + len > xend) throw Error("zip: extra field overruns its entry");
             if (id == 1) {
-                size_t q = x + 4;
-                if (usize == 0xFFFFFFFFu) { usize = get64(z, q); q += 8; }
-                if (csize == 0xFFFFFFFFu) { csize = get64(z, q); q += 8; }
-                if (lho == 0xFFFFFFFFu) { lho = get64(z, q); q += 8; }
+                uint64_t q = x + 4;
+                const uint64_t qend = x + 4 + len;
+                auto next64 = [&]() {
+                    if (q + 8 > qend) throw Error("zip: short zip64 extra field");
+                    const uint64_t v = get64(z, q);
+                    q += 8;
+                    return v;
+                };
+                if (usize == 0xFFFFFFFFu) usize = next64();
+                if (csize == 0xFFFFFFFFu) csize = next64();
+                if (lho == 0xFFFFFFFFu) lho = next64();
             }
             x += 4 + len;
         }
         if (method != 0 || csize != usize) throw Error("zip: record '" + name + "' is compressed");
+        if (lho > z.size() || usize > z.size())
+            throw Error("zip: record '" + name + "' offset or size beyond the file");
         if (get32(z, lho) != 0x04034b50u) throw Error("zip: bad local header");
-        const size_t data = lho + 30 + get16(z, lho + 26) + get16(z, lho + 28);
-        if (data + usize > z.size()) throw Error("zip: record '" + name + "' truncated");
-        out.push_back({name, data, (size_t)usize});
-        p += 46 + nl + xl + cl;
+        // lho + 30 <= size (get16 at lho + 28 passed); the two lengths are < 2^16
+        const uint64_t data = lho + 30 + (uint64_t)get16(z, lho + 26) + get16(z, lho + 28);
+        if (!in_bounds(data, usize, z.size())) throw Error("zip: record '" + name + "' truncated");
+        out.push_back({name, (size_t)data, (size_t)usize});
+        p += 46 + (uint64_t)nl + xl + cl;
     }
     return out;
 }
@@ -410,13 +431,16 @@ VP unpickle(const std::string& b) {
     std::vector<size_t> marks;
     std::map<int64_t, VP> memo;
     size_t p = 0;
-    auto need = [&](size_t n) {
-        if (p + n > b.size()) throw Error("pickle: truncated");
+    // p <= b.size() always holds, so b.size() - p cannot wrap; n comes from
+    // the file (up to 2^64 - 1 for BINUNICODE8) and is never added to p
+    // before this check.
+    auto need = [&](uint64_t n) {
+        if (n > b.size() - p) throw Error("pickle: truncated");
     };
     auto u8 = [&]() { need(1); return (uint8_t)b[p++]; };
     auto u16 = [&]() { need(2); uint16_t v; std::memcpy(&v, b.data() + p, 2); p += 2; return v; };
     auto u32 = [&]() { need(4); uint32_t v; std::memcpy(&v, b.data() + p, 4); p += 4; return v; };
-    auto bytes = [&](size_t n) { need(n); std::string s = b.substr(p, n); p += n; return s; };
+    auto bytes = [&](uint64_t n) { need(n); std::string s = b.substr(p, n); p += n; return s; };
     auto line = [&]() {
         const size_t e = b.find('\n', p);
         if (e == std::string::npos) throw Error("pickle: truncated");
@@ -716,18 +740,25 @@ VP dict_get(const VP& d, const std::string& k) {
 const char* tensor_data(const TorchFile& t, const VP& v, const char* want_type, int64_t* numel) {
     if (!v || v->kind != Value::Tensor) throw Error("expected a tensor");
     if (v->s != want_type) throw Error(std::string("expected a ") + want_type + " tensor, got " + v->s);
-    int64_t n = 1, expect = 1;
-    for (int k = (int)v->shape.size() - 1; k >= 0; --k) {
-        if (v->shape[k] != 1 && v->stride[k] != expect) throw Error("tensor is not contiguous");
-        expect *= v->shape[k];
-        n *= v->shape[k];
-    }
+    if (v->shape.size() != v->stride.size()) throw Error("tensor shape and stride ranks differ");
     auto it = t.data.find(v->key);
     if (it == t.data.end()) throw Error("tensor storage record missing");
     const int eb = storage_elem_bytes(v->s);
-    if (v->offset < 0 || (uint64_t)(v->offset + n) * eb > it->second.size)
+    // Elements the storage record holds; shape, stride and offset come from
+    // the file and are checked against it without overflowing.
+    const uint64_t cap = it->second.size / (uint64_t)eb;
+    uint64_t n = 1, expect = 1;
+    for (int k = (int)v->shape.size() - 1; k >= 0; --k) {
+        if (v->shape[k] < 0) throw Error("tensor has a negative dimension");
+        const uint64_t d = (uint64_t)v->shape[k];
+        if (d != 1 && (uint64_t)v->stride[k] != expect) throw Error("tensor is not contiguous");
+        if (d != 0 && n > cap / d) throw Error("tensor exceeds its storage");
+        n *= d;
+        expect = n;
+    }
+    if (v->offset < 0 || (uint64_t)v->offset > cap || n > cap - (uint64_t)v->offset)
         throw Error("tensor exceeds its storage");
-    *numel = n;
+    *numel = (int64_t)n;
     return t.blob.data() + it->second.offset + (size_t)v->offset * eb;
 }
 
@@ -898,7 +929,7 @@ bool pool_info(const std::string& path, size_t* file_bytes, TQStoreFormat* fmt, 
                      std::fread(&f, 1, sizeof(f), fp) == sizeof(f);
     std::fclose(fp);
     if (!got || std::memcmp(f.magic, kMagic, 8) != 0 || f.footer_bytes != sizeof(Footer) ||
-        f.pool_bytes + sizeof(Footer) != *file_bytes)
+        f.pool_bytes != *file_bytes - sizeof(Footer))
         return false;
     if (fmt) {
         fmt->version = (int32_t)f.version;
@@ -1041,11 +1072,18 @@ struct JsonParser {
         ++p;
         return o;
     }
+    int depth = 0;  // nesting of the value being parsed (bounded: no deep recursion)
     Json value() {
         ws();
         if (p >= t.size()) fail();
         Json j;
         const char c = t[p];
+        if ((c == '{' || c == '[') && depth >= 64) fail();
+        struct Nest {
+            int& d;
+            explicit Nest(int& x) : d(x) { ++d; }
+            ~Nest() { --d; }
+        } nest(depth);
         if (c == '{') {
             j.kind = Json::Obj;
             ++p;

@@ -115,6 +115,7 @@ _P = POINTER
 _I64 = ctypes.c_int64
 SIGNATURES: dict[str, tuple[list, object]] = {
     "tq_last_error": ([], ctypes.c_char_p),
+    "tq_workspace_release": ([], c_int),
     "tq_make_default_config": ([_P(TQConfig)], c_int),
     "tq_make_turbo_prod_layout": ([_P(TQConfig), _P(TQTurboProdPageLayout)], c_int),
     "tq_make_turbo_mse_layout": ([_P(TQConfig), _P(TQTurbomsePageLayout)], c_int),
@@ -616,6 +617,14 @@ class TurboQuantWrapper:
             self._stream(stream))
         if rc != 0:
             self._kernel_raise(rc, "sdpa", "attention_ref")
+
+    def release_workspaces(self) -> None:
+        """Synchronize and free the attention entries' cached split-K
+        workspaces (tq_workspace_release): for callers that cycle through
+        many streams.  Graphs captured before must not be replayed after."""
+        rc = self.lib.tq_workspace_release()
+        if rc != 0:
+            raise RuntimeError(f"tq_workspace_release failed: {self._last_cuda_error()}")
 
     # ── allocation helpers (reference :385-415) ─────────────────────── #
 
