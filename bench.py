@@ -40,6 +40,24 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+# The dominant kernel (the roofline's) and the decode-attention kernels, as
+# rocprofv3 names them (template argument 1 = turbo_prod).
+DEQUANT_KERNEL = "tq::dequant_stream_kernel<128, 1>"
+ATTN_KERNELS = ("tq::attn_mfma_split_kernel<1, 32, 8, false, 1>", "tq::attn_mfma_combine_kernel")
+
+
+def kernel_traffic(name: str):
+    """HBM bytes per dispatch of `name` from profiles/traffic.json (calibrated
+    FETCH_SIZE + WRITE_SIZE), or None when the summary does not hold it."""
+    tf = ROOT / "profiles" / "traffic.json"
+    try:
+        k = json.loads(tf.read_text())["kernels"][name]
+        return {"bytes": int(k["bytes"]), "fetch_B": int(k["fetch_B"]),
+                "write_B": int(k["write_B"]), "source": "profiles/traffic.json"}
+    except (OSError, ValueError, KeyError, TypeError):
+        return None
+
+
 def gpu_kv(N, H, D, seed, dev):
     """Seeded N(0,1) K/V with the synthetic outlier channels, made on the GPU."""
     import torch
@@ -279,18 +297,10 @@ def main() -> int:
     copy_us = event_time_us(copies, reps) / len(srcs)
     del srcs, dsts
 
-    traffic = None
-    tf = ROOT / "profiles" / "traffic.json"
-    if tf.exists():
-        # HBM bytes per dequant dispatch of this workload, from the two
-        # calibrated counter runs (FETCH_SIZE, WRITE_SIZE) stored beside the
-        # profiles.
-        try:
-            for name, k in json.loads(tf.read_text()).get("kernels", {}).items():
-                if "dequant" in name and "true" in name:
-                    traffic = k["bytes"]
-        except (ValueError, OSError, KeyError):
-            traffic = None
+    # HBM bytes per dispatch of the roofline kernel on this workload, from the
+    # two calibrated counter runs (FETCH_SIZE, WRITE_SIZE) summarised in
+    # profiles/traffic.json.
+    traffic = kernel_traffic(DEQUANT_KERNEL)
 
     loader = measure_loader(w)
     log(f"[bench] loader: {w.NL} layers host->device + dequant to [1,H,N,D] in "
@@ -304,7 +314,9 @@ def main() -> int:
 
     pack = measure_pack(w)
     log(f"[bench] pack (36 layers x 8192 tokens): turbo_prod {pack['turbo_prod_us_per_layer']:.1f} "
-        f"us/layer, turbo_mse {pack['turbo_mse_us_per_layer']:.1f} us/layer")
+        f"us/layer, turbo_mse {pack['turbo_mse_us_per_layer']:.1f} us/layer; mismatched bytes "
+        f"vs oracle {pack['parity']['mismatched_page_bytes']}, boundary counts "
+        f"{pack['parity']['turbo_prod_boundary']}")
 
     logits = measure_logits(w)
     log(f"[bench] turbo_prod logits @32K: {logits['us']:.1f} us ({logits['GBps']:.0f} GB/s)")
@@ -315,8 +327,18 @@ def main() -> int:
         f"{legacy['int4_dequant_us']:.1f} us")
 
     batched = measure_batched(w)
-    log(f"[bench] batched decode: {batched['sequences']} sequences, {batched['rows']} rows: "
-        f"append {batched['append_us']:.1f} us + attention {batched['attention_us']:.1f} us")
+    for sch in ("turbo_prod", "turbo_mse"):
+        b_ = batched[sch]
+        log(f"[bench] batched decode {sch}: {b_['sequences']} sequences, {b_['rows']} rows: "
+            f"append {b_['append_us']:.1f} us + attention {b_['attention_us']:.1f} us")
+
+    single = measure_single_query(w)
+    log(f"[bench] single-query decode @32K: {single['us_per_layer']:.2f} us/layer")
+
+    config1 = measure_config1(w)
+    log(f"[bench] config 1 (turbo_mse [2,1143,128], CPU oracle): rel MSE K "
+        f"{config1['rel_mse_k']}, V {config1['rel_mse_v']}; GPU identical: "
+        f"{config1['gpu_pool_identical'] and config1['gpu_dequant_identical']}")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -334,7 +356,8 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32",
+        "dtype": "u8 codes -> fp32 math -> fp16 (dequant); attention: fp16 MFMA on hi/lo-split "
+                 "fp16 operands (~22-bit query and P), fp32 accumulate and softmax",
         "data": "synthetic",
         "config": {
             "workload": "per layer: turbo_prod dequant [32768,2,128] + GQA 16/2 decode "
@@ -351,7 +374,8 @@ def main() -> int:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(deq_gbps / HBM_PEAK_GBPS, 4),
-            "traffic": traffic,
+            "traffic": traffic["bytes"] if traffic else None,
+            "traffic_detail": traffic,
             "algorithmic_bytes": w.deq_bytes,
             "avg_launch_us": round(deq_us, 3),
             "copy_same_bytes_us": round(copy_us, 3),
@@ -368,6 +392,8 @@ def main() -> int:
         "logits": logits,
         "unexported_kernels": legacy,
         "batched_decode": batched,
+        "single_query_decode": single,
+        "config1": config1,
         "step_ms_events": round(ev_ms_per_step, 4),
         "step_ms_one_stream": round(serial_ms, 4),
         "cpu_baseline": cpu,
@@ -522,8 +548,51 @@ def measure_pack(w: Workload, reps: int = 5) -> dict:
         out[f"{name}_GBps"] = round(alg / us / 1e3, 1)
         out[f"{name}_frac_hbm"] = round(alg / us / 1e3 / HBM_PEAK_GBPS, 4)
     out["algorithmic_bytes_per_layer_turbo_prod"] = fp16 + N * 4 + pages * lp.page_size_bytes
+    torch.cuda.synchronize()
+    out["parity"] = pack_parity(w, kv, slots, pp, pm, pages)
     del kv, pp, pm
     return out
+
+
+def pack_parity(w: Workload, kv, slots, pp, pm, pages) -> dict:
+    """Config 2's parity report: every layer's GPU-packed pages against the
+    oracle's pack of the same K/V (mismatching bytes, expected 0), and the
+    decision-boundary counts the north star asks to report: rotated values
+    within one float ulp of a codebook decision boundary, where the exact
+    bits of the reference build's rsqrtf(128) (tq_turbo_prod_kernels.cu:188)
+    or its FMA contraction of the pair sum (tq_turbo_mse_kernels.cu:108)
+    could flip a code.  Both schemes, all layers, the oracle on this host."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    import numpy as np
+
+    from oracle.oracle import load
+    from turborag_amd.synthetic import as_u16
+    orc = load()
+    orc.nthreads = host_cpu()["usable"]
+    slots_np = slots.cpu().numpy()
+    host = [(as_u16(k), as_u16(v)) for k, v in kv]
+    mism = {"turbo_prod": 0, "turbo_mse": 0}
+    for (k, v), p, q in zip(host, pp, pm):
+        mism["turbo_prod"] += int(np.count_nonzero(
+            p.cpu().numpy() != orc.prod_pack(k, v, slots_np, pages, w.B)))
+        mism["turbo_mse"] += int(np.count_nonzero(
+            q.cpu().numpy() != orc.mse_pack(k, v, slots_np, pages, w.B)))
+    with ThreadPoolExecutor(orc.nthreads) as ex:
+        pc = list(ex.map(lambda kv_: orc.boundary_counts("turbo_prod", *kv_), host))
+        mc = list(ex.map(lambda kv_: orc.boundary_counts("turbo_mse", *kv_), host))
+    values = len(host) * host[0][0].size
+    return {
+        "layers_checked": len(host),
+        "mismatched_page_bytes": mism,
+        "values_per_tensor": values,
+        "turbo_prod_boundary": {"k_code": sum(c[0] for c in pc),
+                                "k_residual_sign": sum(c[1] for c in pc),
+                                "v_code": sum(c[2] for c in pc)},
+        "turbo_mse_boundary": {"rows_norm_differs_unfused_pairsum": sum(c[0] for c in mc),
+                               "code_bytes_differ_unfused_pairsum": sum(c[1] for c in mc),
+                               "codes_within_1ulp": sum(c[2] for c in mc)},
+    }
 
 
 def measure_logits(w: Workload, reps: int = 10) -> dict:
@@ -581,8 +650,90 @@ def measure_legacy(w: Workload, reps: int = 10) -> dict:
     return t
 
 
-def batched_setup(w: Workload) -> dict:
-    """The batch of the batched-decode step: 32 turbo_prod sequences, lengths
+def measure_config1(w: Workload) -> dict:
+    """Config 1: K, V [2 kv heads, 1143 tokens, 128] (seed 101, HF [H, S, D]
+    permuted to the ABI's [S, H, D]), turbo_mse pack then dequant on the CPU
+    reference path (the oracle), the same on the GPU for parity.  Reported as
+    the config asks: packed bytes, per-(token, head) fp16 scales and the
+    reconstruction MSE (relative to the input variance, as the reference's
+    tests/test_cag.py:240-247 measures it; its bound is 0.25)."""
+    import hashlib
+
+    import numpy as np
+    import torch
+
+    from oracle.oracle import load
+    from turborag_amd.synthetic import as_u16, kv_tokens_major
+    orc = load()
+    N, H, D, B = 1143, 2, 128, 16
+    k, v = kv_tokens_major(N, H, D, seed=101)
+    slots = np.arange(N, dtype=np.int32)
+    pages = (N + B - 1) // B
+    t0 = time.perf_counter()
+    pool = orc.mse_pack(as_u16(k), as_u16(v), slots, pages, B)
+    ok, ov = orc.mse_dequant(pool, slots, H, D, B)
+    cpu_ms = (time.perf_counter() - t0) * 1e3
+    tq, cfg = w.tq, w.tq.default_config()
+    cfg.num_kv_heads, cfg.head_dim, cfg.block_size = H, D, B
+    lm = tq.make_mse_layout_for(cfg)
+    gpool = torch.zeros(pages * lm.page_size_bytes, dtype=torch.uint8, device=w.dev)
+    gs = torch.from_numpy(slots).to(w.dev)
+    tq.mse_pack(k.to(w.dev), v.to(w.dev), gs, gpool, lm, cfg)
+    gk = torch.empty(N, H, D, dtype=torch.float16, device=w.dev)
+    gv = torch.empty_like(gk)
+    tq.mse_dequant(gpool, gs, gk, gv, lm, cfg)
+    torch.cuda.synchronize()
+    same_pool = bool(np.array_equal(gpool.cpu().numpy(), pool))
+    same_kv = bool(np.array_equal(as_u16(gk), ok) and np.array_equal(as_u16(gv), ov))
+
+    def rel_mse(x, y_u16):
+        y = torch.from_numpy(y_u16.view(np.float16)).float()
+        return float(torch.mean((x.float() - y) ** 2) / torch.var(x.float()))
+
+    codes = 2 * N * H * (D // 2)
+    scales = 2 * N * H
+    kn = pool.reshape(pages, -1)[:, lm.k_norms_offset:lm.k_norms_offset + B * H * 2]
+    return {
+        "shape": "K, V [2, 1143, 128] fp16, seed 101; turbo_mse, 16-token pages",
+        "pool_bytes": int(pool.size), "code_bytes": codes, "scale_count": scales,
+        "scale_bytes": 2 * scales,
+        "pool_sha256": hashlib.sha256(pool.tobytes()).hexdigest(),
+        "k_scales_first": [int(x) for x in kn[0].view(np.uint16)[:4]],
+        "rel_mse_k": round(rel_mse(k, ok), 5), "rel_mse_v": round(rel_mse(v, ov), 5),
+        "rel_mse_bound": 0.25,
+        "cpu_ms": round(cpu_ms, 2),
+        "gpu_pool_identical": same_pool, "gpu_dequant_identical": same_kv,
+    }
+
+
+def measure_single_query(w: Workload, reps: int = 5) -> dict:
+    """Decode attention with one query row per kv head (num_queries = 1, the
+    call the reference's store makes: cag_store.py:284-287) over every layer
+    of the step at 32K, replayed from a graph, beside the GQA 16/2 figure."""
+    import torch
+    qa1 = w.qa[:1].contiguous()
+    outs = [torch.empty(1, w.H, w.D, dtype=torch.float16, device=w.dev) for _ in range(w.NL)]
+    st = w._stream
+
+    def run():
+        for layer in range(w.NL):
+            w.tq.fused_attn_output(qa1, w.pools[layer], w.slots, outs[layer], w.lp, w.cfg, 1,
+                                   w.N, stream=st())
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run()
+    torch.cuda.synchronize()
+    g = capture(run, side)
+    us = event_time_us(g.replay if g is not None else run, reps) / w.NL
+    alg = w.pool_bytes + w.N * 4 + 2 * w.H * w.D * 2
+    return {"us_per_layer": round(us, 3), "algorithmic_bytes": alg,
+            "GBps": round(alg / us / 1e3, 1), "frac_hbm": round(alg / us / 1e3 / HBM_PEAK_GBPS, 4),
+            "path": "matrix-core split kernel (one row per kv head in an 8-row group)"}
+
+
+def batched_setup(w: Workload, scheme: str = "turbo_prod") -> dict:
+    """The batch of the batched-decode step: 32 sequences, lengths
     U[1024, 32768] (seed 500), 1-8 new tokens each (seed 501), appended."""
     import numpy as np
     import torch
@@ -590,7 +741,7 @@ def batched_setup(w: Workload) -> dict:
     from turborag_amd.batched import PagedBatch
     lens = np.random.default_rng(500).integers(1024, 32769, size=32)
     widths = np.random.default_rng(501).integers(1, 9, size=32)
-    b = PagedBatch(w.tq, "turbo_prod", lens, widths, seed=500, device=w.dev)
+    b = PagedBatch(w.tq, scheme, lens, widths, seed=500, device=w.dev)
     b.append_new_tokens(seed=503)
     query, row_seq, row_len = b.decode_rows(seed=504)
     return {"batch": b, "query": query, "row_seq": row_seq, "row_len": row_len,
@@ -599,13 +750,20 @@ def batched_setup(w: Workload) -> dict:
 
 
 def measure_batched(w: Workload, reps: int = 10) -> dict:
+    """Config 5 for both schemes: see measure_batched_scheme."""
+    out = {s: measure_batched_scheme(w, s, reps) for s in ("turbo_prod", "turbo_mse")}
+    out.update(out["turbo_prod"])  # the turbo_prod figures also at the top level
+    return out
+
+
+def measure_batched_scheme(w: Workload, scheme: str, reps: int = 10) -> dict:
     """One serving step of a batch of paged sequences (32 sequences, lengths
     U[1024, 32768], 1-8 new tokens each, pages scattered by the allocator):
     one pack launch appending every new token, then one paged-attention
     launch for 8 GQA rows per new token (causal over the new tokens)."""
     import torch
 
-    st = batched_setup(w)
+    st = batched_setup(w, scheme)
     b, query, row_seq, row_len = st["batch"], st["query"], st["row_seq"], st["row_len"]
     bt, out, lens, widths = st["tables"], st["out"], st["lens"], st["widths"]
     torch.cuda.synchronize()
@@ -614,55 +772,116 @@ def measure_batched(w: Workload, reps: int = 10) -> dict:
     rows = int(query.shape[0])
     # Algorithmic bytes: each sequence's cells once per kv head (+4 B slot
     # per token), the new tokens' fp16 K/V in and cells out, query and output.
-    cell = 134 * w.H  # 64 + 64 + 3 * 2 bytes per (token, head)
+    # turbo_prod: 64 + 64 + 3 * 2 bytes per (token, head); turbo_mse: 64 + 64 + 2 * 2.
+    cell = (134 if scheme == "turbo_prod" else 132) * w.H
     kv_tokens = int((lens + widths).sum())
     alg = kv_tokens * (cell + 4) + int(widths.sum()) * (2 * w.H * 128 * 2 + cell) + 2 * rows * w.H * 256
     # What this kernel reads: every new-token row group reads its own range.
     read = int(sum(sum(L + j + 1 for j in range(wd)) for L, wd in zip(lens, widths))) * cell
     b.close()
-    return {"sequences": 32, "rows": rows, "kv_tokens": kv_tokens,
+    return {"scheme": scheme, "sequences": 32, "rows": rows, "kv_tokens": kv_tokens,
             "new_tokens": int(widths.sum()), "append_us": round(app_us, 2),
             "attention_us": round(att_us, 2), "step_us": round(app_us + att_us, 2),
             "algorithmic_bytes": alg, "GBps_algorithmic": round(alg / (app_us + att_us) / 1e3, 1),
             "cells_read_bytes": read}
 
 
-def cpu_baseline(w: Workload):
-    """The oracle (a C port of the reference's dequant and of its attention
-    kernel's fp32 algorithm) on this host's cores: whole layers of the same
-    step, cycling through the 36 pools, for about 10 s of CPU time."""
+def host_cpu() -> dict:
+    """This host's CPU: logical CPUs (nproc), the ones this process may use,
+    and the model name (lscpu's "Model name", from /proc/cpuinfo)."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    return {"nproc": os.cpu_count(), "usable": usable, "model": model}
+
+
+def cpu_baseline(w: Workload, runs: int = 5, layers_per_run: int = 3):
+    """The reference's CPU path for one decode step of this workload, on this
+    host: per layer, the dequant (the oracle's C
+    restatement of the reference kernel's operation order) to [N, H, D] fp16,
+    the permute to [H, N, D] the reference's store does, and
+    attention_ref_single_head (src/tq_attention_ref.cpp:10-56 semantics) for
+    each of the 16 query heads over its kv head's dequantized K/V.  Timed on
+    1 thread and on every usable core (the dequant's token rows and the
+    query heads split over threads), each as the median of `runs` runs of
+    `layers_per_run` layers after one warm-up run."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    import numpy as np
+
     from oracle.oracle import load
     from turborag_amd.synthetic import as_u16
     orc = load()
-    cores = max(1, min(16, os.cpu_count() or 1))
-    orc.nthreads = cores
+    info = host_cpu()
     slots_np = w.slots.cpu().numpy()
-    q_np = as_u16(w.qa)
-    td = ta = 0.0
-    layers = 0
-    t_start = time.perf_counter()
-    while layers < 8 * w.NL and (layers < 2 or time.perf_counter() - t_start < 10.0):
-        pool_np = w.pools[layers % w.NL].cpu().numpy()
+    q_heads = as_u16(w.qa).transpose(1, 0, 2).reshape(w.q_heads, w.D)  # [h * rows + g]
+    pools = [w.pools[l].cpu().numpy() for l in range(layers_per_run)]
+    group = w.q_heads // w.H
+
+    def layer(pool_np, threads, ex):
+        orc.nthreads = threads
         t0 = time.perf_counter()
-        orc.prod_dequant(pool_np, slots_np, w.H, w.D, w.B)
+        ok, ov = orc.prod_dequant(pool_np, slots_np, w.H, w.D, w.B)
+        kh = np.ascontiguousarray(ok.transpose(1, 0, 2))  # [H, N, D]
+        vh = np.ascontiguousarray(ov.transpose(1, 0, 2))
         t1 = time.perf_counter()
-        orc.prod_attention_f32(q_np, pool_np, slots_np, w.B)
+        heads = range(w.q_heads)
+        fn = lambda j: orc.sdpa_single_head(q_heads[j], kh[j // group], vh[j // group])
+        outs = list(ex.map(fn, heads)) if ex is not None else [fn(j) for j in heads]
         t2 = time.perf_counter()
-        td += t1 - t0
-        ta += t2 - t1
-        layers += 1
-    log(f"[bench] cpu oracle ({cores} threads, {layers} layers): dequant "
-        f"{td / layers * 1e3:.1f} ms/layer, attention {ta / layers * 1e3:.1f} ms/layer")
+        assert len(outs) == w.q_heads
+        return t1 - t0, t2 - t1
+
+    def timed(threads):
+        ex = ThreadPoolExecutor(threads) if threads > 1 else None
+        try:
+            for p in pools:  # warm-up run
+                layer(p, threads, ex)
+            samples = []
+            for _ in range(runs):
+                d = a = 0.0
+                for p in pools:
+                    dd, aa = layer(p, threads, ex)
+                    d += dd
+                    a += aa
+                samples.append((d + a, d, a))
+        finally:
+            if ex is not None:
+                ex.shutdown()
+        samples.sort()
+        tot, d, a = samples[len(samples) // 2]
+        n = len(pools)
+        return {"threads": threads,
+                "value": round(n * (w.deq_bytes + w.att_bytes) / tot / 1e9, 3),
+                "ms_per_layer": round(tot / n * 1e3, 2),
+                "dequant_ms_per_layer": round(d / n * 1e3, 2),
+                "attention_ms_per_layer": round(a / n * 1e3, 2)}
+
+    one = timed(1)
+    allc = timed(max(1, info["usable"]))
+    log(f"[bench] cpu reference path ({info['model']}, nproc {info['nproc']}): "
+        f"1 thread {one['ms_per_layer']:.1f} ms/layer, {allc['threads']} threads "
+        f"{allc['ms_per_layer']:.1f} ms/layer")
     return {
-        "value": round(layers * (w.deq_bytes + w.att_bytes) / (td + ta) / 1e9, 3),
+        "value": allc["value"],
         "unit": "GB/s",
-        "cores": cores,
+        "cores": allc["threads"],
         "kind": "port",
-        "sample": f"{layers} layers (cycling the step's 36 pools): turbo_prod dequant of {w.N} tokens x {w.H} "
-                  f"heads + the reference kernel's fp32 attention algorithm for {w.rows} GQA "
-                  f"rows x {w.H} heads over {w.N} tokens, per layer",
-        "dequant_ms_per_layer": round(td / layers * 1e3, 2),
-        "attention_ms_per_layer": round(ta / layers * 1e3, 2),
+        "sample": f"{len(pools)} layers per run, median of {runs} runs after one warm-up: "
+                  f"turbo_prod dequant of {w.N} tokens x {w.H} heads to fp16, permute to "
+                  f"[H, N, D], then attention_ref_single_head for {w.q_heads} query heads "
+                  f"over {w.N} tokens (GQA {w.q_heads}/{w.H}); same algorithmic bytes as "
+                  f"the GPU step",
+        "single_thread": one,
+        "all_cores": allc,
+        "host": info,
+        "build": "gcc -O3 -march=x86-64-v3 -ffp-contract=off (oracle/build_oracle.sh)",
     }
 
 
