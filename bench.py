@@ -42,7 +42,8 @@ def log(msg: str) -> None:
 
 # The dominant kernel (the roofline's) and the decode-attention kernels, as
 # rocprofv3 names them (template argument 1 = turbo_prod).
-DEQUANT_KERNEL = "tq::dequant_stream_kernel<128, 1>"
+DEQUANT_KERNEL = "tq::dequant_stream_kernel<128, 1, 64>"   # the 36-layer launch
+DEQUANT_KERNEL_1 = "tq::dequant_stream_kernel<128, 1, 1>"  # one layer per launch
 ATTN_KERNELS = ("tq::attn_mfma_split_kernel<1, 32, 8, false, 1>", "tq::attn_mfma_combine_kernel")
 
 
@@ -131,6 +132,13 @@ class Workload:
                                   self.lp, self.cfg, self.rows, self.N, stream=self._stream())
 
     def all_dequant(self):
+        """Every layer's dequant in one call (tq_launch_turbo_prod_dequant_kv_layers):
+        the document's 36 layers load as one launch."""
+        self.tq.dequant_layers("turbo_prod", self.pools, self.slots, self.out_k, self.out_v,
+                               self.lp, self.cfg, self.N, stream=self._stream())
+
+    def all_dequant_per_layer(self):
+        """The reference's form: one tq_launch_turbo_prod_dequant_kv per layer."""
         for layer in range(self.NL):
             self.dequant(layer)
 
@@ -188,7 +196,8 @@ def event_time_us(run, reps):
 
 
 def launch_pass(w: Workload, reps: int) -> None:
-    """Eager launches only: dequant and attention of every layer, one step of
+    """Eager launches only: the 36-layer dequant (one launch and per-layer
+    launches) and attention of every layer, one step of
     the batched paged decode (append + attention), then a plain device copy of
     the dequant's byte count (the calibration kernel for the FETCH_SIZE /
     WRITE_SIZE counters)."""
@@ -199,6 +208,7 @@ def launch_pass(w: Workload, reps: int) -> None:
     bt = batched_setup(w)
     for _ in range(reps):
         w.all_dequant()
+        w.all_dequant_per_layer()
         w.all_attention()
         bt["batch"].repack()
         bt["batch"].attention(bt["query"], bt["row_seq"], bt["row_len"], bt["tables"], bt["out"])
@@ -245,17 +255,19 @@ def main() -> int:
         w.all_attention()
     torch.cuda.synchronize()
     use_graph = not args.no_graph
-    g_step = g_serial = g_deq = g_att = None
+    g_step = g_serial = g_deq = g_att = g_deq1 = None
     if use_graph:
         g_step = capture(w.step, side)
         g_serial = capture(w.serial_step, side)
         g_deq = capture(w.all_dequant, side)
         g_att = capture(w.all_attention, side)
-        use_graph = None not in (g_step, g_serial, g_deq, g_att)
+        g_deq1 = capture(w.all_dequant_per_layer, side)
+        use_graph = None not in (g_step, g_serial, g_deq, g_att, g_deq1)
     run_step = g_step.replay if use_graph else w.step
     run_serial = g_serial.replay if use_graph else w.serial_step
     run_deq = g_deq.replay if use_graph else w.all_dequant
     run_att = g_att.replay if use_graph else w.all_attention
+    run_deq1 = g_deq1.replay if use_graph else w.all_dequant_per_layer
 
     # The timed region: K whole steps.
     for _ in range(args.warmup):
@@ -276,14 +288,20 @@ def main() -> int:
         f"({'graph' if use_graph else 'eager'}; dequant and attention chains on two streams); "
         f"one stream: {serial_ms:.3f} ms")
 
-    # Per-kernel averages: graphs of the 36 dequant launches and of the 36
-    # attention launches (split + combine), replayed and timed with events.
+    # Per-kernel averages, replayed from graphs and timed with events: the
+    # one-launch dequant of the 36 layers (the roofline kernel), the 36
+    # per-layer dequant launches, and the 36 attention launches (split +
+    # combine).
     reps = max(3, args.steps)
-    deq_us = event_time_us(run_deq, reps) / w.NL
+    launch_us = event_time_us(run_deq, reps)
+    deq_us = launch_us / w.NL
+    deq1_us = event_time_us(run_deq1, reps) / w.NL
     att_us = event_time_us(run_att, reps) / w.NL
     deq_gbps = w.deq_bytes / (deq_us * 1e-6) / 1e9
+    deq1_gbps = w.deq_bytes / (deq1_us * 1e-6) / 1e9
     att_gbps = w.att_bytes / (att_us * 1e-6) / 1e9
-    log(f"[bench] dequant {deq_us:.2f} us/layer {deq_gbps:.0f} GB/s; "
+    log(f"[bench] dequant {deq_us:.2f} us/layer {deq_gbps:.0f} GB/s (one launch for {w.NL} "
+        f"layers; {deq1_us:.2f} us/layer {deq1_gbps:.0f} GB/s as per-layer launches); "
         f"attention {att_us:.2f} us/layer {att_gbps:.0f} GB/s")
 
     # A plain device copy of the dequant's byte count, MALL-cold (36 buffers).
@@ -369,15 +387,21 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "turbo_prod dequant (one layer)",
+            "kernel": f"{DEQUANT_KERNEL}: turbo_prod dequant of the {w.NL} layers, one launch",
             "achieved": round(deq_gbps, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(deq_gbps / HBM_PEAK_GBPS, 4),
             "traffic": traffic["bytes"] if traffic else None,
             "traffic_detail": traffic,
-            "algorithmic_bytes": w.deq_bytes,
-            "avg_launch_us": round(deq_us, 3),
+            "algorithmic_bytes": w.NL * w.deq_bytes,
+            "algorithmic_bytes_per_layer": w.deq_bytes,
+            "avg_launch_us": round(launch_us, 3),
+            "us_per_layer": round(deq_us, 3),
+            "per_layer_launches": {"us_per_layer": round(deq1_us, 3),
+                                   "GBps": round(deq1_gbps, 1),
+                                   "frac": round(deq1_gbps / HBM_PEAK_GBPS, 4),
+                                   "kernel": DEQUANT_KERNEL_1},
             "copy_same_bytes_us": round(copy_us, 3),
         },
         "decode_attn": {

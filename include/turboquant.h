@@ -163,6 +163,25 @@ int tq_launch_turbo_mse_dequant_kv_hnd(const uint8_t* page_pool, const int32_t* 
                                        const TQTurbomsePageLayout* layout, const TQConfig* cfg,
                                        int num_tokens, void* stream);
 
+/* Dequant of a document's HBM-resident layers in one call: the reference's
+ * per-layer tq_launch_turbo_prod_dequant_kv (src/tq_capi.cpp:66) for every
+ * l < num_layers, all layers sharing slot_mapping (device int32[num_tokens],
+ * as a document's layers do, cag_store.py:129).  page_pools, out_keys and
+ * out_values are HOST arrays of num_layers device pointers, read during the
+ * call.  Outputs are [num_tokens, H, D] fp16, or [1, H, num_tokens, D] when
+ * head_major != 0.  For D = 128 one launch covers up to 64 layers. */
+int tq_launch_turbo_prod_dequant_kv_layers(const uint8_t* const* page_pools,
+                                           const int32_t* slot_mapping,
+                                           uint16_t* const* out_keys, uint16_t* const* out_values,
+                                           int num_layers, const TQTurboProdPageLayout* layout,
+                                           const TQConfig* cfg, int num_tokens, int head_major,
+                                           void* stream);
+int tq_launch_turbo_mse_dequant_kv_layers(const uint8_t* const* page_pools,
+                                          const int32_t* slot_mapping, uint16_t* const* out_keys,
+                                          uint16_t* const* out_values, int num_layers,
+                                          const TQTurbomsePageLayout* layout, const TQConfig* cfg,
+                                          int num_tokens, int head_major, void* stream);
+
 /* For each layer l < num_layers: copies pool_bytes bytes from host_pools[l]
  * to device_pools[l] on copy_stream and dequantizes device_pools[l] into
  * out_key[l] / out_value[l] ([1, H, num_tokens, D] fp16) on compute_stream,

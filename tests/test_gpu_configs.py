@@ -274,3 +274,50 @@ def test_workspace_kept_for_captured_graph(tq, oracle, cuda):
     del g
     torch.cuda.synchronize()
     tq.release_workspaces()
+
+
+# ── multi-layer dequant (tq_launch_*_dequant_kv_layers) ──────────────── #
+
+def _layer_pools(tq, scheme, NL, N, H, D, B, cuda, seed):
+    cfg, lp, lm = _cfg(tq, H, D, B)
+    prod = scheme == "turbo_prod"
+    lay = lp if prod else lm
+    slots = permuted_slots(N, B, seed=seed).to(cuda)
+    pages = (N + B - 1) // B
+    pools = []
+    for layer in range(NL):
+        g = torch.Generator(device=cuda).manual_seed(seed + 1 + layer)
+        k = torch.randn(N, H, D, generator=g, device=cuda).half()
+        v = torch.randn(N, H, D, generator=g, device=cuda).half()
+        pool = torch.zeros(pages * lay.page_size_bytes, dtype=torch.uint8, device=cuda)
+        (tq.pack if prod else tq.mse_pack)(k, v, slots, pool, lay, cfg)
+        pools.append(pool)
+    return cfg, lay, slots, pools
+
+
+@pytest.mark.parametrize("scheme", ["turbo_prod", "turbo_mse"])
+@pytest.mark.parametrize("NL,N,H,head_major", [
+    (36, 32768, 2, False),    # config 3: 36 layers x 32768 tokens, one launch
+    (36, 32768, 2, True),     # ... into the cache layout [1, H, N, D]
+    (70, 1000, 2, False),     # more than 64 layers: two launches
+    (3, 777, 8, True),        # 8 kv heads, a ragged last page
+])
+def test_dequant_layers_vs_oracle(tq, oracle, cuda, scheme, NL, N, H, head_major):
+    D, B = 128, 16
+    print(f"[dequant_layers {scheme}] {NL} x {N} H={H} head_major={head_major}", flush=True)
+    oracle.nthreads = 16
+    cfg, lay, slots, pools = _layer_pools(tq, scheme, NL, N, H, D, B, cuda, seed=330 + NL)
+    shape = (1, H, N, D) if head_major else (N, H, D)
+    oks = [torch.full(shape, 7.0, dtype=torch.float16, device=cuda) for _ in range(NL)]
+    ovs = [torch.full(shape, 7.0, dtype=torch.float16, device=cuda) for _ in range(NL)]
+    tq.dequant_layers(scheme, pools, slots, oks, ovs, lay, cfg, N, head_major=head_major)
+    torch.cuda.synchronize()
+    fn = oracle.prod_dequant if scheme == "turbo_prod" else oracle.mse_dequant
+    sl = slots.cpu().numpy()
+    for layer in range(NL):
+        wk, wv = fn(pools[layer].cpu().numpy(), sl, H, D, B)
+        gk, gv = as_u16(oks[layer]), as_u16(ovs[layer])
+        if head_major:
+            gk, gv = gk[0].transpose(1, 0, 2), gv[0].transpose(1, 0, 2)
+        assert np.array_equal(gk, wk), layer
+        assert np.array_equal(gv, wv), layer

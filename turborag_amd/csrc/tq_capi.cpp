@@ -67,6 +67,13 @@ void check_grid(int n, const char* what, bool prod) {
         throw tq::Error(std::string(what) + ": invalid configuration argument");
 }
 
+// Kernels index (token, head) rows in int32: num_tokens * H must stay below
+// 2^30 (also leaving room for the persistent loops' look-ahead).
+void check_rows(int num_tokens, int H, const char* what) {
+    if ((long long)num_tokens * H >= (1LL << 30))
+        throw tq::Error(std::string(what) + ": num_tokens * num_kv_heads must be < 2^30");
+}
+
 }  // namespace
 
 namespace tq {
@@ -443,6 +450,7 @@ extern "C" int tq_launch_turbo_prod_pack_kv(const uint16_t* key, const uint16_t*
     return guarded([&] {
         const tq::PageGeom g = tq::prod_geom(*cfg, *layout);
         check_grid(num_tokens, "turbo_prod_pack_kv_kernel", true);
+        check_rows(num_tokens, g.H, "turbo_prod_pack_kv");
         tq::launch_pack(tq::Scheme::Prod, key, value, slot_mapping, page_pool, g, num_tokens,
                         static_cast<hipStream_t>(stream));
     });
@@ -458,6 +466,7 @@ extern "C" int tq_launch_turbo_prod_dequant_kv(const uint8_t* page_pool,
     return guarded([&] {
         const tq::PageGeom g = tq::prod_geom(*cfg, *layout);
         check_grid(num_tokens, "turbo_prod_dequant_kv_kernel", true);
+        check_rows(num_tokens, g.H, "turbo_prod_dequant_kv");
         tq::launch_dequant(tq::Scheme::Prod, page_pool, slot_mapping, out_key, out_value, g,
                            num_tokens, static_cast<hipStream_t>(stream));
     });
@@ -501,6 +510,7 @@ extern "C" int tq_launch_turbo_prod_dequant_kv_hnd(const uint8_t* page_pool,
     return guarded([&] {
         const tq::PageGeom g = tq::prod_geom(*cfg, *layout);
         check_grid(num_tokens, "turbo_prod_dequant_kv_kernel", true);
+        check_rows(num_tokens, g.H, "turbo_prod_dequant_kv_hnd");
         tq::launch_dequant(tq::Scheme::Prod, page_pool, slot_mapping, out_key, out_value, g,
                            num_tokens, static_cast<hipStream_t>(stream), /*head_major=*/true);
     });
@@ -521,11 +531,55 @@ extern "C" int tq_load_turbo_prod_layers(const uint8_t* const* host_pools,
         const tq::PageGeom g = tq::prod_geom(*cfg, *layout);
         if (num_layers < 0 || num_tokens < 0)
             throw tq::Error("turbo_prod load: num_layers and num_tokens must be >= 0");
+        check_rows(num_tokens, g.H, "turbo_prod load");
         tq::load_layers(tq::Scheme::Prod, host_pools, device_pools, pool_bytes, num_layers,
                         slot_mapping, num_tokens, out_key, out_value, g,
                         static_cast<hipStream_t>(copy_stream),
                         static_cast<hipStream_t>(compute_stream));
     });
+}
+
+namespace {
+// tq_launch_*_dequant_kv_layers: one slot mapping, num_layers pools and outputs.
+template <class Layout>
+int dequant_layers(tq::Scheme scheme, const uint8_t* const* page_pools,
+                   const int32_t* slot_mapping, uint16_t* const* out_keys,
+                   uint16_t* const* out_values, int num_layers, const Layout* layout,
+                   const TQConfig* cfg, int num_tokens, int head_major, void* stream) {
+    if (!page_pools || !slot_mapping || !out_keys || !out_values || !layout || !cfg) return -1;
+    const bool prod = scheme == tq::Scheme::Prod;
+    const char* name = prod ? "turbo_prod_dequant_kv_layers" : "turbo_mse_dequant_kv_layers";
+    return guarded([&] {
+        const tq::PageGeom g =
+            prod ? tq::prod_geom(*cfg, *reinterpret_cast<const TQTurboProdPageLayout*>(layout))
+                 : tq::mse_geom(*cfg, *reinterpret_cast<const TQTurbomsePageLayout*>(layout));
+        if (num_layers < 0 || num_tokens < 0)
+            throw tq::Error(std::string(name) + ": num_layers and num_tokens must be >= 0");
+        check_rows(num_tokens, g.H, name);
+        for (int l = 0; l < num_layers; ++l)
+            if (!page_pools[l] || !out_keys[l] || !out_values[l])
+                throw tq::Error(std::string(name) + ": null pool or output pointer for a layer");
+        tq::launch_dequant_layers(scheme, page_pools, slot_mapping, out_keys, out_values, g,
+                                  num_tokens, num_layers, static_cast<hipStream_t>(stream),
+                                  head_major != 0);
+    });
+}
+}  // namespace
+
+extern "C" int tq_launch_turbo_prod_dequant_kv_layers(
+    const uint8_t* const* page_pools, const int32_t* slot_mapping, uint16_t* const* out_keys,
+    uint16_t* const* out_values, int num_layers, const TQTurboProdPageLayout* layout,
+    const TQConfig* cfg, int num_tokens, int head_major, void* stream) {
+    return dequant_layers(tq::Scheme::Prod, page_pools, slot_mapping, out_keys, out_values,
+                          num_layers, layout, cfg, num_tokens, head_major, stream);
+}
+
+extern "C" int tq_launch_turbo_mse_dequant_kv_layers(
+    const uint8_t* const* page_pools, const int32_t* slot_mapping, uint16_t* const* out_keys,
+    uint16_t* const* out_values, int num_layers, const TQTurbomsePageLayout* layout,
+    const TQConfig* cfg, int num_tokens, int head_major, void* stream) {
+    return dequant_layers(tq::Scheme::Mse, page_pools, slot_mapping, out_keys, out_values,
+                          num_layers, layout, cfg, num_tokens, head_major, stream);
 }
 
 // ---------------------------------------------------------------------------
@@ -540,6 +594,7 @@ extern "C" int tq_launch_turbo_mse_pack_kv(const uint16_t* key, const uint16_t* 
     return guarded([&] {
         const tq::PageGeom g = tq::mse_geom(*cfg, *layout);
         check_grid(num_tokens, "turbo_mse_pack_kv_kernel", false);
+        check_rows(num_tokens, g.H, "turbo_mse_pack_kv");
         tq::launch_pack(tq::Scheme::Mse, key, value, slot_mapping, page_pool, g, num_tokens,
                         static_cast<hipStream_t>(stream));
     });
@@ -554,6 +609,7 @@ extern "C" int tq_launch_turbo_mse_dequant_kv(const uint8_t* page_pool,
     return guarded([&] {
         const tq::PageGeom g = tq::mse_geom(*cfg, *layout);
         check_grid(num_tokens, "turbo_mse_dequant_kv_kernel", false);
+        check_rows(num_tokens, g.H, "turbo_mse_dequant_kv");
         tq::launch_dequant(tq::Scheme::Mse, page_pool, slot_mapping, out_key, out_value, g,
                            num_tokens, static_cast<hipStream_t>(stream));
     });
@@ -583,6 +639,7 @@ extern "C" int tq_launch_turbo_mse_dequant_kv_hnd(const uint8_t* page_pool,
     return guarded([&] {
         const tq::PageGeom g = tq::mse_geom(*cfg, *layout);
         check_grid(num_tokens, "turbo_mse_dequant_kv_kernel", false);
+        check_rows(num_tokens, g.H, "turbo_mse_dequant_kv_hnd");
         tq::launch_dequant(tq::Scheme::Mse, page_pool, slot_mapping, out_key, out_value, g,
                            num_tokens, static_cast<hipStream_t>(stream), /*head_major=*/true);
     });
@@ -602,6 +659,7 @@ extern "C" int tq_load_turbo_mse_layers(const uint8_t* const* host_pools,
         const tq::PageGeom g = tq::mse_geom(*cfg, *layout);
         if (num_layers < 0 || num_tokens < 0)
             throw tq::Error("turbo_mse load: num_layers and num_tokens must be >= 0");
+        check_rows(num_tokens, g.H, "turbo_mse load");
         tq::load_layers(tq::Scheme::Mse, host_pools, device_pools, pool_bytes, num_layers,
                         slot_mapping, num_tokens, out_key, out_value, g,
                         static_cast<hipStream_t>(copy_stream),

@@ -500,15 +500,34 @@ __global__ __launch_bounds__(kBlock) void dequant_kernel(
 // ---------------------------------------------------------------------------
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// The layers one dequant launch covers (pools and outputs of each; one slot
+// mapping shared by all), passed by value in the kernel arguments.
+template <int ML>
+struct LayerSet {
+    const uint8_t* pool[ML];
+    uint16_t* out_key[ML];
+    uint16_t* out_value[ML];
+};
+constexpr int kMaxLayersPerLaunch = 64;
+// Dequant workgroups per CU for a multi-layer launch.  32 KB of LDS per
+// workgroup lets 4 reside per CU; a grid of several such rounds balances the
+// tail (36 x 32K-token layers: 4 per CU 9.3 us/layer, 8: 9.0, 24: 8.6, 48-192:
+// 8.8-9.0).
+#ifndef TQ_DEQ_LAYERS_BLOCKS_PER_CU
+#define TQ_DEQ_LAYERS_BLOCKS_PER_CU 24
+#endif
+
 // SCH: 0 turbo_mse, 1 turbo_prod, 2 the reference's unexported QJL-1b page
 // (tq_qjl_kernels.cu:189-245): K = +-ks per sign bit, fed through the same
 // per-row table as 0/1 "nibbles" (the sign byte's bits spread one per
 // nibble), and the rotation's sign flip (-1)^i has no head term.
-template <int D, int SCH>
+// ML > 1: num_layers <= ML layers in one launch; the persistent waves walk
+// (layer, row group) pairs, layer-major, so the launch and the first-code
+// latency are paid once for all of them.
+template <int D, int SCH, int ML = 1>
 __global__ __launch_bounds__(kBlock) void dequant_stream_kernel(
-    const uint8_t* __restrict__ pool, const int32_t* __restrict__ slots,
-    uint16_t* __restrict__ out_key, uint16_t* __restrict__ out_value, PageGeom g, int num_rows,
-    float inv, OutLayout ol) {
+    const LayerSet<ML> layers, const int32_t* __restrict__ slots, PageGeom g, int num_rows,
+    int num_layers, float inv, OutLayout ol) {
     constexpr bool PROD = SCH == 1, QJL = SCH == 2;
     static_assert(!QJL || D == 128, "QJL: D = 128");
     constexpr int E = 32;           // elements per lane
@@ -532,7 +551,8 @@ __global__ __launch_bounds__(kBlock) void dequant_stream_kernel(
     float* TV = &tab[1][0][wave][lane];
     const uint32_t tbase = (uint32_t)reinterpret_cast<uintptr_t>((lds_float*)TK);
     const uint32_t wsplat = 0x01010101u * (uint32_t)wave;
-    const int groups = (num_rows + RPW - 1) / RPW;
+    const int groups = (num_rows + RPW - 1) / RPW;  // row groups per layer
+    const int total = groups * num_layers;          // (layer, group) pairs
     const int stride = gridDim.x * (kBlock / 64);
 
     struct Item {
@@ -540,7 +560,19 @@ __global__ __launch_bounds__(kBlock) void dequant_stream_kernel(
         float ks, re, vs;
         int row, t, h;
         int pt, ph;  // token and head of row ^ 1 (the store partner when LPR = 4)
+        int layer;   // wave-uniform
         bool live, plive;
+    };
+    // pair index -> (layer, group of the layer); wave-uniform
+    auto split_pair = [&](int gi, int& grp) -> int {
+        if constexpr (ML == 1) {
+            grp = gi;
+            return 0;
+        } else {
+            const int l = gi / groups;
+            grp = gi - l * groups;
+            return l;
+        }
     };
     auto token_head = [&](int row, int& t, int& h) {
         if (g.h_shift >= 0) {
@@ -551,18 +583,25 @@ __global__ __launch_bounds__(kBlock) void dequant_stream_kernel(
             h = row - t * g.H;
         }
     };
-    auto load_slot = [&](int grp) -> int {
+    auto load_slot = [&](int gi) -> int {
+        if (gi >= total) return -1;
+        int grp;
+        split_pair(gi, grp);
         const int row = grp * RPW + rw;
-        if (grp >= groups || row >= num_rows) return -1;
+        if (row >= num_rows) return -1;
         int t, h;
         token_head(row, t, h);
         return slots[t];
     };
-    auto fetch = [&](int grp, int slot) -> Item {
+    auto fetch = [&](int gi, int slot) -> Item {
         Item it;
+        int grp;
+        it.layer = __builtin_amdgcn_readfirstlane(gi < total ? split_pair(gi, grp) : 0);
+        if (gi >= total) grp = groups;
+        const uint8_t* pool = layers.pool[it.layer];
         it.row = grp * RPW + rw;
         token_head(min(it.row, num_rows - 1), it.t, it.h);
-        it.live = grp < groups && it.row < num_rows && slot >= 0;
+        it.live = gi < total && it.row < num_rows && slot >= 0;
         it.kw = make_uint4(0, 0, 0, 0);
         it.vw = it.kw;
         it.ks = it.re = it.vs = 0.0f;
@@ -699,12 +738,12 @@ __global__ __launch_bounds__(kBlock) void dequant_stream_kernel(
         }
     };
 
-    int grp = blockIdx.x * (kBlock / 64) + wave;
-    Item cur = fetch(grp, load_slot(grp));
-    int s_next = load_slot(grp + stride);
-    while (grp < groups) {  // wave-uniform
-        const Item nxt = fetch(grp + stride, s_next);
-        s_next = load_slot(grp + 2 * stride);
+    int gi = blockIdx.x * (kBlock / 64) + wave;
+    Item cur = fetch(gi, load_slot(gi));
+    int s_next = load_slot(gi + stride);
+    while (gi < total) {  // wave-uniform
+        const Item nxt = fetch(gi + stride, s_next);
+        s_next = load_slot(gi + 2 * stride);
         // Every lane writes all 16 entries of its own copies (one b32 store
         // per entry and tensor; a wave's 64 stores fill 64 distinct banks).
         {
@@ -723,12 +762,12 @@ __global__ __launch_bounds__(kBlock) void dequant_stream_kernel(
         // The table is private to this wave: wave-scope ordering suffices.
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        transform(cur, cur.kw, 0, out_key);
-        transform(cur, cur.vw, kTabBytes, out_value);
+        transform(cur, cur.kw, 0, layers.out_key[cur.layer]);
+        transform(cur, cur.vw, kTabBytes, layers.out_value[cur.layer]);
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         cur = nxt;
-        grp += stride;
+        gi += stride;
     }
 }
 
@@ -855,8 +894,9 @@ bool launch_qjl_stream_dequant(const uint8_t* pool, const int32_t* slots, uint16
     const int rows_per_block = kBlock / (g.D / 32);
     const int blocks_needed = (rows + rows_per_block - 1) / rows_per_block;
     const dim3 grid(std::max(1, std::min(blocks_needed, 4 * num_cus())));
-    hipLaunchKernelGGL((dequant_stream_kernel<128, 2>), grid, dim3(kBlock), 0, stream, pool, slots,
-                       out_key, out_value, g, rows, inv_sqrt_d(g.D), ol);
+    const LayerSet<1> one{{pool}, {out_key}, {out_value}};
+    hipLaunchKernelGGL((dequant_stream_kernel<128, 2>), grid, dim3(kBlock), 0, stream, one, slots,
+                       g, rows, 1, inv_sqrt_d(g.D), ol);
     check_launch("qjl_dequant_kv_kernel");
     return true;
 }
@@ -878,9 +918,10 @@ void launch_dequant(Scheme s, const uint8_t* pool, const int32_t* slots, uint16_
         const int blocks_needed = (rows + rows_per_block - 1) / rows_per_block;
         const dim3 grid(std::max(1, std::min(blocks_needed, 4 * num_cus())));
         const bool prod = s == Scheme::Prod;
+        const LayerSet<1> one{{pool}, {out_key}, {out_value}};
         auto go = [&](auto kernel) {
-            hipLaunchKernelGGL(kernel, grid, dim3(kBlock), 0, stream, pool, slots, out_key,
-                               out_value, g, rows, inv, ol);
+            hipLaunchKernelGGL(kernel, grid, dim3(kBlock), 0, stream, one, slots, g, rows, 1, inv,
+                               ol);
         };
         if (g.D == 128) prod ? go(dequant_stream_kernel<128, 1>) : go(dequant_stream_kernel<128, 0>);
         else if (g.D == 64) prod ? go(dequant_stream_kernel<64, 1>) : go(dequant_stream_kernel<64, 0>);
@@ -900,6 +941,52 @@ void launch_dequant(Scheme s, const uint8_t* pool, const int32_t* slots, uint16_
                                               stream, pool, slots, out_key, out_value, g, rows,
                                               inv, ol));
         check_launch("turbo_mse_dequant_kv_kernel");
+    }
+}
+
+void launch_dequant_layers(Scheme s, const uint8_t* const* pools, const int32_t* slots,
+                           uint16_t* const* out_key, uint16_t* const* out_value, const PageGeom& g,
+                           int num_tokens, int num_layers, hipStream_t stream, bool head_major) {
+    const int rows = num_tokens * g.H;
+    if (rows <= 0 || num_layers <= 0) return;
+    bool wide = g.D == 128;
+    for (int l = 0; l < num_layers && wide; ++l)
+        wide = wide_dequant_ok(g, pools[l], out_key[l], out_value[l]);
+    if (!wide) {  // the per-layer kernels (other head dims, unaligned buffers)
+        for (int l = 0; l < num_layers; ++l)
+            launch_dequant(s, pools[l], slots, out_key[l], out_value[l], g, num_tokens, stream,
+                           head_major);
+        return;
+    }
+    const float inv = inv_sqrt_d(g.D);
+    OutLayout ol;
+    ol.tok = head_major ? (uint64_t)g.D : (uint64_t)g.H * g.D;
+    ol.head = head_major ? (uint64_t)num_tokens * g.D : (uint64_t)g.D;
+    const bool prod = s == Scheme::Prod;
+    const int rows_per_block = kBlock / (g.D / 32);
+    // The kernel counts (layer, row group) pairs in int32: keep them below 2^30.
+    const int groups = (rows + 15) / 16;
+    const int per_launch = (int)std::max(1LL, std::min<long long>(kMaxLayersPerLaunch,
+                                                                  (1LL << 30) / groups));
+    for (int l0 = 0; l0 < num_layers; l0 += per_launch) {
+        const int n = std::min(per_launch, num_layers - l0);
+        LayerSet<kMaxLayersPerLaunch> set{};
+        for (int l = 0; l < n; ++l) {
+            set.pool[l] = pools[l0 + l];
+            set.out_key[l] = out_key[l0 + l];
+            set.out_value[l] = out_value[l0 + l];
+        }
+        const long long blocks_needed =
+            ((long long)rows * n + rows_per_block - 1) / rows_per_block;
+        const dim3 grid((unsigned)std::max(
+            1LL, std::min<long long>(blocks_needed, TQ_DEQ_LAYERS_BLOCKS_PER_CU * num_cus())));
+        if (prod)
+            hipLaunchKernelGGL((dequant_stream_kernel<128, 1, kMaxLayersPerLaunch>), grid,
+                               dim3(kBlock), 0, stream, set, slots, g, rows, n, inv, ol);
+        else
+            hipLaunchKernelGGL((dequant_stream_kernel<128, 0, kMaxLayersPerLaunch>), grid,
+                               dim3(kBlock), 0, stream, set, slots, g, rows, n, inv, ol);
+        check_launch(prod ? "turbo_prod_dequant_kv_layers" : "turbo_mse_dequant_kv_layers");
     }
 }
 

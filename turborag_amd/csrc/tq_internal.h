@@ -76,6 +76,11 @@ void launch_pack(Scheme s, const uint16_t* key, const uint16_t* value, const int
 void launch_dequant(Scheme s, const uint8_t* pool, const int32_t* slots, uint16_t* out_key,
                     uint16_t* out_value, const PageGeom& g, int num_tokens, hipStream_t stream,
                     bool head_major = false);
+// Dequant of num_layers HBM-resident pools sharing one slot mapping, in as
+// few launches as possible (one per 64 layers for D = 128 and aligned buffers).
+void launch_dequant_layers(Scheme s, const uint8_t* const* pools, const int32_t* slots,
+                           uint16_t* const* out_key, uint16_t* const* out_value, const PageGeom& g,
+                           int num_tokens, int num_layers, hipStream_t stream, bool head_major);
 // Layer-pipelined host -> device copy + dequant into [1, H, N, D] (tq_loader.cpp).
 void load_layers(Scheme s, const uint8_t* const* host_pools, uint8_t* const* device_pools,
                  size_t pool_bytes, int num_layers, const int32_t* slots, int num_tokens,

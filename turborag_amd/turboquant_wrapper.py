@@ -150,6 +150,12 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "tq_launch_turbo_mse_dequant_kv_hnd": ([_P(c_uint8), _P(c_int32), c_void_p, c_void_p,
                                             _P(TQTurbomsePageLayout), _P(TQConfig), c_int,
                                             c_void_p], c_int),
+    "tq_launch_turbo_prod_dequant_kv_layers": ([_P(c_void_p), _P(c_int32), _P(c_void_p),
+                                                _P(c_void_p), c_int, _P(TQTurboProdPageLayout),
+                                                _P(TQConfig), c_int, c_int, c_void_p], c_int),
+    "tq_launch_turbo_mse_dequant_kv_layers": ([_P(c_void_p), _P(c_int32), _P(c_void_p),
+                                               _P(c_void_p), c_int, _P(TQTurbomsePageLayout),
+                                               _P(TQConfig), c_int, c_int, c_void_p], c_int),
     "tq_load_turbo_prod_layers": ([_P(c_void_p), _P(c_void_p), c_size_t, c_int, _P(c_int32),
                                    c_int, _P(c_void_p), _P(c_void_p), _P(TQTurboProdPageLayout),
                                    _P(TQConfig), c_void_p, c_void_p], c_int),
@@ -447,6 +453,32 @@ class TurboQuantWrapper:
                         num_tokens: int, stream: int = 0) -> None:
         self._dequant_hnd("turbo_mse", page_pool, slot_mapping, out_key, out_value, layout,
                           cfg, num_tokens, stream)
+
+    def dequant_layers(self, scheme: str, page_pools, slot_mapping, out_keys, out_values,
+                       layout, cfg, num_tokens: int, head_major: bool = False,
+                       stream: int = 0) -> None:
+        """Dequant every layer's pool (one shared slot mapping) into
+        out_keys[l] / out_values[l]: [N, H, D] fp16, or [1, H, N, D] with
+        head_major; one launch per 64 layers at head_dim 128."""
+        n = len(page_pools)
+        if not (len(out_keys) == len(out_values) == n):
+            raise ValueError("dequant_layers: one pool and two outputs per layer")
+        thd = num_tokens * cfg.num_kv_heads * cfg.head_dim
+        for l in range(n):
+            self._check(scheme, "dequant_kv_layers", page_pool=(page_pools[l], torch.uint8, 0),
+                        slot_mapping=(slot_mapping, torch.int32, num_tokens),
+                        out_key=(out_keys[l], torch.float16, thd),
+                        out_value=(out_values[l], torch.float16, thd))
+        arr = c_void_p * max(n, 1)
+        pools = arr(*[p.data_ptr() for p in page_pools])
+        ks = arr(*[t.data_ptr() for t in out_keys])
+        vs = arr(*[t.data_ptr() for t in out_values])
+        fn = (self._lib.tq_launch_turbo_prod_dequant_kv_layers if scheme == "turbo_prod"
+              else self._lib.tq_launch_turbo_mse_dequant_kv_layers)
+        rc = fn(pools, self._i32p(slot_mapping), ks, vs, n, ctypes.byref(layout),
+                ctypes.byref(cfg), num_tokens, int(head_major), self._stream(stream))
+        if rc != 0:
+            self._kernel_raise(rc, scheme, "dequant_kv_layers")
 
     def load_layers(self, scheme: str, host_pools, device_pools, slot_mapping, out_keys,
                     out_values, layout, cfg, num_tokens: int, copy_stream: int = 0,
