@@ -27,7 +27,9 @@ void launch_paged_attention(Scheme, const uint16_t*, const uint8_t*, const int32
                             const int32_t*, const int32_t*, uint16_t*, const PageGeom&, int, int,
                             hipStream_t) { no_device("paged attention"); }
 void launch_attention(Scheme, const uint16_t*, const uint8_t*, const int32_t*, uint16_t*,
-                      const PageGeom&, int, int, hipStream_t) { no_device("attention"); }
+                      const PageGeom&, int, int, hipStream_t, const Scratch&) {
+    no_device("attention");
+}
 void launch_qjl_pack(const uint16_t*, const uint16_t*, const int32_t*, uint8_t*, const QjlGeom&,
                      int, hipStream_t) { no_device("qjl pack"); }
 void launch_qjl_dequant(const uint8_t*, const int32_t*, uint16_t*, uint16_t*, const QjlGeom&, int,

@@ -1540,7 +1540,7 @@ template <int SCH>
 void launch_mfma_attention(const uint16_t* query, const uint8_t* pool, const int32_t* slots,
                            uint16_t* output, const PageGeom& g, int num_queries,
                            int num_kv_tokens, float inv, hipStream_t stream, const char* split_name,
-                           const char* combine_name) {
+                           const char* combine_name, const Scratch& scratch = Scratch{}) {
     using namespace mfma;
     const int rows = num_queries * g.H;
     const int row_groups = (num_queries + kRows - 1) / kRows;
@@ -1553,8 +1553,8 @@ void launch_mfma_attention(const uint16_t* query, const uint8_t* pool, const int
     const int tps = num_kv_tokens > 0 ? (num_kv_tokens + splits - 1) / splits : 0;
     if (tps > 0) splits = (num_kv_tokens + tps - 1) / tps;
     const size_t blocks = (size_t)splits * heads;
-    float* ws =
-        static_cast<float*>(workspace(stream, blocks * kRows * kPartStride * sizeof(float)));
+    float* ws = static_cast<float*>(
+        scratch.get(stream, blocks * kRows * kPartStride * sizeof(float), split_name));
     constexpr int kCH = kSplitChunk, kNW = kSplitWaves;
     const PagedRows none{};
     if (num_kv_tokens == 0) {  // no partials: the combine writes the zero output
@@ -1579,7 +1579,7 @@ void launch_mfma_attention(const uint16_t* query, const uint8_t* pool, const int
 
 void launch_attention(Scheme s, const uint16_t* query, const uint8_t* pool, const int32_t* slots,
                       uint16_t* output, const PageGeom& g, int num_queries, int num_kv_tokens,
-                      hipStream_t stream) {
+                      hipStream_t stream, const Scratch& scratch) {
     const int rows = num_queries * g.H;
     if (rows <= 0) return;
     const float inv = inv_sqrt_d(g.D);
@@ -1588,12 +1588,12 @@ void launch_attention(Scheme s, const uint16_t* query, const uint8_t* pool, cons
             launch_mfma_attention<mfma::kSchProd>(query, pool, slots, output, g, num_queries,
                                                   num_kv_tokens, inv, stream,
                                                   "turbo_prod_fused_attn_split",
-                                                  "turbo_prod_fused_attn_combine");
+                                                  "turbo_prod_fused_attn_combine", scratch);
         else
             launch_mfma_attention<mfma::kSchMse>(query, pool, slots, output, g, num_queries,
                                                  num_kv_tokens, inv, stream,
                                                  "turbo_mse_fused_attn_split",
-                                                 "turbo_mse_fused_attn_combine");
+                                                 "turbo_mse_fused_attn_combine", scratch);
         return;
     }
     // Enough waves to cover the chip several times, at least 32 tokens each.
@@ -1603,8 +1603,9 @@ void launch_attention(Scheme s, const uint16_t* query, const uint8_t* pool, cons
     const int tps = num_kv_tokens > 0 ? (num_kv_tokens + splits - 1) / splits : 0;
     if (tps > 0) splits = (num_kv_tokens + tps - 1) / tps;
     const size_t ws_bytes = (size_t)splits * rows * (g.D + 2) * sizeof(float);
-    float* ws = static_cast<float*>(workspace(stream, ws_bytes));
     const bool prod = s == Scheme::Prod;
+    float* ws = static_cast<float*>(scratch.get(
+        stream, ws_bytes, prod ? "turbo_prod_fused_attn_partial" : "turbo_mse_fused_attn_partial"));
     if (prod) {
         TQ_DISPATCH_D(g.D, hipLaunchKernelGGL((attn_partial_kernel<kD, true>),
                                               dim3(splits * rows), dim3(64), 0, stream, query,

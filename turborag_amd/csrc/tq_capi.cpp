@@ -372,6 +372,15 @@ void* workspace(hipStream_t stream, size_t bytes) {
     return p;
 }
 
+void* Scratch::get(hipStream_t stream, size_t bytes, const char* what) const {
+    if (!ptr) return workspace(stream, bytes);
+    if (bytes > cap)
+        throw Error(std::string(what) + ": needs " + std::to_string(bytes) +
+                    " bytes of split-K scratch, more than the " + std::to_string(cap) +
+                    " bytes available");
+    return ptr;
+}
+
 void release_workspaces() {
     std::lock_guard<std::mutex> lock(g_ws_mu);
     release_all();

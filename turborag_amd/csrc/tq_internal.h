@@ -66,6 +66,14 @@ void check_launch(const char* what);
 // Per-(device, stream) scratch for split-K partials.  Grows; an outgrown
 // buffer is freed once the stream's earlier kernels have finished.
 void* workspace(hipStream_t stream, size_t bytes);
+// Where an attention launch takes its split-K partials from: the cached
+// per-stream workspace above (ptr null), or memory the caller provides
+// (ptr, cap bytes), in which case a launch that needs more throws.
+struct Scratch {
+    void* ptr = nullptr;
+    size_t cap = 0;
+    void* get(hipStream_t stream, size_t bytes, const char* what) const;
+};
 // Synchronizes the devices and frees every cached workspace (tq_workspace_release).
 void release_workspaces();
 
@@ -96,7 +104,7 @@ void launch_paged_attention(Scheme s, const uint16_t* query, const uint8_t* pool
                             int num_rows, int max_kv_len, hipStream_t stream);
 void launch_attention(Scheme s, const uint16_t* query, const uint8_t* pool, const int32_t* slots,
                       uint16_t* output, const PageGeom& g, int num_queries, int num_kv_tokens,
-                      hipStream_t stream);
+                      hipStream_t stream, const Scratch& scratch = Scratch{});
 
 // ---- the reference's unexported kernels (tq_legacy.hip) -------------------
 // Byte geometry of a QJL-1b page (cell c = tib * H + h; K signs at
