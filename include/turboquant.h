@@ -242,6 +242,20 @@ int tq_launch_turbo_mse_paged_attention(const uint16_t* query, const uint8_t* pa
  * host threads. */
 int tq_workspace_release(void);
 
+/* No reference counterpart.  For callers that cannot allocate device memory
+ * (code under graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc): tq_launch_turbo_prod_fused_attention_output (src/tq_capi.cpp:99
+ * semantics, same arguments and result) with its split-K partials in a
+ * static 4 MiB device array instead of an allocated workspace; it calls no
+ * hipMalloc, hipFree or allocating library routine.  A launch whose
+ * partials exceed 4 MiB (more than 993 split workgroups of 8 query rows)
+ * returns -2.  Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (other streams, threads or graph replays) race. */
+int tq_launch_turbo_prod_fused_attention_output_noalloc(
+    const uint16_t* query, const uint8_t* page_pool, const int32_t* slot_mapping,
+    uint16_t* output, const TQTurboProdPageLayout* layout, const TQConfig* cfg, int num_queries,
+    int num_kv_tokens, void* stream);
+
 /* ---------------------------------------------------------------------- */
 /* Page allocator and block table (host bookkeeping).                       */
 /* Replaces TQAllocator (src/tq_allocator.cpp:5-31, include/tq_allocator.h) */

@@ -36,7 +36,7 @@ HIPCC_FLAGS = [
 ]
 
 SOURCES = ["tq_capi.cpp", "tq_pool.cpp", "tq_loader.cpp", "tq_store.cpp", "tq_codec.hip",
-           "tq_legacy.hip", "tq_attention.hip"]
+           "tq_legacy.hip", "tq_attention.hip", "tq_noalloc.hip"]
 
 
 def _hipcc() -> str:

@@ -133,6 +133,10 @@ SIGNATURES: dict[str, tuple[list, object]] = {
                                                      c_void_p, _P(TQTurboProdPageLayout),
                                                      _P(TQConfig), c_int, c_int, c_void_p],
                                                     c_int),
+    "tq_launch_turbo_prod_fused_attention_output_noalloc": ([c_void_p, _P(c_uint8), _P(c_int32),
+                                                             c_void_p, _P(TQTurboProdPageLayout),
+                                                             _P(TQConfig), c_int, c_int,
+                                                             c_void_p], c_int),
     "tq_launch_turbo_mse_pack_kv": ([c_void_p, c_void_p, _P(c_int32), _P(c_uint8),
                                      _P(TQTurbomsePageLayout), _P(TQConfig), c_int, c_void_p],
                                     c_int),
@@ -383,6 +387,24 @@ class TurboQuantWrapper:
             self._stream(stream))
         if rc != 0:
             self._kernel_raise(rc, "turbo_prod", "fused_attn_output")
+
+    def fused_attn_output_noalloc(self, query, page_pool, slot_mapping, output, layout, cfg,
+                                  num_queries: int, num_kv_tokens: int, stream: int = 0) -> None:
+        """fused_attn_output with its split-K partials in the library's static
+        4 MiB device scratch (tq_launch_turbo_prod_fused_attention_output_noalloc):
+        no device allocation; calls overlapping on one GPU race."""
+        H, D = cfg.num_kv_heads, cfg.head_dim
+        self._check("turbo_prod", "fused_attn_output_noalloc",
+                    query=(query, torch.float16, num_queries * H * D),
+                    page_pool=(page_pool, torch.uint8, 0),
+                    slot_mapping=(slot_mapping, torch.int32, num_kv_tokens),
+                    output=(output, torch.float16, num_queries * H * D))
+        rc = self._lib.tq_launch_turbo_prod_fused_attention_output_noalloc(
+            self._vp(query), self._u8p(page_pool), self._i32p(slot_mapping), self._vp(output),
+            ctypes.byref(layout), ctypes.byref(cfg), num_queries, num_kv_tokens,
+            self._stream(stream))
+        if rc != 0:
+            self._kernel_raise(rc, "turbo_prod", "fused_attn_output_noalloc")
 
     # ── turbo_mse ───────────────────────────────────────────────────── #
 
