@@ -321,3 +321,22 @@ def test_dequant_layers_vs_oracle(tq, oracle, cuda, scheme, NL, N, H, head_major
             gk, gv = gk[0].transpose(1, 0, 2), gv[0].transpose(1, 0, 2)
         assert np.array_equal(gk, wk), layer
         assert np.array_equal(gv, wv), layer
+
+
+# ── debug-sync mode ──────────────────────────────────────────────────── #
+
+def test_debug_sync_mode_runs_the_smoke_path():
+    """TQ_DEBUG_SYNC=1 (the reference's TQ_DEBUG_SYNC build switch, as an
+    environment variable): every launching entry synchronizes its stream;
+    the smoke path (pack, dequant, attention against the oracle) still
+    passes.  Run in a child process, since the switch is read once."""
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+    root = Path(__file__).resolve().parent.parent
+    env = dict(os.environ, TQ_DEBUG_SYNC="1")
+    r = subprocess.run([sys.executable, "-c", "import __graft_entry__ as g; g.smoke()"],
+                       cwd=root, env=env, capture_output=True, text=True, timeout=240)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+    assert "smoke ok" in r.stdout

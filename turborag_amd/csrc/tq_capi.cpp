@@ -8,6 +8,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstdio>
 #include <cstring>
 #include <map>
@@ -36,6 +37,48 @@ int guarded(F&& f) {
         set_error("unknown error");
         return -2;
     }
+}
+
+// Debug-sync mode (the reference's TQ_DEBUG_SYNC / TQ_CHECK_ASYNC,
+// include/tq_cuda_check.h:26-37): built with -DTQ_DEBUG_SYNC, or run with
+// the environment variable TQ_DEBUG_SYNC set to a non-zero value, every
+// launching entry synchronizes its stream after the launch, so a fault in its
+// kernels is reported by that call (rc -2, "async kernel error: ...").
+// Skipped while the stream is being captured into a graph.
+bool debug_sync_enabled() {
+#ifdef TQ_DEBUG_SYNC
+    return true;
+#else
+    static const bool on = [] {
+        const char* v = std::getenv("TQ_DEBUG_SYNC");
+        return v && *v && std::strcmp(v, "0") != 0;
+    }();
+    return on;
+#endif
+}
+
+}  // namespace
+
+void tq::debug_sync(void* stream) {
+    if (!debug_sync_enabled()) return;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &st) == hipSuccess && st != hipStreamCaptureStatusNone) return;
+    const hipError_t e = hipStreamSynchronize(s);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        throw tq::Error(std::string("async kernel error: ") + hipGetErrorString(e));
+    }
+}
+
+namespace {
+// guarded() for an entry that launches work on `stream`.
+template <class F>
+int guarded_sync(void* stream, F&& f) {
+    return guarded([&] {
+        f();
+        tq::debug_sync(stream);
+    });
 }
 
 size_t align_up(size_t x, size_t a) { return ((x + a - 1) / a) * a; }
@@ -456,7 +499,7 @@ extern "C" int tq_launch_turbo_prod_pack_kv(const uint16_t* key, const uint16_t*
                                             const TQTurboProdPageLayout* layout,
                                             const TQConfig* cfg, int num_tokens, void* stream) {
     if (!key || !value || !slot_mapping || !page_pool || !layout || !cfg) return -1;
-    return guarded([&] {
+    return guarded_sync(stream, [&] {
         const tq::PageGeom g = tq::prod_geom(*cfg, *layout);
         check_grid(num_tokens, "turbo_prod_pack_kv_kernel", true);
         check_rows(num_tokens, g.H, "turbo_prod_pack_kv");
@@ -472,7 +515,7 @@ extern "C" int tq_launch_turbo_prod_dequant_kv(const uint8_t* page_pool,
                                                const TQConfig* cfg, int num_tokens,
                                                void* stream) {
     if (!page_pool || !slot_mapping || !out_key || !out_value || !layout || !cfg) return -1;
-    return guarded([&] {
+    return guarded_sync(stream, [&] {
         const tq::PageGeom g = tq::prod_geom(*cfg, *layout);
         check_grid(num_tokens, "turbo_prod_dequant_kv_kernel", true);
         check_rows(num_tokens, g.H, "turbo_prod_dequant_kv");
@@ -486,7 +529,7 @@ extern "C" int tq_launch_turbo_prod_fused_attention_logits(
     const TQTurboProdPageLayout* layout, const TQConfig* cfg, int num_queries, int num_kv_tokens,
     void* stream) {
     if (!query || !page_pool || !slot_mapping || !logits || !layout || !cfg) return -1;
-    return guarded([&] {
+    return guarded_sync(stream, [&] {
         const tq::PageGeom g = tq::prod_geom(*cfg, *layout);
         check_grid(num_queries, "turbo_prod_fused_attention_logits_kernel", true);
         if (num_kv_tokens < 0) throw tq::Error("turbo_prod logits: num_kv_tokens < 0");
@@ -500,7 +543,7 @@ extern "C" int tq_launch_turbo_prod_fused_attention_output(
     uint16_t* output, const TQTurboProdPageLayout* layout, const TQConfig* cfg, int num_queries,
     int num_kv_tokens, void* stream) {
     if (!query || !page_pool || !slot_mapping || !output || !layout || !cfg) return -1;
-    return guarded([&] {
+    return guarded_sync(stream, [&] {
         const tq::PageGeom g = tq::prod_geom(*cfg, *layout);
         check_grid(num_queries, "turbo_prod_fused_attn_online_kernel", true);
         if (num_kv_tokens < 0) throw tq::Error("turbo_prod attention: num_kv_tokens < 0");
@@ -516,7 +559,7 @@ extern "C" int tq_launch_turbo_prod_dequant_kv_hnd(const uint8_t* page_pool,
                                                    const TQConfig* cfg, int num_tokens,
                                                    void* stream) {
     if (!page_pool || !slot_mapping || !out_key || !out_value || !layout || !cfg) return -1;
-    return guarded([&] {
+    return guarded_sync(stream, [&] {
         const tq::PageGeom g = tq::prod_geom(*cfg, *layout);
         check_grid(num_tokens, "turbo_prod_dequant_kv_kernel", true);
         check_rows(num_tokens, g.H, "turbo_prod_dequant_kv_hnd");
@@ -536,7 +579,7 @@ extern "C" int tq_load_turbo_prod_layers(const uint8_t* const* host_pools,
     if (!host_pools || !device_pools || !slot_mapping || !out_key || !out_value || !layout ||
         !cfg)
         return -1;
-    return guarded([&] {
+    return guarded_sync(compute_stream, [&] {
         const tq::PageGeom g = tq::prod_geom(*cfg, *layout);
         if (num_layers < 0 || num_tokens < 0)
             throw tq::Error("turbo_prod load: num_layers and num_tokens must be >= 0");
@@ -558,7 +601,7 @@ int dequant_layers(tq::Scheme scheme, const uint8_t* const* page_pools,
     if (!page_pools || !slot_mapping || !out_keys || !out_values || !layout || !cfg) return -1;
     const bool prod = scheme == tq::Scheme::Prod;
     const char* name = prod ? "turbo_prod_dequant_kv_layers" : "turbo_mse_dequant_kv_layers";
-    return guarded([&] {
+    return guarded_sync(stream, [&] {
         const tq::PageGeom g =
             prod ? tq::prod_geom(*cfg, *reinterpret_cast<const TQTurboProdPageLayout*>(layout))
                  : tq::mse_geom(*cfg, *reinterpret_cast<const TQTurbomsePageLayout*>(layout));
@@ -600,7 +643,7 @@ extern "C" int tq_launch_turbo_mse_pack_kv(const uint16_t* key, const uint16_t* 
                                            const TQTurbomsePageLayout* layout,
                                            const TQConfig* cfg, int num_tokens, void* stream) {
     if (!key || !value || !slot_mapping || !page_pool || !layout || !cfg) return -1;
-    return guarded([&] {
+    return guarded_sync(stream, [&] {
         const tq::PageGeom g = tq::mse_geom(*cfg, *layout);
         check_grid(num_tokens, "turbo_mse_pack_kv_kernel", false);
         check_rows(num_tokens, g.H, "turbo_mse_pack_kv");
@@ -615,7 +658,7 @@ extern "C" int tq_launch_turbo_mse_dequant_kv(const uint8_t* page_pool,
                                               const TQTurbomsePageLayout* layout,
                                               const TQConfig* cfg, int num_tokens, void* stream) {
     if (!page_pool || !slot_mapping || !out_key || !out_value || !layout || !cfg) return -1;
-    return guarded([&] {
+    return guarded_sync(stream, [&] {
         const tq::PageGeom g = tq::mse_geom(*cfg, *layout);
         check_grid(num_tokens, "turbo_mse_dequant_kv_kernel", false);
         check_rows(num_tokens, g.H, "turbo_mse_dequant_kv");
@@ -629,7 +672,7 @@ extern "C" int tq_launch_turbo_mse_fused_attention_output(
     uint16_t* output, const TQTurbomsePageLayout* layout, const TQConfig* cfg, int num_queries,
     int num_kv_tokens, void* stream) {
     if (!query || !page_pool || !slot_mapping || !output || !layout || !cfg) return -1;
-    return guarded([&] {
+    return guarded_sync(stream, [&] {
         const tq::PageGeom g = tq::mse_geom(*cfg, *layout);
         check_grid(num_queries, "turbo_mse_fused_attn_online_kernel", false);
         if (num_kv_tokens < 0) throw tq::Error("turbo_mse attention: num_kv_tokens < 0");
@@ -645,7 +688,7 @@ extern "C" int tq_launch_turbo_mse_dequant_kv_hnd(const uint8_t* page_pool,
                                                   const TQConfig* cfg, int num_tokens,
                                                   void* stream) {
     if (!page_pool || !slot_mapping || !out_key || !out_value || !layout || !cfg) return -1;
-    return guarded([&] {
+    return guarded_sync(stream, [&] {
         const tq::PageGeom g = tq::mse_geom(*cfg, *layout);
         check_grid(num_tokens, "turbo_mse_dequant_kv_kernel", false);
         check_rows(num_tokens, g.H, "turbo_mse_dequant_kv_hnd");
@@ -664,7 +707,7 @@ extern "C" int tq_load_turbo_mse_layers(const uint8_t* const* host_pools,
     if (!host_pools || !device_pools || !slot_mapping || !out_key || !out_value || !layout ||
         !cfg)
         return -1;
-    return guarded([&] {
+    return guarded_sync(compute_stream, [&] {
         const tq::PageGeom g = tq::mse_geom(*cfg, *layout);
         if (num_layers < 0 || num_tokens < 0)
             throw tq::Error("turbo_mse load: num_layers and num_tokens must be >= 0");
@@ -689,7 +732,7 @@ int paged_attention(tq::Scheme scheme, const uint16_t* query, const uint8_t* pag
     if (!query || !page_pool || !block_tables || !row_seq || !row_kv_len || !output || !layout ||
         !cfg)
         return -1;
-    return guarded([&] {
+    return guarded_sync(stream, [&] {
         const bool prod = scheme == tq::Scheme::Prod;
         const tq::PageGeom g = prod ? tq::prod_geom(*cfg, *reinterpret_cast<const TQTurboProdPageLayout*>(layout))
                                     : tq::mse_geom(*cfg, *reinterpret_cast<const TQTurbomsePageLayout*>(layout));
@@ -748,7 +791,7 @@ extern "C" int tq_launch_qjl_pack_kv(const uint16_t* key, const uint16_t* value,
                                      const TQQJLPageLayout* layout, const TQConfig* cfg,
                                      int num_tokens, void* stream) {
     if (!key || !value || !slot_mapping || !page_pool || !layout || !cfg) return -1;
-    return guarded([&] {
+    return guarded_sync(stream, [&] {
         const tq::QjlGeom g = tq::qjl_geom(*cfg, *layout);
         check_count(num_tokens, "qjl_pack_kv");
         need_aligned4(key, "qjl_pack_kv key");
@@ -763,7 +806,7 @@ extern "C" int tq_launch_qjl_dequant_kv(const uint8_t* page_pool, const int32_t*
                                         const TQQJLPageLayout* layout, const TQConfig* cfg,
                                         int num_tokens, void* stream) {
     if (!page_pool || !slot_mapping || !out_key || !out_value || !layout || !cfg) return -1;
-    return guarded([&] {
+    return guarded_sync(stream, [&] {
         const tq::QjlGeom g = tq::qjl_geom(*cfg, *layout);
         check_count(num_tokens, "qjl_dequant_kv");
         need_aligned4(out_key, "qjl_dequant_kv out_key");
@@ -780,7 +823,7 @@ extern "C" int tq_launch_qjl_fused_attention_output(const uint16_t* query,
                                                     const TQConfig* cfg, int num_queries,
                                                     int num_kv_tokens, void* stream) {
     if (!query || !page_pool || !slot_mapping || !output || !layout || !cfg) return -1;
-    return guarded([&] {
+    return guarded_sync(stream, [&] {
         const tq::QjlGeom g = tq::qjl_geom(*cfg, *layout);
         check_count(num_queries, "qjl_fused_attention_output");
         check_count(num_kv_tokens, "qjl_fused_attention_output");
@@ -801,7 +844,7 @@ extern "C" int tq_launch_int4_pack_kv(const uint16_t* key, const uint16_t* value
                                       const TQPageLayout* layout, const TQConfig* cfg,
                                       int num_tokens, void* stream) {
     if (!key || !value || !slot_mapping || !page_pool || !layout || !cfg) return -1;
-    return guarded([&] {
+    return guarded_sync(stream, [&] {
         const tq::Int4Geom g = tq::int4_geom(*cfg, *layout);
         check_count(num_tokens, "int4_pack_kv");
         need_aligned4(key, "int4_pack_kv key");
@@ -816,7 +859,7 @@ extern "C" int tq_launch_int4_dequant_kv(const uint8_t* page_pool, const int32_t
                                          const TQPageLayout* layout, const TQConfig* cfg,
                                          int num_tokens, void* stream) {
     if (!page_pool || !slot_mapping || !out_key || !out_value || !layout || !cfg) return -1;
-    return guarded([&] {
+    return guarded_sync(stream, [&] {
         const tq::Int4Geom g = tq::int4_geom(*cfg, *layout);
         check_count(num_tokens, "int4_dequant_kv");
         need_aligned4(out_key, "int4_dequant_kv out_key");
@@ -837,7 +880,7 @@ extern "C" int tq_launch_dense_store_kv(const uint16_t* key, const uint16_t* val
                                         const TQDensePageLayout* layout, const TQConfig* cfg,
                                         int num_tokens, void* stream) {
     if (!key || !value || !slot_mapping || !page_pool || !layout || !cfg) return -1;
-    return guarded([&] {
+    return guarded_sync(stream, [&] {
         const tq::DenseGeom g = tq::dense_geom(*cfg, *layout);
         check_count(num_tokens, "dense_store_kv");
         need_aligned4(key, "dense_store_kv key");
@@ -853,7 +896,7 @@ extern "C" int tq_launch_dense_load_kv(const uint8_t* page_pool, const int32_t* 
                                        const TQDensePageLayout* layout, const TQConfig* cfg,
                                        int num_tokens, void* stream) {
     if (!page_pool || !slot_mapping || !out_key || !out_value || !layout || !cfg) return -1;
-    return guarded([&] {
+    return guarded_sync(stream, [&] {
         const tq::DenseGeom g = tq::dense_geom(*cfg, *layout);
         check_count(num_tokens, "dense_load_kv");
         need_aligned4(out_key, "dense_load_kv out_key");
@@ -870,7 +913,7 @@ extern "C" int tq_launch_attention_ref(const uint16_t* query, const uint16_t* ke
                                        float* logit_scratch, const TQConfig* cfg,
                                        int num_queries, int num_kv_tokens, void* stream) {
     if (!query || !key || !value || !output || !logit_scratch || !cfg) return -1;
-    return guarded([&] {
+    return guarded_sync(stream, [&] {
         // tq_attention_ref_kernel.cu:127-128
         if (cfg->head_dim > 128)
             throw tq::Error("attention_ref_gpu: head_dim > 128 is not supported");

@@ -23,6 +23,12 @@ struct Error : std::runtime_error {
 // Stores msg in the calling thread's tq_last_error() buffer.
 void set_last_error(const char* msg);
 
+// Debug-sync mode (-DTQ_DEBUG_SYNC or the TQ_DEBUG_SYNC environment
+// variable): synchronizes `stream` (a hipStream_t) after a launch and throws
+// "async kernel error: ..." if its kernels failed; no-op otherwise, and while
+// the stream is being captured.
+void debug_sync(void* stream);
+
 // Byte geometry of one page, resolved from a TQTurboProdPageLayout or a
 // TQTurbomsePageLayout.  Passed to kernels by value.
 //   cell c = tib * H + h;  K codes at kc_off + c*code_stride, V codes at

@@ -68,6 +68,7 @@ extern "C" int tq_launch_turbo_prod_fused_attention_output_noalloc(
         s.cap = kScratchBytes;
         tq::launch_attention(tq::Scheme::Prod, query, page_pool, slot_mapping, output, g,
                              num_queries, num_kv_tokens, static_cast<hipStream_t>(stream), s);
+        tq::debug_sync(stream);
         return 0;
     } catch (const std::exception& e) {
         tq::set_last_error(e.what());
