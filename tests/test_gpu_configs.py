@@ -162,6 +162,31 @@ def test_attention_d128_shapes(tq, oracle, cuda, scheme, Q, H, N, seed):
     assert err < ATT_TOL
 
 
+def test_attention_more_row_groups_than_a_grid_dimension(tq, oracle, cuda):
+    """65,537 row groups of one kv head: more than a grid's y/z dimension
+    holds, so the split launch falls back to its one-dimensional grid.
+    Sampled rows (the first and the last row group included) against the
+    fp64 oracle."""
+    Q, H, D, B, N = 65537 * 8, 1, 128, 16, 40
+    print(f"[attention 1-D grid] Q={Q} H={H} N={N}", flush=True)
+    k, v = kv_tokens_major(N, H, D, seed=46)
+    slots = permuted_slots(N, B, seed=47)
+    pages = int(slots.max()) // B + 1
+    pool_np = oracle.prod_pack(as_u16(k), as_u16(v), slots.numpy(), pages, B)
+    q = torch.from_numpy(np.random.default_rng(48).standard_normal((Q, H, D)).astype(np.float16))
+    cfg, lp, _ = _cfg(tq, H, D, B)
+    out = torch.zeros(Q, H, D, dtype=torch.float16, device=cuda)
+    tq.fused_attn_output(q.to(cuda), torch.from_numpy(pool_np).to(cuda), slots.to(cuda), out, lp,
+                         cfg, Q, N)
+    torch.cuda.synchronize()
+    rows = np.concatenate([np.arange(16), np.arange(Q - 16, Q),
+                           np.random.default_rng(49).choice(Q, size=64, replace=False)])
+    ref = oracle.prod_attention_f64(as_u16(q)[rows].copy(), pool_np, slots.numpy(), B)
+    err = _rel_err(out.cpu().float().numpy()[rows], ref)
+    print(f"    {rows.size} sampled rows, rel err {err:.3e}", flush=True)
+    assert err < ATT_TOL
+
+
 # ── the attention workspace ──────────────────────────────────────────── #
 
 def _att_case(oracle, N, seed, H=2, D=128, B=16, Q=8):

@@ -559,6 +559,15 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
         // Every wave replicates staged rows with conflict-free 1 KB stores.
         {
             constexpr int kRowsPerWave = 256 / kWaves;
+            // (all staged words read before the first store: one LDS round trip)
+            uint32_t stv[kRowsPerWave / 4];
+            if constexpr (!QJL) {
+#pragma unroll
+                for (int k = 0; k < kRowsPerWave; k += 4) {
+                    const int e = w * kRowsPerWave + k + (lane >> 4);
+                    stv[k / 4] = (lane & 8) ? vstage[e] : kstage[e];  // words 32..63: V
+                }
+            }
 #pragma unroll
             for (int k = 0; k < kRowsPerWave; k += 4) {
                 const int e = w * kRowsPerWave + k + (lane >> 4);
@@ -577,7 +586,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                     }
                     *reinterpret_cast<uint4*>(&lut[e][4 * (lane & 15)]) = v4;
                 } else {
-                    const uint32_t v = (lane & 8) ? vstage[e] : kstage[e];  // words 32..63: V
+                    const uint32_t v = stv[k / 4];
                     *reinterpret_cast<uint4*>(&lut[e][4 * (lane & 15)]) = make_uint4(v, v, v, v);
                 }
             }
@@ -1183,9 +1192,23 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
             }
         }
     } else {
-        const int split = blockIdx.x % num_splits, hr = blockIdx.x / num_splits;
+        // Grid (split, kv head, row group), or one dimension of splits x heads
+        // when there are more row groups than a grid dimension holds (the
+        // first form needs no divisions before the first loads).
+        int split, h, rg;
+        if (gridDim.x == (unsigned)num_splits) {
+            split = blockIdx.x;
+            h = blockIdx.y;
+            rg = blockIdx.z;
+        } else {
+            split = blockIdx.x % num_splits;
+            const int hr = blockIdx.x / num_splits;
+            h = hr % g.H;
+            rg = hr / g.H;
+        }
         const int t_begin = split * tokens_per_split;
-        item(threadIdx.x, hr % g.H, hr / g.H, 1, t_begin, t_begin + tokens_per_split, blockIdx.x);
+        item(threadIdx.x, h, rg, 1, t_begin, t_begin + tokens_per_split,
+             ((size_t)rg * g.H + h) * num_splits + split);
     }
 }
 // Sum of the split partials of one output row (q, h): o = sum_s 2^(m_s - M)
@@ -1563,9 +1586,13 @@ void launch_mfma_attention(const uint16_t* query, const uint8_t* pool, const int
         check_launch(combine_name);
         return;
     }
-    hipLaunchKernelGGL((attn_mfma_split_kernel<SCH, kCH, kNW, false>), dim3(blocks),
-                       dim3(64 * kNW), 0, stream, query, pool, slots, ws, g, num_queries,
-                       num_kv_tokens, tps, splits, inv, none);
+    constexpr int kMaxGridYZ = 65535;
+    const dim3 grid = row_groups <= kMaxGridYZ && g.H <= kMaxGridYZ
+                          ? dim3(splits, g.H, row_groups)
+                          : dim3((unsigned)blocks);
+    hipLaunchKernelGGL((attn_mfma_split_kernel<SCH, kCH, kNW, false>), grid, dim3(64 * kNW), 0,
+                       stream, query, pool, slots, ws, g, num_queries, num_kv_tokens, tps, splits,
+                       inv, none);
     check_launch(split_name);
     if (splits <= kItemCombineMaxSplits)
         hipLaunchKernelGGL(attn_mfma_combine_items_kernel, dim3(heads), dim3(256), 0, stream,
