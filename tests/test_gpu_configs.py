@@ -185,6 +185,12 @@ def test_attention_more_row_groups_than_a_grid_dimension(tq, oracle, cuda):
     err = _rel_err(out.cpu().float().numpy()[rows], ref)
     print(f"    {rows.size} sampled rows, rel err {err:.3e}", flush=True)
     assert err < ATT_TOL
+    # No kv tokens: the combine alone writes zeros, on its one-dimensional grid.
+    out.fill_(1.0)
+    tq.fused_attn_output(q.to(cuda), torch.from_numpy(pool_np).to(cuda), slots.to(cuda), out, lp,
+                         cfg, Q, 0)
+    torch.cuda.synchronize()
+    assert int(torch.count_nonzero(out)) == 0
 
 
 # ── the attention workspace ──────────────────────────────────────────── #

@@ -351,8 +351,8 @@ __device__ __forceinline__ uint32_t lo_pair(float x0, float x1, uint32_t h) {
 template <int SCH, int CH, int NW, bool PAGED, int NP = 1>
 __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     const uint16_t* __restrict__ query, const uint8_t* __restrict__ pool,
-    const int32_t* __restrict__ slots, float* __restrict__ ws, PageGeom g, int num_queries,
-    int num_kv_tokens, int tokens_per_split, int num_splits, float inv, mfma::PagedRows pr) {
+    const int32_t* __restrict__ slots, float* __restrict__ ws, float inv, int num_queries,
+    int num_kv_tokens, int tokens_per_split, int num_splits, PageGeom g, mfma::PagedRows pr) {
     using namespace mfma;
     constexpr int kChunk = CH, kWaves = NW;
     constexpr int kTiles = CH / 16, kSteps = CH / 32;
@@ -1112,7 +1112,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                 float L = 0.f, o0 = 0.f, o1 = 0.f;
 #pragma unroll
                 for (int u = 0; u < kWaves; ++u) {
-                    const float wt = exp2f(mm[u][r] - M);
+                    const float wt = __builtin_amdgcn_exp2f(mm[u][r] - M);  // (argument <= 0)
                     L += ml[u][r] * wt;
                     o0 += mo[u][rr][2 * lane] * wt;
                     o1 += mo[u][rr][2 * lane + 1] * wt;
@@ -1120,7 +1120,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                 if (NP >= 2 && npos == 1) {  // one position: + its lo columns 8-15
 #pragma unroll
                     for (int u = 0; u < kWaves; ++u) {
-                        const float wt = exp2f(mm[u][r] - M);
+                        const float wt = __builtin_amdgcn_exp2f(mm[u][r] - M);  // (argument <= 0)
                         o0 += mo[u][rr + kRows][2 * lane] * wt;
                         o1 += mo[u][rr + kRows][2 * lane + 1] * wt;
                     }
@@ -1223,8 +1223,20 @@ __global__ __launch_bounds__(256) void attn_mfma_combine_kernel(const float* __r
     constexpr int kBatch = 16;
     __shared__ float red_m[8], red_l[8];
     __shared__ float red_o[8][33];
-    const int row = blockIdx.x >> 2, dq = blockIdx.x & 3;  // row = q * H + h
-    const int q = row / H, h = row - q * H;
+    // Grid (slice, kv head, query), or one dimension of 4 x rows when there
+    // are more queries than a grid dimension holds; row = q * H + h.
+    int dq, h, q;
+    if (gridDim.x == 4) {
+        dq = blockIdx.x;
+        h = blockIdx.y;
+        q = blockIdx.z;
+    } else {
+        dq = blockIdx.x & 3;
+        const int rw = blockIdx.x >> 2;
+        q = rw / H;
+        h = rw - q * H;
+    }
+    const int row = q * H + h;
     const int rg = q / kRows, r = q % kRows;
     const int t = threadIdx.x, dd = t & 31, sg = t >> 5;
     const int d = 32 * dq + dd;
@@ -1239,19 +1251,22 @@ __global__ __launch_bounds__(256) void attn_mfma_combine_kernel(const float* __r
         for (int k = 0; k < kBatch; ++k) {
             const int s = base + 8 * k;
             const float* p = part(s < S ? s : base);
-            pm[k] = s < S ? p[128] : kInitMax;
-            pl[k] = p[129];
+            const float2 ml2 = *reinterpret_cast<const float2*>(p + 128);  // (m, l)
+            pm[k] = s < S ? ml2.x : kInitMax;
+            pl[k] = ml2.y;
             po[k] = p[d];
         }
         float mb = M;
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) mb = fmaxf(mb, pm[k]);
-        const float sc = exp2f(M - mb);
+        // v_exp_f32 without denormal handling: arguments are <= 0 and a weight
+        // below 2^-126 of the largest is negligible.
+        const float sc = __builtin_amdgcn_exp2f(M - mb);
         L *= sc;
         acc *= sc;
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
-            const float wt = exp2f(pm[k] - mb);
+            const float wt = __builtin_amdgcn_exp2f(pm[k] - mb);
             L += pl[k] * wt;
             acc += po[k] * wt;
         }
@@ -1270,7 +1285,7 @@ __global__ __launch_bounds__(256) void attn_mfma_combine_kernel(const float* __r
         float Lt = 0.f, o = 0.f;
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-            const float wt = exp2f(red_m[u] - Mx);
+            const float wt = __builtin_amdgcn_exp2f(red_m[u] - Mx);
             Lt += red_l[u] * wt;
             o += red_o[u][t] * wt;
         }
@@ -1308,7 +1323,7 @@ __global__ __launch_bounds__(256) void attn_mfma_combine_items_kernel(
         float mb = M;
 #pragma unroll
         for (int k = 0; k < 8; ++k) mb = fmaxf(mb, pm[k]);
-        const float sc = exp2f(M - mb);
+        const float sc = __builtin_amdgcn_exp2f(M - mb);  // (argument <= 0)
         L *= sc;
         acc.x *= sc;
         acc.y *= sc;
@@ -1316,7 +1331,7 @@ __global__ __launch_bounds__(256) void attn_mfma_combine_items_kernel(
         acc.w *= sc;
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-            const float wt = exp2f(pm[k] - mb);
+            const float wt = __builtin_amdgcn_exp2f(pm[k] - mb);
             L += pl[k] * wt;
             acc.x += po[k].x * wt;
             acc.y += po[k].y * wt;
@@ -1382,7 +1397,7 @@ __global__ __launch_bounds__(256) void attn_paged_combine_kernel(
         float mb = M;
 #pragma unroll
         for (int k = 0; k < 8; ++k) mb = fmaxf(mb, pm[k]);
-        const float sc = exp2f(M - mb);
+        const float sc = __builtin_amdgcn_exp2f(M - mb);  // (argument <= 0)
         L *= sc;
         acc.x *= sc;
         acc.y *= sc;
@@ -1390,7 +1405,7 @@ __global__ __launch_bounds__(256) void attn_paged_combine_kernel(
         acc.w *= sc;
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-            const float wt = exp2f(pm[k] - mb);
+            const float wt = __builtin_amdgcn_exp2f(pm[k] - mb);
             L += pl[k] * wt;
             acc.x += po[k].x * wt;
             acc.y += po[k].y * wt;
@@ -1580,25 +1595,28 @@ void launch_mfma_attention(const uint16_t* query, const uint8_t* pool, const int
         scratch.get(stream, blocks * kRows * kPartStride * sizeof(float), split_name));
     constexpr int kCH = kSplitChunk, kNW = kSplitWaves;
     const PagedRows none{};
+    constexpr int kMaxGridYZ = 65535;
+    const dim3 combine_grid = num_queries <= kMaxGridYZ && g.H <= kMaxGridYZ
+                                  ? dim3(4, g.H, num_queries)
+                                  : dim3(4 * rows);
     if (num_kv_tokens == 0) {  // no partials: the combine writes the zero output
-        hipLaunchKernelGGL(attn_mfma_combine_kernel, dim3(4 * rows), dim3(256), 0, stream, ws,
+        hipLaunchKernelGGL(attn_mfma_combine_kernel, combine_grid, dim3(256), 0, stream, ws,
                            output, g.H, 0);
         check_launch(combine_name);
         return;
     }
-    constexpr int kMaxGridYZ = 65535;
     const dim3 grid = row_groups <= kMaxGridYZ && g.H <= kMaxGridYZ
                           ? dim3(splits, g.H, row_groups)
                           : dim3((unsigned)blocks);
     hipLaunchKernelGGL((attn_mfma_split_kernel<SCH, kCH, kNW, false>), grid, dim3(64 * kNW), 0,
-                       stream, query, pool, slots, ws, g, num_queries, num_kv_tokens, tps, splits,
-                       inv, none);
+                       stream, query, pool, slots, ws, inv, num_queries, num_kv_tokens, tps, splits,
+                       g, none);
     check_launch(split_name);
     if (splits <= kItemCombineMaxSplits)
         hipLaunchKernelGGL(attn_mfma_combine_items_kernel, dim3(heads), dim3(256), 0, stream,
                            ws, output, g.H, splits, num_queries);
     else
-        hipLaunchKernelGGL(attn_mfma_combine_kernel, dim3(4 * rows), dim3(256), 0, stream, ws,
+        hipLaunchKernelGGL(attn_mfma_combine_kernel, combine_grid, dim3(256), 0, stream, ws,
                            output, g.H, splits);
     check_launch(combine_name);
 }
@@ -1693,12 +1711,12 @@ void launch_paged_attention(Scheme s, const uint16_t* query, const uint8_t* pool
     if (max_kv_len > 0) {
         if (prod)
             hipLaunchKernelGGL((attn_mfma_split_kernel<kSchProd, kCH, kNW, true, kPagedPositions>),
-                               dim3(G), dim3(64 * kNW), 0, stream, query, pool, nullptr, ws, g,
-                               num_rows, max_kv_len, 0, 0, inv, pr);
+                               dim3(G), dim3(64 * kNW), 0, stream, query, pool, nullptr, ws, inv,
+                               num_rows, max_kv_len, 0, 0, g, pr);
         else
             hipLaunchKernelGGL((attn_mfma_split_kernel<kSchMse, kCH, kNW, true, kPagedPositions>),
-                               dim3(G), dim3(64 * kNW), 0, stream, query, pool, nullptr, ws, g,
-                               num_rows, max_kv_len, 0, 0, inv, pr);
+                               dim3(G), dim3(64 * kNW), 0, stream, query, pool, nullptr, ws, inv,
+                               num_rows, max_kv_len, 0, 0, g, pr);
         check_launch(prod ? "turbo_prod_paged_attn_split" : "turbo_mse_paged_attn_split");
     }
     hipLaunchKernelGGL(attn_paged_combine_kernel, dim3(heads), dim3(256), 0, stream, ws, output,
