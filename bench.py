@@ -60,16 +60,11 @@ def kernel_traffic(name: str):
 
 
 def gpu_kv(N, H, D, seed, dev):
-    """Seeded N(0,1) K/V with the synthetic outlier channels, made on the GPU."""
-    import torch
-    from turborag_amd.synthetic import OUTLIER_SCALE, outlier_channels
-    g = torch.Generator(device=dev).manual_seed(seed)
-    k = torch.randn(N, H, D, generator=g, device=dev)
-    v = torch.randn(N, H, D, generator=g, device=dev)
-    for h, ch in enumerate(outlier_channels(H, D)):
-        k[:, h, ch] *= OUTLIER_SCALE
-        v[:, h, ch] *= OUTLIER_SCALE
-    return k.half(), v.half()
+    """Seeded K/V of the synthetic spec (splitmix64, Box-Muller, outlier
+    channels; turborag_amd/synthetic.py), drawn on the host, on the GPU."""
+    from turborag_amd.synthetic import kv_tokens_major
+    k, v = kv_tokens_major(N, H, D, seed=seed)
+    return k.to(dev), v.to(dev)
 
 
 class Workload:
@@ -356,6 +351,10 @@ def main() -> int:
         log(f"[bench] batched decode {sch}: {b_['sequences']} sequences, {b_['rows']} rows: "
             f"append {b_['append_us']:.1f} us + attention {b_['attention_us']:.1f} us")
 
+    floor = measure_graph_floor(w)
+    log(f"[bench] graph floor: {floor['one_kernel_us']:.2f} us per small kernel, "
+        f"{floor['two_dependent_kernels_us']:.2f} us per dependent pair")
+
     single = measure_single_query(w)
     log(f"[bench] single-query decode @32K: {single['us_per_layer']:.2f} us/layer")
 
@@ -416,6 +415,8 @@ def main() -> int:
             "achieved_GBps": round(att_gbps, 1),
             "frac_hbm": round(att_gbps / HBM_PEAK_GBPS, 4),
             "algorithmic_bytes": w.att_bytes,
+            "kernels_per_layer": 2,
+            "graph_floor": floor,
         },
         "loader": loader,
         "store": store,
@@ -763,6 +764,36 @@ def measure_single_query(w: Workload, reps: int = 5) -> dict:
             "path": "matrix-core split kernel (one row per kv head in an 8-row group)"}
 
 
+def measure_graph_floor(w: Workload, reps: int = 10) -> dict:
+    """What a graph-replayed layer costs before any attention work: 36 nodes
+    of one small kernel (a 1 MB fill, the size of the split-K partials), and
+    36 pairs of dependent small kernels (the fill, then a 16 KB read of what
+    it wrote: the split/combine pair with trivial bodies), in µs per node and
+    per pair."""
+    import torch
+    buf = torch.empty(1 << 18, dtype=torch.float32, device=w.dev)
+    out = torch.empty(1 << 12, dtype=torch.float32, device=w.dev)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+
+    def one():
+        for _ in range(w.NL):
+            buf.fill_(1.0)
+
+    def pair():
+        for _ in range(w.NL):
+            buf.fill_(1.0)
+            out.copy_(buf[: out.numel()])
+    res = {}
+    for name, fn in (("one_kernel_us", one), ("two_dependent_kernels_us", pair)):
+        with torch.cuda.stream(side):
+            fn()
+        torch.cuda.synchronize()
+        g = capture(fn, side)
+        res[name] = round(event_time_us(g.replay if g is not None else fn, reps) / w.NL, 3)
+    return res
+
+
 def batched_setup(w: Workload, scheme: str = "turbo_prod") -> dict:
     """The batch of the batched-decode step: 32 sequences, lengths
     U[1024, 32768] (seed 500), 1-8 new tokens each (seed 501), appended."""
@@ -770,8 +801,9 @@ def batched_setup(w: Workload, scheme: str = "turbo_prod") -> dict:
     import torch
 
     from turborag_amd.batched import PagedBatch
-    lens = np.random.default_rng(500).integers(1024, 32769, size=32)
-    widths = np.random.default_rng(501).integers(1, 9, size=32)
+    from turborag_amd.synthetic import uniform_ints
+    lens = uniform_ints(500, 32, 1024, 32768)
+    widths = uniform_ints(501, 32, 1, 8)
     b = PagedBatch(w.tq, scheme, lens, widths, seed=500, device=w.dev)
     b.append_new_tokens(seed=503)
     query, row_seq, row_len = b.decode_rows(seed=504)

@@ -25,6 +25,11 @@ they pin the oracle against regressions and give the GPU tests fixed data):
       (turbo_prod), attention in fp64 and with the reference kernel's fp32
       algorithm.
 
+Generator records:
+  synthetic_sha256.json      SHA-256 of the synthetic-input spec's tensors
+                             (tests/test_synthetic.py: spec_inputs), so a
+                             change of the generator or of numpy's math shows.
+
 Usage: python tests/golden/make_fixtures.py
 """
 from __future__ import annotations
@@ -86,6 +91,16 @@ def oracle_fixtures() -> None:
     print("wrote prod_n37_h2_d128.npz, mse_n37_h2_d128.npz")
 
 
+def synthetic_records() -> None:
+    import json
+    sys.path.insert(0, str(HERE.parent))
+    from test_synthetic import _sha, spec_inputs
+    rec = {name: _sha(a) for name, a in spec_inputs().items()}
+    (HERE / "synthetic_sha256.json").write_text(json.dumps(rec, indent=1) + "\n")
+    print("wrote synthetic_sha256.json")
+
+
 if __name__ == "__main__":
     reference_outputs()
     oracle_fixtures()
+    synthetic_records()

@@ -22,7 +22,8 @@ import pytest
 import torch
 
 from turborag_amd.batched import PagedBatch
-from turborag_amd.synthetic import as_u16, gqa_rows, kv_tokens_major, permuted_slots, query
+from turborag_amd.synthetic import (as_u16, gqa_rows, kv_tokens_major, permuted_slots, query,
+                                    uniform_ints)
 
 pytestmark = pytest.mark.gpu
 ATT_TOL = 1e-3
@@ -44,8 +45,8 @@ def _cfg(tq, H, D, B=16):
 
 @pytest.mark.parametrize("scheme", ["turbo_prod", "turbo_mse"])
 def test_config5_batched_step_full_shape(tq, oracle, cuda, scheme):
-    lens = np.random.default_rng(500).integers(1024, 32769, size=32)
-    widths = np.random.default_rng(501).integers(1, 9, size=32)
+    lens = uniform_ints(500, 32, 1024, 32768)
+    widths = uniform_ints(501, 32, 1, 8)
     print(f"[config 5 {scheme}] {int(lens.sum())} prefill tokens, {int(widths.sum())} new",
           flush=True)
     oracle.nthreads = 16

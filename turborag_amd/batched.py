@@ -19,7 +19,8 @@ from __future__ import annotations
 import numpy as np
 import torch
 
-from turborag_amd.synthetic import gqa_rows, kv_tokens_major
+from turborag_amd.synthetic import fisher_yates, gqa_rows, kv_tokens_major
+from turborag_amd.synthetic import query as draw_query
 from turborag_amd.turboquant_wrapper import BlockTable, PageAllocator, TurboQuantWrapper
 
 
@@ -66,13 +67,12 @@ class PagedBatch:
     def _prefill(self) -> None:
         """Every sequence's first L_s tokens, appended one page at a time in a
         seeded random order of sequences (scattered pages)."""
-        rng = np.random.default_rng(self.seed + 2)
         self.kv = [kv_tokens_major(L, self.H, self.D, seed=self.seed + 3 + s)
                    for s, L in enumerate(self.lens)]
-        todo = []
+        pages = []
         for s, L in enumerate(self.lens):
-            todo += [s] * ((L + self.B - 1) // self.B)
-        rng.shuffle(todo)
+            pages += [s] * ((L + self.B - 1) // self.B)
+        todo = [pages[i] for i in fisher_yates(len(pages), self.seed + 2)]
         done = [0] * self.S
         keys, vals, slots = [], [], []
         for s in todo:
@@ -117,8 +117,7 @@ class PagedBatch:
         q, row_seq, row_len = [], [], []
         for s, (L, w) in enumerate(zip(self.lens, self.widths)):
             for j in range(w):
-                g = torch.Generator().manual_seed(seed + 1000 * s + j)
-                qh = torch.randn(self.group * self.H, self.D, generator=g).half()
+                qh = draw_query(self.group * self.H, self.D, seed=seed + 1000 * s + j)
                 q.append(gqa_rows(qh, self.H))
                 row_seq += [s] * self.group
                 row_len += [L + j + 1] * self.group
