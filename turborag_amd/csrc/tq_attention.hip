@@ -265,8 +265,8 @@ __device__ __forceinline__ half8 as_h8(uint32_t a, uint32_t b, uint32_t c, uint3
 // sequence from row group `first` on, computed together.  It has one item
 // per kv head; each item is n passes (workgroup-wide chunk steps of kPass
 // tokens) over the unit's first kv_end tokens, a pass weighing w work units,
-// and item h takes work positions [start + h*w*n, start + (h+1)*w*n) of the
-// step's total work.
+// at work positions [start, start + w*n) of its head's work (every head has
+// the same work, split into segments per head).
 struct PagedUnit {
     int32_t first, npos, kv_end, start, n, w, index, pad;  // index: the unit's number
 };
@@ -1138,17 +1138,22 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     };  // item
 
     if constexpr (PAGED) {
-        // This workgroup's segment of the step's work.  Workgroup b runs on
-        // XCD b % 8 and the segments of one XCD are consecutive, so the items
-        // that read the same pages (the heads and positions of a sequence)
-        // mostly share an L2.
+        // Every kv head has the same work (the units' passes over their kv
+        // lengths), split into Gh = G / H segments; workgroup b takes head
+        // b / Gh and segment seg(b % Gh) of it.  Gh is a multiple of 8 and
+        // workgroup b runs on XCD b % 8, so the H workgroups of one segment
+        // share an XCD and walk the same tokens at the same time: the heads
+        // of a token share its cache lines (cell tib * H + h), and the second
+        // reader finds them in that XCD's L2.  The segments of one XCD are
+        // consecutive, so the units of a sequence mostly share it too.
         constexpr int kPass = kChunk * kWaves;
-        const int G = gridDim.x;
-        const int seg = (G & 7) == 0 ? (int)(blockIdx.x & 7) * (G >> 3) + (int)(blockIdx.x >> 3)
-                                     : (int)blockIdx.x;
+        const int Gh = (int)gridDim.x / g.H;
+        const int hh = (int)blockIdx.x / Gh;
+        const int bl = (int)blockIdx.x - hh * Gh;
+        const int seg = (bl & 7) * (Gh >> 3) + (bl >> 3);
         const int nu = __builtin_amdgcn_readfirstlane(pr.plan[0]);
         const int total = __builtin_amdgcn_readfirstlane(pr.plan[1]);
-        const Segments sg(total, G);
+        const Segments sg(total, Gh);
         const int b0 = sg.bound(seg), b1 = sg.bound(seg + 1);
         if (b0 >= b1) return;  // an empty segment (less work than workgroups)
         // The unit holding work position b0 (exactly one: the units' work
@@ -1157,38 +1162,28 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
         for (int u = threadIdx.x; u < nu; u += 64 * kWaves)
             if (pr.units[u].start <= b0 && b0 < pr.units[u + 1].start) s_unit = u;
         __syncthreads();
-        // The walk over the items overlapping the segment, in work order.  Its
-        // position (unit, head) lives in LDS (one copy per wave, volatile
-        // accesses), so no walk state is held in registers across an item.
-        __shared__ int s_walk[kWaves][2];
+        // The walk over the units overlapping the segment, in work order.  Its
+        // position lives in LDS (one copy per wave, volatile accesses), so no
+        // walk state is held in registers across an item.
+        __shared__ int s_walk[kWaves];
         const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-        volatile int* walk = s_walk[wv];
-        {
-            const int u = __builtin_amdgcn_readfirstlane(s_unit);
-            const PagedUnit un = pr.units[u];
-            if ((threadIdx.x & 63) == 0) {
-                walk[0] = u;
-                walk[1] = (b0 - un.start) / (un.w * un.n);
-            }
-        }
+        volatile int* walk = &s_walk[wv];
+        if ((threadIdx.x & 63) == 0) walk[0] = __builtin_amdgcn_readfirstlane(s_unit);
         for (;;) {
             const int u = __builtin_amdgcn_readfirstlane(walk[0]);
-            const int hh = __builtin_amdgcn_readfirstlane(walk[1]);
             if (u >= nu) break;
             const PagedUnit un = pr.units[u];
-            const int S = un.start + hh * un.w * un.n;
-            if (S >= b1) break;
-            if ((threadIdx.x & 63) == 0) {
-                walk[0] = hh + 1 == g.H ? u + 1 : u;
-                walk[1] = hh + 1 == g.H ? 0 : hh + 1;
-            }
+            if (un.start >= b1) break;
+            if ((threadIdx.x & 63) == 0) walk[0] = u + 1;
             int x0, x1;
-            item_passes(S, un.n, un.w, b0, b1, x0, x1);
+            item_passes(un.start, un.n, un.w, b0, b1, x0, x1);
             if (x0 < x1) {
                 int tid = threadIdx.x;
                 asm volatile("" : "+v"(tid));  // opaque per item (see item)
+                // partial slot: (unit + segment) * H + head, unique (the
+                // pieces of one head form a staircase in (unit, segment))
                 item(tid, hh, un.first, un.npos, x0 * kPass, min(x1 * kPass, un.kv_end),
-                     (size_t)(u * g.H + hh + seg));
+                     (size_t)(u + seg) * g.H + hh);
             }
         }
     } else {
@@ -1367,7 +1362,7 @@ __global__ __launch_bounds__(256) void attn_paged_combine_kernel(
 #pragma unroll
     for (int k = 0; k < kRows; ++k)
         kv = max(kv, rg * kRows + k < num_queries ? pr.row_kv_len[rg * kRows + k] : 0);
-    const int S = un.start + h * un.w * un.n;
+    const int S = un.start;  // every head has the unit's work range, in its own segments
     // segments holding the item's first and last pass starts
     int g_lo = 0, g_hi = -1;
     const Segments sg(max(total, 1), G);
@@ -1375,7 +1370,7 @@ __global__ __launch_bounds__(256) void attn_paged_combine_kernel(
         g_lo = sg.of(S, total);
         g_hi = sg.of(S + un.w * (un.n - 1), total);
     }
-    const size_t slot0 = (size_t)u * H + h;
+    const size_t unit0 = (size_t)u;
     float M = kInitMax, L = 0.f;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int b = g_lo; b <= g_hi; b += 8) {
@@ -1388,7 +1383,7 @@ __global__ __launch_bounds__(256) void attn_paged_combine_kernel(
             item_passes(S, un.n, un.w, sg.bound(gs), sg.bound(gs + 1), x0, x1);
             const bool ok = b + k <= g_hi && x0 < x1 && x0 * pass < kv;
             const float* pp =
-                ws + (((slot0 + gs) * positions + p) * kRows + r) * kPartStride;
+                ws + ((((unit0 + gs) * H + h) * positions + p) * kRows + r) * kPartStride;
             pm[k] = ok ? pp[128] : kInitMax;
             pl[k] = ok ? pp[129] : 0.f;
             po[k] = ok ? *reinterpret_cast<const float4*>(pp + d0)
@@ -1451,7 +1446,7 @@ __device__ int block_scan_1024(int v, int ident, int* s_tot, Op op) {
 template <int U>
 __global__ __launch_bounds__(1024) void paged_plan_kernel(
     const int32_t* __restrict__ row_seq, const int32_t* __restrict__ row_kv_len, int num_rows,
-    int groups, int H, int pass, int max_kv_len, mfma::PagedUnit* __restrict__ units,
+    int groups, int pass, int max_kv_len, mfma::PagedUnit* __restrict__ units,
     mfma::PagedUnit* __restrict__ group_unit, int32_t* __restrict__ plan) {
     static_assert(U >= 1 && U <= 4 && (U & (U - 1)) == 0, "1, 2 or 4 groups per unit");
     using mfma::kRows;
@@ -1496,7 +1491,7 @@ __global__ __launch_bounds__(1024) void paged_plan_kernel(
             }
         const int w = U > 2 ? (c > 2 ? 4 : 3) : 1;
         const int n = (kv + pass - 1) / pass;
-        const int work = start ? H * w * n : 0;
+        const int work = start ? w * n : 0;  // per kv head (every head has it)
         const int ui = block_scan_1024(start ? 1 : 0, 0, s_tot, add);
         const int wi = block_scan_1024(work, 0, s_tot, add);
         if (start) {
@@ -1680,18 +1675,21 @@ void launch_paged_attention(Scheme s, const uint16_t* query, const uint8_t* pool
     const float inv = inv_sqrt_d(g.D);
     const int row_groups = (num_rows + kRows - 1) / kRows;
     const int heads = g.H * row_groups;
-    // The plan splits the step's work (every unit's passes over its kv
-    // length, for every kv head) into G equal segments, one workgroup each:
-    // G a multiple of 8 (the kernel's XCD mapping).
+    // The plan gives every kv head the same work (each unit's passes over
+    // its kv length), split into Gh equal segments per head, one workgroup
+    // each: G = H * Gh workgroups, Gh a multiple of 8 (the kernel's XCD
+    // mapping).
     constexpr int kPass = kSplitChunk * kSplitWaves;
-    const int G = 8 * ((kPagedSegmentsPerCU * num_cus() + 7) / 8);
+    const int Gh = 8 * ((kPagedSegmentsPerCU * num_cus() + 8 * g.H - 1) / (8 * g.H));
+    const int G = Gh * g.H;
     // The plan counts work in int32: at most H * 4 * ceil(max_kv_len / kPass)
     // per row group.
     if ((long long)row_groups * g.H * 4 * ((std::max(max_kv_len, 0) + kPass - 1) / kPass) >
         INT32_MAX)
         throw Error("paged attention: too many rows for this max_kv_len");
-    // Workspace: the partials (slot item + segment: at most heads + G - 1
-    // slots of kPagedPositions positions), then the plan: the units and a
+    // Workspace: the partials (slot (unit + segment) * H + head: fewer than
+    // (row_groups + Gh) * H = heads + G slots of kPagedPositions positions),
+    // then the plan: the units and a
     // sentinel, each row group's unit, the unit count and total work.
     const size_t part_bytes =
         ((size_t)heads + G) * kPagedPositions * kRows * kPartStride * sizeof(float);
@@ -1705,8 +1703,8 @@ void launch_paged_attention(Scheme s, const uint16_t* query, const uint8_t* pool
     const bool prod = s == Scheme::Prod;
     constexpr int kCH = kSplitChunk, kNW = kSplitWaves;
     hipLaunchKernelGGL(paged_plan_kernel<kPagedPositions>, dim3(1), dim3(1024), 0, stream, row_seq,
-                       row_kv_len, num_rows, row_groups, g.H, kPass, std::max(max_kv_len, 0),
-                       units, group_unit, plan);
+                       row_kv_len, num_rows, row_groups, kPass, std::max(max_kv_len, 0), units,
+                       group_unit, plan);
     check_launch(prod ? "turbo_prod_paged_attn_plan" : "turbo_mse_paged_attn_plan");
     if (max_kv_len > 0) {
         if (prod)
@@ -1720,7 +1718,7 @@ void launch_paged_attention(Scheme s, const uint16_t* query, const uint8_t* pool
         check_launch(prod ? "turbo_prod_paged_attn_split" : "turbo_mse_paged_attn_split");
     }
     hipLaunchKernelGGL(attn_paged_combine_kernel, dim3(heads), dim3(256), 0, stream, ws, output,
-                       g.H, num_rows, G, kPagedPositions, kPass, pr);
+                       g.H, num_rows, Gh, kPagedPositions, kPass, pr);
     check_launch(prod ? "turbo_prod_paged_attn_combine" : "turbo_mse_paged_attn_combine");
 }
 
