@@ -193,6 +193,104 @@ __global__ __launch_bounds__(256) void prod_logits_kernel(
     logits[(size_t)row * num_kv_tokens + t] = (s1 * ks + s2 * (ks * re)) * inv;
 }
 
+// D = 128: one workgroup of 4 waves per (token tile, kv head, group of up to 8
+// query rows), so each K cell is read and decoded once for all the rows of
+// its group.  A wave takes 4 tokens per step: lane l handles token l / 16 and
+// code dword j = l % 16 (dimensions 8j .. 8j + 7), holding those dimensions
+// of every row's rotated query in registers.  Each dimension contributes
+// q_r[d] * (K3[code] +- re) (nibble bit 3: +), the reference's
+// s1*ks + s2*ks*re (:513-531) with the two sums taken together; the 16
+// lanes of a token are summed by a butterfly that halves the rows each lane
+// keeps (rows 4*b3 + 2*b2 + b1 of lane bits b3..b1), so lanes j and j ^ 1
+// end with the total of one row and the even one stores it.
+constexpr int kLogitTile = 128;  // tokens per workgroup (32 per wave, 8 steps)
+__global__ __launch_bounds__(256) void prod_logits_rows_kernel(
+    const uint16_t* __restrict__ query, const uint8_t* __restrict__ pool,
+    const int32_t* __restrict__ slots, float* __restrict__ logits, PageGeom g, int num_queries,
+    int num_kv_tokens, float inv) {
+    constexpr int D = 128, kRowsG = 8, kSteps = kLogitTile / 16;
+    __shared__ float qs[kRowsG][D];
+    __shared__ float tk[8];
+    const int h = blockIdx.y, rg = blockIdx.z;
+    const int nrows = min(kRowsG, num_queries - rg * kRowsG);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int j = lane & 15, ti = lane >> 4;
+    const int t_base = blockIdx.x * kLogitTile + w * (kLogitTile / 4);
+    // Every load of the wave's 32 tokens is issued before any is used: the
+    // slots (lane l: token t_base + l), then per step the lane's code dword
+    // and its token's two scales (tokens past the end or with a negative
+    // slot read the query's first bytes, always valid memory, and are
+    // dropped).
+    const int my_slot = lane < kLogitTile / 4 && t_base + lane < num_kv_tokens
+                            ? slots[t_base + lane] : -1;
+    uint32_t word[kSteps];
+    uint16_t ksr[kSteps], rer[kSteps];
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+        const int slot = __shfl(my_slot, 4 * s + ti);
+        int page, tib;
+        split_slot(slot < 0 ? 0 : slot, g, page, tib);
+        const uint64_t base = (uint64_t)page * g.page_size;
+        const uint64_t cell = (uint64_t)(tib * g.H + h);
+        const bool ok = slot >= 0;
+        const uint8_t* dummy = reinterpret_cast<const uint8_t*>(query);
+        word[s] = *reinterpret_cast<const uint32_t*>(
+            ok ? pool + base + g.kc_off + cell * g.code_stride + 4 * j : dummy);
+        ksr[s] = ld_u16(ok ? pool + base + g.ks_off + cell * g.scale_stride : dummy);
+        rer[s] = ld_u16(ok ? pool + base + g.kres_off + cell * g.scale_stride : dummy + 2);
+    }
+    if (threadIdx.x < 8) tk[threadIdx.x] = kK3[threadIdx.x];
+    for (int r = w; r < kRowsG; r += 4) {  // wave-uniform
+        float q0 = 0.f, q1 = 0.f;
+        if (r < nrows)
+            rotate_query<D / 2>(query + ((size_t)(rg * kRowsG + r) * g.H + h) * D, h, lane, inv,
+                                q0, q1);
+        qs[r][2 * lane] = q0;
+        qs[r][2 * lane + 1] = q1;
+    }
+    __syncthreads();
+    float qr[kRowsG][8];
+#pragma unroll
+    for (int r = 0; r < kRowsG; ++r)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qr[r][e] = qs[r][8 * j + e];
+    const int my_row = ((j >> 3) & 1) * 4 + ((j >> 2) & 1) * 2 + ((j >> 1) & 1);
+    const bool writer = (j & 1) == 0 && my_row < nrows;
+    float* out_row = logits + ((size_t)(rg * kRowsG + my_row) * g.H + h) * num_kv_tokens;
+    const bool b3 = (j & 8) != 0, b2 = (j & 4) != 0, b1 = (j & 2) != 0;
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+        const int t = t_base + 4 * s + ti;
+        const float re = h2f(rer[s]), ks = h2f(ksr[s]);
+        float acc[kRowsG];
+#pragma unroll
+        for (int r = 0; r < kRowsG; ++r) acc[r] = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t n = (word[s] >> (4 * e)) & 0xFu;
+            const float v = tk[n & 7u] + ((n & 8u) ? re : -re);
+#pragma unroll
+            for (int r = 0; r < kRowsG; ++r) acc[r] = fmaf(qr[r][e], v, acc[r]);
+        }
+        // 16 lanes of a token -> one row total per lane pair
+        float a4[4], a2[2];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float keep = b3 ? acc[i + 4] : acc[i], send = b3 ? acc[i] : acc[i + 4];
+            a4[i] = keep + lane_xor<8>(send);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const float keep = b2 ? a4[i + 2] : a4[i], send = b2 ? a4[i] : a4[i + 2];
+            a2[i] = keep + lane_xor<4>(send);
+        }
+        float a1 = (b1 ? a2[1] : a2[0]) + lane_xor<2>(b1 ? a2[0] : a2[1]);
+        a1 += lane_xor<1>(a1);
+        const int slot = __shfl(my_slot, 4 * s + ti);
+        if (writer && t < num_kv_tokens) out_row[t] = slot < 0 ? -INFINITY : a1 * ks * inv;
+    }
+}
+
 // ===========================================================================
 // Matrix-core path: D = 128, up to 8 query rows per kv head per workgroup.
 //
@@ -1756,6 +1854,16 @@ void launch_logits(const uint16_t* query, const uint8_t* pool, const int32_t* sl
     if (rows <= 0 || num_kv_tokens <= 0) return;
     const int tiles = (num_kv_tokens + 255) / 256;
     const float inv = inv_sqrt_d(g.D);
+    const int row_groups = (num_queries + 7) / 8;
+    if (g.D == 128 && g.code_stride == 64 && (g.kc_off & 3) == 0 && (g.page_size & 3) == 0 &&
+        (reinterpret_cast<uintptr_t>(pool) & 3) == 0 && g.H <= 65535 && row_groups <= 65535) {
+        hipLaunchKernelGGL(prod_logits_rows_kernel,
+                           dim3((num_kv_tokens + kLogitTile - 1) / kLogitTile, g.H, row_groups),
+                           dim3(256), 0, stream, query, pool, slots, logits, g, num_queries,
+                           num_kv_tokens, inv);
+        check_launch("turbo_prod_fused_attention_logits_kernel");
+        return;
+    }
     TQ_DISPATCH_D(g.D, hipLaunchKernelGGL(prod_logits_kernel<kD>, dim3(rows * tiles), dim3(256),
                                           0, stream, query, pool, slots, logits, g,
                                           num_kv_tokens, tiles, inv));
