@@ -333,7 +333,9 @@ def main() -> int:
 
     pack = measure_pack(w)
     log(f"[bench] pack (36 layers x 8192 tokens): turbo_prod {pack['turbo_prod_us_per_layer']:.1f} "
-        f"us/layer, turbo_mse {pack['turbo_mse_us_per_layer']:.1f} us/layer; mismatched bytes "
+        f"us/layer ({pack['turbo_prod_one_launch_us_per_layer']:.1f} as one launch), turbo_mse "
+        f"{pack['turbo_mse_us_per_layer']:.1f} us/layer "
+        f"({pack['turbo_mse_one_launch_us_per_layer']:.1f}); mismatched bytes "
         f"vs oracle {pack['parity']['mismatched_page_bytes']}, boundary counts "
         f"{pack['parity']['turbo_prod_boundary']}")
 
@@ -541,10 +543,14 @@ def measure_store(w: Workload, reps: int = 3) -> dict:
 
 
 def measure_pack(w: Workload, reps: int = 5) -> dict:
-    """Quantize on append: 36 layers x 8192 tokens of K/V (H = 2, D = 128,
-    shuffled 16-token pages) packed into turbo_prod and turbo_mse pools, one
-    graph of 36 pack launches per scheme.  Algorithmic bytes per layer: fp16
-    K/V and slots read, pages written."""
+    """Config 2, quantize on append: 36 layers x 8192 tokens of K/V (H = 2,
+    D = 128, seeds 200 + layer) packed into turbo_prod and turbo_mse pools,
+    as 36 per-layer launches (the reference's form) and as one launch for the
+    36 layers (tq_launch_*_pack_kv_layers), with slots = arange (as the
+    reference's store packs a document, cag_store.py:129) and with shuffled
+    16-token pages.  Graph replays, HIP events.  Algorithmic bytes per layer:
+    fp16 K/V and slots read, pages written.  The pools of the last (one-launch,
+    shuffled) fill are checked against the oracle."""
     import torch
 
     from turborag_amd.synthetic import permuted_slots
@@ -552,37 +558,59 @@ def measure_pack(w: Workload, reps: int = 5) -> dict:
     cfg = tq.default_config()
     cfg.num_kv_heads, cfg.head_dim, cfg.block_size = w.H, w.D, w.B
     lp, lm = tq.make_layout_for(cfg), tq.make_mse_layout_for(cfg)
-    slots = permuted_slots(N, w.B, seed=402).to(w.dev)
-    kv = [gpu_kv(N, w.H, w.D, 700 + l, w.dev) for l in range(NL)]
+    slot_sets = {"arange": torch.arange(N, dtype=torch.int32, device=w.dev),
+                 "shuffled": permuted_slots(N, w.B, seed=402).to(w.dev)}
+    kv = [gpu_kv(N, w.H, w.D, 200 + l, w.dev) for l in range(NL)]
+    keys, values = [k for k, _ in kv], [v for _, v in kv]
     pages = (N + w.B - 1) // w.B
-    pp = [torch.zeros(pages * lp.page_size_bytes, dtype=torch.uint8, device=w.dev)
-          for _ in range(NL)]
-    pm = [torch.zeros(pages * lm.page_size_bytes, dtype=torch.uint8, device=w.dev)
-          for _ in range(NL)]
+    pools = {"turbo_prod": [torch.zeros(pages * lp.page_size_bytes, dtype=torch.uint8,
+                                        device=w.dev) for _ in range(NL)],
+             "turbo_mse": [torch.zeros(pages * lm.page_size_bytes, dtype=torch.uint8,
+                                       device=w.dev) for _ in range(NL)]}
+    lays = {"turbo_prod": lp, "turbo_mse": lm}
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
 
-    def prod():
-        for (k, v), p in zip(kv, pp):
-            tq.pack(k, v, slots, p, lp, cfg, stream=torch.cuda.current_stream().cuda_stream)
+    def per_layer(scheme, slots):
+        fn = tq.pack if scheme == "turbo_prod" else tq.mse_pack
 
-    def mse():
-        for (k, v), p in zip(kv, pm):
-            tq.mse_pack(k, v, slots, p, lm, cfg, stream=torch.cuda.current_stream().cuda_stream)
+        def run():
+            st = torch.cuda.current_stream().cuda_stream
+            for (k, v), p in zip(kv, pools[scheme]):
+                fn(k, v, slots, p, lays[scheme], cfg, stream=st)
+        return run
+
+    def one_launch(scheme, slots):
+        def run():
+            tq.pack_layers(scheme, keys, values, slots, pools[scheme], lays[scheme], cfg,
+                           stream=torch.cuda.current_stream().cuda_stream)
+        return run
+
+    def timed(fn):
+        with torch.cuda.stream(side):
+            fn()
+        torch.cuda.synchronize()
+        g = capture(fn, side)
+        return event_time_us(g.replay if g is not None else fn, reps) / NL
 
     out = {"layers": NL, "tokens": N}
     fp16 = 2 * N * w.H * w.D * 2
-    for name, fn, lay in (("turbo_prod", prod, lp), ("turbo_mse", mse, lm)):
-        g = capture(fn, side)
-        us = event_time_us(g.replay if g is not None else fn, reps) / NL
-        alg = fp16 + N * 4 + pages * lay.page_size_bytes
-        out[f"{name}_us_per_layer"] = round(us, 2)
-        out[f"{name}_GBps"] = round(alg / us / 1e3, 1)
-        out[f"{name}_frac_hbm"] = round(alg / us / 1e3 / HBM_PEAK_GBPS, 4)
+    for scheme in ("turbo_prod", "turbo_mse"):
+        alg = fp16 + N * 4 + pages * lays[scheme].page_size_bytes
+        for form, make in (("", per_layer), ("one_launch_", one_launch)):
+            for sk, slots in slot_sets.items():
+                us = timed(make(scheme, slots))
+                key = f"{scheme}_{form}{'' if sk == 'arange' else 'shuffled_'}us_per_layer"
+                out[key] = round(us, 2)
+                if sk == "arange":
+                    out[f"{scheme}_{form}GBps"] = round(alg / us / 1e3, 1)
+                    out[f"{scheme}_{form}frac_hbm"] = round(alg / us / 1e3 / HBM_PEAK_GBPS, 4)
     out["algorithmic_bytes_per_layer_turbo_prod"] = fp16 + N * 4 + pages * lp.page_size_bytes
+    out["slots"] = "arange (the store's form); *_shuffled_*: a permutation of 16-token pages"
     torch.cuda.synchronize()
-    out["parity"] = pack_parity(w, kv, slots, pp, pm, pages)
-    del kv, pp, pm
+    out["parity"] = pack_parity(w, kv, slot_sets["shuffled"], pools["turbo_prod"],
+                                pools["turbo_mse"], pages)
+    del kv, keys, values, pools
     return out
 
 

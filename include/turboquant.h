@@ -163,6 +163,23 @@ int tq_launch_turbo_mse_dequant_kv_hnd(const uint8_t* page_pool, const int32_t* 
                                        const TQTurbomsePageLayout* layout, const TQConfig* cfg,
                                        int num_tokens, void* stream);
 
+/* Pack of a document's layers in one call: the reference's per-layer
+ * tq_launch_turbo_prod_pack_kv (src/tq_capi.cpp:49) for every l < num_layers,
+ * all layers sharing slot_mapping (device int32[num_tokens]; cag_store.py:129
+ * packs every layer with the same slots).  keys, values and page_pools are
+ * HOST arrays of num_layers device pointers, read during the call; keys[l],
+ * values[l] are [num_tokens, H, D] fp16.  For D = 64 and 128 one launch
+ * covers up to 64 layers.  Pools are bit-identical to per-layer packs. */
+int tq_launch_turbo_prod_pack_kv_layers(const uint16_t* const* keys,
+                                        const uint16_t* const* values,
+                                        const int32_t* slot_mapping, uint8_t* const* page_pools,
+                                        int num_layers, const TQTurboProdPageLayout* layout,
+                                        const TQConfig* cfg, int num_tokens, void* stream);
+int tq_launch_turbo_mse_pack_kv_layers(const uint16_t* const* keys, const uint16_t* const* values,
+                                       const int32_t* slot_mapping, uint8_t* const* page_pools,
+                                       int num_layers, const TQTurbomsePageLayout* layout,
+                                       const TQConfig* cfg, int num_tokens, void* stream);
+
 /* Dequant of a document's HBM-resident layers in one call: the reference's
  * per-layer tq_launch_turbo_prod_dequant_kv (src/tq_capi.cpp:66) for every
  * l < num_layers, all layers sharing slot_mapping (device int32[num_tokens],

@@ -124,6 +124,24 @@ int run_abi() {
     TQTurboProdPageLayout wrong = lp;
     wrong.k4_bytes_per_token_head = 7;
     CHECK(tq_launch_turbo_prod_pack_kv(fk, fk, fs, fp, &wrong, &cfg, 4, nullptr) == -2);
+    // Multi-layer entries: host arrays of device pointers, checked per layer.
+    const uint16_t* ks2[2] = {fk, fk};
+    const uint16_t* vs2[2] = {fk, nullptr};
+    uint8_t* ps2[2] = {fp, fp};
+    const uint8_t* cps2[2] = {fp, fp};
+    uint16_t* os2[2] = {fk, fk};
+    CHECK(tq_launch_turbo_prod_pack_kv_layers(nullptr, ks2, fs, ps2, 2, &lp, &cfg, 4, nullptr) ==
+          -1);
+    CHECK(tq_launch_turbo_prod_pack_kv_layers(ks2, vs2, fs, ps2, 2, &lp, &cfg, 4, nullptr) == -2);
+    CHECK(std::strstr(tq_last_error(), "null input or pool pointer") != nullptr);
+    CHECK(tq_launch_turbo_mse_pack_kv_layers(ks2, ks2, fs, ps2, -1, &lm, &cfg, 4, nullptr) == -2);
+    CHECK(tq_launch_turbo_prod_pack_kv_layers(ks2, ks2, fs, ps2, 2, &lp, &cfg, 0, nullptr) == -2);
+    CHECK(tq_launch_turbo_prod_pack_kv_layers(ks2, ks2, fs, ps2, 2, &lp, &cfg, 4, nullptr) == -2);
+    CHECK(std::strstr(tq_last_error(), "sanitizer build") != nullptr);
+    CHECK(tq_launch_turbo_prod_dequant_kv_layers(cps2, fs, os2, nullptr, 2, &lp, &cfg, 4, 0,
+                                                 nullptr) == -1);
+    CHECK(tq_launch_turbo_mse_dequant_kv_layers(cps2, fs, os2, os2, 2, &lm, &cfg, 1 << 30, 0,
+                                                nullptr) == -2);
     CHECK(tq_launch_turbo_prod_paged_attention(fk, fp, fs, 0, fs, fs, fk, &lp, &cfg, 8, 16,
                                                nullptr) == -2);
     CHECK(tq_launch_turbo_prod_paged_attention(fk, fp, fs, 1, fs, fs, fk, &lp, &cfg, 8, 17,

@@ -17,6 +17,10 @@ void launch_pack(Scheme, const uint16_t*, const uint16_t*, const int32_t*, uint8
                  const PageGeom&, int, hipStream_t) { no_device("pack"); }
 void launch_dequant(Scheme, const uint8_t*, const int32_t*, uint16_t*, uint16_t*,
                     const PageGeom&, int, hipStream_t, bool) { no_device("dequant"); }
+void launch_pack_layers(Scheme, const uint16_t* const*, const uint16_t* const*, const int32_t*,
+                        uint8_t* const*, const PageGeom&, int, int, hipStream_t) {
+    no_device("pack layers");
+}
 void launch_dequant_layers(Scheme, const uint8_t* const*, const int32_t*, uint16_t* const*,
                            uint16_t* const*, const PageGeom&, int, int, hipStream_t, bool) {
     no_device("dequant layers");

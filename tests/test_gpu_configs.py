@@ -10,6 +10,7 @@
   pass of the persistent dequant grid (40000 x 2, 16384 x 8).
 * Matrix-core attention with 8 kv heads at head_dim 128, and single-query
   decode (num_queries = 1, the reference store's call) at 32K context.
+* Config 2's 36-layer pack as one launch, and the multi-layer dequant.
 * The attention workspace: growth, retirement, stream cycling and graphs.
 
 Bars: pools and dequantized halves bit-exact; attention max rel err per
@@ -353,6 +354,49 @@ def test_dequant_layers_vs_oracle(tq, oracle, cuda, scheme, NL, N, H, head_major
             gk, gv = gk[0].transpose(1, 0, 2), gv[0].transpose(1, 0, 2)
         assert np.array_equal(gk, wk), layer
         assert np.array_equal(gv, wv), layer
+
+
+# ── multi-layer pack (config 2 in one launch) ───────────────────────── #
+
+@pytest.mark.parametrize("scheme", ["turbo_prod", "turbo_mse"])
+@pytest.mark.parametrize("NL,N,H,D,slot_kind", [
+    (36, 8192, 2, 128, "arange"),    # config 2: 36 layers x 8192 tokens, the store's slots
+    (36, 8192, 2, 128, "shuffled"),  # ... shuffled 16-token pages
+    (70, 100, 2, 128, "shuffled"),   # more than 64 layers: two launches
+    (3, 300, 8, 64, "shuffled"),     # head_dim 64, 8 kv heads, a ragged last page
+])
+def test_pack_layers_vs_oracle(tq, oracle, cuda, scheme, NL, N, H, D, slot_kind):
+    """Every layer's pool from one tq_launch_*_pack_kv_layers call equals the
+    oracle's pack of that layer (seeds 200 + layer, one shared slot map) and
+    the per-layer entry's pool."""
+    B = 16
+    print(f"[pack_layers {scheme}] {NL} x {N} H={H} D={D} {slot_kind}", flush=True)
+    oracle.nthreads = 16
+    cfg = tq.default_config()
+    cfg.num_kv_heads, cfg.head_dim, cfg.block_size = H, D, B
+    prod = scheme == "turbo_prod"
+    lay = tq.make_layout_for(cfg) if prod else tq.make_mse_layout_for(cfg)
+    slots = (torch.arange(N, dtype=torch.int32) if slot_kind == "arange"
+             else permuted_slots(N, B, seed=402, num_pages=N // B + 3))
+    pages = int(slots.max()) // B + 1
+    kv = [kv_tokens_major(N, H, D, seed=200 + layer) for layer in range(NL)]
+    keys = [k.to(cuda) for k, _ in kv]
+    values = [v.to(cuda) for _, v in kv]
+    pools = [torch.zeros(pages * lay.page_size_bytes, dtype=torch.uint8, device=cuda)
+             for _ in range(NL)]
+    sl = slots.to(cuda)
+    tq.pack_layers(scheme, keys, values, sl, pools, lay, cfg)
+    one = torch.zeros_like(pools[0])
+    torch.cuda.synchronize()
+    pack = oracle.prod_pack if prod else oracle.mse_pack
+    for layer in range(NL):
+        want = pack(as_u16(kv[layer][0]), as_u16(kv[layer][1]), slots.numpy(), pages, B)
+        assert np.array_equal(pools[layer].cpu().numpy(), want), layer
+        if layer in (0, NL - 1):  # the per-layer entry gives the same bytes
+            one.zero_()
+            (tq.pack if prod else tq.mse_pack)(keys[layer], values[layer], sl, one, lay, cfg)
+            torch.cuda.synchronize()
+            assert torch.equal(one, pools[layer]), layer
 
 
 # ── debug-sync mode ──────────────────────────────────────────────────── #

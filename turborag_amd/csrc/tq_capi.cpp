@@ -592,8 +592,31 @@ extern "C" int tq_load_turbo_prod_layers(const uint8_t* const* host_pools,
 }
 
 namespace {
+// tq_launch_*_pack_kv_layers: one slot mapping, num_layers inputs and pools.
+template <typename Layout>
+int pack_layers(tq::Scheme scheme, const uint16_t* const* keys, const uint16_t* const* values,
+                const int32_t* slot_mapping, uint8_t* const* page_pools, int num_layers,
+                const Layout* layout, const TQConfig* cfg, int num_tokens, void* stream) {
+    if (!keys || !values || !slot_mapping || !page_pools || !layout || !cfg) return -1;
+    const bool prod = scheme == tq::Scheme::Prod;
+    const char* name = prod ? "turbo_prod_pack_kv_layers" : "turbo_mse_pack_kv_layers";
+    return guarded_sync(stream, [&] {
+        const tq::PageGeom g =
+            prod ? tq::prod_geom(*cfg, *reinterpret_cast<const TQTurboProdPageLayout*>(layout))
+                 : tq::mse_geom(*cfg, *reinterpret_cast<const TQTurbomsePageLayout*>(layout));
+        if (num_layers < 0) throw tq::Error(std::string(name) + ": num_layers must be >= 0");
+        check_grid(num_tokens, name, prod);
+        check_rows(num_tokens, g.H, name);
+        for (int l = 0; l < num_layers; ++l)
+            if (!keys[l] || !values[l] || !page_pools[l])
+                throw tq::Error(std::string(name) + ": null input or pool pointer for a layer");
+        tq::launch_pack_layers(scheme, keys, values, slot_mapping, page_pools, g, num_tokens,
+                               num_layers, static_cast<hipStream_t>(stream));
+    });
+}
+
 // tq_launch_*_dequant_kv_layers: one slot mapping, num_layers pools and outputs.
-template <class Layout>
+template <typename Layout>
 int dequant_layers(tq::Scheme scheme, const uint8_t* const* page_pools,
                    const int32_t* slot_mapping, uint16_t* const* out_keys,
                    uint16_t* const* out_values, int num_layers, const Layout* layout,
@@ -617,6 +640,28 @@ int dequant_layers(tq::Scheme scheme, const uint8_t* const* page_pools,
     });
 }
 }  // namespace
+
+extern "C" int tq_launch_turbo_prod_pack_kv_layers(const uint16_t* const* keys,
+                                                   const uint16_t* const* values,
+                                                   const int32_t* slot_mapping,
+                                                   uint8_t* const* page_pools, int num_layers,
+                                                   const TQTurboProdPageLayout* layout,
+                                                   const TQConfig* cfg, int num_tokens,
+                                                   void* stream) {
+    return pack_layers(tq::Scheme::Prod, keys, values, slot_mapping, page_pools, num_layers,
+                       layout, cfg, num_tokens, stream);
+}
+
+extern "C" int tq_launch_turbo_mse_pack_kv_layers(const uint16_t* const* keys,
+                                                  const uint16_t* const* values,
+                                                  const int32_t* slot_mapping,
+                                                  uint8_t* const* page_pools, int num_layers,
+                                                  const TQTurbomsePageLayout* layout,
+                                                  const TQConfig* cfg, int num_tokens,
+                                                  void* stream) {
+    return pack_layers(tq::Scheme::Mse, keys, values, slot_mapping, page_pools, num_layers,
+                       layout, cfg, num_tokens, stream);
+}
 
 extern "C" int tq_launch_turbo_prod_dequant_kv_layers(
     const uint8_t* const* page_pools, const int32_t* slot_mapping, uint16_t* const* out_keys,

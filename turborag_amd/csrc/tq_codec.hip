@@ -280,14 +280,28 @@ __device__ __forceinline__ void quantize_chunks(const uint32_t (&w)[C], int j, f
     for (int c = 0; c < C; ++c) bytes[c] = n4[2 * c] | (n4[2 * c + 1] << 4);
 }
 
+// The K/V inputs and page pool of each layer of a pack launch (passed by
+// value in the kernel arguments); every layer shares the slot mapping.
+template <int ML>
+struct PackSet {
+    const uint16_t* key[ML];
+    const uint16_t* value[ML];
+    uint8_t* pool[ML];
+};
+constexpr int kMaxPackLayersPerLaunch = 64;
+
 // SCH: 0 turbo_mse, 1 turbo_prod, 2 the reference's unexported QJL-1b page
 // (tq_qjl_kernels.cu:72-181: K sign bits, V 4-bit codes, sign flip (-1)^i
-// without the head term).
-template <int D, int SCH>
-__global__ __launch_bounds__(kBlock) void pack_wide_kernel(
-    const uint16_t* __restrict__ key, const uint16_t* __restrict__ value,
-    const int32_t* __restrict__ slots, uint8_t* __restrict__ pool, PageGeom g, int num_rows,
-    float inv) {
+// without the head term).  ML > 1: layer blockIdx.y of the set (one launch
+// packs every layer of a document).
+template <int D, int SCH, int ML = 1>
+__global__ __launch_bounds__(kBlock) void pack_wide_kernel(const PackSet<ML> set,
+                                                           const int32_t* __restrict__ slots,
+                                                           PageGeom g, int num_rows, float inv) {
+    const int layer = ML == 1 ? 0 : (int)blockIdx.y;
+    const uint16_t* __restrict__ key = set.key[layer];
+    const uint16_t* __restrict__ value = set.value[layer];
+    uint8_t* __restrict__ pool = set.pool[layer];
     constexpr int R = kPackLanes, C = D / (2 * R);
     static_assert(C == 4 || C == 8, "D = 64 or 128");
     constexpr bool PROD = SCH == 1, QJL = SCH == 2;
@@ -810,9 +824,9 @@ void launch_pack(Scheme s, const uint16_t* key, const uint16_t* value, const int
         constexpr int R = kPackLanes;
         const dim3 wgrid((rows + kBlock / R - 1) / (kBlock / R));
         const bool prod = s == Scheme::Prod;
+        const PackSet<1> one{{key}, {value}, {pool}};
         auto go = [&](auto kernel) {
-            hipLaunchKernelGGL(kernel, wgrid, dim3(kBlock), 0, stream, key, value, slots, pool, g,
-                               rows, inv);
+            hipLaunchKernelGGL(kernel, wgrid, dim3(kBlock), 0, stream, one, slots, g, rows, inv);
         };
         if (g.D == 128) prod ? go(pack_wide_kernel<128, 1>) : go(pack_wide_kernel<128, 0>);
         else prod ? go(pack_wide_kernel<64, 1>) : go(pack_wide_kernel<64, 0>);
@@ -827,6 +841,46 @@ void launch_pack(Scheme s, const uint16_t* key, const uint16_t* value, const int
         TQ_DISPATCH_D(g.D, hipLaunchKernelGGL(mse_pack_kernel<kD>, grid, dim3(kBlock), 0, stream,
                                               key, value, slots, pool, g, rows, inv));
         check_launch("turbo_mse_pack_kv_kernel");
+    }
+}
+
+void launch_pack_layers(Scheme s, const uint16_t* const* keys, const uint16_t* const* values,
+                        const int32_t* slots, uint8_t* const* pools, const PageGeom& g,
+                        int num_tokens, int num_layers, hipStream_t stream) {
+    const int rows = num_tokens * g.H;
+    if (rows <= 0 || num_layers <= 0) return;
+    const auto al = [](uint64_t v, uint64_t a) { return (v & (a - 1)) == 0; };
+    bool wide = (g.D == 64 || g.D == 128) && al(g.kc_off, 4) && al(g.vc_off, 4) &&
+                al(g.page_size, 4);
+    for (int l = 0; l < num_layers && wide; ++l)
+        wide = al(reinterpret_cast<uintptr_t>(pools[l]), 4) &&
+               al(reinterpret_cast<uintptr_t>(keys[l]), 4) &&
+               al(reinterpret_cast<uintptr_t>(values[l]), 4);
+    if (!wide) {  // the per-layer kernels (other head dims, unaligned buffers)
+        for (int l = 0; l < num_layers; ++l)
+            launch_pack(s, keys[l], values[l], slots, pools[l], g, num_tokens, stream);
+        return;
+    }
+    const float inv = inv_sqrt_d(g.D);
+    const bool prod = s == Scheme::Prod;
+    constexpr int R = kPackLanes, ML = kMaxPackLayersPerLaunch;
+    for (int l0 = 0; l0 < num_layers; l0 += ML) {
+        const int n = std::min(ML, num_layers - l0);
+        PackSet<ML> set{};
+        for (int l = 0; l < n; ++l) {
+            set.key[l] = keys[l0 + l];
+            set.value[l] = values[l0 + l];
+            set.pool[l] = pools[l0 + l];
+        }
+        const dim3 grid((rows + kBlock / R - 1) / (kBlock / R), n);
+        auto go = [&](auto kernel) {
+            hipLaunchKernelGGL(kernel, grid, dim3(kBlock), 0, stream, set, slots, g, rows, inv);
+        };
+        if (g.D == 128)
+            prod ? go(pack_wide_kernel<128, 1, ML>) : go(pack_wide_kernel<128, 0, ML>);
+        else
+            prod ? go(pack_wide_kernel<64, 1, ML>) : go(pack_wide_kernel<64, 0, ML>);
+        check_launch(prod ? "turbo_prod_pack_kv_layers" : "turbo_mse_pack_kv_layers");
     }
 }
 
@@ -854,12 +908,13 @@ bool launch_qjl_wide_pack(const uint16_t* key, const uint16_t* value, const int3
     g.h_shift = (q.H & (q.H - 1)) == 0 ? __builtin_ctz(q.H) : -1;
     const dim3 grid((rows + kBlock / kPackLanes - 1) / (kBlock / kPackLanes));
     const float inv = inv_sqrt_d(g.D);
+    const PackSet<1> one{{key}, {value}, {pool}};
     if (g.D == 128)
-        hipLaunchKernelGGL((pack_wide_kernel<128, 2>), grid, dim3(kBlock), 0, stream, key, value,
-                           slots, pool, g, rows, inv);
+        hipLaunchKernelGGL((pack_wide_kernel<128, 2>), grid, dim3(kBlock), 0, stream, one, slots, g,
+                           rows, inv);
     else
-        hipLaunchKernelGGL((pack_wide_kernel<64, 2>), grid, dim3(kBlock), 0, stream, key, value,
-                           slots, pool, g, rows, inv);
+        hipLaunchKernelGGL((pack_wide_kernel<64, 2>), grid, dim3(kBlock), 0, stream, one, slots, g,
+                           rows, inv);
     check_launch("qjl_pack_kv_kernel");
     return true;
 }

@@ -86,6 +86,11 @@ void release_workspaces();
 // ---- launchers (tq_prod.hip, tq_mse.hip, tq_attention.hip) ---------------
 void launch_pack(Scheme s, const uint16_t* key, const uint16_t* value, const int32_t* slots,
                  uint8_t* pool, const PageGeom& g, int num_tokens, hipStream_t stream);
+// Pack of num_layers layers' K/V sharing one slot mapping, in as few launches
+// as possible (one per 64 layers for D = 64, 128 and aligned buffers).
+void launch_pack_layers(Scheme s, const uint16_t* const* keys, const uint16_t* const* values,
+                        const int32_t* slots, uint8_t* const* pools, const PageGeom& g,
+                        int num_tokens, int num_layers, hipStream_t stream);
 // head_major: outputs [H, N, D] (a [1, H, N, D] cache tensor) instead of [N, H, D].
 void launch_dequant(Scheme s, const uint8_t* pool, const int32_t* slots, uint16_t* out_key,
                     uint16_t* out_value, const PageGeom& g, int num_tokens, hipStream_t stream,

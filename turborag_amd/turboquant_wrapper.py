@@ -154,6 +154,12 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "tq_launch_turbo_mse_dequant_kv_hnd": ([_P(c_uint8), _P(c_int32), c_void_p, c_void_p,
                                             _P(TQTurbomsePageLayout), _P(TQConfig), c_int,
                                             c_void_p], c_int),
+    "tq_launch_turbo_prod_pack_kv_layers": ([_P(c_void_p), _P(c_void_p), _P(c_int32),
+                                             _P(c_void_p), c_int, _P(TQTurboProdPageLayout),
+                                             _P(TQConfig), c_int, c_void_p], c_int),
+    "tq_launch_turbo_mse_pack_kv_layers": ([_P(c_void_p), _P(c_void_p), _P(c_int32),
+                                            _P(c_void_p), c_int, _P(TQTurbomsePageLayout),
+                                            _P(TQConfig), c_int, c_void_p], c_int),
     "tq_launch_turbo_prod_dequant_kv_layers": ([_P(c_void_p), _P(c_int32), _P(c_void_p),
                                                 _P(c_void_p), c_int, _P(TQTurboProdPageLayout),
                                                 _P(TQConfig), c_int, c_int, c_void_p], c_int),
@@ -475,6 +481,33 @@ class TurboQuantWrapper:
                         num_tokens: int, stream: int = 0) -> None:
         self._dequant_hnd("turbo_mse", page_pool, slot_mapping, out_key, out_value, layout,
                           cfg, num_tokens, stream)
+
+    def pack_layers(self, scheme: str, keys, values, slot_mapping, page_pools, layout, cfg,
+                    stream: int = 0) -> None:
+        """Pack every layer's K/V [N, H, D] fp16 (one shared slot mapping) into
+        page_pools[l]; one launch per 64 layers at head_dim 64 and 128."""
+        n = len(keys)
+        if not (len(values) == len(page_pools) == n):
+            raise ValueError("pack_layers: one key, value and pool per layer")
+        num_tokens = keys[0].shape[0] if n else 0
+        thd = num_tokens * cfg.num_kv_heads * cfg.head_dim
+        for l in range(n):
+            self._check(scheme, "pack_kv_layers", key=(keys[l], torch.float16, thd),
+                        value=(values[l], torch.float16, thd),
+                        slot_mapping=(slot_mapping, torch.int32, num_tokens),
+                        page_pool=(page_pools[l], torch.uint8, 0))
+            if keys[l].shape[0] != num_tokens:
+                raise ValueError("pack_layers: every layer has the same number of tokens")
+        arr = c_void_p * max(n, 1)
+        ks = arr(*[t.data_ptr() for t in keys])
+        vs = arr(*[t.data_ptr() for t in values])
+        pools = arr(*[p.data_ptr() for p in page_pools])
+        fn = (self._lib.tq_launch_turbo_prod_pack_kv_layers if scheme == "turbo_prod"
+              else self._lib.tq_launch_turbo_mse_pack_kv_layers)
+        rc = fn(ks, vs, self._i32p(slot_mapping), pools, n, ctypes.byref(layout),
+                ctypes.byref(cfg), num_tokens, self._stream(stream))
+        if rc != 0:
+            self._kernel_raise(rc, scheme, "pack_kv_layers")
 
     def dequant_layers(self, scheme: str, page_pools, slot_mapping, out_keys, out_values,
                        layout, cfg, num_tokens: int, head_major: bool = False,
