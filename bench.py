@@ -656,24 +656,35 @@ def pack_parity(w: Workload, kv, slots, pp, pm, pages) -> dict:
 
 
 def measure_logits(w: Workload, reps: int = 10) -> dict:
-    """The turbo_prod logits entry on one layer of the step (GQA 16/2 rows,
-    32K tokens): fp32 logits [8, 2, 32768] written.  Algorithmic bytes: pool +
-    slots + query read, logits written."""
+    """The turbo_prod logits entry on every layer of the step (GQA 16/2 rows,
+    32K tokens): fp32 logits [8, 2, 32768] written per layer, 36 calls
+    replayed from a graph.  Algorithmic bytes: pool + slots + query read,
+    logits written."""
     import torch
-    lg = torch.empty(w.rows * w.H * w.N, dtype=torch.float32, device=w.dev)
-    us = event_time_us(lambda: w.tq.fused_attn_logits(w.qa, w.pools[0], w.slots, lg, w.lp, w.cfg,
-                                                      w.rows, w.N, stream=w._stream()), reps)
-    alg = w.pools[0].numel() + w.N * 4 + w.qa.numel() * 2 + lg.numel() * 4
+    lg = [torch.empty(w.rows * w.H * w.N, dtype=torch.float32, device=w.dev) for _ in range(w.NL)]
+
+    def run():
+        for layer in range(w.NL):
+            w.tq.fused_attn_logits(w.qa, w.pools[layer], w.slots, lg[layer], w.lp, w.cfg, w.rows,
+                                   w.N, stream=w._stream())
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run()
+    torch.cuda.synchronize()
+    g = capture(run, side)
+    us = event_time_us(g.replay if g is not None else run, reps) / w.NL
+    alg = w.pools[0].numel() + w.N * 4 + w.qa.numel() * 2 + lg[0].numel() * 4
     del lg
     return {"us": round(us, 2), "algorithmic_bytes": alg, "GBps": round(alg / us / 1e3, 1),
-            "shape": "8 GQA rows x 2 kv heads x 32768 tokens, fp32"}
+            "shape": "8 GQA rows x 2 kv heads x 32768 tokens, fp32; 36 layers from a graph"}
 
 
 def measure_legacy(w: Workload, reps: int = 10) -> dict:
     """The kernels the reference compiles but does not export, on one layer
     of the step's shape (32K tokens, H = 2, D = 128, the step's shuffled
     slots): QJL-1b pack / dequant / GQA 16/2 attention and legacy INT4 pack /
-    dequant.  Event-timed eager launches on the current stream."""
+    dequant.  Each timed as a graph of 10 launches (HIP events), per launch."""
     import torch
     tq = w.tq
     cfg = tq.default_config()
@@ -687,17 +698,27 @@ def measure_legacy(w: Workload, reps: int = 10) -> dict:
     ov = torch.empty_like(ok)
     out = torch.empty_like(w.att[0])
     st = w._stream
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+
+    def graph_us(call, n=10):
+        def run():
+            for _ in range(n):
+                call()
+        with torch.cuda.stream(side):
+            run()
+        torch.cuda.synchronize()
+        g = capture(run, side)
+        return event_time_us(g.replay if g is not None else run, reps) / n
+
+    # (pack first: the dequant and attention read its pages)
     t = {
-        "qjl_pack_us": event_time_us(lambda: tq.qjl_pack(k, v, w.slots, pq, lq, cfg, st()), reps),
-        "qjl_dequant_us": event_time_us(
-            lambda: tq.qjl_dequant(pq, w.slots, ok, ov, lq, cfg, st()), reps),
-        "qjl_attention_us": event_time_us(
-            lambda: tq.qjl_fused_attn_output(w.qa, pq, w.slots, out, lq, cfg, w.rows, w.N, st()),
-            reps),
-        "int4_pack_us": event_time_us(lambda: tq.int4_pack(k, v, w.slots, pi, li, cfg, st()),
-                                      reps),
-        "int4_dequant_us": event_time_us(
-            lambda: tq.int4_dequant(pi, w.slots, ok, ov, li, cfg, st()), reps),
+        "qjl_pack_us": graph_us(lambda: tq.qjl_pack(k, v, w.slots, pq, lq, cfg, st())),
+        "qjl_dequant_us": graph_us(lambda: tq.qjl_dequant(pq, w.slots, ok, ov, lq, cfg, st())),
+        "qjl_attention_us": graph_us(
+            lambda: tq.qjl_fused_attn_output(w.qa, pq, w.slots, out, lq, cfg, w.rows, w.N, st())),
+        "int4_pack_us": graph_us(lambda: tq.int4_pack(k, v, w.slots, pi, li, cfg, st())),
+        "int4_dequant_us": graph_us(lambda: tq.int4_dequant(pi, w.slots, ok, ov, li, cfg, st())),
     }
     fp16 = 2 * w.N * w.H * w.D * 2
     t = {k_: round(v_, 2) for k_, v_ in t.items()}
@@ -858,8 +879,20 @@ def measure_batched_scheme(w: Workload, scheme: str, reps: int = 10) -> dict:
     b, query, row_seq, row_len = st["batch"], st["query"], st["row_seq"], st["row_len"]
     bt, out, lens, widths = st["tables"], st["out"], st["lens"], st["widths"]
     torch.cuda.synchronize()
-    att_us = event_time_us(lambda: b.attention(query, row_seq, row_len, bt, out), reps)
-    app_us = event_time_us(b.repack, reps)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+
+    def graph_us(call, n=10):  # n launches replayed from a graph, per launch
+        def run():
+            for _ in range(n):
+                call(torch.cuda.current_stream().cuda_stream)
+        with torch.cuda.stream(side):
+            run()
+        torch.cuda.synchronize()
+        g = capture(run, side)
+        return event_time_us(g.replay if g is not None else run, reps) / n
+    att_us = graph_us(lambda st: b.attention(query, row_seq, row_len, bt, out, stream=st))
+    app_us = graph_us(lambda st: b.repack(stream=st))
     rows = int(query.shape[0])
     # Algorithmic bytes: each sequence's cells once per kv head (+4 B slot
     # per token), the new tokens' fp16 K/V in and cells out, query and output.
