@@ -86,16 +86,21 @@ class Workload:
         cfg.num_kv_heads, cfg.head_dim, cfg.block_size = H, D, B
         self.cfg = cfg
         self.lp = lp = tq.make_layout_for(cfg)
+        self.lm = lm = tq.make_mse_layout_for(cfg)
         pages = (N + B - 1) // B
 
         log(f"[bench] setup: {NL} layers x {N} tokens, packing on the GPU")
         self.slots = permuted_slots(N, B, seed=401).to(dev)
         self.pools = []
+        self.mse_pools = []  # the same K/V in turbo_mse pages (config 3's second scheme)
         for layer in range(NL):
             k, v = gpu_kv(N, H, D, 300 + layer, dev)
             pool = torch.zeros(pages * lp.page_size_bytes, dtype=torch.uint8, device=dev)
             tq.pack(k, v, self.slots, pool, lp, cfg)
             self.pools.append(pool)
+            pool = torch.zeros(pages * lm.page_size_bytes, dtype=torch.uint8, device=dev)
+            tq.mse_pack(k, v, self.slots, pool, lm, cfg)
+            self.mse_pools.append(pool)
         del k, v
         self.out_k = [torch.empty(N, H, D, dtype=torch.float16, device=dev) for _ in range(NL)]
         self.out_v = [torch.empty(N, H, D, dtype=torch.float16, device=dev) for _ in range(NL)]
@@ -131,6 +136,16 @@ class Workload:
         the document's 36 layers load as one launch."""
         self.tq.dequant_layers("turbo_prod", self.pools, self.slots, self.out_k, self.out_v,
                                self.lp, self.cfg, self.N, stream=self._stream())
+
+    def all_dequant_mse(self):
+        """Config 3's turbo_mse pools, every layer in one call."""
+        self.tq.dequant_layers("turbo_mse", self.mse_pools, self.slots, self.out_k, self.out_v,
+                               self.lm, self.cfg, self.N, stream=self._stream())
+
+    def all_dequant_mse_per_layer(self):
+        for layer in range(self.NL):
+            self.tq.mse_dequant(self.mse_pools[layer], self.slots, self.out_k[layer],
+                                self.out_v[layer], self.lm, self.cfg, stream=self._stream())
 
     def all_dequant_per_layer(self):
         """The reference's form: one tq_launch_turbo_prod_dequant_kv per layer."""
@@ -197,7 +212,8 @@ def event_time_us(run, reps):
 
 def launch_pass(w: Workload, reps: int) -> None:
     """Eager launches only: the 36-layer dequant (one launch and per-layer
-    launches) and attention of every layer, the one-launch pack of the 36
+    launches) and attention of every layer, the turbo_mse 36-layer dequant,
+    the one-launch pack of the 36
     layers, the logits entry, one step of the batched paged decode (append +
     attention), then a plain device copy of the dequant's byte count (the
     calibration kernel for the FETCH_SIZE / WRITE_SIZE counters)."""
@@ -212,6 +228,7 @@ def launch_pass(w: Workload, reps: int) -> None:
         w.all_dequant()
         w.all_dequant_per_layer()
         w.all_attention()
+        w.all_dequant_mse()
         # the one-launch pack of the 36 dequantized layers into other pools,
         # and the logits entry on one layer
         w.tq.pack_layers("turbo_prod", w.out_k, w.out_v, w.slots, repacked, w.lp, w.cfg,
@@ -327,6 +344,29 @@ def main() -> int:
         for s, d in zip(srcs, dsts):
             d.copy_(s)
     copy_us = event_time_us(copies, reps) / len(srcs)
+
+    # Config 3's turbo_mse form: the same 36 layers in turbo_mse pages.
+    def four_mse():
+        for _ in range(4):
+            w.all_dequant_mse()
+    with torch.cuda.stream(side):
+        w.all_dequant_mse()
+        w.all_dequant_mse_per_layer()
+    torch.cuda.synchronize()
+    g_m4 = capture(four_mse, side) if use_graph else None
+    g_m1 = capture(w.all_dequant_mse_per_layer, side) if use_graph else None
+    mse_us = event_time_us(g_m4.replay if g_m4 is not None else four_mse, reps) / 4 / w.NL
+    mse1_us = event_time_us(g_m1.replay if g_m1 is not None else w.all_dequant_mse_per_layer,
+                            reps) / w.NL
+    # turbo_mse pages read (the used bytes: codes and the two norms) + fp16 written + slots
+    mse_bytes = w.N * w.H * (w.D + 4) + 2 * w.N * w.H * w.D * 2 + w.N * 4
+    dequant_mse = {"us_per_layer": round(mse_us, 3),
+                   "GBps": round(mse_bytes / mse_us / 1e3, 1),
+                   "frac_hbm": round(mse_bytes / mse_us / 1e3 / HBM_PEAK_GBPS, 4),
+                   "per_layer_launches_us_per_layer": round(mse1_us, 3),
+                   "algorithmic_bytes_per_layer": mse_bytes,
+                   "kernel": "tq::dequant_stream_kernel<128, 0, 64>: 36 layers, one launch"}
+    log(f"[bench] turbo_mse dequant {mse_us:.2f} us/layer one launch, {mse1_us:.2f} per-layer")
     del srcs, dsts
 
     # HBM bytes per dispatch of the roofline kernel on this workload, from the
@@ -425,6 +465,7 @@ def main() -> int:
                                    "kernel": DEQUANT_KERNEL_1},
             "copy_same_bytes_us": round(copy_us, 3),
         },
+        "dequant_turbo_mse": dequant_mse,
         "decode_attn": {
             "us_per_layer": round(att_us, 3),
             "achieved_GBps": round(att_gbps, 1),

@@ -527,6 +527,10 @@ constexpr int kMaxLayersPerLaunch = 64;
 // workgroup lets 4 reside per CU; a grid of several such rounds balances the
 // tail (36 x 32K-token layers: 4 per CU 9.3 us/layer, 8: 9.0, 24: 8.6, 48-192:
 // 8.8-9.0).
+// Dequant workgroups per CU for a one-layer launch.
+#ifndef TQ_DEQ_BLOCKS_PER_CU
+#define TQ_DEQ_BLOCKS_PER_CU 4
+#endif
 #ifndef TQ_DEQ_LAYERS_BLOCKS_PER_CU
 #define TQ_DEQ_LAYERS_BLOCKS_PER_CU 24
 #endif
@@ -971,7 +975,7 @@ void launch_dequant(Scheme s, const uint8_t* pool, const int32_t* slots, uint16_
         // 1 or 2 and equals 8 at the 32K-token layer).
         const int rows_per_block = kBlock / (g.D / 32);
         const int blocks_needed = (rows + rows_per_block - 1) / rows_per_block;
-        const dim3 grid(std::max(1, std::min(blocks_needed, 4 * num_cus())));
+        const dim3 grid(std::max(1, std::min(blocks_needed, TQ_DEQ_BLOCKS_PER_CU * num_cus())));
         const bool prod = s == Scheme::Prod;
         const LayerSet<1> one{{pool}, {out_key}, {out_value}};
         auto go = [&](auto kernel) {
