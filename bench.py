@@ -491,35 +491,41 @@ def main() -> int:
 
 
 def measure_loader(w: Workload, reps: int = 3) -> dict:
-    """The layer-pipelined loader (tq_load_turbo_prod_layers): every layer's
-    pages from pinned host memory to the GPU on a copy stream, each layer
-    dequantized into [1, H, N, D] on the compute stream as its copy lands.
-    PCIe-inclusive, so reported beside the HBM-resident figures, not as them."""
+    """The layer-pipelined loader (tq_load_*_layers), config 3 for both
+    schemes: every layer's pages from pinned host memory to the GPU on a copy
+    stream, each layer dequantized into [1, H, N, D] on the compute stream as
+    its copy lands.  PCIe-inclusive, so reported beside the HBM-resident
+    figures, not as them.  The turbo_prod figures are also at the top level."""
     import torch
-    host = [p.cpu().pin_memory() for p in w.pools]
-    dev = [torch.empty_like(p) for p in w.pools]
     copy = torch.cuda.Stream()
     compute = torch.cuda.current_stream()
+    out = {}
+    for scheme, pools, lay in (("turbo_prod", w.pools, w.lp), ("turbo_mse", w.mse_pools, w.lm)):
+        host = [p.cpu().pin_memory() for p in pools]
+        dev = [torch.empty_like(p) for p in pools]
 
-    def load():
-        w.tq.load_layers("turbo_prod", host, dev, w.slots, w.out_k, w.out_v, w.lp, w.cfg, w.N,
-                         copy_stream=copy.cuda_stream, compute_stream=compute.cuda_stream)
+        def load():
+            w.tq.load_layers(scheme, host, dev, w.slots, w.out_k, w.out_v, lay, w.cfg, w.N,
+                             copy_stream=copy.cuda_stream, compute_stream=compute.cuda_stream)
 
-    def copies_only():
-        with torch.cuda.stream(copy):
-            for h, d in zip(host, dev):
-                d.copy_(h, non_blocking=True)
-        compute.wait_stream(copy)
+        def copies_only():
+            with torch.cuda.stream(copy):
+                for h, d in zip(host, dev):
+                    d.copy_(h, non_blocking=True)
+            compute.wait_stream(copy)
 
-    load()
-    torch.cuda.synchronize()
-    ms = event_time_us(load, reps) / 1e3
-    h2d = event_time_us(copies_only, reps) / 1e3
-    del host, dev
-    page_bytes = w.NL * w.pool_bytes
-    return {"layers": w.NL, "ms": round(ms, 3), "host_GBps": round(page_bytes / ms / 1e6, 2),
-            "h2d_only_ms": round(h2d, 3), "h2d_GBps": round(page_bytes / h2d / 1e6, 2),
-            "output": "[1, H, N, D] fp16 per layer", "host_memory": "pinned"}
+        load()
+        torch.cuda.synchronize()
+        ms = event_time_us(load, reps) / 1e3
+        h2d = event_time_us(copies_only, reps) / 1e3
+        page_bytes = sum(p.numel() for p in pools)
+        out[scheme] = {"layers": w.NL, "ms": round(ms, 3),
+                       "host_GBps": round(page_bytes / ms / 1e6, 2), "h2d_only_ms": round(h2d, 3),
+                       "h2d_GBps": round(page_bytes / h2d / 1e6, 2),
+                       "output": "[1, H, N, D] fp16 per layer", "host_memory": "pinned"}
+        del host, dev
+    out.update(out["turbo_prod"])
+    return out
 
 
 def measure_store(w: Workload, reps: int = 3) -> dict:

@@ -193,35 +193,36 @@ __global__ __launch_bounds__(256) void prod_logits_kernel(
     logits[(size_t)row * num_kv_tokens + t] = (s1 * ks + s2 * (ks * re)) * inv;
 }
 
-// D = 128: one workgroup of 4 waves per (token tile, kv head, group of up to 8
-// query rows), so each K cell is read and decoded once for all the rows of
-// its group.  A wave takes 4 tokens per step: lane l handles token l / 16 and
-// code dword j = l % 16 (dimensions 8j .. 8j + 7), holding those dimensions
-// of every row's rotated query in registers.  Each dimension contributes
+// D = 128: one workgroup of 8 waves per (128-token tile, kv head, group of up
+// to 8 query rows), so each K cell is read and decoded once for all the rows
+// of its group.  A wave takes 16 tokens, 4 per step: lane l handles token
+// l / 16 and code dword j = l % 16 (dimensions 8j .. 8j + 7), holding those
+// dimensions of every row's rotated query in registers.  Each dimension contributes
 // q_r[d] * (K3[code] +- re) (nibble bit 3: +), the reference's
 // s1*ks + s2*ks*re (:513-531) with the two sums taken together; the 16
 // lanes of a token are summed by a butterfly that halves the rows each lane
 // keeps (rows 4*b3 + 2*b2 + b1 of lane bits b3..b1), so lanes j and j ^ 1
 // end with the total of one row and the even one stores it.
-constexpr int kLogitTile = 128;  // tokens per workgroup (32 per wave, 8 steps)
-__global__ __launch_bounds__(256) void prod_logits_rows_kernel(
+constexpr int kLogitTile = 128;  // tokens per workgroup
+constexpr int kLogitWaves = 8;   // 16 tokens per wave (7.4 us at 32K, 8.1 with 4 waves of 32)
+__global__ __launch_bounds__(64 * kLogitWaves) void prod_logits_rows_kernel(
     const uint16_t* __restrict__ query, const uint8_t* __restrict__ pool,
     const int32_t* __restrict__ slots, float* __restrict__ logits, PageGeom g, int num_queries,
     int num_kv_tokens, float inv) {
-    constexpr int D = 128, kRowsG = 8, kSteps = kLogitTile / 16;
+    constexpr int D = 128, kRowsG = 8, kSteps = kLogitTile / (4 * kLogitWaves);
     __shared__ float qs[kRowsG][D];
     __shared__ float tk[8];
     const int h = blockIdx.y, rg = blockIdx.z;
     const int nrows = min(kRowsG, num_queries - rg * kRowsG);
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int j = lane & 15, ti = lane >> 4;
-    const int t_base = blockIdx.x * kLogitTile + w * (kLogitTile / 4);
-    // Every load of the wave's 32 tokens is issued before any is used: the
+    const int t_base = blockIdx.x * kLogitTile + w * (kLogitTile / kLogitWaves);
+    // Every load of the wave's 16 tokens is issued before any is used: the
     // slots (lane l: token t_base + l), then per step the lane's code dword
     // and its token's two scales (tokens past the end or with a negative
     // slot read the query's first bytes, always valid memory, and are
     // dropped).
-    const int my_slot = lane < kLogitTile / 4 && t_base + lane < num_kv_tokens
+    const int my_slot = lane < kLogitTile / kLogitWaves && t_base + lane < num_kv_tokens
                             ? slots[t_base + lane] : -1;
     uint32_t word[kSteps];
     uint16_t ksr[kSteps], rer[kSteps];
@@ -240,7 +241,7 @@ __global__ __launch_bounds__(256) void prod_logits_rows_kernel(
         rer[s] = ld_u16(ok ? pool + base + g.kres_off + cell * g.scale_stride : dummy + 2);
     }
     if (threadIdx.x < 8) tk[threadIdx.x] = kK3[threadIdx.x];
-    for (int r = w; r < kRowsG; r += 4) {  // wave-uniform
+    for (int r = w; r < kRowsG; r += kLogitWaves) {  // wave-uniform
         float q0 = 0.f, q1 = 0.f;
         if (r < nrows)
             rotate_query<D / 2>(query + ((size_t)(rg * kRowsG + r) * g.H + h) * D, h, lane, inv,
@@ -1859,7 +1860,7 @@ void launch_logits(const uint16_t* query, const uint8_t* pool, const int32_t* sl
         (reinterpret_cast<uintptr_t>(pool) & 3) == 0 && g.H <= 65535 && row_groups <= 65535) {
         hipLaunchKernelGGL(prod_logits_rows_kernel,
                            dim3((num_kv_tokens + kLogitTile - 1) / kLogitTile, g.H, row_groups),
-                           dim3(256), 0, stream, query, pool, slots, logits, g, num_queries,
+                           dim3(64 * kLogitWaves), 0, stream, query, pool, slots, logits, g, num_queries,
                            num_kv_tokens, inv);
         check_launch("turbo_prod_fused_attention_logits_kernel");
         return;
