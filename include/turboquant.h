@@ -169,7 +169,8 @@ int tq_launch_turbo_mse_dequant_kv_hnd(const uint8_t* page_pool, const int32_t* 
  * packs every layer with the same slots).  keys, values and page_pools are
  * HOST arrays of num_layers device pointers, read during the call; keys[l],
  * values[l] are [num_tokens, H, D] fp16.  For D = 64 and 128 one launch
- * covers up to 64 layers.  Pools are bit-identical to per-layer packs. */
+ * covers up to 64 layers.  Pools are bit-identical to per-layer packs; the
+ * layers run concurrently, so page_pools[l] must not overlap each other. */
 int tq_launch_turbo_prod_pack_kv_layers(const uint16_t* const* keys,
                                         const uint16_t* const* values,
                                         const int32_t* slot_mapping, uint8_t* const* page_pools,
@@ -186,7 +187,8 @@ int tq_launch_turbo_mse_pack_kv_layers(const uint16_t* const* keys, const uint16
  * as a document's layers do, cag_store.py:129).  page_pools, out_keys and
  * out_values are HOST arrays of num_layers device pointers, read during the
  * call.  Outputs are [num_tokens, H, D] fp16, or [1, H, num_tokens, D] when
- * head_major != 0.  For D = 128 one launch covers up to 64 layers. */
+ * head_major != 0.  For D = 128 one launch covers up to 64 layers; the layers
+ * run concurrently, so the outputs must not overlap each other. */
 int tq_launch_turbo_prod_dequant_kv_layers(const uint8_t* const* page_pools,
                                            const int32_t* slot_mapping,
                                            uint16_t* const* out_keys, uint16_t* const* out_values,
