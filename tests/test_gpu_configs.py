@@ -356,6 +356,49 @@ def test_dequant_layers_vs_oracle(tq, oracle, cuda, scheme, NL, N, H, head_major
         assert np.array_equal(gv, wv), layer
 
 
+@pytest.mark.parametrize("scheme,NL,N,H,B,head_major", [
+    ("turbo_prod", 3, 531, 2, 16, False),  # row-per-lane kernel, holes, ragged last group
+    ("turbo_mse", 3, 531, 3, 7, True),     # ... 3 kv heads, 7-token blocks (division paths)
+    ("turbo_prod", 2, 300, 3, 7, False),   # page not 16-byte aligned: the per-layer kernels
+])
+def test_dequant_layers_holes_and_geometry(tq, oracle, cuda, scheme, NL, N, H, B, head_major):
+    """Unmapped tokens (slot -1) keep their output untouched; mapped ones are
+    bit-exact against the oracle, with non-power-of-two heads and blocks."""
+    D = 128
+    print(f"[dequant_layers holes {scheme}] {NL} x {N} H={H} B={B} head_major={head_major}",
+          flush=True)
+    cfg, lp, lm = _cfg(tq, H, D, B)
+    prod = scheme == "turbo_prod"
+    lay = lp if prod else lm
+    slots = permuted_slots(N, B, seed=350 + N)
+    slots[::5] = -1
+    pages = int(slots.max().item()) // B + 1
+    pools = []
+    for layer in range(NL):
+        k, v = kv_tokens_major(N, H, D, seed=360 + layer)
+        pool = torch.zeros(pages * lay.page_size_bytes, dtype=torch.uint8, device=cuda)
+        (tq.pack if prod else tq.mse_pack)(k.to(cuda), v.to(cuda), slots.to(cuda), pool, lay, cfg)
+        pools.append(pool)
+    shape = (1, H, N, D) if head_major else (N, H, D)
+    oks = [torch.full(shape, 7.0, dtype=torch.float16, device=cuda) for _ in range(NL)]
+    ovs = [torch.full(shape, 7.0, dtype=torch.float16, device=cuda) for _ in range(NL)]
+    tq.dequant_layers(scheme, pools, slots.to(cuda), oks, ovs, lay, cfg, N,
+                      head_major=head_major)
+    torch.cuda.synchronize()
+    fn = oracle.prod_dequant if prod else oracle.mse_dequant
+    sl = slots.numpy()
+    live = sl >= 0
+    seven = np.float16(7.0).view(np.uint16)
+    for layer in range(NL):
+        wk, wv = fn(pools[layer].cpu().numpy(), sl, H, D, B)
+        gk, gv = as_u16(oks[layer]), as_u16(ovs[layer])
+        if head_major:
+            gk, gv = gk[0].transpose(1, 0, 2), gv[0].transpose(1, 0, 2)
+        assert np.array_equal(gk[live], wk[live]), layer
+        assert np.array_equal(gv[live], wv[live]), layer
+        assert np.all(gk[~live] == seven) and np.all(gv[~live] == seven), layer
+
+
 # ── multi-layer pack (config 2 in one launch) ───────────────────────── #
 
 @pytest.mark.parametrize("scheme", ["turbo_prod", "turbo_mse"])

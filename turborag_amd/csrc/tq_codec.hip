@@ -531,6 +531,12 @@ constexpr int kMaxLayersPerLaunch = 64;
 #ifndef TQ_DEQ_BLOCKS_PER_CU
 #define TQ_DEQ_BLOCKS_PER_CU 4
 #endif
+// Row-per-lane dequant workgroups per CU for a multi-layer launch (two
+// reside per CU; a grid of several rounds balances the tail: 36 x 32K-token
+// layers, 2 per CU 8.5 us/layer, 8: 8.2, 16-64: 7.9-8.0).
+#ifndef TQ_DEQ_ROWS_BLOCKS_PER_CU
+#define TQ_DEQ_ROWS_BLOCKS_PER_CU 24
+#endif
 #ifndef TQ_DEQ_LAYERS_BLOCKS_PER_CU
 #define TQ_DEQ_LAYERS_BLOCKS_PER_CU 24
 #endif
@@ -789,6 +795,248 @@ __global__ __launch_bounds__(kBlock) void dequant_stream_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------
+// Dequant, one row per lane (D = 128; turbo_prod and turbo_mse).  Every WHT
+// stage and both decode tables stay inside the lane: no cross-lane butterfly
+// (a DPP move plus an fmac per value per stage) and one table build per row
+// instead of one per lane of a row: 45 VALU instructions per row against 72
+// for the four-lanes-per-row form, which is VALU-bound here.  Lane l of a wave
+// group owns row 64*group + l; it loads the row's 64 code bytes per tensor
+// as four 16-byte loads.  The 128 outputs of a tensor leave in two halves
+// of one 128-byte line per row: each lane writes its half-row into a padded
+// wave-private LDS stage (144-byte rows: the 16-byte writes of eight
+// consecutive lanes cover the 32 banks once), then store r of the wave
+// writes rows 8r .. 8r + 7 of the group, eight whole lines per store.
+// Waves walk (layer, row group) pairs grid-stride with the next pair's
+// slot, codes and scales in flight.
+// ---------------------------------------------------------------------------
+constexpr int kRowStageBytes = 144;  // staged bytes per row: one output line + 16 of pad
+
+template <int SCH, int ML>
+__global__ __launch_bounds__(kBlock, 2) void dequant_rows_kernel(
+    const LayerSet<ML> layers, const int32_t* __restrict__ slots, PageGeom g, int num_rows,
+    int num_layers, float inv, OutLayout ol) {
+    constexpr bool PROD = SCH == 1;
+    static_assert(SCH == 0 || SCH == 1, "turbo_mse or turbo_prod pages");
+    constexpr int kWaves = kBlock / 64;
+    static_assert(kWaves == 4, "byte 1 of a table address holds 4*nibble + wave");
+    // Tables as in dequant_stream_kernel: entry n of (wave w, lane l) is word
+    // (n*4 + w)*64 + l of the tensor's 16 KiB, K first; then one stage per
+    // wave, 64 rows of kRowStageBytes: the row's half line (bytes 0..127) and
+    // the addresses of its K and V output rows (bytes 128 and 136; 0 for a
+    // row not written).
+    constexpr uint32_t kTabBytes = 16 * kWaves * 64 * sizeof(float);
+    constexpr uint32_t kStageBytes = 64 * kRowStageBytes;
+    // The kernel's only LDS object: it starts at LDS address 0, so byte 1 of
+    // an entry's address is 4*nibble + wave and the bytes above it are zero.
+    __shared__ __attribute__((aligned(1024))) uint32_t lds[(2 * kTabBytes + kWaves * kStageBytes) / 4];
+    typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+    typedef __attribute__((address_space(3))) uint64_t lds_u64;
+    typedef __attribute__((address_space(1))) u32x4 global_u32x4;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((lds_float*)(void*)lds);
+    const uint32_t tbase = lds0 + 4u * lane + 256u * wave;  // entry 0 of this lane's K table
+    const uint32_t wsplat = 0x01010101u * (uint32_t)wave;
+    const uint32_t stage = lds0 + 2 * kTabBytes + wave * kStageBytes;
+    const uint32_t my_row = stage + lane * kRowStageBytes;        // staged by this lane
+    const uint32_t rd_row = stage + (lane >> 3) * kRowStageBytes;  // read by store 0 (+ 8 rows per store)
+    const int groups = (num_rows + 63) / 64;  // row groups per layer
+    const int total = groups * num_layers;    // (layer, group) pairs
+    const int stride = gridDim.x * kWaves;
+
+    // A group's cell: this lane's row, its page and cell, and whether it is
+    // written.  Loads are branch-free (so the in-order vector-memory counter
+    // never waits on a later load early): a row not written reads the first
+    // bytes of its layer's K output instead (valid memory; the values are
+    // not used).
+    struct Loc {
+        const uint8_t* base;   // page start
+        const uint8_t* dummy;  // the layer's first output row
+        int cell;              // tib * H + h
+        int row, layer;        // layer wave-uniform
+        bool live;
+    };
+    auto split_pair = [&](int gi, int& grp) -> int {
+        if constexpr (ML == 1) {
+            grp = gi;
+            return 0;
+        } else {
+            const int l = gi / groups;
+            grp = gi - l * groups;
+            return l;
+        }
+    };
+    auto token_head = [&](int row, int& t, int& h) {
+        if (g.h_shift >= 0) {
+            t = row >> g.h_shift;
+            h = row & (g.H - 1);
+        } else {
+            t = row / g.H;
+            h = row - t * g.H;
+        }
+    };
+    // (branch-free and unchecked: past the end it reads the slot of the last
+    // row, which locate does not use)
+    auto load_slot = [&](int gi) -> int {
+        int grp;
+        split_pair(min(gi, total - 1), grp);
+        int t, h;
+        token_head(min(grp * 64 + lane, num_rows - 1), t, h);
+        return slots[t];
+    };
+    auto locate = [&](int gi, int slot) -> Loc {
+        Loc c;
+        int grp = groups;
+        c.layer = gi < total ? split_pair(gi, grp) : 0;
+        c.row = grp * 64 + lane;
+        c.live = gi < total && c.row < num_rows && slot >= 0;
+        int t, h, page, tib;
+        token_head(min(c.row, num_rows - 1), t, h);
+        split_slot(c.live ? slot : 0, g, page, tib);
+        c.cell = tib * g.H + h;
+        c.base = layers.pool[c.layer] + (size_t)page * g.page_size;
+        c.dummy = reinterpret_cast<const uint8_t*>(layers.out_key[c.layer]);
+        return c;
+    };
+    // 64 code bytes of the row (dword 4q + e holds elements 8(4q + e) .. + 7).
+    auto load_codes = [&](const Loc& c, uint64_t off, uint4 (&w)[4]) {
+        const uint4* p = reinterpret_cast<const uint4*>(
+            c.live ? c.base + off + (size_t)c.cell * 64 : c.dummy);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) w[q] = p[q];
+    };
+    struct Scales {
+        uint32_t ks, re, vs;  // raw fp16 in the low halves (converted when used)
+    };
+    auto load_scales = [&](const Loc& c, Scales& sc) {
+        const uint8_t* p = c.base + (size_t)c.cell * g.scale_stride;
+        sc.ks = ld_u16(c.live ? p + g.ks_off : c.dummy);
+        sc.vs = ld_u16(c.live ? p + g.vs_off : c.dummy);
+        sc.re = PROD ? ld_u16(c.live ? p + g.kres_off : c.dummy) : 0u;
+    };
+
+    // Decode, transform and store one tensor of the group (toff: its table;
+    // aoff: its output row address in the stage rows).
+    auto transform = [&](const uint4 (&cw)[4], uint32_t toff, uint32_t aoff, float se) {
+        float x[128];
+#pragma unroll
+        for (int c = 0; c < 16; ++c) {
+            const uint4 q = cw[c / 4];
+            const uint32_t w = c % 4 == 0 ? q.x : c % 4 == 1 ? q.y : c % 4 == 2 ? q.z : q.w;
+            // bytes 4*nibble + wave, for even and odd elements
+            const uint32_t ev = ((w << 2) & 0x3C3C3C3Cu) | wsplat;
+            const uint32_t od = ((w >> 2) & 0x3C3C3C3Cu) | wsplat;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                // bytes 0, 2, 3 from tbase, byte 1 = 4*nibble + wave
+                const uint32_t sel = 0x03020000u | ((uint32_t)(4 + b) << 8);
+                const uint32_t ae = __builtin_amdgcn_perm(ev, tbase, sel) + toff;
+                const uint32_t ao = __builtin_amdgcn_perm(od, tbase, sel) + toff;
+                x[8 * c + 2 * b] = *reinterpret_cast<const lds_float*>(ae);
+                x[8 * c + 2 * b + 1] = *reinterpret_cast<const lds_float*>(ao);
+            }
+            // (each dword's addresses die at its lookups: 128 live addresses
+            // on top of the 128 values would not fit two waves per SIMD)
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // The reference's stages in its order, len = 1, 2, ..., 64.
+#pragma unroll
+        for (int len = 1; len < 128; len *= 2) {
+#pragma unroll
+            for (int k = 0; k < 128; ++k) {
+                if ((k & len) == 0) {
+                    const float a = x[k], b = x[k + len];
+                    x[k] = a + b;
+                    x[k + len] = a - b;
+                }
+            }
+        }
+        // Element e has sign (-1)^(e + h): se for even e, -se for odd.
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            const float* c = x + 64 * half;
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                *reinterpret_cast<lds_u32x4*>(my_row + 16 * k) =
+                    u32x4{f2h2(c[8 * k] * se, c[8 * k + 1] * -se),
+                          f2h2(c[8 * k + 2] * se, c[8 * k + 3] * -se),
+                          f2h2(c[8 * k + 4] * se, c[8 * k + 5] * -se),
+                          f2h2(c[8 * k + 6] * se, c[8 * k + 7] * -se)};
+            // The stage is private to this wave: wave-scope ordering suffices.
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                const uint32_t src = rd_row + 8 * r * kRowStageBytes;
+                const u32x4 v = *reinterpret_cast<const lds_u32x4*>(src + 16 * (lane & 7));
+                const uint64_t a = *reinterpret_cast<const lds_u64*>(src + aoff);
+                global_u32x4* dst = reinterpret_cast<global_u32x4*>(a + 128 * half) + (lane & 7);
+                if (a != 0) __builtin_nontemporal_store(v, dst);
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+    };
+
+    // Loads in flight for half a group each: this group's V codes during its
+    // K transform; the next group's K codes, scales and the slot after it
+    // during its V transform.  Each lands in the registers its previous
+    // contents left (no copies, which would wait for the loads).
+    int gi = blockIdx.x * kWaves + wave;
+    Loc cur = locate(gi, load_slot(gi));
+    uint4 kw[4], vw[4];
+    Scales sc;
+    load_codes(cur, g.kc_off, kw);
+    load_scales(cur, sc);
+    int s_next = load_slot(gi + stride);
+    while (gi < total) {  // wave-uniform
+        load_codes(cur, g.vc_off, vw);
+        const Loc nxt = locate(gi + stride, s_next);
+        // This lane's row: its tables (16 entries per tensor, the reference's
+        // exact operations) and its output offset for the stores.
+        {
+            const float ks = h2f(sc.ks), vs = h2f(sc.vs), re = h2f(sc.re);
+#pragma unroll
+            for (int n = 0; n < 16; ++n) {
+                const float kv = PROD ? (kK3[n & 7] + re * ((n & 8) ? 1.0f : -1.0f)) * ks
+                                      : kV4[n] * ks;
+                *reinterpret_cast<lds_float*>(tbase + 1024u * n) = kv;
+                *reinterpret_cast<lds_float*>(tbase + kTabBytes + 1024u * n) = kV4[n] * vs;
+            }
+        }
+        int t, h;
+        token_head(min(cur.row, num_rows - 1), t, h);
+        {
+            const uint64_t eo = ol.offset(t, h);
+            const uint64_t ka = reinterpret_cast<uintptr_t>(layers.out_key[cur.layer] + eo);
+            const uint64_t va = reinterpret_cast<uintptr_t>(layers.out_value[cur.layer] + eo);
+            *reinterpret_cast<lds_u64*>(my_row + 128) = cur.live ? ka : 0;
+            *reinterpret_cast<lds_u64*>(my_row + 136) = cur.live ? va : 0;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const float se = (h & 1) ? -inv : inv;  // s(2j, h) * inv; s(2j+1, h) = -s(2j, h)
+        transform(kw, 0, 128, se);
+        load_codes(nxt, g.kc_off, kw);
+        load_scales(nxt, sc);
+        s_next = load_slot(gi + 2 * stride);
+        transform(vw, kTabBytes, 136, se);
+        cur = nxt;
+        gi += stride;
+    }
+}
+
+// The row-per-lane kernel reads codes as 16-byte pieces.
+bool rows_dequant_ok(const PageGeom& g, const void* pool, const void* ok, const void* ov) {
+    const auto al = [](uint64_t v, uint64_t a) { return (v & (a - 1)) == 0; };
+    return g.D == 128 && g.code_stride == 64 && al(g.page_size, 16) && al(g.kc_off, 16) &&
+           al(g.vc_off, 16) && al(g.ks_off, 2) && al(g.vs_off, 2) && al(g.kres_off, 2) &&
+           al(reinterpret_cast<uintptr_t>(pool), 16) &&
+           al(reinterpret_cast<uintptr_t>(ok), 16) && al(reinterpret_cast<uintptr_t>(ov), 16);
+}
+
 // The streaming kernel reads codes as dwords and writes 16-byte output chunks.
 bool wide_dequant_ok(const PageGeom& g, const void* pool, const void* ok, const void* ov) {
     const auto al = [](uint64_t v, uint64_t a) { return (v & (a - 1)) == 0; };
@@ -1022,7 +1270,14 @@ void launch_dequant_layers(Scheme s, const uint8_t* const* pools, const int32_t*
     ol.tok = head_major ? (uint64_t)g.D : (uint64_t)g.H * g.D;
     ol.head = head_major ? (uint64_t)num_tokens * g.D : (uint64_t)g.D;
     const bool prod = s == Scheme::Prod;
-    const int rows_per_block = kBlock / (g.D / 32);
+    // The row-per-lane kernel when every layer's buffers allow 16-byte code
+    // loads (per-layer launches keep the streaming kernel: one launch's 1024
+    // row groups of 64 fill a CU with one wave per SIMD, 12.8 against 10.4 us
+    // per 32K-token layer).
+    bool rows_ok = true;
+    for (int l = 0; l < num_layers && rows_ok; ++l)
+        rows_ok = rows_dequant_ok(g, pools[l], out_key[l], out_value[l]);
+    const int rows_per_block = rows_ok ? kBlock : kBlock / (g.D / 32);
     // The kernel counts (layer, row group) pairs in int32: keep them below 2^30.
     const int groups = (rows + 15) / 16;
     const int per_launch = (int)std::max(1LL, std::min<long long>(kMaxLayersPerLaunch,
@@ -1037,9 +1292,17 @@ void launch_dequant_layers(Scheme s, const uint8_t* const* pools, const int32_t*
         }
         const long long blocks_needed =
             ((long long)rows * n + rows_per_block - 1) / rows_per_block;
+        const int per_cu = rows_ok ? TQ_DEQ_ROWS_BLOCKS_PER_CU : TQ_DEQ_LAYERS_BLOCKS_PER_CU;
         const dim3 grid((unsigned)std::max(
-            1LL, std::min<long long>(blocks_needed, TQ_DEQ_LAYERS_BLOCKS_PER_CU * num_cus())));
-        if (prod)
+            1LL, std::min<long long>(blocks_needed, (long long)per_cu * num_cus())));
+        if (rows_ok) {
+            if (prod)
+                hipLaunchKernelGGL((dequant_rows_kernel<1, kMaxLayersPerLaunch>), grid,
+                                   dim3(kBlock), 0, stream, set, slots, g, rows, n, inv, ol);
+            else
+                hipLaunchKernelGGL((dequant_rows_kernel<0, kMaxLayersPerLaunch>), grid,
+                                   dim3(kBlock), 0, stream, set, slots, g, rows, n, inv, ol);
+        } else if (prod)
             hipLaunchKernelGGL((dequant_stream_kernel<128, 1, kMaxLayersPerLaunch>), grid,
                                dim3(kBlock), 0, stream, set, slots, g, rows, n, inv, ol);
         else
