@@ -425,5 +425,18 @@ __device__ __forceinline__ uint16_t ld_u16(const uint8_t* p) {
     return *reinterpret_cast<const uint16_t*>(p);
 }
 
+// Non-temporal loads (data read once: the L2 keeps what is reused).
+__device__ __forceinline__ uint16_t ld_u16_nt(const uint8_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(p));
+}
+__device__ __forceinline__ uint32_t ld_u32_nt(const uint8_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
+}
+__device__ __forceinline__ uint4 ld_u4_nt(const uint8_t* p) {
+    typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+    const v4u x = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
+    return make_uint4(x[0], x[1], x[2], x[3]);
+}
+
 }  // namespace dev
 }  // namespace tq
