@@ -556,6 +556,18 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
         // flight until the chunk is computed.
         const uint64_t dummy_off =
             (uint64_t)(reinterpret_cast<uintptr_t>(query) - reinterpret_cast<uintptr_t>(pool));
+        // Slot-mapped rows read each pool byte once: non-temporal loads keep
+        // the L2 for the slots and queries (10.3 -> 10.0 us per 32K layer).
+        // Paged rows keep plain loads: the workgroups of the two kv heads of
+        // a work segment read each 128-byte code line together, one through
+        // the other's L2 copy.
+        auto ld16 = [](const uint8_t* p) -> uint16_t { return PAGED ? ld_u16(p) : ld_u16_nt(p); };
+        auto ld32 = [](const uint8_t* p) -> uint32_t {
+            return PAGED ? *reinterpret_cast<const uint32_t*>(p) : ld_u32_nt(p);
+        };
+        auto ld128 = [](const uint8_t* p) -> uint4 {
+            return PAGED ? *reinterpret_cast<const uint4*>(p) : ld_u4_nt(p);
+        };
         auto fetch = [&](int t0, int slot, Chunk& c) {
             c.valid = t0 + (lane & (kChunk - 1)) < t_end && slot >= 0;
             int page, tib;
@@ -565,11 +577,9 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
             // Byte offsets from pool (integer selects: no branches around loads).
             // (distinct dummy bytes per field, so the three loads stay separate)
             const uint64_t so = pb + cell * g.scale_stride;
-            // (pool bytes are read once: non-temporal loads, which keep the L2
-            // for the slots, queries and partials; 10.3 -> 10.0 us per layer)
-            c.ks = ld_u16_nt(pool + (c.valid ? so + g.ks_off : dummy_off));
-            c.vs = ld_u16_nt(pool + (c.valid ? so + g.vs_off : dummy_off + 2));
-            c.re = PROD ? ld_u16_nt(pool + (c.valid ? so + g.kres_off : dummy_off + 4)) : (uint16_t)0;
+            c.ks = ld16(pool + (c.valid ? so + g.ks_off : dummy_off));
+            c.vs = ld16(pool + (c.valid ? so + g.vs_off : dummy_off + 2));
+            c.re = PROD ? ld16(pool + (c.valid ? so + g.kres_off : dummy_off + 4)) : (uint16_t)0;
             // (with 32-token chunks lanes l and l + 32 hold the same token)
             // K row: code_stride bytes, or QJL's D/8 = 16 sign bytes
             const uint64_t kstride = QJL ? 16u : (uint64_t)g.code_stride;
@@ -586,7 +596,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                         0u,
                         0u, 0u);
                 else
-                    c.kw[tau] = ld_u4_nt(pool + (tko[w][16 * tau + i] + 16 * gq));
+                    c.kw[tau] = ld128(pool + (tko[w][16 * tau + i] + 16 * gq));
             }
             // k-step p covers tiles 2p, 2p+1; k-index 8gq + e is token
             // 32p + 4gq + e (e < 4) or 32p + 16 + 4gq + (e - 4).
@@ -595,7 +605,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const int tok = 32 * p + (e < 4 ? 4 * gq + e : 16 + 4 * gq + (e - 4));
-                    c.vw[p][e] = ld_u32_nt(pool + (tvo[w][tok] + 4 * i));
+                    c.vw[p][e] = ld32(pool + (tvo[w][tok] + 4 * i));
                 }
         };
 
