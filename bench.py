@@ -989,7 +989,7 @@ def host_cpu() -> dict:
 
 def cpu_baseline(w: Workload, runs: int = 5, layers_per_run: int = 3):
     """The reference's CPU path for one decode step of this workload, on this
-    host (BASELINE.md section 3): per layer, the dequant (the oracle's C
+    host: per layer, the dequant (the oracle's C
     restatement of the reference kernel's operation order) to [N, H, D] fp16,
     the permute to [H, N, D] the reference's store does, and
     attention_ref_single_head (src/tq_attention_ref.cpp:10-56 semantics) for

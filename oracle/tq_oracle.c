@@ -786,7 +786,7 @@ void tqo_lloyd_max_gaussian(int M, int max_iter, double tol, double* levels, dou
 }
 
 /* ======================================================================== */
-/* Kernels the reference compiles but does not export:       */
+/* Kernels the reference compiles but does not export:                      */
 /* QJL-1b, the legacy INT4 and dense pages, and the GPU SDPA reference.       */
 /* ======================================================================== */
 

@@ -1,7 +1,7 @@
 """GPU parity: libturboquant.so (through the C ABI) against the CPU oracle on
 identical seeded inputs.
 
-Bar (BASELINE north_star): packed codes, scales and dequantized halves
+Bar: packed codes, scales and dequantized halves
 bit-exact; attention output within max rel err 1e-3 of the exact oracle,
 where rel err = max|o - r| / max|r| per (query row, kv head).
 """
@@ -314,7 +314,7 @@ def test_logits_unmapped_tokens_are_neg_inf(tq, oracle, cuda):
     assert (np.abs(got[:, :, live] - ref32[:, :, live]) / scale).max() < 1e-5
 
 
-# ---- full-size properties (BASELINE configs 2 and 3), sampled against the oracle ---
+# ---- full-size properties (32K-token layers), sampled against the oracle ---
 
 def test_full_size_prod_codec_sampled(tq, oracle, cuda):
     """Config 2/3 shape: 32768 tokens, 2 heads, D=128, shuffled pages.  The

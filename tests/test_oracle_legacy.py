@@ -4,7 +4,8 @@ QJL-1b (src/cuda/tq_qjl_kernels.cu), the legacy INT4 and dense pages
 the GPU SDPA reference (src/cuda/tq_attention_ref_kernel.cu).
 
 Pinned by: the reference's own layout factories built and run
-(tests/golden/ref_legacy_layouts.txt), SURVEY's published QJL page layout,
+(tests/golden/ref_legacy_layouts.txt), the QJL layout factory's arithmetic
+(src/tq_qjl.cpp:7-35) worked by hand for one page,
 float64 linear algebra (scipy's Hadamard matrix), numpy brute force
 (rint half-to-even, argmin), hand-derived known answers, and the reference's
 CPU SDPA (src/tq_attention_ref.cpp semantics)."""
@@ -68,7 +69,8 @@ def test_legacy_layout_rejects_what_reference_rejects(oracle):
 
 
 def test_qjl_layout_published_figures(oracle):
-    # k1 @0 (512), ks @512 (64), v4 @576 (2048), vs @2624 (64), page 2688
+    # src/tq_qjl.cpp:7-35 by hand for B = 16, H = 2, D = 128 (32 token-heads):
+    # k1 @0 (32 x 16 = 512), ks @512 (64), v4 @576 (32 x 64 = 2048), vs @2624 (64), page 2688
     L = oracle.qjl_layout(16, 2, 128)
     assert (L.k1_off, L.ks_off, L.v4_off, L.vs_off, L.page_size) == (0, 512, 576, 2624, 2688)
     assert (L.k1_bytes, L.v4_bytes, L.scale_bytes) == (16, 64, 2)
