@@ -1,7 +1,7 @@
 #!/usr/bin/env bash
 # Compiles the parts of the reference's CPU path that build from their own
 # sources with the system compiler (no CUDA headers, no stand-ins), straight
-# from /root/reference, into oracle/_ref/ (git-ignored, travels with gpurun):
+# from /root/reference, into oracle/_ref/ (git-ignored; the built files are used in place):
 #   gaussian_codebook   src/gaussian_codebook.cpp (its own main(): prints the
 #                       Lloyd-Max 8-level design that produced kK3Codebook)
 #   ref_layouts         src/tq_turbo_mse_layout.cpp + src/tq_layout.cpp with
