@@ -42,8 +42,8 @@ def log(msg: str) -> None:
 
 # The dominant kernel (the roofline's) and the decode-attention kernels, as
 # rocprofv3 names them (template argument 1 = turbo_prod).
-DEQUANT_KERNEL = "tq::dequant_rows_kernel<1, 64>"            # the 36-layer launch
-DEQUANT_KERNEL_1 = "tq::dequant_stream_kernel<128, 1, 1>"  # one layer per launch
+DEQUANT_KERNEL = "tq::dequant_rows_kernel<1, 64, 128>"       # the 36-layer launch
+DEQUANT_KERNEL_1 = "tq::dequant_rows_kernel<1, 1, 64>"     # one layer per launch
 ATTN_KERNELS = ("tq::attn_mfma_split_kernel<1, 32, 8, false, 1>", "tq::attn_mfma_combine_kernel")
 
 
@@ -365,7 +365,7 @@ def main() -> int:
                    "frac_hbm": round(mse_bytes / mse_us / 1e3 / HBM_PEAK_GBPS, 4),
                    "per_layer_launches_us_per_layer": round(mse1_us, 3),
                    "algorithmic_bytes_per_layer": mse_bytes,
-                   "kernel": "tq::dequant_rows_kernel<0, 64>: 36 layers, one launch"}
+                   "kernel": "tq::dequant_rows_kernel<0, 64, 128>: 36 layers, one launch"}
     log(f"[bench] turbo_mse dequant {mse_us:.2f} us/layer one launch, {mse1_us:.2f} per-layer")
     del srcs, dsts
 

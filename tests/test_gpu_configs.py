@@ -363,7 +363,8 @@ def test_dequant_layers_vs_oracle(tq, oracle, cuda, scheme, NL, N, H, head_major
 ])
 def test_dequant_layers_holes_and_geometry(tq, oracle, cuda, scheme, NL, N, H, B, head_major):
     """Unmapped tokens (slot -1) keep their output untouched; mapped ones are
-    bit-exact against the oracle, with non-power-of-two heads and blocks."""
+    bit-exact against the oracle, with non-power-of-two heads and blocks; for
+    the multi-layer entry and the one-layer entry."""
     D = 128
     print(f"[dequant_layers holes {scheme}] {NL} x {N} H={H} B={B} head_major={head_major}",
           flush=True)
@@ -397,6 +398,19 @@ def test_dequant_layers_holes_and_geometry(tq, oracle, cuda, scheme, NL, N, H, B
         assert np.array_equal(gk[live], wk[live]), layer
         assert np.array_equal(gv[live], wv[live]), layer
         assert np.all(gk[~live] == seven) and np.all(gv[~live] == seven), layer
+    # the one-layer entry on layer 0 (its own kernel choice), same bar
+    ok1 = torch.full(shape, 7.0, dtype=torch.float16, device=cuda)
+    ov1 = torch.full(shape, 7.0, dtype=torch.float16, device=cuda)
+    one = {(True, False): tq.dequant, (False, False): tq.mse_dequant,
+           (True, True): tq.dequant_hnd, (False, True): tq.mse_dequant_hnd}[(prod, head_major)]
+    one(pools[0], slots.to(cuda), ok1, ov1, lay, cfg, *((N,) if head_major else ()))
+    torch.cuda.synchronize()
+    wk, wv = fn(pools[0].cpu().numpy(), sl, H, D, B)
+    gk, gv = as_u16(ok1), as_u16(ov1)
+    if head_major:
+        gk, gv = gk[0].transpose(1, 0, 2), gv[0].transpose(1, 0, 2)
+    assert np.array_equal(gk[live], wk[live]) and np.array_equal(gv[live], wv[live])
+    assert np.all(gk[~live] == seven) and np.all(gv[~live] == seven)
 
 
 # ── multi-layer pack (config 2 in one launch) ───────────────────────── #

@@ -534,6 +534,11 @@ constexpr int kMaxLayersPerLaunch = 64;
 // Row-per-lane dequant workgroups per CU for a multi-layer launch (two
 // reside per CU; a grid of several rounds balances the tail: 36 x 32K-token
 // layers, 2 per CU 8.5 us/layer, 8: 8.2, 16-64: 7.9-8.0).
+// Half-row-per-lane dequant workgroups per CU for a one-layer launch (a
+// 32K-token, two-head layer needs 512: two per CU, all resident).
+#ifndef TQ_DEQ_ONE_BLOCKS_PER_CU
+#define TQ_DEQ_ONE_BLOCKS_PER_CU 8
+#endif
 #ifndef TQ_DEQ_ROWS_BLOCKS_PER_CU
 #define TQ_DEQ_ROWS_BLOCKS_PER_CU 24
 #endif
@@ -796,35 +801,44 @@ __global__ __launch_bounds__(kBlock) void dequant_stream_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Dequant, one row per lane (D = 128; turbo_prod and turbo_mse).  Every WHT
-// stage and both decode tables stay inside the lane: no cross-lane butterfly
-// (a DPP move plus an fmac per value per stage) and one table build per row
-// instead of one per lane of a row: 45 VALU instructions per row against 72
-// for the four-lanes-per-row form, which is VALU-bound here.  Lane l of a wave
-// group owns row 64*group + l; it loads the row's 64 code bytes per tensor
-// as four 16-byte loads.  The 128 outputs of a tensor leave in two halves
-// of one 128-byte line per row: each lane writes its half-row into a padded
-// wave-private LDS stage (144-byte rows: the 16-byte writes of eight
-// consecutive lanes cover the 32 banks once), then store r of the wave
-// writes rows 8r .. 8r + 7 of the group, eight whole lines per store.
-// Waves walk (layer, row group) pairs grid-stride with the next pair's
-// slot, codes and scales in flight.
+// Dequant, one row (E = 128) or half a row (E = 64) per lane (D = 128;
+// turbo_prod and turbo_mse).  With a whole row every WHT stage and both
+// decode tables stay inside the lane: no cross-lane butterfly (a DPP move
+// plus an fmac per value per stage) and one table build per row instead of
+// one per lane of a row: 45 VALU instructions per row against 72 for the
+// four-lanes-per-row form, which is VALU-bound here.  Half a row per lane
+// (52 per row) keeps one DPP stage and twice the waves, for launches with
+// few row groups.  Lane l of a wave group owns row 64*group + l (E = 64:
+// half l % 2 of row 32*group + l / 2); it loads its E/2 code bytes per
+// tensor as 16-byte loads.  The outputs leave one 128-byte line per lane at
+// a time: each lane writes its line into a padded wave-private LDS stage
+// (144-byte rows: the 16-byte writes of eight consecutive lanes cover the
+// 32 banks once), then store r of the wave writes the lines of lanes 8r ..
+// 8r + 7, eight whole lines per store.  Waves walk (layer, row group) pairs
+// grid-stride with the next pair's slot, codes and scales in flight.
 // ---------------------------------------------------------------------------
-constexpr int kRowStageBytes = 144;  // staged bytes per row: one output line + 16 of pad
+constexpr int kRowStageBytes = 144;  // staged bytes per lane: one output line + 16 of pad
 
-template <int SCH, int ML>
+template <int SCH, int ML, int E>
 __global__ __launch_bounds__(kBlock, 2) void dequant_rows_kernel(
     const LayerSet<ML> layers, const int32_t* __restrict__ slots, PageGeom g, int num_rows,
     int num_layers, float inv, OutLayout ol) {
     constexpr bool PROD = SCH == 1;
     static_assert(SCH == 0 || SCH == 1, "turbo_mse or turbo_prod pages");
+    // E = 128: lane l owns row l of the group's 64; E = 64: lanes 2r and
+    // 2r + 1 own halves 0 and 1 (elements 64j .. 64j + 63) of row r of 32, and
+    // the last WHT stage (len = 64) pairs them across the lane pair.
+    static_assert(E == 128 || E == 64, "a whole row or half a row per lane");
+    constexpr int LPR = 128 / E;   // lanes per row
+    constexpr int RPG = 64 / LPR;  // rows per wave group
+    constexpr int NQ = E / 32;     // 16-byte code loads per tensor and lane
     constexpr int kWaves = kBlock / 64;
     static_assert(kWaves == 4, "byte 1 of a table address holds 4*nibble + wave");
     // Tables as in dequant_stream_kernel: entry n of (wave w, lane l) is word
     // (n*4 + w)*64 + l of the tensor's 16 KiB, K first; then one stage per
-    // wave, 64 rows of kRowStageBytes: the row's half line (bytes 0..127) and
-    // the addresses of its K and V output rows (bytes 128 and 136; 0 for a
-    // row not written).
+    // wave, one kRowStageBytes row per lane: the lane's output line (bytes
+    // 0..127) and the addresses of its K and V output rows (bytes 128 and
+    // 136; 0 for a row not written).
     constexpr uint32_t kTabBytes = 16 * kWaves * 64 * sizeof(float);
     constexpr uint32_t kStageBytes = 64 * kRowStageBytes;
     // The kernel's only LDS object: it starts at LDS address 0, so byte 1 of
@@ -835,6 +849,8 @@ __global__ __launch_bounds__(kBlock, 2) void dequant_rows_kernel(
     typedef __attribute__((address_space(1))) u32x4 global_u32x4;
 
     const int lane = threadIdx.x & 63;
+    const int half_j = LPR == 2 ? (lane & 1) : 0;  // the half of the row this lane owns
+    const int rw = LPR == 2 ? (lane >> 1) : lane;   // its row in the group
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((lds_float*)(void*)lds);
     const uint32_t tbase = lds0 + 4u * lane + 256u * wave;  // entry 0 of this lane's K table
@@ -842,7 +858,7 @@ __global__ __launch_bounds__(kBlock, 2) void dequant_rows_kernel(
     const uint32_t stage = lds0 + 2 * kTabBytes + wave * kStageBytes;
     const uint32_t my_row = stage + lane * kRowStageBytes;        // staged by this lane
     const uint32_t rd_row = stage + (lane >> 3) * kRowStageBytes;  // read by store 0 (+ 8 rows per store)
-    const int groups = (num_rows + 63) / 64;  // row groups per layer
+    const int groups = (num_rows + RPG - 1) / RPG;  // row groups per layer
     const int total = groups * num_layers;    // (layer, group) pairs
     const int stride = gridDim.x * kWaves;
 
@@ -883,14 +899,14 @@ __global__ __launch_bounds__(kBlock, 2) void dequant_rows_kernel(
         int grp;
         split_pair(min(gi, total - 1), grp);
         int t, h;
-        token_head(min(grp * 64 + lane, num_rows - 1), t, h);
+        token_head(min(grp * RPG + rw, num_rows - 1), t, h);
         return slots[t];
     };
     auto locate = [&](int gi, int slot) -> Loc {
         Loc c;
         int grp = groups;
         c.layer = gi < total ? split_pair(gi, grp) : 0;
-        c.row = grp * 64 + lane;
+        c.row = grp * RPG + rw;
         c.live = gi < total && c.row < num_rows && slot >= 0;
         int t, h, page, tib;
         token_head(min(c.row, num_rows - 1), t, h);
@@ -900,12 +916,13 @@ __global__ __launch_bounds__(kBlock, 2) void dequant_rows_kernel(
         c.dummy = reinterpret_cast<const uint8_t*>(layers.out_key[c.layer]);
         return c;
     };
-    // 64 code bytes of the row (dword 4q + e holds elements 8(4q + e) .. + 7).
-    auto load_codes = [&](const Loc& c, uint64_t off, uint4 (&w)[4]) {
+    // The lane's E/2 code bytes of the row (dword 4q + e of them holds
+    // elements 64j + 8(4q + e) .. + 7).
+    auto load_codes = [&](const Loc& c, uint64_t off, uint4 (&w)[NQ]) {
         const uint4* p = reinterpret_cast<const uint4*>(
-            c.live ? c.base + off + (size_t)c.cell * 64 : c.dummy);
+            c.live ? c.base + off + (size_t)c.cell * 64 + 32 * half_j : c.dummy);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) w[q] = p[q];
+        for (int q = 0; q < NQ; ++q) w[q] = p[q];
     };
     struct Scales {
         uint32_t ks, re, vs;  // raw fp16 in the low halves (converted when used)
@@ -919,10 +936,10 @@ __global__ __launch_bounds__(kBlock, 2) void dequant_rows_kernel(
 
     // Decode, transform and store one tensor of the group (toff: its table;
     // aoff: its output row address in the stage rows).
-    auto transform = [&](const uint4 (&cw)[4], uint32_t toff, uint32_t aoff, float se) {
-        float x[128];
+    auto transform = [&](const uint4 (&cw)[NQ], uint32_t toff, uint32_t aoff, float se) {
+        float x[E];
 #pragma unroll
-        for (int c = 0; c < 16; ++c) {
+        for (int c = 0; c < E / 8; ++c) {
             const uint4 q = cw[c / 4];
             const uint32_t w = c % 4 == 0 ? q.x : c % 4 == 1 ? q.y : c % 4 == 2 ? q.z : q.w;
             // bytes 4*nibble + wave, for even and odd elements
@@ -941,11 +958,12 @@ __global__ __launch_bounds__(kBlock, 2) void dequant_rows_kernel(
             // on top of the 128 values would not fit two waves per SIMD)
             __builtin_amdgcn_sched_barrier(0);
         }
-        // The reference's stages in its order, len = 1, 2, ..., 64.
+        // The reference's stages in its order, len = 1, 2, ..., 64: in the
+        // lane up to E / 2 ...
 #pragma unroll
-        for (int len = 1; len < 128; len *= 2) {
+        for (int len = 1; len < E; len *= 2) {
 #pragma unroll
-            for (int k = 0; k < 128; ++k) {
+            for (int k = 0; k < E; ++k) {
                 if ((k & len) == 0) {
                     const float a = x[k], b = x[k + len];
                     x[k] = a + b;
@@ -953,9 +971,18 @@ __global__ __launch_bounds__(kBlock, 2) void dequant_rows_kernel(
                 }
             }
         }
-        // Element e has sign (-1)^(e + h): se for even e, -se for odd.
+        // ... and len = 64 across the lane pair: the lower half needs mine +
+        // partner, the upper partner - mine, both fmaf(mine, +-1, partner)
+        // exactly (exact product, one rounding of the sum).
+        if constexpr (LPR == 2) {
+            const float sg = half_j ? -1.0f : 1.0f;
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
+            for (int k = 0; k < E; ++k) x[k] = fmaf(x[k], sg, quad_xor<1>(x[k]));
+        }
+        // Element e has sign (-1)^(e + h): se for even e, -se for odd (64j is
+        // even).  Each lane's E outputs are E / 64 lines of 128 bytes.
+#pragma unroll
+        for (int half = 0; half < E / 64; ++half) {
             const float* c = x + 64 * half;
 #pragma unroll
             for (int k = 0; k < 8; ++k)
@@ -986,7 +1013,7 @@ __global__ __launch_bounds__(kBlock, 2) void dequant_rows_kernel(
     // contents left (no copies, which would wait for the loads).
     int gi = blockIdx.x * kWaves + wave;
     Loc cur = locate(gi, load_slot(gi));
-    uint4 kw[4], vw[4];
+    uint4 kw[NQ], vw[NQ];
     Scales sc;
     load_codes(cur, g.kc_off, kw);
     load_scales(cur, sc);
@@ -1009,7 +1036,7 @@ __global__ __launch_bounds__(kBlock, 2) void dequant_rows_kernel(
         int t, h;
         token_head(min(cur.row, num_rows - 1), t, h);
         {
-            const uint64_t eo = ol.offset(t, h);
+            const uint64_t eo = ol.offset(t, h) + 64 * half_j;
             const uint64_t ka = reinterpret_cast<uintptr_t>(layers.out_key[cur.layer] + eo);
             const uint64_t va = reinterpret_cast<uintptr_t>(layers.out_value[cur.layer] + eo);
             *reinterpret_cast<lds_u64*>(my_row + 128) = cur.live ? ka : 0;
@@ -1217,6 +1244,24 @@ void launch_dequant(Scheme s, const uint8_t* pool, const int32_t* slots, uint16_
     OutLayout ol;  // element offset of row (t, h): [N, H, D] or [H, N, D]
     ol.tok = head_major ? (uint64_t)g.D : (uint64_t)g.H * g.D;
     ol.head = head_major ? (uint64_t)num_tokens * g.D : (uint64_t)g.D;
+    // D = 128 with 16-byte aligned codes: half a row per lane (2,048 waves
+    // for a 32K-token, two-head layer: two per SIMD; 9.8 against 10.05 us for
+    // the four-lanes-per-row kernel, 12.8 for a whole row per lane).
+    if (rows_dequant_ok(g, pool, out_key, out_value)) {
+        constexpr int E1 = 64;
+        const int rows_per_block = kBlock * E1 / 128;
+        const int blocks_needed = (rows + rows_per_block - 1) / rows_per_block;
+        const dim3 grid(std::max(1, std::min(blocks_needed, TQ_DEQ_ONE_BLOCKS_PER_CU * num_cus())));
+        const LayerSet<1> one{{pool}, {out_key}, {out_value}};
+        if (s == Scheme::Prod)
+            hipLaunchKernelGGL((dequant_rows_kernel<1, 1, E1>), grid, dim3(kBlock), 0, stream, one,
+                               slots, g, rows, 1, inv, ol);
+        else
+            hipLaunchKernelGGL((dequant_rows_kernel<0, 1, E1>), grid, dim3(kBlock), 0, stream, one,
+                               slots, g, rows, 1, inv, ol);
+        check_launch(s == Scheme::Prod ? "turbo_prod_dequant_kv_kernel" : "turbo_mse_dequant_kv_kernel");
+        return;
+    }
     if (wide_dequant_ok(g, pool, out_key, out_value)) {
         // Persistent waves: up to four workgroups (one wave per SIMD each) per
         // CU, fewer when there is not enough work (measured: 4 per CU beats
@@ -1270,10 +1315,8 @@ void launch_dequant_layers(Scheme s, const uint8_t* const* pools, const int32_t*
     ol.tok = head_major ? (uint64_t)g.D : (uint64_t)g.H * g.D;
     ol.head = head_major ? (uint64_t)num_tokens * g.D : (uint64_t)g.D;
     const bool prod = s == Scheme::Prod;
-    // The row-per-lane kernel when every layer's buffers allow 16-byte code
-    // loads (per-layer launches keep the streaming kernel: one launch's 1024
-    // row groups of 64 fill a CU with one wave per SIMD, 12.8 against 10.4 us
-    // per 32K-token layer).
+    // A whole row per lane when every layer's buffers allow 16-byte code
+    // loads (half a row per lane: 9.1 against 8.0 us per 32K-token layer).
     bool rows_ok = true;
     for (int l = 0; l < num_layers && rows_ok; ++l)
         rows_ok = rows_dequant_ok(g, pools[l], out_key[l], out_value[l]);
@@ -1297,10 +1340,10 @@ void launch_dequant_layers(Scheme s, const uint8_t* const* pools, const int32_t*
             1LL, std::min<long long>(blocks_needed, (long long)per_cu * num_cus())));
         if (rows_ok) {
             if (prod)
-                hipLaunchKernelGGL((dequant_rows_kernel<1, kMaxLayersPerLaunch>), grid,
+                hipLaunchKernelGGL((dequant_rows_kernel<1, kMaxLayersPerLaunch, 128>), grid,
                                    dim3(kBlock), 0, stream, set, slots, g, rows, n, inv, ol);
             else
-                hipLaunchKernelGGL((dequant_rows_kernel<0, kMaxLayersPerLaunch>), grid,
+                hipLaunchKernelGGL((dequant_rows_kernel<0, kMaxLayersPerLaunch, 128>), grid,
                                    dim3(kBlock), 0, stream, set, slots, g, rows, n, inv, ol);
         } else if (prod)
             hipLaunchKernelGGL((dequant_stream_kernel<128, 1, kMaxLayersPerLaunch>), grid,
