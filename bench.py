@@ -200,12 +200,14 @@ def capture(fn, side):
         return None
 
 
-def event_time_us(run, reps):
-    """Mean duration of run() in µs from HIP events on the current stream."""
+def event_time_us(run, reps, warm: int = 1):
+    """Mean duration of run() in µs from HIP events on the current stream,
+    after `warm` untimed calls."""
     import torch
     a = torch.cuda.Event(enable_timing=True)
     b = torch.cuda.Event(enable_timing=True)
-    run()
+    for _ in range(warm):
+        run()
     a.record()
     for _ in range(reps):
         run()
@@ -328,7 +330,9 @@ def main() -> int:
         for _ in range(4):
             w.all_dequant()
     g4 = capture(four_dequants, side) if use_graph else None
-    launch_us = event_time_us(g4.replay if g4 is not None else four_dequants, reps) / 4
+    # (at least 100 timed launches after 12 untimed ones)
+    launch_us = event_time_us(g4.replay if g4 is not None else four_dequants, max(25, reps),
+                              warm=3) / 4
     deq_us = launch_us / w.NL
     deq1_us = event_time_us(run_deq1, reps) / w.NL
     att_us = event_time_us(run_att, reps) / w.NL
