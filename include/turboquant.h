@@ -236,7 +236,9 @@ int tq_load_turbo_mse_layers(const uint8_t* const* host_pools, uint8_t* const* d
  * t % block_size of page block_tables[s * max_blocks_per_seq + t /
  * block_size]; pages for every token a row attends must be valid.
  * max_kv_len >= every row_kv_len sizes the launch and must fit in
- * max_blocks_per_seq pages.  Rows with kv length 0 get 0.  head_dim 128. */
+ * max_blocks_per_seq pages.  Rows with kv length 0 get 0.  head_dim 128,
+ * and the pool and page size 16-byte aligned (a turbo_prod page is 134 bytes
+ * per token-head: block_size x num_kv_heads a multiple of 8); otherwise -2. */
 int tq_launch_turbo_prod_paged_attention(const uint16_t* query, const uint8_t* page_pool,
                                          const int32_t* block_tables, int max_blocks_per_seq,
                                          const int32_t* row_seq, const int32_t* row_kv_len,
