@@ -523,27 +523,29 @@ struct LayerSet {
     uint16_t* out_value[ML];
 };
 constexpr int kMaxLayersPerLaunch = 64;
-// Dequant workgroups per CU for a multi-layer launch.  32 KB of LDS per
-// workgroup lets 4 reside per CU; a grid of several such rounds balances the
-// tail (36 x 32K-token layers: 4 per CU 9.3 us/layer, 8: 9.0, 24: 8.6, 48-192:
-// 8.8-9.0).
-// Dequant workgroups per CU for a one-layer launch.
+// Launch shapes (workgroups per CU; measured on 32K-token, two-head layers).
+// The four-lanes-per-row kernel, one layer per launch (D = 32, 64, QJL,
+// buffers not 16-byte aligned): up to four persistent workgroups per CU.
 #ifndef TQ_DEQ_BLOCKS_PER_CU
 #define TQ_DEQ_BLOCKS_PER_CU 4
 #endif
-// Row-per-lane dequant workgroups per CU for a multi-layer launch (two
-// reside per CU; a grid of several rounds balances the tail: 36 x 32K-token
-// layers, 2 per CU 8.5 us/layer, 8: 8.2, 16-64: 7.9-8.0).
-// Half-row-per-lane dequant workgroups per CU for a one-layer launch (a
-// 32K-token, two-head layer needs 512: two per CU, all resident).
-#ifndef TQ_DEQ_ONE_BLOCKS_PER_CU
-#define TQ_DEQ_ONE_BLOCKS_PER_CU 8
+// The four-lanes-per-row kernel, several layers per launch (D = 128 with
+// unaligned buffers): 32 KB of LDS per workgroup lets 4 reside per CU; a
+// grid of several such rounds balances the tail (36 layers: 4 per CU
+// 9.3 us/layer, 8: 9.0, 24: 8.6, 48-192: 8.8-9.0).
+#ifndef TQ_DEQ_LAYERS_BLOCKS_PER_CU
+#define TQ_DEQ_LAYERS_BLOCKS_PER_CU 24
 #endif
+// A row per lane, several layers per launch: two workgroups reside per CU; a
+// grid of several rounds balances the tail (36 layers: 2 per CU 8.5 us/layer,
+// 8: 8.2, 16-64: 7.9-8.0).
 #ifndef TQ_DEQ_ROWS_BLOCKS_PER_CU
 #define TQ_DEQ_ROWS_BLOCKS_PER_CU 24
 #endif
-#ifndef TQ_DEQ_LAYERS_BLOCKS_PER_CU
-#define TQ_DEQ_LAYERS_BLOCKS_PER_CU 24
+// Half a row per lane, one layer per launch (a layer needs 512: two per CU,
+// all resident).
+#ifndef TQ_DEQ_ONE_BLOCKS_PER_CU
+#define TQ_DEQ_ONE_BLOCKS_PER_CU 8
 #endif
 
 // SCH: 0 turbo_mse, 1 turbo_prod, 2 the reference's unexported QJL-1b page
@@ -1264,8 +1266,8 @@ void launch_dequant(Scheme s, const uint8_t* pool, const int32_t* slots, uint16_
     }
     if (wide_dequant_ok(g, pool, out_key, out_value)) {
         // Persistent waves: up to four workgroups (one wave per SIMD each) per
-        // CU, fewer when there is not enough work (measured: 4 per CU beats
-        // 1 or 2 and equals 8 at the 32K-token layer).
+        // CU, fewer when there is not enough work (measured at D = 128: 4 per
+        // CU beat 1 or 2 and equalled 8).
         const int rows_per_block = kBlock / (g.D / 32);
         const int blocks_needed = (rows + rows_per_block - 1) / rows_per_block;
         const dim3 grid(std::max(1, std::min(blocks_needed, TQ_DEQ_BLOCKS_PER_CU * num_cus())));
