@@ -2,13 +2,15 @@
 library picks (a whole row per lane for several layers, half a row per lane
 for one layer, four lanes per row for other head dims, the generic kernel for
 pages not 4-byte aligned), both schemes, both output layouts, unmapped tokens,
-and attention on the same pools.
+and attention (and turbo_prod logits) on the same pools.
 
 Each case draws N in [1, 3000], H in {1, 2, 3, 4, 8}, a block size in
 {1, 3, 7, 16, 32} and D in {32, 64, 128} (mostly 128) from the splitmix64
 stream of the synthetic-input generator, so the cases are the same on every
 machine.  Bars: pools and dequantized halves bit-exact (unmapped tokens keep
-their output); attention within max rel err 1e-3 of the fp64 oracle.
+their output); attention within max rel err 1e-3 of the fp64 oracle;
+turbo_prod logits within 1e-5 of the oracle's fp32 logits (-inf for unmapped
+tokens).
 """
 from __future__ import annotations
 
@@ -122,3 +124,18 @@ def test_random_geometry_pack_dequant_attention(tq, oracle, cuda, i):
     r = ref.reshape(-1, D)
     err = (np.abs(g - r).max(axis=1) / np.maximum(np.abs(r).max(axis=1), 1e-30)).max()
     assert err <= 1e-3, err
+
+    # turbo_prod logits of 1-13 query rows over layer 0: within 1e-5 of the
+    # oracle's reference-order fp32 logits per row, -inf for unmapped tokens
+    if not prod:
+        return
+    Q = 1 + i % 13
+    q = kv_tokens_major(Q, H, D, seed=9500 + i)[0]
+    logits = torch.zeros(Q * H * N, dtype=torch.float32, device=cuda)
+    tq.fused_attn_logits(q.to(cuda), pools[0], slots, logits, lay, cfg, Q, N)
+    torch.cuda.synchronize()
+    got = logits.cpu().numpy().reshape(Q, H, N)
+    ref32 = oracle.prod_logits(as_u16(q), want_pools[0], sl, B)
+    assert np.all(np.isneginf(got[:, :, ~live]))
+    scale = np.abs(ref32[:, :, live]).max(axis=-1, keepdims=True) + 1e-30
+    assert (np.abs(got[:, :, live] - ref32[:, :, live]) / scale).max() < 1e-5
