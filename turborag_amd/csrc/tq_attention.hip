@@ -788,40 +788,62 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                     slot_nx = load_slot(t1 + kWaves * kChunk);
                 }
 
-                // QK: one decoded A operand per k-step, an MFMA per position
-                f32x4 cb[NPA][kTiles], cs[NPA][kTiles];
-        #pragma unroll
+                // The scale rows of this lane's tokens, read before any lookup
+                // (LDS reads complete in order: a read issued after the V
+                // lookups would wait for all of them).
+                float4 scv[kTiles][4];
+#pragma unroll
+                for (int tau = 0; tau < kTiles; ++tau)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) scv[tau][e] = tsc[w][16 * tau + 4 * gq + e];
+                // QK: every table lookup of the chunk's K codes is issued before
+                // the first MFMA, so their LDS latencies overlap.  prod: aK*K3
+                // (table 0); mse: aV*V4 hi parts (table 1) and lo parts (table 0)
+                // in kl; QJL: the sign octets.
+                half8 ka[kTiles][4], kl[kTiles][4];
+#pragma unroll
                 for (int tau = 0; tau < kTiles; ++tau) {
-        #pragma unroll
+                    const uint32_t wd[4] = {kw[tau].x, kw[tau].y, kw[tau].z, kw[tau].w};
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) {
+                        if constexpr (QJL) {  // sign byte s of the lane's word
+                            ka[tau][s] = signs(wd[0], s);
+                        } else {
+                            const int kt = PROD ? 0 : 1;
+                            ka[tau][s] = as_h8(lookup(wd[s], 0, kt), lookup(wd[s], 1, kt),
+                                               lookup(wd[s], 2, kt), lookup(wd[s], 3, kt));
+                            if constexpr (!PROD)
+                                kl[tau][s] = as_h8(lookup(wd[s], 0, 0), lookup(wd[s], 1, 0),
+                                                   lookup(wd[s], 2, 0), lookup(wd[s], 3, 0));
+                        }
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                f32x4 cb[NPA][kTiles], cs[NPA][kTiles];
+#pragma unroll
+                for (int tau = 0; tau < kTiles; ++tau) {
+#pragma unroll
                     for (int p = 0; p < NPA; ++p) {
                         cb[p][tau] = (f32x4){0.f, 0.f, 0.f, 0.f};
                         cs[p][tau] = cb[p][tau];
                     }
                     const uint32_t wd[4] = {kw[tau].x, kw[tau].y, kw[tau].z, kw[tau].w};
-        #pragma unroll
+#pragma unroll
                     for (int s = 0; s < 4; ++s) {
-                        if constexpr (QJL) {  // sign byte s of the lane's word
-                            const half8 sa = signs(wd[0], s);
-        #pragma unroll
+                        if constexpr (QJL) {
+#pragma unroll
                             for (int p = 0; p < NPA; ++p)
-                                cs[p][tau] = mma(sa, bq[p][s], cs[p][tau]);
+                                cs[p][tau] = mma(ka[tau][s], bq[p][s], cs[p][tau]);
                             continue;
                         }
-                        // prod: aK*K3 (table 0); mse: aV*V4 hi parts (table 1)
-                        const int kt = PROD ? 0 : 1;
-                        const half8 a = as_h8(lookup(wd[s], 0, kt), lookup(wd[s], 1, kt),
-                                              lookup(wd[s], 2, kt), lookup(wd[s], 3, kt));
-        #pragma unroll
+#pragma unroll
                         for (int p = 0; p < NPA; ++p)
-                            cb[p][tau] = mma(a, bq[p][s], cb[p][tau]);
-                        if (!PROD) {  // mse: the lo parts (table 0) into cs
-                            const half8 al = as_h8(lookup(wd[s], 0, 0), lookup(wd[s], 1, 0),
-                                                   lookup(wd[s], 2, 0), lookup(wd[s], 3, 0));
-        #pragma unroll
+                            cb[p][tau] = mma(ka[tau][s], bq[p][s], cb[p][tau]);
+                        if constexpr (!PROD) {  // mse: the lo parts into cs
+#pragma unroll
                             for (int p = 0; p < NPA; ++p)
-                                cs[p][tau] = mma(al, bq[p][s], cs[p][tau]);
-                        }
-                        if (PROD) {
+                                cs[p][tau] = mma(kl[tau][s], bq[p][s], cs[p][tau]);
+                        } else {
                             // Residual signs (nibble bit 3: 1 -> +1) as fp16 pairs in
                             // registers: high bytes 0x3C / 0xBC, low bytes 0.
                             // even d, odd d
@@ -831,24 +853,41 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                                                    __builtin_amdgcn_perm(ho, he, 0x050C010Cu),
                                                    __builtin_amdgcn_perm(ho, he, 0x060C020Cu),
                                                    __builtin_amdgcn_perm(ho, he, 0x070C030Cu));
-        #pragma unroll
+#pragma unroll
                             for (int p = 0; p < NPA; ++p)
                                 cs[p][tau] = mma(sa, bq[p][s], cs[p][tau]);
                         }
                     }
                 }
+                // The V lookups (B operands of PV) go out now: the softmax below
+                // runs while they are in flight.
+                uint32_t bv[kSteps][8][4];  // [step][N-tile v = d - 8i][token pair]
+#pragma unroll
+                for (int st = 0; st < kSteps; ++st)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const uint32_t we = vw[st][2 * q], wo = vw[st][2 * q + 1];
+                        const uint32_t lob = (we & 0x0F0F0F0Fu) | ((wo & 0x0F0F0F0Fu) << 4);
+                        const uint32_t hib = ((we >> 4) & 0x0F0F0F0Fu) | (wo & 0xF0F0F0F0u);
+#pragma unroll
+                        for (int b = 0; b < 4; ++b) {
+                            bv[st][2 * b][q] = lookup(lob, b, 1);
+                            bv[st][2 * b + 1][q] = lookup(hib, b, 1);
+                        }
+                    }
+                __builtin_amdgcn_sched_barrier(0);
                 // Logits (base 2) of tokens 16*tau + 4*gq + e; hi + lo columns summed.
                 float lg[NPA][kTiles][4];
-        #pragma unroll
+#pragma unroll
                 for (int p = 0; p < NPA; ++p) {
                     // rows shorter than the chunk's end need the causal mask
                     const bool masked = PAGED && t0 + kChunk > gmin[p];
                     float mloc = -INFINITY;
-        #pragma unroll
+#pragma unroll
                     for (int tau = 0; tau < kTiles; ++tau)
-        #pragma unroll
+#pragma unroll
                         for (int e = 0; e < 4; ++e) {
-                            const float4 sc = tsc[w][16 * tau + 4 * gq + e];
+                            const float4 sc = scv[tau][e];
                             if constexpr (QJL) {
                                 const float sr = cs[p][tau][e] + quad_xor<1>(cs[p][tau][e]);
                                 lg[p][tau][e] = fmaf(sr, sc.y, sc.w);
@@ -870,9 +909,9 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                     const float alpha = first ? 0.0f : __builtin_amdgcn_exp2f(m_run[p] - m_new);
                     m_run[p] = m_new;
                     float lsum = 0.0f;
-        #pragma unroll
+#pragma unroll
                     for (int tau = 0; tau < kTiles; ++tau)
-        #pragma unroll
+#pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             lg[p][tau][e] = __builtin_amdgcn_exp2f(lg[p][tau][e] - m_new);
                             lsum += lg[p][tau][e];
@@ -881,7 +920,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                     if (!first && __any(alpha != 1.0f)) {
                         // acc lane (d, gq) holds columns 4gq..4gq+3 = rows 2gq, 2gq+1.
                         const float a0 = __shfl(alpha, 4 * gq), a1 = __shfl(alpha, 4 * gq + 2);
-        #pragma unroll
+#pragma unroll
                         for (int v = 0; v < 8; ++v) {
                             acc[p][v][0] *= a0;
                             acc[p][v][1] *= a0;
@@ -891,33 +930,21 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                     }
                 }
                 // PV: one decoded B operand per N-tile, an MFMA per position
-        #pragma unroll
+#pragma unroll
                 for (int st = 0; st < kSteps; ++st) {
                     half8 ap[NPA];
-        #pragma unroll
+#pragma unroll
                     for (int p = 0; p < NPA; ++p)
-        #pragma unroll
+#pragma unroll
                         for (int e = 0; e < 8; ++e) {
                             const int tau = 2 * st + (e >> 2), ee = e & 3;
-                            const float vs = tsc[w][16 * tau + 4 * gq + ee].z;
-                            ap[p][e] = hi_lo(lg[p][tau][ee] * vs, lo_col);
+                            ap[p][e] = hi_lo(lg[p][tau][ee] * scv[tau][ee].z, lo_col);
                         }
-                    uint32_t bv[8][4];  // [N-tile v = d - 8i][token pair]
-        #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const uint32_t we = vw[st][2 * q], wo = vw[st][2 * q + 1];
-                        const uint32_t lob = (we & 0x0F0F0F0Fu) | ((wo & 0x0F0F0F0Fu) << 4);
-                        const uint32_t hib = ((we >> 4) & 0x0F0F0F0Fu) | (wo & 0xF0F0F0F0u);
-        #pragma unroll
-                        for (int b = 0; b < 4; ++b) {
-                            bv[2 * b][q] = lookup(lob, b, 1);
-                            bv[2 * b + 1][q] = lookup(hib, b, 1);
-                        }
-                    }
-        #pragma unroll
+#pragma unroll
                     for (int v = 0; v < 8; ++v) {
-                        const half8 bvv = as_h8(bv[v][0], bv[v][1], bv[v][2], bv[v][3]);
-        #pragma unroll
+                        const half8 bvv =
+                            as_h8(bv[st][v][0], bv[st][v][1], bv[st][v][2], bv[st][v][3]);
+#pragma unroll
                         for (int p = 0; p < NPA; ++p)
                             acc[p][v] = mma(ap[p], bvv, acc[p][v]);
                     }
