@@ -9,6 +9,7 @@
 // to the reference's CUDA kernels (given correctly rounded / and sqrt, which
 // this library is compiled for).
 #include <algorithm>
+#include <type_traits>
 
 #include "tq_device.h"
 
@@ -820,6 +821,13 @@ __global__ __launch_bounds__(kBlock) void dequant_stream_kernel(
 // grid-stride with the next pair's slot, codes and scales in flight.
 // ---------------------------------------------------------------------------
 constexpr int kRowStageBytes = 144;  // staged bytes per lane: one output line + 16 of pad
+// Half a row per lane (one layer per launch) stores through buffer
+// descriptors of num_rows * 256 bytes: a skipped row's byte offset is
+// kBufSkip, past the end of every buffer the launcher allows (rows up to
+// kBufMaxRows), so the hardware's range check drops its stores.
+constexpr uint32_t kBufSkip = 0x80000000u;
+constexpr int kBufMaxRows = (int)(kBufSkip / 256u) - 1;
+constexpr uint32_t kBufWord3 = 0x00020000u;  // descriptor word 3 on gfx9: 32-bit data format
 // Row-per-lane dequant: staged output lines (and their row addresses) read
 // from LDS this many stores ahead of the store that writes them, 1..7 (36
 // layers of 32K tokens in one launch: 8.20 us per layer with each read just
@@ -845,16 +853,26 @@ __global__ __launch_bounds__(kBlock, 2) void dequant_rows_kernel(
     constexpr int NQ = E / 32;     // 16-byte code loads per tensor and lane
     constexpr int kWaves = kBlock / 64;
     static_assert(kWaves == 4, "byte 1 of a table address holds 4*nibble + wave");
+    // Stores of half a row per lane (E = 64, one layer per launch) are buffer
+    // stores at the row's byte offset in its layer's output, a skipped row's
+    // offset lying past the buffer's end (the store is dropped, no branch);
+    // K and V share one decode table, the V table written after the K
+    // transform.  (Per-layer launches: 9.4 -> 9.1 us per 32K-token layer.
+    // The same form in the whole-row kernel, three waves per SIMD by its
+    // registers and LDS, ran 4% slower than branch-masked 64-bit stores.)
+    constexpr bool kBuf = E == 64;
     // Tables as in dequant_stream_kernel: entry n of (wave w, lane l) is word
-    // (n*4 + w)*64 + l of the tensor's 16 KiB, K first; then one stage per
-    // wave, one kRowStageBytes row per lane: the lane's output line (bytes
-    // 0..127) and the addresses of its K and V output rows (bytes 128 and
-    // 136; 0 for a row not written).
+    // (n*4 + w)*64 + l of the tensor's 16 KiB, K first (kBuf: one table);
+    // then one stage per wave, one kRowStageBytes row per lane: the lane's
+    // output line (bytes 0..127) and where its K and V output rows go (bytes
+    // 128 and 136, their addresses, 0 for a row not written; kBuf: bytes 128,
+    // the byte offset of both, kBufSkip for a row not written).
     constexpr uint32_t kTabBytes = 16 * kWaves * 64 * sizeof(float);
+    constexpr uint32_t kTables = kBuf ? 1 : 2;
     constexpr uint32_t kStageBytes = 64 * kRowStageBytes;
     // The kernel's only LDS object: it starts at LDS address 0, so byte 1 of
     // an entry's address is 4*nibble + wave and the bytes above it are zero.
-    __shared__ __attribute__((aligned(1024))) uint32_t lds[(2 * kTabBytes + kWaves * kStageBytes) / 4];
+    __shared__ __attribute__((aligned(1024))) uint32_t lds[(kTables * kTabBytes + kWaves * kStageBytes) / 4];
     typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
     typedef __attribute__((address_space(3))) uint64_t lds_u64;
     typedef __attribute__((address_space(1))) u32x4 global_u32x4;
@@ -866,7 +884,7 @@ __global__ __launch_bounds__(kBlock, 2) void dequant_rows_kernel(
     const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((lds_float*)(void*)lds);
     const uint32_t tbase = lds0 + 4u * lane + 256u * wave;  // entry 0 of this lane's K table
     const uint32_t wsplat = 0x01010101u * (uint32_t)wave;
-    const uint32_t stage = lds0 + 2 * kTabBytes + wave * kStageBytes;
+    const uint32_t stage = lds0 + kTables * kTabBytes + wave * kStageBytes;
     const uint32_t my_row = stage + lane * kRowStageBytes;        // staged by this lane
     const uint32_t rd_row = stage + (lane >> 3) * kRowStageBytes;  // read by store 0 (+ 8 rows per store)
     const int groups = (num_rows + RPG - 1) / RPG;  // row groups per layer
@@ -946,8 +964,10 @@ __global__ __launch_bounds__(kBlock, 2) void dequant_rows_kernel(
     };
 
     // Decode, transform and store one tensor of the group (toff: its table;
-    // aoff: its output row address in the stage rows).
-    auto transform = [&](const uint4 (&cw)[NQ], uint32_t toff, uint32_t aoff, float se) {
+    // aoff: its output row address in the stage rows; rs: kBuf's buffer of
+    // the tensor's output in this layer).
+    auto transform = [&](const uint4 (&cw)[NQ], uint32_t toff, uint32_t aoff, float se,
+                         __amdgpu_buffer_rsrc_t rs) {
         float x[E];
 #pragma unroll
         for (int c = 0; c < E / 8; ++c) {
@@ -1009,21 +1029,30 @@ __global__ __launch_bounds__(kBlock, 2) void dequant_rows_kernel(
             // ahead, so the LDS round trips overlap the stores instead of
             // preceding each one.
             constexpr int P = kStoreAhead;
+            using Where = typename std::conditional<kBuf, uint32_t, uint64_t>::type;
             u32x4 vr[P + 1];
-            uint64_t ar[P + 1];
+            Where ar[P + 1];
             auto read = [&](int r) {
                 const uint32_t src = rd_row + 8 * r * kRowStageBytes;
                 vr[r % (P + 1)] = *reinterpret_cast<const lds_u32x4*>(src + 16 * (lane & 7));
-                ar[r % (P + 1)] = *reinterpret_cast<const lds_u64*>(src + aoff);
+                ar[r % (P + 1)] = *reinterpret_cast<const __attribute__((address_space(3))) Where*>(
+                    src + aoff);
             };
 #pragma unroll
             for (int r = 0; r < P; ++r) read(r);
 #pragma unroll
             for (int r = 0; r < 8; ++r) {
                 if (r + P < 8) read(r + P);
-                const uint64_t a = ar[r % (P + 1)];
-                global_u32x4* dst = reinterpret_cast<global_u32x4*>(a + 128 * half) + (lane & 7);
-                if (a != 0) __builtin_nontemporal_store(vr[r % (P + 1)], dst);
+                if constexpr (kBuf) {  // (aux 2: non-temporal)
+                    __builtin_amdgcn_raw_buffer_store_b128(
+                        vr[r % (P + 1)], rs, ar[r % (P + 1)] + 128 * half + 16 * (lane & 7), 0,
+                        2);
+                } else {
+                    const uint64_t a = ar[r % (P + 1)];
+                    global_u32x4* dst =
+                        reinterpret_cast<global_u32x4*>(a + 128 * half) + (lane & 7);
+                    if (a != 0) __builtin_nontemporal_store(vr[r % (P + 1)], dst);
+                }
             }
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -1046,20 +1075,28 @@ __global__ __launch_bounds__(kBlock, 2) void dequant_rows_kernel(
         const Loc nxt = locate(gi + stride, s_next);
         // This lane's row: its tables (16 entries per tensor, the reference's
         // exact operations) and its output offset for the stores.
+        const float vs = h2f(sc.vs);
+        auto v_table = [&](uint32_t toff) {
+#pragma unroll
+            for (int n = 0; n < 16; ++n)
+                *reinterpret_cast<lds_float*>(tbase + toff + 1024u * n) = kV4[n] * vs;
+        };
         {
-            const float ks = h2f(sc.ks), vs = h2f(sc.vs), re = h2f(sc.re);
+            const float ks = h2f(sc.ks), re = h2f(sc.re);
 #pragma unroll
             for (int n = 0; n < 16; ++n) {
                 const float kv = PROD ? (kK3[n & 7] + re * ((n & 8) ? 1.0f : -1.0f)) * ks
                                       : kV4[n] * ks;
                 *reinterpret_cast<lds_float*>(tbase + 1024u * n) = kv;
-                *reinterpret_cast<lds_float*>(tbase + kTabBytes + 1024u * n) = kV4[n] * vs;
             }
+            if constexpr (!kBuf) v_table(kTabBytes);
         }
         int t, h;
         token_head(min(cur.row, num_rows - 1), t, h);
-        {
-            const uint64_t eo = ol.offset(t, h) + 64 * half_j;
+        const uint64_t eo = ol.offset(t, h) + 64 * half_j;
+        if constexpr (kBuf) {
+            *reinterpret_cast<lds_u32*>(my_row + 128) = cur.live ? (uint32_t)(2 * eo) : kBufSkip;
+        } else {
             const uint64_t ka = reinterpret_cast<uintptr_t>(layers.out_key[cur.layer] + eo);
             const uint64_t va = reinterpret_cast<uintptr_t>(layers.out_value[cur.layer] + eo);
             *reinterpret_cast<lds_u64*>(my_row + 128) = cur.live ? ka : 0;
@@ -1068,11 +1105,22 @@ __global__ __launch_bounds__(kBlock, 2) void dequant_rows_kernel(
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         const float se = (h & 1) ? -inv : inv;  // s(2j, h) * inv; s(2j+1, h) = -s(2j, h)
-        transform(kw, 0, 128, se);
+        // kBuf: the layer's K and V outputs as buffers of num_rows * 256 bytes
+        // (below kBufSkip: the launcher's row limit)
+        const int lyr = __builtin_amdgcn_readfirstlane(cur.layer);
+        const uint32_t out_bytes = kBuf ? (uint32_t)num_rows * 256u : 0u;
+        transform(kw, 0, 128, se,
+                  __builtin_amdgcn_make_buffer_rsrc(layers.out_key[lyr], 0, out_bytes, kBufWord3));
         load_codes(nxt, g.kc_off, kw);
         load_scales(nxt, sc);
         s_next = load_slot(gi + 2 * stride);
-        transform(vw, kTabBytes, 136, se);
+        if constexpr (kBuf) {  // the V table over the K table (this lane's K lookups are done)
+            v_table(0);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+        transform(vw, kBuf ? 0 : kTabBytes, kBuf ? 128 : 136, se,
+                  __builtin_amdgcn_make_buffer_rsrc(layers.out_value[lyr], 0, out_bytes, kBufWord3));
         cur = nxt;
         gi += stride;
     }
@@ -1270,7 +1318,7 @@ void launch_dequant(Scheme s, const uint8_t* pool, const int32_t* slots, uint16_
     // D = 128 with 16-byte aligned codes: half a row per lane (2,048 waves
     // for a 32K-token, two-head layer: two per SIMD; 9.8 against 10.05 us for
     // the four-lanes-per-row kernel, 12.8 for a whole row per lane).
-    if (rows_dequant_ok(g, pool, out_key, out_value)) {
+    if (rows <= kBufMaxRows && rows_dequant_ok(g, pool, out_key, out_value)) {
         constexpr int E1 = 64;
         const int rows_per_block = kBlock * E1 / 128;
         const int blocks_needed = (rows + rows_per_block - 1) / rows_per_block;
