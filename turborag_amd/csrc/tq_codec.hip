@@ -9,7 +9,6 @@
 // to the reference's CUDA kernels (given correctly rounded / and sqrt, which
 // this library is compiled for).
 #include <algorithm>
-#include <type_traits>
 
 #include "tq_device.h"
 
@@ -821,10 +820,10 @@ __global__ __launch_bounds__(kBlock) void dequant_stream_kernel(
 // grid-stride with the next pair's slot, codes and scales in flight.
 // ---------------------------------------------------------------------------
 constexpr int kRowStageBytes = 144;  // staged bytes per lane: one output line + 16 of pad
-// Half a row per lane (one layer per launch) stores through buffer
-// descriptors of num_rows * 256 bytes: a skipped row's byte offset is
-// kBufSkip, past the end of every buffer the launcher allows (rows up to
-// kBufMaxRows), so the hardware's range check drops its stores.
+// The row kernels store through buffer descriptors of a layer's output,
+// num_rows * 256 bytes each: a skipped row's byte offset is kBufSkip, past
+// the end of every buffer the launchers allow (rows up to kBufMaxRows), so
+// the hardware's range check drops its stores without a branch.
 constexpr uint32_t kBufSkip = 0x80000000u;
 constexpr int kBufMaxRows = (int)(kBufSkip / 256u) - 1;
 constexpr uint32_t kBufWord3 = 0x00020000u;  // descriptor word 3 on gfx9: 32-bit data format
@@ -853,29 +852,24 @@ __global__ __launch_bounds__(kBlock, 2) void dequant_rows_kernel(
     constexpr int NQ = E / 32;     // 16-byte code loads per tensor and lane
     constexpr int kWaves = kBlock / 64;
     static_assert(kWaves == 4, "byte 1 of a table address holds 4*nibble + wave");
-    // Stores of half a row per lane (E = 64, one layer per launch) are buffer
-    // stores at the row's byte offset in its layer's output, a skipped row's
-    // offset lying past the buffer's end (the store is dropped, no branch);
-    // K and V share one decode table, the V table written after the K
-    // transform.  (Per-layer launches: 9.4 -> 9.1 us per 32K-token layer.
-    // The same form in the whole-row kernel, three waves per SIMD by its
-    // registers and LDS, ran 4% slower than branch-masked 64-bit stores.)
-    constexpr bool kBuf = E == 64;
+    // Half a row per lane: K and V share one decode table, the V table
+    // written after the K transform (52 KB of LDS per workgroup against 68;
+    // per-layer launches 9.4 -> 9.1 us per 32K-token layer).  A whole row
+    // per lane keeps two tables: sharing them gives it three waves per SIMD,
+    // 4% slower.
+    constexpr bool kShare = E == 64;
     // Tables as in dequant_stream_kernel: entry n of (wave w, lane l) is word
-    // (n*4 + w)*64 + l of the tensor's 16 KiB, K first (kBuf: one table);
+    // (n*4 + w)*64 + l of the tensor's 16 KiB, K first (kShare: one table);
     // then one stage per wave, one kRowStageBytes row per lane: the lane's
-    // output line (bytes 0..127) and where its K and V output rows go (bytes
-    // 128 and 136, their addresses, 0 for a row not written; kBuf: bytes 128,
-    // the byte offset of both, kBufSkip for a row not written).
+    // output line (bytes 0..127) and the byte offset of its K and V output
+    // rows in their buffers (bytes 128..131; kBufSkip for a row not written).
     constexpr uint32_t kTabBytes = 16 * kWaves * 64 * sizeof(float);
-    constexpr uint32_t kTables = kBuf ? 1 : 2;
+    constexpr uint32_t kTables = kShare ? 1 : 2;
     constexpr uint32_t kStageBytes = 64 * kRowStageBytes;
     // The kernel's only LDS object: it starts at LDS address 0, so byte 1 of
     // an entry's address is 4*nibble + wave and the bytes above it are zero.
     __shared__ __attribute__((aligned(1024))) uint32_t lds[(kTables * kTabBytes + kWaves * kStageBytes) / 4];
     typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
-    typedef __attribute__((address_space(3))) uint64_t lds_u64;
-    typedef __attribute__((address_space(1))) u32x4 global_u32x4;
 
     const int lane = threadIdx.x & 63;
     const int half_j = LPR == 2 ? (lane & 1) : 0;  // the half of the row this lane owns
@@ -964,9 +958,8 @@ __global__ __launch_bounds__(kBlock, 2) void dequant_rows_kernel(
     };
 
     // Decode, transform and store one tensor of the group (toff: its table;
-    // aoff: its output row address in the stage rows; rs: kBuf's buffer of
-    // the tensor's output in this layer).
-    auto transform = [&](const uint4 (&cw)[NQ], uint32_t toff, uint32_t aoff, float se,
+    // rs: the tensor's output in this layer as a buffer).
+    auto transform = [&](const uint4 (&cw)[NQ], uint32_t toff, float se,
                          __amdgpu_buffer_rsrc_t rs) {
         float x[E];
 #pragma unroll
@@ -1025,34 +1018,25 @@ __global__ __launch_bounds__(kBlock, 2) void dequant_rows_kernel(
             // The stage is private to this wave: wave-scope ordering suffices.
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            // Store r's line and row address are read kStoreAhead stores
+            // Store r's line and row offset are read kStoreAhead stores
             // ahead, so the LDS round trips overlap the stores instead of
             // preceding each one.
             constexpr int P = kStoreAhead;
-            using Where = typename std::conditional<kBuf, uint32_t, uint64_t>::type;
             u32x4 vr[P + 1];
-            Where ar[P + 1];
+            uint32_t ar[P + 1];
             auto read = [&](int r) {
                 const uint32_t src = rd_row + 8 * r * kRowStageBytes;
                 vr[r % (P + 1)] = *reinterpret_cast<const lds_u32x4*>(src + 16 * (lane & 7));
-                ar[r % (P + 1)] = *reinterpret_cast<const __attribute__((address_space(3))) Where*>(
-                    src + aoff);
+                ar[r % (P + 1)] = *reinterpret_cast<const lds_u32*>(src + 128);
             };
 #pragma unroll
             for (int r = 0; r < P; ++r) read(r);
 #pragma unroll
             for (int r = 0; r < 8; ++r) {
                 if (r + P < 8) read(r + P);
-                if constexpr (kBuf) {  // (aux 2: non-temporal)
-                    __builtin_amdgcn_raw_buffer_store_b128(
-                        vr[r % (P + 1)], rs, ar[r % (P + 1)] + 128 * half + 16 * (lane & 7), 0,
-                        2);
-                } else {
-                    const uint64_t a = ar[r % (P + 1)];
-                    global_u32x4* dst =
-                        reinterpret_cast<global_u32x4*>(a + 128 * half) + (lane & 7);
-                    if (a != 0) __builtin_nontemporal_store(vr[r % (P + 1)], dst);
-                }
+                // (aux 2: non-temporal)
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    vr[r % (P + 1)], rs, ar[r % (P + 1)] + 128 * half + 16 * (lane & 7), 0, 2);
             }
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -1089,37 +1073,30 @@ __global__ __launch_bounds__(kBlock, 2) void dequant_rows_kernel(
                                       : kV4[n] * ks;
                 *reinterpret_cast<lds_float*>(tbase + 1024u * n) = kv;
             }
-            if constexpr (!kBuf) v_table(kTabBytes);
+            if constexpr (!kShare) v_table(kTabBytes);
         }
         int t, h;
         token_head(min(cur.row, num_rows - 1), t, h);
-        const uint64_t eo = ol.offset(t, h) + 64 * half_j;
-        if constexpr (kBuf) {
-            *reinterpret_cast<lds_u32*>(my_row + 128) = cur.live ? (uint32_t)(2 * eo) : kBufSkip;
-        } else {
-            const uint64_t ka = reinterpret_cast<uintptr_t>(layers.out_key[cur.layer] + eo);
-            const uint64_t va = reinterpret_cast<uintptr_t>(layers.out_value[cur.layer] + eo);
-            *reinterpret_cast<lds_u64*>(my_row + 128) = cur.live ? ka : 0;
-            *reinterpret_cast<lds_u64*>(my_row + 136) = cur.live ? va : 0;
-        }
+        const uint64_t eo = ol.offset(t, h) + 64 * half_j;  // element offset of the lane's line
+        *reinterpret_cast<lds_u32*>(my_row + 128) = cur.live ? (uint32_t)(2 * eo) : kBufSkip;
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         const float se = (h & 1) ? -inv : inv;  // s(2j, h) * inv; s(2j+1, h) = -s(2j, h)
-        // kBuf: the layer's K and V outputs as buffers of num_rows * 256 bytes
-        // (below kBufSkip: the launcher's row limit)
+        // The layer's K and V outputs as buffers of num_rows * 256 bytes
+        // (below kBufSkip: the launchers' row limit).
         const int lyr = __builtin_amdgcn_readfirstlane(cur.layer);
-        const uint32_t out_bytes = kBuf ? (uint32_t)num_rows * 256u : 0u;
-        transform(kw, 0, 128, se,
+        const uint32_t out_bytes = (uint32_t)num_rows * 256u;
+        transform(kw, 0, se,
                   __builtin_amdgcn_make_buffer_rsrc(layers.out_key[lyr], 0, out_bytes, kBufWord3));
         load_codes(nxt, g.kc_off, kw);
         load_scales(nxt, sc);
         s_next = load_slot(gi + 2 * stride);
-        if constexpr (kBuf) {  // the V table over the K table (this lane's K lookups are done)
+        if constexpr (kShare) {  // the V table over the K table (this lane's K lookups are done)
             v_table(0);
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
-        transform(vw, kBuf ? 0 : kTabBytes, kBuf ? 128 : 136, se,
+        transform(vw, kShare ? 0 : kTabBytes, se,
                   __builtin_amdgcn_make_buffer_rsrc(layers.out_value[lyr], 0, out_bytes, kBufWord3));
         cur = nxt;
         gi += stride;
@@ -1388,7 +1365,7 @@ void launch_dequant_layers(Scheme s, const uint8_t* const* pools, const int32_t*
     const bool prod = s == Scheme::Prod;
     // A whole row per lane when every layer's buffers allow 16-byte code
     // loads (half a row per lane: 9.1 against 8.0 us per 32K-token layer).
-    bool rows_ok = true;
+    bool rows_ok = rows <= kBufMaxRows;
     for (int l = 0; l < num_layers && rows_ok; ++l)
         rows_ok = rows_dequant_ok(g, pools[l], out_key[l], out_value[l]);
     const int rows_per_block = rows_ok ? kBlock : kBlock / (g.D / 32);
