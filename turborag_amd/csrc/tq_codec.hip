@@ -852,23 +852,21 @@ __global__ __launch_bounds__(kBlock, 2) void dequant_rows_kernel(
     constexpr int NQ = E / 32;     // 16-byte code loads per tensor and lane
     constexpr int kWaves = kBlock / 64;
     static_assert(kWaves == 4, "byte 1 of a table address holds 4*nibble + wave");
-    // Half a row per lane: K and V share one decode table, the V table
-    // written after the K transform (52 KB of LDS per workgroup against 68;
-    // per-layer launches 9.4 -> 9.1 us per 32K-token layer).  A whole row
-    // per lane keeps two tables: sharing them gives it three waves per SIMD,
-    // 4% slower.
-    constexpr bool kShare = E == 64;
     // Tables as in dequant_stream_kernel: entry n of (wave w, lane l) is word
-    // (n*4 + w)*64 + l of the tensor's 16 KiB, K first (kShare: one table);
-    // then one stage per wave, one kRowStageBytes row per lane: the lane's
-    // output line (bytes 0..127) and the byte offset of its K and V output
-    // rows in their buffers (bytes 128..131; kBufSkip for a row not written).
+    // (n*4 + w)*64 + l of the tensor's 16 KiB, K first; then one stage per
+    // wave, one kRowStageBytes row per lane: the lane's output line (bytes
+    // 0..127) and the byte offset of its K and V output rows in their
+    // buffers (bytes 128..131; kBufSkip for a row not written).  68 KB per
+    // workgroup.  (One table shared by K and V, the V table written after
+    // the K transform, takes 52 KB: per-layer launches alone ran 1% faster,
+    // but with three such workgroups per CU the decode attention's 82.5 KB
+    // workgroups found no room beside them: the two-stream step went from
+    // 0.55 to 0.60 ms.)
     constexpr uint32_t kTabBytes = 16 * kWaves * 64 * sizeof(float);
-    constexpr uint32_t kTables = kShare ? 1 : 2;
     constexpr uint32_t kStageBytes = 64 * kRowStageBytes;
     // The kernel's only LDS object: it starts at LDS address 0, so byte 1 of
     // an entry's address is 4*nibble + wave and the bytes above it are zero.
-    __shared__ __attribute__((aligned(1024))) uint32_t lds[(kTables * kTabBytes + kWaves * kStageBytes) / 4];
+    __shared__ __attribute__((aligned(1024))) uint32_t lds[(2 * kTabBytes + kWaves * kStageBytes) / 4];
     typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
 
     const int lane = threadIdx.x & 63;
@@ -878,7 +876,7 @@ __global__ __launch_bounds__(kBlock, 2) void dequant_rows_kernel(
     const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((lds_float*)(void*)lds);
     const uint32_t tbase = lds0 + 4u * lane + 256u * wave;  // entry 0 of this lane's K table
     const uint32_t wsplat = 0x01010101u * (uint32_t)wave;
-    const uint32_t stage = lds0 + kTables * kTabBytes + wave * kStageBytes;
+    const uint32_t stage = lds0 + 2 * kTabBytes + wave * kStageBytes;
     const uint32_t my_row = stage + lane * kRowStageBytes;        // staged by this lane
     const uint32_t rd_row = stage + (lane >> 3) * kRowStageBytes;  // read by store 0 (+ 8 rows per store)
     const int groups = (num_rows + RPG - 1) / RPG;  // row groups per layer
@@ -1059,21 +1057,15 @@ __global__ __launch_bounds__(kBlock, 2) void dequant_rows_kernel(
         const Loc nxt = locate(gi + stride, s_next);
         // This lane's row: its tables (16 entries per tensor, the reference's
         // exact operations) and its output offset for the stores.
-        const float vs = h2f(sc.vs);
-        auto v_table = [&](uint32_t toff) {
-#pragma unroll
-            for (int n = 0; n < 16; ++n)
-                *reinterpret_cast<lds_float*>(tbase + toff + 1024u * n) = kV4[n] * vs;
-        };
         {
-            const float ks = h2f(sc.ks), re = h2f(sc.re);
+            const float ks = h2f(sc.ks), vs = h2f(sc.vs), re = h2f(sc.re);
 #pragma unroll
             for (int n = 0; n < 16; ++n) {
                 const float kv = PROD ? (kK3[n & 7] + re * ((n & 8) ? 1.0f : -1.0f)) * ks
                                       : kV4[n] * ks;
                 *reinterpret_cast<lds_float*>(tbase + 1024u * n) = kv;
+                *reinterpret_cast<lds_float*>(tbase + kTabBytes + 1024u * n) = kV4[n] * vs;
             }
-            if constexpr (!kShare) v_table(kTabBytes);
         }
         int t, h;
         token_head(min(cur.row, num_rows - 1), t, h);
@@ -1091,12 +1083,7 @@ __global__ __launch_bounds__(kBlock, 2) void dequant_rows_kernel(
         load_codes(nxt, g.kc_off, kw);
         load_scales(nxt, sc);
         s_next = load_slot(gi + 2 * stride);
-        if constexpr (kShare) {  // the V table over the K table (this lane's K lookups are done)
-            v_table(0);
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        }
-        transform(vw, kShare ? 0 : kTabBytes, se,
+        transform(vw, kTabBytes, se,
                   __builtin_amdgcn_make_buffer_rsrc(layers.out_value[lyr], 0, out_bytes, kBufWord3));
         cur = nxt;
         gi += stride;
