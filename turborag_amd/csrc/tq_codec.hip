@@ -815,9 +815,10 @@ __global__ __launch_bounds__(kBlock) void dequant_stream_kernel(
 // tensor as 16-byte loads.  The outputs leave one 128-byte line per lane at
 // a time: each lane writes its line into a padded wave-private LDS stage
 // (144-byte rows: the 16-byte writes of eight consecutive lanes cover the
-// 32 banks once), then store r of the wave writes the lines of lanes 8r ..
-// 8r + 7, eight whole lines per store.  Waves walk (layer, row group) pairs
-// grid-stride with the next pair's slot, codes and scales in flight.
+// 32 banks once) with the line's byte offset in the layer's output, then
+// store r of the wave writes the lines of lanes 8r .. 8r + 7, eight whole
+// lines per buffer store.  Waves walk (layer, row group) pairs grid-stride
+// with the next pair's slot, codes and scales in flight.
 // ---------------------------------------------------------------------------
 constexpr int kRowStageBytes = 144;  // staged bytes per lane: one output line + 16 of pad
 // The row kernels store through buffer descriptors of a layer's output,
@@ -827,7 +828,7 @@ constexpr int kRowStageBytes = 144;  // staged bytes per lane: one output line +
 constexpr uint32_t kBufSkip = 0x80000000u;
 constexpr int kBufMaxRows = (int)(kBufSkip / 256u) - 1;
 constexpr uint32_t kBufWord3 = 0x00020000u;  // descriptor word 3 on gfx9: 32-bit data format
-// Row-per-lane dequant: staged output lines (and their row addresses) read
+// Row-per-lane dequant: staged output lines (and their row offsets) read
 // from LDS this many stores ahead of the store that writes them, 1..7 (36
 // layers of 32K tokens in one launch: 8.20 us per layer with each read just
 // before its store, 7.86 with 2; 1, 3 and 7 within 0.1 us of 2).
