@@ -1004,12 +1004,16 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                         cb[t][tau] = (f32x4){0.f, 0.f, 0.f, 0.f};
                         cs[t][tau] = cb[t][tau];
                     }
-#pragma unroll
-                for (int s = 0; s < 4; ++s) {
+                // The operands of k-step s + 1 (query parts, decoded codes) are
+                // read from LDS before the MFMAs of step s.
+                struct Ops {
                     half8 bk[2 * NTA];  // k-step s of each tile's hi and lo query
+                    half8 a[kTiles], al[kTiles];
+                };
+                auto load_ops = [&](int s, Ops& o) {
 #pragma unroll
                     for (int pp = 0; pp < (COLS ? 1 : 2 * NTA); ++pp)
-                        bk[pp] = __builtin_bit_cast(half8, bqs[pp][s][lane]);
+                        o.bk[pp] = __builtin_bit_cast(half8, bqs[pp][s][lane]);
 #pragma unroll
                     for (int tau = 0; tau < kTiles; ++tau) {
                         const uint32_t wd = s == 0   ? kw[tau].x
@@ -1017,20 +1021,37 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                                             : s == 2 ? kw[tau].z
                                                      : kw[tau].w;
                         const int kt = PROD ? 0 : 1;  // mse: the hi parts are the V table
-                        const half8 a = as_h8(lookup(wd, 0, kt), lookup(wd, 1, kt),
-                                              lookup(wd, 2, kt), lookup(wd, 3, kt));
+                        o.a[tau] = as_h8(lookup(wd, 0, kt), lookup(wd, 1, kt), lookup(wd, 2, kt),
+                                         lookup(wd, 3, kt));
+                        if (!PROD)  // mse: the lo parts (table 0)
+                            o.al[tau] = as_h8(lookup(wd, 0, 0), lookup(wd, 1, 0),
+                                              lookup(wd, 2, 0), lookup(wd, 3, 0));
+                    }
+                };
+                Ops ops[2];
+                load_ops(0, ops[0]);
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    if (s < 3) load_ops(s + 1, ops[(s + 1) & 1]);
+                    __builtin_amdgcn_sched_barrier(0);
+                    const Ops& o = ops[s & 1];
+#pragma unroll
+                    for (int tau = 0; tau < kTiles; ++tau) {
+                        const uint32_t wd = s == 0   ? kw[tau].x
+                                            : s == 1 ? kw[tau].y
+                                            : s == 2 ? kw[tau].z
+                                                     : kw[tau].w;
 #pragma unroll
                         for (int t = 0; t < NTA; ++t) {
-                            cb[t][tau] = mma(a, bk[2 * t], cb[t][tau]);
-                            if (!COLS) cb[t][tau] = mma(a, bk[2 * t + 1], cb[t][tau]);
+                            cb[t][tau] = mma(o.a[tau], o.bk[2 * t], cb[t][tau]);
+                            if (!COLS) cb[t][tau] = mma(o.a[tau], o.bk[2 * t + 1], cb[t][tau]);
                         }
-                        if (!PROD) {  // mse: the lo parts (table 0) into cs
-                            const half8 al = as_h8(lookup(wd, 0, 0), lookup(wd, 1, 0),
-                                                   lookup(wd, 2, 0), lookup(wd, 3, 0));
+                        if (!PROD) {  // mse: the lo parts into cs
 #pragma unroll
                             for (int t = 0; t < NTA; ++t) {
-                                cs[t][tau] = mma(al, bk[2 * t], cs[t][tau]);
-                                if (!COLS) cs[t][tau] = mma(al, bk[2 * t + 1], cs[t][tau]);
+                                cs[t][tau] = mma(o.al[tau], o.bk[2 * t], cs[t][tau]);
+                                if (!COLS)
+                                    cs[t][tau] = mma(o.al[tau], o.bk[2 * t + 1], cs[t][tau]);
                             }
                         }
                         if (PROD) {
@@ -1042,11 +1063,12 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                                                    __builtin_amdgcn_perm(ho, he, 0x070C030Cu));
 #pragma unroll
                             for (int t = 0; t < NTA; ++t) {
-                                cs[t][tau] = mma(sa, bk[2 * t], cs[t][tau]);
-                                if (!COLS) cs[t][tau] = mma(sa, bk[2 * t + 1], cs[t][tau]);
+                                cs[t][tau] = mma(sa, o.bk[2 * t], cs[t][tau]);
+                                if (!COLS) cs[t][tau] = mma(sa, o.bk[2 * t + 1], cs[t][tau]);
                             }
                         }
                     }
+                    __builtin_amdgcn_sched_barrier(0);
                 }
                 const bool masked = t0 + kChunk > gmin_live;
                 // Logits (base 2) of tokens 16*tau + 4*gq + e for this lane's column.
@@ -1065,6 +1087,23 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                             }
                             lg[t][tau][e] = fmaf(b, sc.x, fmaf(r, sc.y, sc.w));
                         }
+                // The V lookups (B operands of PV) go out before the softmax,
+                // whose VALU work hides their LDS latency.
+                uint32_t bv[kSteps][8][4];  // [step][N-tile v = d - 8i][token pair]
+#pragma unroll
+                for (int st = 0; st < kSteps; ++st)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const uint32_t we = vw[st][2 * q], wo = vw[st][2 * q + 1];
+                        const uint32_t lob = (we & 0x0F0F0F0Fu) | ((wo & 0x0F0F0F0Fu) << 4);
+                        const uint32_t hib = ((we >> 4) & 0x0F0F0F0Fu) | (wo & 0xF0F0F0F0u);
+#pragma unroll
+                        for (int b = 0; b < 4; ++b) {
+                            bv[st][2 * b][q] = lookup(lob, b, 1);
+                            bv[st][2 * b + 1][q] = lookup(hib, b, 1);
+                        }
+                    }
+                __builtin_amdgcn_sched_barrier(0);
                 if (masked) {  // a row of the unit ends in this chunk (wave-uniform)
                     asm volatile("" ::: "memory");  // a branch: no selects on every chunk
 #pragma unroll
@@ -1146,21 +1185,10 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                             al[t] = as_h8(lw[0], lw[1], lw[2], lw[3]);
                         }
                     }
-                    uint32_t bv[8][4];  // [N-tile v = d - 8i][token pair]
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const uint32_t we = vw[st][2 * q], wo = vw[st][2 * q + 1];
-                        const uint32_t lob = (we & 0x0F0F0F0Fu) | ((wo & 0x0F0F0F0Fu) << 4);
-                        const uint32_t hib = ((we >> 4) & 0x0F0F0F0Fu) | (wo & 0xF0F0F0F0u);
-#pragma unroll
-                        for (int b = 0; b < 4; ++b) {
-                            bv[2 * b][q] = lookup(lob, b, 1);
-                            bv[2 * b + 1][q] = lookup(hib, b, 1);
-                        }
-                    }
 #pragma unroll
                     for (int v = 0; v < 8; ++v) {
-                        const half8 bvv = as_h8(bv[v][0], bv[v][1], bv[v][2], bv[v][3]);
+                        const half8 bvv =
+                            as_h8(bv[st][v][0], bv[st][v][1], bv[st][v][2], bv[st][v][3]);
 #pragma unroll
                         for (int t = 0; t < NTA; ++t) {
                             acc_col[t][v] = mma(ah[t], bvv, acc_col[t][v]);
