@@ -1029,10 +1029,18 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                     }
                 };
                 Ops ops[2];
+                float4 scq[kTiles][4];  // the logits' per-token scales, read during the last k-step
                 load_ops(0, ops[0]);
 #pragma unroll
                 for (int s = 0; s < 4; ++s) {
-                    if (s < 3) load_ops(s + 1, ops[(s + 1) & 1]);
+                    if (s < 3) {
+                        load_ops(s + 1, ops[(s + 1) & 1]);
+                    } else {
+#pragma unroll
+                        for (int tau = 0; tau < kTiles; ++tau)
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) scq[tau][e] = tsc[w][16 * tau + 4 * gq + e];
+                    }
                     __builtin_amdgcn_sched_barrier(0);
                     const Ops& o = ops[s & 1];
 #pragma unroll
@@ -1079,7 +1087,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                     for (int tau = 0; tau < kTiles; ++tau)
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
-                            const float4 sc = tsc[w][16 * tau + 4 * gq + e];
+                            const float4 sc = scq[tau][e];
                             float b = cb[t][tau][e], r = cs[t][tau][e];
                             if constexpr (COLS) {  // + the partner column (lane ^ 8)
                                 b += lane_xor<8>(b);
