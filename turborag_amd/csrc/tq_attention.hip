@@ -991,10 +991,6 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
                 Chunk nxt;
                 const int t1 = t0 + kWaves * kChunk;
-                if (t1 < t_end) {  // codes of the next chunk, slots of the one after
-                    fetch(t1, slot_nx, nxt);
-                    slot_nx = load_slot(t1 + kWaves * kChunk);
-                }
                 // QK: each decoded A operand against every tile's hi and lo query
                 f32x4 cb[NTA][kTiles], cs[NTA][kTiles];
 #pragma unroll
@@ -1031,6 +1027,13 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                 Ops ops[2];
                 float4 scq[kTiles][4];  // the logits' per-token scales, read during the last k-step
                 load_ops(0, ops[0]);
+                // The next chunk's codes and the slots of the one after, fetched
+                // behind the first k-step's LDS reads (its address exchange
+                // through LDS would otherwise delay them).
+                if (t1 < t_end) {
+                    fetch(t1, slot_nx, nxt);
+                    slot_nx = load_slot(t1 + kWaves * kChunk);
+                }
 #pragma unroll
                 for (int s = 0; s < 4; ++s) {
                     if (s < 3) {
