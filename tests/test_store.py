@@ -443,6 +443,29 @@ def test_cag_store_paths(tq, tmp_path):
     assert st.vram_bytes("turbo_prod", 32, (2, 128)) == 2 * 4288
 
 
+def test_cag_store_manifest_and_hash_helpers(tq, tmp_path):
+    """The reference's private helpers (cag_store.py:32-48): the manifest
+    read falls back to an empty v1 manifest for a missing or corrupt file,
+    and the document hash is the SHA-256 of its UTF-8 bytes."""
+    st = CAGStore(tmp_path, tq=tq)
+    assert st._load_manifest() == {"v": 1, "entries": {}}
+    (tmp_path / "manifest.json").write_text("{not json")
+    assert st._load_manifest() == {"v": 1, "entries": {}}
+    st.io.manifest_update(tmp_path, "d", 0, "turbo_prod", 12)
+    assert list(st._load_manifest()["entries"]) == ["d"]
+    for doc in ("doc", "", "dökümän"):
+        assert st._doc_hash(doc) == hashlib.sha256(doc.encode()).hexdigest()
+
+
+def test_compute_mse_matches_its_definition(tq):
+    """TurboQuantWrapper.compute_mse (turboquant_wrapper.py:422): mean squared
+    difference in fp32, checked on values whose squares are exact."""
+    a = torch.tensor([[1.0, -2.0], [0.5, 3.0]], dtype=torch.float16)
+    b = torch.tensor([[0.0, -1.0], [0.5, 1.0]], dtype=torch.float16)
+    assert tq.compute_mse(a, b) == (1.0 + 1.0 + 0.0 + 4.0) / 4
+    assert tq.compute_mse(a, a) == 0.0
+
+
 def test_load_rejects_mismatched_footer(tq, tmp_path):
     """A .bin whose footer disagrees with the requested geometry is refused
     before anything reaches the GPU."""
