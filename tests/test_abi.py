@@ -202,6 +202,7 @@ def test_allocator_lifo_semantics(tq):
             return 0x10000
 
     a = PageAllocator(tq, 4288, 4, device_pool=FakePool())
+    assert a.device_pool_ptr() == 0x10000                          # the caller's pool, as given
     assert [a.alloc_block() for _ in range(4)] == [0, 1, 2, 3]   # free list [N-1..0]
     assert a.alloc_block() == -1                                   # empty -> -1
     a.free_block(2)
