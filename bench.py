@@ -44,7 +44,7 @@ def log(msg: str) -> None:
 # rocprofv3 names them (template argument 1 = turbo_prod).
 DEQUANT_KERNEL = "tq::dequant_rows_kernel<1, 64, 128>"       # the 36-layer launch
 DEQUANT_KERNEL_1 = "tq::dequant_rows_kernel<1, 1, 64>"     # one layer per launch
-ATTN_KERNELS = ("tq::attn_mfma_split_kernel<1, 32, 8, false, 1>", "tq::attn_mfma_combine_kernel")
+ATTN_KERNELS = ("tq::dec::attn_decode_split_kernel<1>", "tq::dec::attn_decode_combine_kernel")
 
 
 def kernel_traffic(name: str):

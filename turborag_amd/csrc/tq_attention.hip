@@ -1696,6 +1696,539 @@ __global__ __launch_bounds__(1024) void paged_plan_kernel(
     }
 }
 
+// ===========================================================================
+// Decode over slot-mapped tokens: the reference's fused attention entries
+// (src/cuda/tq_turbo_prod_kernels.cu:439-571, 650-671;
+// src/cuda/tq_turbo_mse_kernels.cu:302-417, 459-479) for D = 128 and
+// turbo_prod / turbo_mse pages.
+//
+// Flash-decoding split-K on a (split, kv head, row group) grid, 8 waves of
+// 32-token chunks per workgroup, the same MFMA formulation as
+// attn_mfma_split_kernel (QK: A = decoded K, B = the rotated query as fp16
+// hi/lo columns; PV: A = P', B = decoded V), with a setup and a chunk loop
+// cut to what the decode needs:
+//  - one LDS lookup per K code byte returns two fp16 pairs: turbo_prod's
+//    aK*K3 pair and its pair of residual signs (+-1; no VALU builds the sign
+//    matrix), turbo_mse's hi and lo parts of aV*V4 (its V lookups read the
+//    hi pair of the same entry);
+//  - the tables are copied into LDS from compile-time constants while the
+//    slots and codes are in flight (no per-entry arithmetic, no staging
+//    pass);
+//  - each wave rotates one query row and stores its fp16 hi and lo parts
+//    straight into the B-operand layout: one barrier for the whole setup;
+//  - P' = p * vs / aV enters the PV product as its fp16 hi part, or on the
+//    lo columns as fp16(p * vs / aV - hi) of the exact product (three
+//    mixed-precision ops per value pair and lane);
+//  - per split and row the partial o[128] and (m, l) go to two arrays, the
+//    (m, l) of one row contiguous over the splits, for
+//    attn_decode_combine_kernel.
+// ===========================================================================
+namespace dec {
+using namespace mfma;
+
+constexpr uint16_t f16_bits(float x) { return __builtin_bit_cast(uint16_t, (_Float16)x); }
+constexpr uint32_t f16_pair(float a, float b) {
+    return (uint32_t)f16_bits(a) | ((uint32_t)f16_bits(b) << 16);
+}
+// (x - fp16(x)) * 2^kLoShift, exact in fp32 (mfma::lo_part at compile time).
+constexpr float lo_part_c(float x) { return (x - (float)(_Float16)x) * (float)(1 << kLoShift); }
+
+// fp16 bits of the codebook values the decode tables hold: aK*K3[j],
+// aV*V4[j], and the lo parts (x - fp16(x)) * 2^kLoShift of aV*V4[j].
+struct Fp16Tables {
+    uint32_t k3[8], v4[16], v4lo[16];
+};
+constexpr Fp16Tables make_fp16_tables() {
+    Fp16Tables t{};
+    for (int j = 0; j < 8; ++j) t.k3[j] = f16_bits(kAlphaK * dev::kK3[j]);
+    for (int j = 0; j < 16; ++j) {
+        t.v4[j] = f16_bits(kAlphaV * dev::kV4[j]);
+        t.v4lo[j] = f16_bits(lo_part_c(kAlphaV * dev::kV4[j]));
+    }
+    return t;
+}
+constexpr Fp16Tables kF16 = make_fp16_tables();
+// The fp16 pair (t[j], t[j + 1]).
+template <int N>
+constexpr uint32_t f16_pair_of(const uint32_t (&t)[N], int j) {
+    return t[j] | (t[j + 1] << 16);
+}
+// Selector of entry g < 4 of a 4-entry fp16 table held as two fp16 pairs:
+// bytes 2g, 2g + 1, then zeros.
+__device__ __forceinline__ uint32_t lut4_sel(int g) {
+    return (uint32_t)(2 * g) | ((uint32_t)(2 * g + 1) << 8) | 0x0C0C0000u;
+}
+// t[4m + g] (in the low half) for the 4-entry slice m of t, g given by sel.
+template <int N>
+__device__ __forceinline__ uint32_t lut4(const uint32_t (&t)[N], int m, uint32_t sel) {
+    return __builtin_amdgcn_perm(f16_pair_of(t, 4 * m + 2), f16_pair_of(t, 4 * m), sel);
+}
+// fp16 pairs of the table entries for code byte b (low nibble = even d):
+//   K table: turbo_prod (aK*K3[b & 7], aK*K3[(b >> 4) & 7]); turbo_mse the hi
+//            parts fp16(aV*V4[b & 15]), fp16(aV*V4[b >> 4]) (its V pairs too);
+//   S table: turbo_prod the residual signs (nibble bit 3 set: +1.0, else
+//            -1.0); turbo_mse the lo parts of aV*V4;
+//   V table (turbo_prod): (aV*V4[b & 15], aV*V4[b >> 4]).
+
+// LDS layout of the tables (32 copies of each entry, copy c at 4c; lane l
+// reads copy l % 32, so a half-wave's random lookups hit distinct banks):
+//   S table: byte 256b + 4c (the rows' upper halves unused: the table ends
+//   below kOffK);
+//   K table: byte kOffK + 256b + 4c (turbo_mse's V lookups read it too);
+//   turbo_prod's V table: kOffK + 256b + 128 + 4c.
+// A K lookup reads its S and K entries from one address register with
+// offsets 0 and kOffK: no two-address LDS read reaches that pair (ds_read2
+// spans up to 1020 bytes, ds_read2st64 multiples of 256), so each result
+// goes straight into its MFMA operand registers.
+constexpr int kOffK = 65520;
+constexpr int kLutWords = (kOffK + 256 * 256) / 4;
+
+// LDS address of copy (lane & 31) of entry `byte b of word` in a table of
+// 256-byte entries at `base` (base = table + copy offset): v_perm puts the
+// code byte in byte 1, and byte 1 of the base is added back.
+__device__ __forceinline__ uint32_t lut_addr(uint32_t word, int b, uint32_t base) {
+    return __builtin_amdgcn_perm(word, base, 0x03020000u | ((4u + b) << 8)) + (base & 0xFF00u);
+}
+
+// fp16 pair of x0 = a0 * b0, x1 = a1 * b1 for this lane's MFMA column: the
+// hi parts fp16(x), or with lomask = ~0 the lo parts fp16(x - hi) of the
+// exact products (v_fma_mix: one rounding to fp16).
+__device__ __forceinline__ uint32_t hilo_pair(float a0, float b0, float a1, float b1,
+                                              uint32_t lomask) {
+    uint32_t h, r;
+    asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel_hi:[0,0,0]\n\t"
+        "v_fma_mixhi_f16 %0, %3, %4, 0 op_sel_hi:[0,0,0]"
+        : "=&v"(h)
+        : "v"(a0), "v"(b0), "v"(a1), "v"(b1));
+    const uint32_t m = h & lomask;
+    asm("v_fma_mixlo_f16 %0, %1, %2, -%5 op_sel_hi:[0,0,1]\n\t"
+        "v_fma_mixhi_f16 %0, %3, %4, -%5 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
+        : "=&v"(r)
+        : "v"(a0), "v"(b0), "v"(a1), "v"(b1), "v"(m));
+    return r;
+}
+
+constexpr int kWaves = 8, kChunk = 32, kPass = kWaves * kChunk;
+// Partial of (split, row): o[128] at po[(pid * 8 + r) * 128], (m, l) at
+// pml[(item * 8 + r) * S + split] with pid = item * S + split and item =
+// row group * H + kv head.
+constexpr size_t kPartBytes = kRows * (128 * sizeof(float) + 2 * sizeof(float));
+
+template <int SCH>
+__global__ __launch_bounds__(64 * kWaves) void attn_decode_split_kernel(
+    const uint16_t* __restrict__ query, const uint8_t* __restrict__ pool,
+    const int32_t* __restrict__ slots, float* __restrict__ po, float2* __restrict__ pml,
+    float inv, int num_queries, int num_kv_tokens, int tokens_per_split, int num_splits,
+    PageGeom g) {
+    constexpr bool PROD = SCH == kSchProd;
+    static_assert(SCH == kSchProd || SCH == kSchMse, "turbo_prod or turbo_mse pages");
+    // The decode tables (layout above); after the chunk loop the space holds
+    // the waves' results for the merge.
+    __shared__ __attribute__((aligned(256))) uint32_t lut[kLutWords];
+    __shared__ uint4 bqs[4][64];  // QK B operand of k-step s for lane l
+    __shared__ uint64_t tko[kWaves][kChunk], tvo[kWaves][kChunk];
+    __shared__ float4 tsc[kWaves][kChunk];  // per token: K scale, residual scale, vs / aV, bias
+    __shared__ float mm[kWaves][kRows], ml[kWaves][kRows];
+    float(*mo)[kRows][128] = reinterpret_cast<float(*)[kRows][128]>(&lut[0]);
+    static_assert(sizeof(float) * kWaves * kRows * 128 <= sizeof(lut), "merge space");
+
+    int split, h, rg;
+    if (gridDim.x == (unsigned)num_splits) {
+        split = blockIdx.x;
+        h = blockIdx.y;
+        rg = blockIdx.z;
+    } else {  // one dimension of splits x heads x row groups
+        split = blockIdx.x % num_splits;
+        const int hr = blockIdx.x / num_splits;
+        h = hr % g.H;
+        rg = hr / g.H;
+    }
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int i = lane & 15, gq = lane >> 4;
+    const int t_begin = split * tokens_per_split;
+    const int t_end = min(num_kv_tokens, t_begin + tokens_per_split);
+    const float ck = inv * kLog2e / (PROD ? kAlphaK : kAlphaV);  // logit scale per unit ks
+    const float cr = inv * kLog2e;                                 // residual: ks * re
+    constexpr float iav = 1.0f / kAlphaV;
+
+    // 1. Loads, in the order they are needed: this wave's query row, the
+    //    first chunk's slots, then the decode-table words.
+    const int qrow = rg * kRows + w;
+    const uint32_t qraw = *reinterpret_cast<const uint32_t*>(
+        query + ((size_t)min(qrow, num_queries - 1) * g.H + h) * 128 + 2 * lane);
+    int t0 = t_begin + w * kChunk;
+    auto load_slot = [&](int t) -> int {
+        return slots[max(min(t + (lane & (kChunk - 1)), t_end - 1), 0)];
+    };
+    const int slot0 = load_slot(t0);
+    // 2. The chunk's codes and per-token scales.  slot -> cell offsets
+    //    (exchanged through this wave's LDS rows) -> scale and code loads.
+    //    Tokens past the range or with a negative slot read the first bytes
+    //    of the query instead (always valid memory) and get bias -inf.
+    struct Chunk {
+        uint4 kw[2];     // K: tile tau, token 16 tau + i, bytes [16 gq, 16 gq + 16)
+        uint32_t vw[8];  // V: k-index 8 gq + e (token below), dword i
+        uint16_t ks, re, vs;
+        bool valid;
+    };
+    const uint64_t dummy_off =
+        (uint64_t)(reinterpret_cast<uintptr_t>(query) - reinterpret_cast<uintptr_t>(pool));
+    auto fetch = [&](int tc, int slot, Chunk& c) {
+        c.valid = tc + (lane & (kChunk - 1)) < t_end && slot >= 0;
+        int page, tib;
+        split_slot(c.valid ? slot : 0, g, page, tib);
+        const uint64_t cell = (uint64_t)(tib * g.H + h);
+        const uint64_t pb = (uint64_t)page * g.page_size;
+        const uint64_t so = pb + cell * g.scale_stride;
+        c.ks = ld_u16_nt(pool + (c.valid ? so + g.ks_off : dummy_off));
+        c.vs = ld_u16_nt(pool + (c.valid ? so + g.vs_off : dummy_off + 2));
+        c.re = PROD ? ld_u16_nt(pool + (c.valid ? so + g.kres_off : dummy_off + 4)) : (uint16_t)0;
+        tko[w][lane & (kChunk - 1)] = c.valid ? pb + g.kc_off + cell * g.code_stride : dummy_off;
+        tvo[w][lane & (kChunk - 1)] = c.valid ? pb + g.vc_off + cell * g.code_stride : dummy_off;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int tau = 0; tau < 2; ++tau) c.kw[tau] = ld_u4_nt(pool + (tko[w][16 * tau + i] + 16 * gq));
+        // k-index 8 gq + e is token 4 gq + e (e < 4) or 16 + 4 gq + (e - 4)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int tok = e < 4 ? 4 * gq + e : 16 + 4 * gq + (e - 4);
+            c.vw[e] = ld_u32_nt(pool + (tvo[w][tok] + 4 * i));
+        }
+    };
+    Chunk cur;
+    fetch(t0, slot0, cur);
+    int slot_nx = load_slot(t0 + kPass);
+    __builtin_amdgcn_sched_barrier(0);  // the code loads go out before any setup work
+
+    // The tables' words, computed in registers while the codes are in flight
+    // (no memory traffic).  Each 16-byte store writes four copies; a store
+    // instruction covers whole rows (128 or 256 bytes per 8 or 16 lanes).
+    // With the rows a wave writes, one nibble of every entry is the same
+    // across the wave (a scalar) and the other comes from a 4-entry fp16 table
+    // by v_perm.
+    //   S table, and turbo_mse's K table: store k < 4 of wave w writes row
+    //     32w + 8k + lane / 8, copies 4q .. 4q + 3 (q = lane % 8): low nibble
+    //     8(k % 2) + lane / 8, high nibble 2w + k / 2;
+    //   turbo_prod's K | V rows: store k < 8 writes row 32w + 4k + lane / 16,
+    //     group lane % 16 (K copies, then V copies): low nibble
+    //     4(k % 4) + lane / 16, high nibble 2w + k / 4.
+    constexpr int kR1Stores = PROD ? 8 : 4;
+    uint32_t r0[4], r1[kR1Stores];
+    {
+        const int g4 = lane >> 4, g8 = lane >> 3;
+        const uint32_t sel4 = lut4_sel(g4), sel8 = lut4_sel(g8 & 3);
+        const bool hi8 = (g8 & 4) != 0;
+        if constexpr (PROD) {
+            const uint32_t sh = (w & 4) ? 0x3C000000u : 0xBC000000u;  // row bit 7 = w bit 2
+#pragma unroll
+            for (int k = 0; k < 4; ++k) r0[k] = ((k & 1) ? 0x3C00u : 0xBC00u) | sh;  // row bit 3
+            const bool vq = (lane & 8) != 0;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const uint32_t vpair =
+                    lut4(kF16.v4, k & 3, sel4) | (kF16.v4[2 * w + (k >> 2)] << 16);
+                const uint32_t kpair =
+                    lut4(kF16.k3, k & 1, sel4) | (kF16.k3[(2 * w + (k >> 2)) & 7] << 16);
+                r1[k] = vq ? vpair : kpair;
+            }
+        } else {
+            uint32_t llo[2], vlo[2];
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                llo[hh] = hi8 ? lut4(kF16.v4lo, 2 * hh + 1, sel8) : lut4(kF16.v4lo, 2 * hh, sel8);
+                vlo[hh] = hi8 ? lut4(kF16.v4, 2 * hh + 1, sel8) : lut4(kF16.v4, 2 * hh, sel8);
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                r0[k] = llo[k & 1] | (kF16.v4lo[2 * w + (k >> 1)] << 16);
+                r1[k] = vlo[k & 1] | (kF16.v4[2 * w + (k >> 1)] << 16);
+            }
+        }
+    }
+
+    // 3. This wave's query row: qrot = WHT(q * s) * inv, stored as fp16 hi
+    //    and lo parts into the B operand (column 2w: hi, 2w + 1: lo; lane l
+    //    holds d = 2l, 2l + 1: k-group l / 16, k-step (l / 4) % 4, halves
+    //    2(l % 4), + 1 of the half8).
+    {
+        const float sh = (h & 1) ? -1.0f : 1.0f;
+        float q0 = h2f(qraw & 0xffff) * sh, q1 = h2f(qraw >> 16) * (-sh);
+        wht_pair<64>(q0, q1, lane);
+        const bool live = qrow < num_queries;
+        q0 = live ? q0 * inv : 0.0f;
+        q1 = live ? q1 * inv : 0.0f;
+        const uint32_t hi = pack_h2(q0, q1);
+        const uint32_t lo = lo_pair(q0, q1, hi);
+        uint32_t* b = reinterpret_cast<uint32_t*>(&bqs[(lane >> 2) & 3][16 * (lane >> 4) + 2 * w]);
+        b[lane & 3] = hi;
+        b[4 + (lane & 3)] = lo;  // the next lane's (column 2w + 1) half8
+    }
+    // 4. The decode tables.
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        *reinterpret_cast<u32x4*>(&lut[(32 * w + 8 * k + (lane >> 3)) * 64 + 4 * (lane & 7)]) =
+            (u32x4){r0[k], r0[k], r0[k], r0[k]};
+#pragma unroll
+    for (int k = 0; k < kR1Stores; ++k) {
+        const int row = PROD ? 32 * w + 4 * k + (lane >> 4) : 32 * w + 8 * k + (lane >> 3);
+        const int q = PROD ? lane & 15 : lane & 7;
+        *reinterpret_cast<u32x4*>(&lut[kOffK / 4 + row * 64 + 4 * q]) =
+            (u32x4){r1[k], r1[k], r1[k], r1[k]};
+    }
+    lds_barrier();
+    half8 bq[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) bq[s] = __builtin_bit_cast(half8, bqs[s][lane]);
+
+    // Lookup bases: copy lane % 32 of entry 0 of the S table (the K table
+    // is kOffK above it; turbo_mse's V lookups read it that way), and of
+    // turbo_prod's V table.
+    const uint32_t basek = (uint32_t)reinterpret_cast<uintptr_t>((lds_u32*)&lut[lane & 31]);
+    const uint32_t basev =
+        PROD ? (uint32_t)reinterpret_cast<uintptr_t>((lds_u32*)&lut[kOffK / 4 + 32 + (lane & 31)])
+             : basek;
+    constexpr uint32_t offv = PROD ? 0u : (uint32_t)kOffK;
+    const bool lo_col = (i & 1) != 0;
+    const uint32_t lomask = lo_col ? 0xFFFFFFFFu : 0u;
+
+    float m_run = kInitMax, l_run = 0.0f;
+    f32x4 acc[8];
+#pragma unroll
+    for (int v = 0; v < 8; ++v) acc[v] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    bool first = true;
+
+    while (t0 < t_end) {  // wave-uniform
+        {
+            const float ks = h2f(cur.ks), vs = h2f(cur.vs), re = PROD ? h2f(cur.re) : 0.0f;
+            const float4 sc = PROD ? make_float4(ks * ck, ks * re * cr, vs * iav, 0.0f)
+                                   : make_float4(ks * ck, ks * ck * kLoScale, vs * iav, 0.0f);
+            tsc[w][lane & (kChunk - 1)] = cur.valid ? sc : make_float4(0.f, 0.f, 0.f, -INFINITY);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        Chunk nxt;
+        const int t1 = t0 + kPass;
+        if (t1 < t_end) {  // codes of the next chunk, slots of the one after
+            fetch(t1, slot_nx, nxt);
+            slot_nx = load_slot(t1 + kPass);
+        }
+        // Per-token scales of this lane's logits (read before the lookups:
+        // LDS reads complete in order).
+        float4 scv[2][4];
+#pragma unroll
+        for (int tau = 0; tau < 2; ++tau)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) scv[tau][e] = tsc[w][16 * tau + 4 * gq + e];
+        // QK: every K lookup of the chunk issued before the first MFMA.
+        half8 ka[2][4], kb[2][4];
+#pragma unroll
+        for (int tau = 0; tau < 2; ++tau) {
+            const uint32_t wd[4] = {cur.kw[tau].x, cur.kw[tau].y, cur.kw[tau].z, cur.kw[tau].w};
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                uint32_t e0[4], e1[4];  // K entries, S entries
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    const uint32_t a = lut_addr(wd[s], b, basek);
+                    e0[b] = *reinterpret_cast<const lds_u32*>(a + kOffK);
+                    e1[b] = *reinterpret_cast<const lds_u32*>(a);
+                }
+                ka[tau][s] = as_h8(e0[0], e0[1], e0[2], e0[3]);
+                kb[tau][s] = as_h8(e1[0], e1[1], e1[2], e1[3]);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        f32x4 cb[2], cs[2];
+#pragma unroll
+        for (int tau = 0; tau < 2; ++tau) {
+            cb[tau] = (f32x4){0.f, 0.f, 0.f, 0.f};
+            cs[tau] = cb[tau];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                cb[tau] = mma(ka[tau][s], bq[s], cb[tau]);
+                cs[tau] = mma(kb[tau][s], bq[s], cs[tau]);  // prod: residual signs; mse: lo parts
+            }
+        }
+        // V lookups (B operands of PV), in flight during the softmax.
+        uint32_t bv[8][4];  // [N-tile v = d - 8i][token pair]
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t we = cur.vw[2 * q], wo = cur.vw[2 * q + 1];
+            const uint32_t lob = (we & 0x0F0F0F0Fu) | ((wo & 0x0F0F0F0Fu) << 4);
+            const uint32_t hib = ((we >> 4) & 0x0F0F0F0Fu) | (wo & 0xF0F0F0F0u);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                bv[2 * b][q] = *reinterpret_cast<const lds_u32*>(lut_addr(lob, b, basev) + offv);
+                bv[2 * b + 1][q] = *reinterpret_cast<const lds_u32*>(lut_addr(hib, b, basev) + offv);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // Logits (base 2) of tokens 16 tau + 4 gq + e; hi + lo columns summed.
+        float lg[2][4];
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int tau = 0; tau < 2; ++tau)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float4 sc = scv[tau][e];
+                const float sb = cb[tau][e] + quad_xor<1>(cb[tau][e]);
+                const float sr = cs[tau][e] + quad_xor<1>(cs[tau][e]);
+                lg[tau][e] = fmaf(sb, sc.x, fmaf(sr, sc.y, sc.w));
+                mloc = fmaxf(mloc, lg[tau][e]);
+            }
+        mloc = fmaxf(mloc, lane_xor<16>(mloc));
+        mloc = fmaxf(mloc, lane_xor<32>(mloc));
+        // v_exp_f32 without denormal handling: arguments are <= 0 and a weight
+        // below 2^-126 of the running maximum is negligible.
+        const float m_new = fmaxf(m_run, mloc);
+        const float alpha = first ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+        m_run = m_new;
+        float lsum = 0.0f;
+#pragma unroll
+        for (int tau = 0; tau < 2; ++tau)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                lg[tau][e] = __builtin_amdgcn_exp2f(lg[tau][e] - m_new);
+                lsum += lg[tau][e];
+            }
+        l_run = l_run * alpha + lsum;
+        if (!first && __any(alpha != 1.0f)) {
+            // acc lane (d, g) holds columns 4g .. 4g + 3 = rows 2g, 2g + 1
+            const float a0 = __shfl(alpha, 4 * gq), a1 = __shfl(alpha, 4 * gq + 2);
+#pragma unroll
+            for (int v = 0; v < 8; ++v) {
+                acc[v][0] *= a0;
+                acc[v][1] *= a0;
+                acc[v][2] *= a1;
+                acc[v][3] *= a1;
+            }
+        }
+        // PV: P' = p * vs / aV as this column's fp16 part; k-index 8 gq + e is
+        // the logit of tile e / 4, element e % 4.
+        const half8 ap = as_h8(hilo_pair(lg[0][0], scv[0][0].z, lg[0][1], scv[0][1].z, lomask),
+                               hilo_pair(lg[0][2], scv[0][2].z, lg[0][3], scv[0][3].z, lomask),
+                               hilo_pair(lg[1][0], scv[1][0].z, lg[1][1], scv[1][1].z, lomask),
+                               hilo_pair(lg[1][2], scv[1][2].z, lg[1][3], scv[1][3].z, lomask));
+#pragma unroll
+        for (int v = 0; v < 8; ++v)
+            acc[v] = mma(ap, as_h8(bv[v][0], bv[v][1], bv[v][2], bv[v][3]), acc[v]);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        cur = nxt;
+        t0 = t1;
+        first = false;
+    }
+
+    // Wave results: l summed over the 4 lane groups of each column; o rows
+    // from the hi + lo columns.  Then the waves are merged per row, the
+    // inverse WHT and sign flip applied, and the partial written.
+    {
+        float l_tot = l_run + lane_xor<16>(l_run);
+        l_tot += lane_xor<32>(l_tot);
+        if (gq == 0 && !lo_col) {
+            mm[w][i >> 1] = m_run;
+            ml[w][i >> 1] = l_tot;
+        }
+    }
+    lds_barrier();  // every wave is done with the tables mo overwrites
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+        mo[w][2 * gq][8 * i + v] = acc[v][0] + acc[v][1];
+        mo[w][2 * gq + 1][8 * i + v] = acc[v][2] + acc[v][3];
+    }
+    lds_barrier();
+    const int r = w;  // this wave's row of the group
+    if (rg * kRows + r >= num_queries) return;  // wave-uniform, after the last barrier
+    float M = mm[0][r];
+#pragma unroll
+    for (int u = 1; u < kWaves; ++u) M = fmaxf(M, mm[u][r]);
+    float L = 0.f, o0 = 0.f, o1 = 0.f;
+#pragma unroll
+    for (int u = 0; u < kWaves; ++u) {
+        const float wt = __builtin_amdgcn_exp2f(mm[u][r] - M);  // (argument <= 0)
+        const float2 ov = *reinterpret_cast<const float2*>(&mo[u][r][2 * lane]);
+        L += ml[u][r] * wt;
+        o0 += ov.x * wt;
+        o1 += ov.y * wt;
+    }
+    wht_pair<64>(o0, o1, lane);
+    const float s0 = (h & 1) ? -inv : inv;
+    const size_t item = (size_t)rg * g.H + h;
+    const size_t pid = item * num_splits + split;
+    *reinterpret_cast<float2*>(po + (pid * kRows + r) * 128 + 2 * lane) = make_float2(o0 * s0, o1 * -s0);
+    if (lane == 0) pml[(item * kRows + r) * num_splits + split] = make_float2(M, L);
+}
+
+// Sum of the split partials of one output row (q, h): o = sum_s 2^(m_s - M)
+// o_s / sum_s 2^(m_s - M) l_s.  One wave per (row, 8-element slice of d):
+// lane = 8 split groups x 8 elements; group j takes splits j, j + 8, ..., 16
+// at a time (every load of a batch in flight together), merges them with a
+// running maximum, then the groups are merged across lanes (no LDS, no
+// barrier).  The 4 slices of one 128-byte line of the partials run on one
+// XCD (block b on XCD b % 8), so three of them find the line in that XCD's
+// L2.
+__global__ __launch_bounds__(64) void attn_decode_combine_kernel(
+    const float* __restrict__ po, const float2* __restrict__ pml, uint16_t* __restrict__ output,
+    int H, int rows, int S) {
+    using namespace mfma;
+    const int b = blockIdx.x;
+    const int xcd = b & 7, m = b >> 3;
+    const int p = (m >> 2) * 8 + xcd;  // (row, line) pair
+    const int row = p >> 2;
+    if (row >= rows) return;
+    const int t = threadIdx.x, dd = t & 7, grp = t >> 3;
+    const int d = 32 * (p & 3) + 8 * (m & 3) + dd;
+    const int q = row / H, h = row - q * H;
+    const int rg = q / kRows, r = q % kRows;
+    const size_t item = (size_t)rg * H + h;
+    const float2* mlr = pml + (item * kRows + r) * S;
+    const float* orow = po + (item * S * kRows + r) * 128 + d;  // split s: + s * kRows * 128
+    constexpr int kB = 16;
+    float M = kInitMax, L = 0.f, A = 0.f;
+    for (int base = grp; base < S; base += 8 * kB) {
+        float pm[kB], pl[kB], pv[kB];
+#pragma unroll
+        for (int k = 0; k < kB; ++k) {
+            const int s = base + 8 * k;
+            const int sc = s < S ? s : base;
+            const float2 v = mlr[sc];
+            pm[k] = s < S ? v.x : kInitMax;
+            pl[k] = v.y;
+            pv[k] = orow[(size_t)sc * kRows * 128];
+        }
+        float mb = M;
+#pragma unroll
+        for (int k = 0; k < kB; ++k) mb = fmaxf(mb, pm[k]);
+        // v_exp_f32 without denormal handling: arguments are <= 0 and a weight
+        // below 2^-126 of the largest is negligible.
+        const float sc = __builtin_amdgcn_exp2f(M - mb);
+        L *= sc;
+        A *= sc;
+#pragma unroll
+        for (int k = 0; k < kB; ++k) {
+            const float wt = __builtin_amdgcn_exp2f(pm[k] - mb);
+            L += pl[k] * wt;
+            A += pv[k] * wt;
+        }
+        M = mb;
+    }
+    auto merge = [&](float Mp, float Lp, float Ap) {
+        const float mn = fmaxf(M, Mp);
+        const float a = __builtin_amdgcn_exp2f(M - mn), c = __builtin_amdgcn_exp2f(Mp - mn);
+        L = L * a + Lp * c;
+        A = A * a + Ap * c;
+        M = mn;
+    };
+    merge(lane_xor<8>(M), lane_xor<8>(L), lane_xor<8>(A));
+    merge(lane_xor<16>(M), lane_xor<16>(L), lane_xor<16>(A));
+    merge(lane_xor<32>(M), lane_xor<32>(L), lane_xor<32>(A));
+    if (t < 8) output[(size_t)row * 128 + d] = f2h(L > 0.f ? A / L : A);
+}
+
+}  // namespace dec
+
 // New-token positions (row groups of one sequence) per paged workgroup.
 #ifndef TQ_PAGED_POSITIONS
 #define TQ_PAGED_POSITIONS 4
@@ -1791,6 +2324,47 @@ void launch_mfma_attention(const uint16_t* query, const uint8_t* pool, const int
                            output, g.H, splits);
     check_launch(combine_name);
 }
+
+// The slot-mapped decode (turbo_prod, turbo_mse; D = 128): split + combine.
+template <int SCH>
+void launch_decode_attention(const uint16_t* query, const uint8_t* pool, const int32_t* slots,
+                             uint16_t* output, const PageGeom& g, int num_queries,
+                             int num_kv_tokens, float inv, hipStream_t stream,
+                             const char* split_name, const char* combine_name,
+                             const Scratch& scratch) {
+    using namespace mfma;
+    const int rows = num_queries * g.H;
+    const int row_groups = (num_queries + kRows - 1) / kRows;
+    const int heads = g.H * row_groups;
+    // One 256-token split per workgroup, or longer splits once there are
+    // more than ~2 workgroups per CU.
+    const int max_splits = std::max(1, (num_kv_tokens + kSplitMinTokens - 1) / kSplitMinTokens);
+    const int want = std::max(1, (kSplitBlocksPerCU * num_cus() + heads - 1) / heads);
+    int splits = std::min(std::min(max_splits, want), 1024);
+    const int tps = num_kv_tokens > 0 ? (num_kv_tokens + splits - 1) / splits : 0;
+    if (tps > 0) splits = (num_kv_tokens + tps - 1) / tps;
+    // The combine: 32 blocks per pair of output rows (8-element slices).
+    const long long combine_blocks = ((long long)rows + 1) / 2 * 32;
+    if (combine_blocks > INT32_MAX) throw Error(std::string(combine_name) + ": too many query rows");
+    const size_t blocks = (size_t)splits * heads;
+    char* ws = static_cast<char*>(scratch.get(stream, blocks * dec::kPartBytes, split_name));
+    float* po = reinterpret_cast<float*>(ws);
+    float2* pml = reinterpret_cast<float2*>(ws + blocks * kRows * 128 * sizeof(float));
+    if (num_kv_tokens > 0) {
+        constexpr int kMaxGridYZ = 65535;
+        const dim3 grid = row_groups <= kMaxGridYZ && g.H <= kMaxGridYZ
+                              ? dim3(splits, g.H, row_groups)
+                              : dim3((unsigned)blocks);
+        hipLaunchKernelGGL((dec::attn_decode_split_kernel<SCH>), grid, dim3(64 * dec::kWaves), 0,
+                           stream, query, pool, slots, po, pml, inv, num_queries, num_kv_tokens,
+                           tps, splits, g);
+        check_launch(split_name);
+    }
+    // (no partials for an empty context: the combine writes zeros)
+    hipLaunchKernelGGL(dec::attn_decode_combine_kernel, dim3((unsigned)combine_blocks), dim3(64),
+                       0, stream, po, pml, output, g.H, rows, num_kv_tokens > 0 ? splits : 0);
+    check_launch(combine_name);
+}
 }  // namespace
 
 void launch_attention(Scheme s, const uint16_t* query, const uint8_t* pool, const int32_t* slots,
@@ -1801,15 +2375,15 @@ void launch_attention(Scheme s, const uint16_t* query, const uint8_t* pool, cons
     const float inv = inv_sqrt_d(g.D);
     if (mfma_attention_ok(g, pool)) {
         if (s == Scheme::Prod)
-            launch_mfma_attention<mfma::kSchProd>(query, pool, slots, output, g, num_queries,
-                                                  num_kv_tokens, inv, stream,
-                                                  "turbo_prod_fused_attn_split",
-                                                  "turbo_prod_fused_attn_combine", scratch);
+            launch_decode_attention<mfma::kSchProd>(query, pool, slots, output, g, num_queries,
+                                                    num_kv_tokens, inv, stream,
+                                                    "turbo_prod_fused_attn_split",
+                                                    "turbo_prod_fused_attn_combine", scratch);
         else
-            launch_mfma_attention<mfma::kSchMse>(query, pool, slots, output, g, num_queries,
-                                                 num_kv_tokens, inv, stream,
-                                                 "turbo_mse_fused_attn_split",
-                                                 "turbo_mse_fused_attn_combine", scratch);
+            launch_decode_attention<mfma::kSchMse>(query, pool, slots, output, g, num_queries,
+                                                   num_kv_tokens, inv, stream,
+                                                   "turbo_mse_fused_attn_split",
+                                                   "turbo_mse_fused_attn_combine", scratch);
         return;
     }
     // Enough waves to cover the chip several times, at least 32 tokens each.
