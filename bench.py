@@ -707,16 +707,39 @@ def pack_parity(w: Workload, kv, slots, pp, pm, pages) -> dict:
         mism["turbo_mse"] += int(np.count_nonzero(
             q.cpu().numpy() != orc.mse_pack(k, v, slots_np, pages, w.B)))
     with ThreadPoolExecutor(orc.nthreads) as ex:
-        pc = list(ex.map(lambda kv_: orc.boundary_counts("turbo_prod", *kv_), host))
+        pl = list(ex.map(lambda kv_: orc.prod_boundary_list(*kv_), host))
         mc = list(ex.map(lambda kv_: orc.boundary_counts("turbo_mse", *kv_), host))
+    # Each flagged turbo_prod value beside the GPU's own normalised value: the
+    # debug pack (tq_launch_turbo_prod_pack_kv_debug) of the same layer.
+    import torch
+    cfg = w.tq.default_config()
+    cfg.num_kv_heads, cfg.head_dim, cfg.block_size = w.H, w.D, w.B
+    lp = w.tq.make_layout_for(cfg)
+    scratch = torch.zeros(pages * lp.page_size_bytes, dtype=torch.uint8, device=w.dev)
+    kinds = ("k_code", "k_residual_sign", "v_code")
+    flagged = []
+    for layer, ((k, v), (elem, kind, val)) in enumerate(zip(kv, pl)):
+        if len(elem) == 0:
+            continue
+        dbg = w.tq.pack_debug(k, v, slots, scratch, lp, cfg)
+        idx = torch.from_numpy(elem).to(w.dev)
+        gkn = dbg["kn"].reshape(-1)[idx].cpu().numpy()
+        gvn = dbg["vn"].reshape(-1)[idx].cpu().numpy()
+        for e, kd, x, a, b in zip(elem, kind, val, gkn, gvn):
+            t, rest = divmod(int(e), w.H * w.D)
+            g_ = float(b if kd == 2 else a)
+            flagged.append({"layer": layer, "token": t, "head": rest // w.D, "d": rest % w.D,
+                            "kind": kinds[int(kd)], "oracle": float(x), "gpu": g_})
+        del dbg
     values = len(host) * host[0][0].size
     return {
         "layers_checked": len(host),
         "mismatched_page_bytes": mism,
         "values_per_tensor": values,
-        "turbo_prod_boundary": {"k_code": sum(c[0] for c in pc),
-                                "k_residual_sign": sum(c[1] for c in pc),
-                                "v_code": sum(c[2] for c in pc)},
+        "turbo_prod_boundary": {kinds[c]: int(sum(int((kd == c).sum()) for _, kd, _ in pl))
+                                for c in range(3)},
+        "turbo_prod_boundary_values": flagged,
+        "turbo_prod_boundary_gpu_equals_oracle": all(f["gpu"] == f["oracle"] for f in flagged),
         "turbo_mse_boundary": {"rows_norm_differs_unfused_pairsum": sum(c[0] for c in mc),
                                "code_bytes_differ_unfused_pairsum": sum(c[1] for c in mc),
                                "codes_within_1ulp": sum(c[2] for c in mc)},

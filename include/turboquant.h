@@ -101,6 +101,24 @@ int tq_launch_turbo_prod_pack_kv(const uint16_t* key, const uint16_t* value,
                                  const TQTurboProdPageLayout* layout, const TQConfig* cfg,
                                  int num_tokens, void* stream);
 
+/* Debug pack (no counterpart among the reference's C entries: it is the
+ * reference's C++ launcher launch_tq_turbo_prod_pack_kv with its six optional
+ * debug buffers, include/tq_turbo_prod.cuh:51-65, written by the kernel at
+ * src/cuda/tq_turbo_prod_kernels.cu:216-217, 243-246).  Packs exactly like
+ * tq_launch_turbo_prod_pack_kv (identical pages) and also writes, for every
+ * token and head, D values each in [num_tokens, H, D] layout: the rotated K
+ * and V (fp32, WHT(x * sign) / sqrt(D)), the clamped normalised K and V
+ * (fp32, clamp(rot / rms, +-2.5) and +-2.75: the values the codes are chosen
+ * from), and the 3-bit K and 4-bit V code indices (int32).  Every debug
+ * pointer may be NULL (not written); non-null ones must be 8-byte aligned
+ * device memory.  For parity triage, not for speed. */
+int tq_launch_turbo_prod_pack_kv_debug(const uint16_t* key, const uint16_t* value,
+                                       const int32_t* slot_mapping, uint8_t* page_pool,
+                                       const TQTurboProdPageLayout* layout, const TQConfig* cfg,
+                                       int num_tokens, void* stream, float* debug_k_rot,
+                                       float* debug_v_rot, float* debug_kn, float* debug_vn,
+                                       int32_t* debug_kidx, int32_t* debug_vidx);
+
 /* src/tq_capi.cpp:66 — dequantize to fp16 [num_tokens, H, D]. */
 int tq_launch_turbo_prod_dequant_kv(const uint8_t* page_pool, const int32_t* slot_mapping,
                                     uint16_t* out_key, uint16_t* out_value,

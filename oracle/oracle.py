@@ -146,6 +146,10 @@ class Oracle:
         L.tqo_prod_attention_f32.argtypes = [vp, vp, vp, c_int, c_int, c_int, c_int, c_int,
                                              POINTER(ProdLayout), vp, c_int]
         L.tqo_prod_pack_row.argtypes = [vp, vp, c_int, c_int, vp, vp, vp, vp, vp, vp, vp]
+        L.tqo_prod_pack_row_debug.argtypes = [vp, vp, c_int, c_int] + [vp] * 11
+        L.tqo_prod_pack_debug.argtypes = [vp, vp, c_int, c_int, c_int] + [vp] * 6 + [c_int]
+        L.tqo_prod_boundary_list.argtypes = [vp, vp, c_int, c_int, c_int, vp, vp, vp, c_longlong]
+        L.tqo_prod_boundary_list.restype = c_longlong
         L.tqo_mse_pack.argtypes = [vp, vp, vp, c_int, c_int, c_int, c_int, POINTER(MseLayout),
                                    vp, c_int, c_int]
         L.tqo_mse_pack_row.argtypes = [vp, c_int, c_int, c_int, vp, vp, vp]
@@ -266,6 +270,34 @@ class Oracle:
         self.lib.tqo_prod_pack_row(_p(k), _p(v), head, D, _p(k4), _p(v4), _p(sc[0:]),
                                    _p(sc[1:]), _p(sc[2:]), _p(kn), _p(vn))
         return dict(k4=k4, v4=v4, ks=int(sc[0]), kres=int(sc[1]), vs=int(sc[2]), kn=kn, vn=vn)
+
+    def prod_pack_debug(self, key, value) -> dict:
+        """The reference pack kernel's debug buffers for K, V [N, H, D]
+        (tq_turbo_prod_kernels.cu:216-217, 243-246): rotated K/V, clamped
+        normalised K/V (fp32) and the K / V code indices (int32), each
+        [N, H, D]."""
+        key, value = _u16(key), _u16(value)
+        N, H, D = key.shape
+        out = {n: np.zeros((N, H, D), np.float32) for n in ("k_rot", "v_rot", "kn", "vn")}
+        out.update({n: np.zeros((N, H, D), np.int32) for n in ("kidx", "vidx")})
+        self.lib.tqo_prod_pack_debug(_p(key), _p(value), N, H, D, _p(out["k_rot"]),
+                                     _p(out["v_rot"]), _p(out["kn"]), _p(out["vn"]),
+                                     _p(out["kidx"]), _p(out["vidx"]), self.nthreads)
+        return out
+
+    def prod_boundary_list(self, key, value, max_out: int = 1 << 16):
+        """The values boundary_counts('turbo_prod') counts: (flat element
+        index into [N, H, D], kind 0 K code / 1 K residual sign / 2 V code,
+        normalised value)."""
+        key, value = _u16(key), _u16(value)
+        N, H, D = key.shape
+        elem = np.zeros(max_out, np.int64)
+        kind = np.zeros(max_out, np.int32)
+        val = np.zeros(max_out, np.float32)
+        n = int(self.lib.tqo_prod_boundary_list(_p(key), _p(value), N * H, H, D, _p(elem),
+                                                _p(kind), _p(val), max_out))
+        n = min(n, max_out)
+        return elem[:n], kind[:n], val[:n]
 
     def prod_dequant(self, pool, slots, H: int, D: int, block_size: int = 16):
         pool = np.ascontiguousarray(pool, dtype=np.uint8)

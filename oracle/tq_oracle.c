@@ -254,14 +254,21 @@ static void rotate_row(const uint16_t* src, int head, int D, float* x) {
     for (int i = 0; i < D; ++i) x[i] *= inv;
 }
 
-/* B.1: src/cuda/tq_turbo_prod_kernels.cu:180-259 for one (token, head). */
-void tqo_prod_pack_row(const uint16_t* k, const uint16_t* v, int head, int D, uint8_t* k4,
-                       uint8_t* v4, uint16_t* ks, uint16_t* kres, uint16_t* vs, float* kn_out,
-                       float* vn_out) {
+/* B.1: src/cuda/tq_turbo_prod_kernels.cu:180-259 for one (token, head).
+ * The optional outputs are the reference kernel's debug buffers
+ * (:216-217, :243-246): rotated K/V, clamped normalised K/V, code indices. */
+void tqo_prod_pack_row_debug(const uint16_t* k, const uint16_t* v, int head, int D, uint8_t* k4,
+                             uint8_t* v4, uint16_t* ks, uint16_t* kres, uint16_t* vs,
+                             float* krot_out, float* vrot_out, float* kn_out, float* vn_out,
+                             int* kidx_out, int* vidx_out) {
     float sk[TQO_MAX_D], sv[TQO_MAX_D], red[TQO_MAX_D], e[TQO_MAX_D];
     int kc[TQO_MAX_D], kb[TQO_MAX_D], vc[TQO_MAX_D];
     rotate_row(k, head, D, sk);
     rotate_row(v, head, D, sv);
+    for (int i = 0; i < D; ++i) {
+        if (krot_out) krot_out[i] = sk[i];
+        if (vrot_out) vrot_out[i] = sv[i];
+    }
     for (int i = 0; i < D; ++i) red[i] = sk[i] * sk[i];
     float krms = rms_of(red, D, D);
     *ks = tqo_f2h(krms);
@@ -277,6 +284,8 @@ void tqo_prod_pack_row(const uint16_t* k, const uint16_t* v, int head, int D, ui
         e[i] = kn - kK3[kc[i]];
         kb[i] = (e[i] >= 0.0f) ? 1 : 0;
         vc[i] = tqo_nearest_v4(vn);
+        if (kidx_out) kidx_out[i] = kc[i];
+        if (vidx_out) vidx_out[i] = vc[i];
     }
     for (int i = 0; i < D; ++i) red[i] = e[i] * e[i];
     *kres = tqo_f2h(rms_of(red, D, D));
@@ -285,6 +294,39 @@ void tqo_prod_pack_row(const uint16_t* k, const uint16_t* v, int head, int D, ui
         k4[j] = (uint8_t)(a | (b << 4));
         v4[j] = (uint8_t)(vc[2 * j] | (vc[2 * j + 1] << 4));
     }
+}
+
+void tqo_prod_pack_row(const uint16_t* k, const uint16_t* v, int head, int D, uint8_t* k4,
+                       uint8_t* v4, uint16_t* ks, uint16_t* kres, uint16_t* vs, float* kn_out,
+                       float* vn_out) {
+    tqo_prod_pack_row_debug(k, v, head, D, k4, v4, ks, kres, vs, NULL, NULL, kn_out, vn_out, NULL,
+                            NULL);
+}
+
+typedef struct {
+    const uint16_t *key, *value;
+    int H, D;
+    float *krot, *vrot, *kn, *vn;
+    int *kidx, *vidx;
+} dbg_ctx;
+
+static void prod_debug_one(void* p, long long row) {
+    dbg_ctx* c = (dbg_ctx*)p;
+    const size_t off = (size_t)row * (size_t)c->D;
+    uint8_t k4[TQO_MAX_D / 2], v4[TQO_MAX_D / 2];
+    uint16_t a, b, cc;
+#define TQO_AT(ptr) ((ptr) ? (ptr) + off : NULL)
+    tqo_prod_pack_row_debug(c->key + off, c->value + off, (int)(row % c->H), c->D, k4, v4, &a, &b,
+                            &cc, TQO_AT(c->krot), TQO_AT(c->vrot), TQO_AT(c->kn), TQO_AT(c->vn),
+                            TQO_AT(c->kidx), TQO_AT(c->vidx));
+#undef TQO_AT
+}
+
+void tqo_prod_pack_debug(const uint16_t* key, const uint16_t* value, int num_tokens, int H, int D,
+                         float* krot, float* vrot, float* kn, float* vn, int* kidx, int* vidx,
+                         int nthreads) {
+    dbg_ctx c = {key, value, H, D, krot, vrot, kn, vn, kidx, vidx};
+    parallel_rows((long long)num_tokens * H, nthreads, prod_debug_one, &c);
 }
 
 typedef struct {
@@ -685,6 +727,39 @@ void tqo_prod_boundary_count(const uint16_t* key, const uint16_t* value, int num
             counts[2] += code_boundary(vn[i], tqo_nearest_v4);
         }
     }
+}
+
+/* The values tqo_prod_boundary_count counts, listed: element index
+ * row * D + i, kind (0: K code, 1: K residual sign, 2: V code) and the
+ * normalised value (kn or vn).  Returns the number found; at most max_out
+ * are written. */
+long long tqo_prod_boundary_list(const uint16_t* key, const uint16_t* value, int num_rows, int H,
+                                 int D, long long* out_elem, int* out_kind, float* out_val,
+                                 long long max_out) {
+    long long n = 0;
+    float kn[TQO_MAX_D], vn[TQO_MAX_D];
+    uint8_t k4[TQO_MAX_D / 2], v4[TQO_MAX_D / 2];
+    uint16_t a, b, cc;
+    for (int r = 0; r < num_rows; ++r) {
+        tqo_prod_pack_row(key + (size_t)r * D, value + (size_t)r * D, r % H, D, k4, v4, &a, &b,
+                          &cc, kn, vn);
+        for (int i = 0; i < D; ++i) {
+            float lvl = kK3[tqo_nearest_k3(kn[i])];
+            float up = nextafterf(kn[i], INFINITY) - lvl, dn = nextafterf(kn[i], -INFINITY) - lvl;
+            const int hit[3] = {code_boundary(kn[i], tqo_nearest_k3), (up >= 0.0f) != (dn >= 0.0f),
+                                code_boundary(vn[i], tqo_nearest_v4)};
+            for (int kind = 0; kind < 3; ++kind) {
+                if (!hit[kind]) continue;
+                if (n < max_out) {
+                    out_elem[n] = (long long)r * D + i;
+                    out_kind[n] = kind;
+                    out_val[n] = kind == 2 ? vn[i] : kn[i];
+                }
+                ++n;
+            }
+        }
+    }
+    return n;
 }
 
 void tqo_mse_boundary_count(const uint16_t* key, const uint16_t* value, int num_rows, int H,

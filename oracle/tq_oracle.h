@@ -72,6 +72,17 @@ void tqo_prod_pack(const uint16_t* key, const uint16_t* value, const int32_t* sl
 void tqo_prod_pack_row(const uint16_t* k, const uint16_t* v, int head, int D,
                        uint8_t* k4, uint8_t* v4, uint16_t* ks, uint16_t* kres, uint16_t* vs,
                        float* kn, float* vn);
+/* The same, with the reference kernel's debug outputs (tq_turbo_prod_kernels.cu:
+ * 216-217, 243-246): rotated K/V, clamped normalised K/V, 3-bit K and 4-bit V
+ * code indices, D values each (every pointer may be NULL). */
+void tqo_prod_pack_row_debug(const uint16_t* k, const uint16_t* v, int head, int D,
+                             uint8_t* k4, uint8_t* v4, uint16_t* ks, uint16_t* kres,
+                             uint16_t* vs, float* krot, float* vrot, float* kn, float* vn,
+                             int* kidx, int* vidx);
+/* Those outputs for K, V [num_tokens, H, D], as [num_tokens, H, D] arrays. */
+void tqo_prod_pack_debug(const uint16_t* key, const uint16_t* value, int num_tokens, int H, int D,
+                         float* krot, float* vrot, float* kn, float* vn, int* kidx, int* vidx,
+                         int nthreads);
 void tqo_prod_dequant(const uint8_t* pool, const int32_t* slots, int num_tokens, int H, int D,
                       int block_size, const tqo_prod_layout* L, uint16_t* out_key,
                       uint16_t* out_value, int nthreads);
@@ -116,6 +127,12 @@ void tqo_mse_attention_f32(const uint16_t* query, const uint8_t* pool, const int
  * counts[2] = V code boundary (turbo_prod) / K+V code boundary (turbo_mse). */
 void tqo_prod_boundary_count(const uint16_t* key, const uint16_t* value, int num_rows, int H,
                              int D, long long counts[3]);
+/* The values tqo_prod_boundary_count counts: element row * D + i, kind
+ * (0 K code, 1 K residual sign, 2 V code) and the normalised value; returns
+ * how many there are (at most max_out written). */
+long long tqo_prod_boundary_list(const uint16_t* key, const uint16_t* value, int num_rows, int H,
+                                 int D, long long* out_elem, int* out_kind, float* out_val,
+                                 long long max_out);
 void tqo_mse_boundary_count(const uint16_t* key, const uint16_t* value, int num_rows, int H,
                             int D, long long counts[3]);
 

@@ -508,6 +508,28 @@ extern "C" int tq_launch_turbo_prod_pack_kv(const uint16_t* key, const uint16_t*
     });
 }
 
+extern "C" int tq_launch_turbo_prod_pack_kv_debug(
+    const uint16_t* key, const uint16_t* value, const int32_t* slot_mapping, uint8_t* page_pool,
+    const TQTurboProdPageLayout* layout, const TQConfig* cfg, int num_tokens, void* stream,
+    float* debug_k_rot, float* debug_v_rot, float* debug_kn, float* debug_vn, int32_t* debug_kidx,
+    int32_t* debug_vidx) {
+    if (!key || !value || !slot_mapping || !page_pool || !layout || !cfg) return -1;
+    return guarded_sync(stream, [&] {
+        const tq::PageGeom g = tq::prod_geom(*cfg, *layout);
+        check_grid(num_tokens, "turbo_prod_pack_kv_kernel", true);
+        check_rows(num_tokens, g.H, "turbo_prod_pack_kv");
+        tq::PackDebug dbg;
+        dbg.k_rot = debug_k_rot;
+        dbg.v_rot = debug_v_rot;
+        dbg.kn = debug_kn;
+        dbg.vn = debug_vn;
+        dbg.kidx = debug_kidx;
+        dbg.vidx = debug_vidx;
+        tq::launch_prod_pack_debug(key, value, slot_mapping, page_pool, g, num_tokens, dbg,
+                                   static_cast<hipStream_t>(stream));
+    });
+}
+
 extern "C" int tq_launch_turbo_prod_dequant_kv(const uint8_t* page_pool,
                                                const int32_t* slot_mapping, uint16_t* out_key,
                                                uint16_t* out_value,

@@ -26,11 +26,13 @@ constexpr int kPackLanes = 8;
 // ---------------------------------------------------------------------------
 // turbo_prod pack — src/cuda/tq_turbo_prod_kernels.cu:110-260
 // ---------------------------------------------------------------------------
+// dbg: the reference kernel's debug buffers (:216-217, :243-246), written
+// for every row when non-null (they depend on K/V only, not on the slot).
 template <int D>
 __global__ __launch_bounds__(kBlock) void prod_pack_kernel(
     const uint16_t* __restrict__ key, const uint16_t* __restrict__ value,
     const int32_t* __restrict__ slots, uint8_t* __restrict__ pool, PageGeom g, int num_rows,
-    float inv) {
+    float inv, PackDebug dbg) {
     constexpr int L = D / 2;
     const int j = threadIdx.x % L;
     const int row = blockIdx.x * (kBlock / L) + threadIdx.x / L;
@@ -65,6 +67,12 @@ __global__ __launch_bounds__(kBlock) void prod_pack_kernel(
     const int q0 = nearest_v4(vn0), q1 = nearest_v4(vn1);
 
     if (!valid) return;
+    if (dbg.k_rot) *reinterpret_cast<float2*>(dbg.k_rot + off) = make_float2(k0, k1);
+    if (dbg.v_rot) *reinterpret_cast<float2*>(dbg.v_rot + off) = make_float2(v0, v1);
+    if (dbg.kn) *reinterpret_cast<float2*>(dbg.kn + off) = make_float2(kn0, kn1);
+    if (dbg.vn) *reinterpret_cast<float2*>(dbg.vn + off) = make_float2(vn0, vn1);
+    if (dbg.kidx) *reinterpret_cast<int2*>(dbg.kidx + off) = make_int2(c0, c1);
+    if (dbg.vidx) *reinterpret_cast<int2*>(dbg.vidx + off) = make_int2(q0, q1);
     const int slot = slots[t];
     if (slot < 0) return;
     int page, tib;
@@ -1150,13 +1158,31 @@ void launch_pack(Scheme s, const uint16_t* key, const uint16_t* value, const int
     }
     if (s == Scheme::Prod) {
         TQ_DISPATCH_D(g.D, hipLaunchKernelGGL(prod_pack_kernel<kD>, grid, dim3(kBlock), 0, stream,
-                                              key, value, slots, pool, g, rows, inv));
+                                              key, value, slots, pool, g, rows, inv, PackDebug{}));
         check_launch("turbo_prod_pack_kv_kernel");
     } else {
         TQ_DISPATCH_D(g.D, hipLaunchKernelGGL(mse_pack_kernel<kD>, grid, dim3(kBlock), 0, stream,
                                               key, value, slots, pool, g, rows, inv));
         check_launch("turbo_mse_pack_kv_kernel");
     }
+}
+
+void launch_prod_pack_debug(const uint16_t* key, const uint16_t* value, const int32_t* slots,
+                            uint8_t* pool, const PageGeom& g, int num_tokens, const PackDebug& dbg,
+                            hipStream_t stream) {
+    const int rows = num_tokens * g.H;
+    if (rows <= 0) return;
+    // (debug buffers are written as float2 / int2 pairs)
+    const auto al8 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7) == 0; };
+    if (!al8(dbg.k_rot) || !al8(dbg.v_rot) || !al8(dbg.kn) || !al8(dbg.vn) || !al8(dbg.kidx) ||
+        !al8(dbg.vidx))
+        throw Error("turbo_prod pack debug: debug buffers must be 8-byte aligned");
+    const int rpb = kBlock / (g.D / 2);
+    const dim3 grid((rows + rpb - 1) / rpb);
+    const float inv = inv_sqrt_d(g.D);
+    TQ_DISPATCH_D(g.D, hipLaunchKernelGGL(prod_pack_kernel<kD>, grid, dim3(kBlock), 0, stream, key,
+                                          value, slots, pool, g, rows, inv, dbg));
+    check_launch("turbo_prod_pack_kv_kernel");
 }
 
 void launch_pack_layers(Scheme s, const uint16_t* const* keys, const uint16_t* const* values,

@@ -86,6 +86,17 @@ void release_workspaces();
 // ---- launchers (tq_prod.hip, tq_mse.hip, tq_attention.hip) ---------------
 void launch_pack(Scheme s, const uint16_t* key, const uint16_t* value, const int32_t* slots,
                  uint8_t* pool, const PageGeom& g, int num_tokens, hipStream_t stream);
+// The reference pack kernel's optional debug buffers (include/tq_turbo_prod.cuh:
+// 60-65), [num_tokens, H, D] each, null = not written: rotated K/V, clamped
+// normalised K/V (fp32), 3-bit K and 4-bit V code indices (int32).
+struct PackDebug {
+    float *k_rot = nullptr, *v_rot = nullptr, *kn = nullptr, *vn = nullptr;
+    int32_t *kidx = nullptr, *vidx = nullptr;
+};
+// turbo_prod pack that also writes `dbg` (pages identical to launch_pack's).
+void launch_prod_pack_debug(const uint16_t* key, const uint16_t* value, const int32_t* slots,
+                            uint8_t* pool, const PageGeom& g, int num_tokens, const PackDebug& dbg,
+                            hipStream_t stream);
 // Pack of num_layers layers' K/V sharing one slot mapping, in as few launches
 // as possible (one per 64 layers for D = 64, 128 and aligned buffers).
 void launch_pack_layers(Scheme s, const uint16_t* const* keys, const uint16_t* const* values,

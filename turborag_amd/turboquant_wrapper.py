@@ -122,6 +122,9 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "tq_launch_turbo_prod_pack_kv": ([c_void_p, c_void_p, _P(c_int32), _P(c_uint8),
                                       _P(TQTurboProdPageLayout), _P(TQConfig), c_int,
                                       c_void_p], c_int),
+    "tq_launch_turbo_prod_pack_kv_debug": ([c_void_p, c_void_p, _P(c_int32), _P(c_uint8),
+                                            _P(TQTurboProdPageLayout), _P(TQConfig), c_int,
+                                            c_void_p] + [c_void_p] * 6, c_int),
     "tq_launch_turbo_prod_dequant_kv": ([_P(c_uint8), _P(c_int32), c_void_p, c_void_p,
                                          _P(TQTurboProdPageLayout), _P(TQConfig), c_int,
                                          c_void_p], c_int),
@@ -346,6 +349,31 @@ class TurboQuantWrapper:
             ctypes.byref(layout), ctypes.byref(cfg), N, self._stream(stream))
         if rc != 0:
             self._kernel_raise(rc, "turbo_prod", "pack_kv")
+
+    def pack_debug(self, key, value, slot_mapping, page_pool, layout, cfg,
+                   stream: int = 0) -> dict:
+        """pack() plus the reference pack kernel's debug buffers
+        (include/tq_turbo_prod.cuh:60-65; tq_launch_turbo_prod_pack_kv_debug):
+        k_rot, v_rot (rotated K/V), kn, vn (clamped normalised K/V) as fp32
+        and kidx, vidx (code indices) as int32, each [N, H, D] on key's
+        device."""
+        N = key.shape[0]
+        H, D = cfg.num_kv_heads, cfg.head_dim
+        thd = N * H * D
+        self._check("turbo_prod", "pack_kv", key=(key, torch.float16, thd),
+                    value=(value, torch.float16, thd), slot_mapping=(slot_mapping, torch.int32, N),
+                    page_pool=(page_pool, torch.uint8, 0))
+        out = {n: torch.empty(N, H, D, dtype=torch.float32, device=key.device)
+               for n in ("k_rot", "v_rot", "kn", "vn")}
+        out.update({n: torch.empty(N, H, D, dtype=torch.int32, device=key.device)
+                    for n in ("kidx", "vidx")})
+        rc = self._lib.tq_launch_turbo_prod_pack_kv_debug(
+            self._vp(key), self._vp(value), self._i32p(slot_mapping), self._u8p(page_pool),
+            ctypes.byref(layout), ctypes.byref(cfg), N, self._stream(stream),
+            *[self._vp(out[n]) for n in ("k_rot", "v_rot", "kn", "vn", "kidx", "vidx")])
+        if rc != 0:
+            self._kernel_raise(rc, "turbo_prod", "pack_kv")
+        return out
 
     def dequant(self, page_pool, slot_mapping, out_key, out_value, layout, cfg,
                 stream: int = 0) -> None:
