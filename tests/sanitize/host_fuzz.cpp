@@ -105,6 +105,8 @@ int run_abi() {
     uint8_t* fp = reinterpret_cast<uint8_t*>(0x3000);
     CHECK(tq_launch_turbo_prod_pack_kv(nullptr, fk, fs, fp, &lp, &cfg, 4, nullptr) == -1);
     CHECK(tq_launch_turbo_prod_dequant_kv(fp, fs, fk, nullptr, &lp, &cfg, 4, nullptr) == -1);
+    CHECK(tq_launch_turbo_prod_pack_kv_debug(fk, fk, nullptr, fp, &lp, &cfg, 4, nullptr, nullptr,
+                                             nullptr, nullptr, nullptr, nullptr, nullptr) == -1);
     CHECK(tq_launch_turbo_prod_fused_attention_output(fk, fp, fs, fk, nullptr, &cfg, 8, 4,
                                                       nullptr) == -1);
     CHECK(tq_launch_turbo_mse_pack_kv(fk, fk, fs, fp, &lm, nullptr, 4, nullptr) == -1);

@@ -15,6 +15,10 @@ namespace {
 
 void launch_pack(Scheme, const uint16_t*, const uint16_t*, const int32_t*, uint8_t*,
                  const PageGeom&, int, hipStream_t) { no_device("pack"); }
+void launch_prod_pack_debug(const uint16_t*, const uint16_t*, const int32_t*, uint8_t*,
+                            const PageGeom&, int, const PackDebug&, hipStream_t) {
+    no_device("pack debug");
+}
 void launch_dequant(Scheme, const uint8_t*, const int32_t*, uint16_t*, uint16_t*,
                     const PageGeom&, int, hipStream_t, bool) { no_device("dequant"); }
 void launch_pack_layers(Scheme, const uint16_t* const*, const uint16_t* const*, const int32_t*,

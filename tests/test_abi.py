@@ -95,6 +95,9 @@ def test_null_pointers_return_minus_one(tq):
     assert L.tq_make_turbo_mse_layout(byref(cfg), nul) == -1
     assert L.tq_launch_turbo_prod_pack_kv(fake, nul, i32, u8, byref(lp), byref(cfg), 1, None) == -1
     assert L.tq_launch_turbo_prod_dequant_kv(u8, i32, fake, fake, nul, byref(cfg), 1, None) == -1
+    # (the debug pack's six debug pointers may be NULL; the pack's own may not)
+    assert L.tq_launch_turbo_prod_pack_kv_debug(fake, fake, i32, nul, byref(lp), byref(cfg), 1,
+                                                None, fake, fake, fake, fake, fake, fake) == -1
     assert L.tq_launch_turbo_prod_fused_attention_logits(fake, u8, i32, nul, byref(lp),
                                                          byref(cfg), 1, 1, None) == -1
     assert L.tq_launch_turbo_prod_fused_attention_output(fake, u8, i32, fake, byref(lp), nul,

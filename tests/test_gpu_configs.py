@@ -240,9 +240,10 @@ def _hip():
 
 
 def test_workspace_many_streams(tq, oracle, cuda):
-    """70 distinct HIP streams (default priority), one call each: past 64
-    cached streams the cache is synchronized and freed; outputs stay right
-    before and after."""
+    """70 distinct HIP streams (default priority), one call each with no
+    synchronization in between: past 64 cached streams the least recently
+    used buffers are evicted (freed, or retired behind an event on their
+    stream while its kernels still run); every output stays right."""
     import ctypes
     cfg, lp, _ = _cfg(tq, 2, 128)
     q, pool, slots, ref = _att_case(oracle, 1200, 70)
@@ -264,6 +265,52 @@ def test_workspace_many_streams(tq, oracle, cuda):
         torch.cuda.synchronize()
         for out in outs:
             assert _rel_err(out.cpu().float().numpy(), ref) < ATT_TOL
+    finally:
+        torch.cuda.synchronize()
+        tq.release_workspaces()
+        for st in streams:
+            hip.hipStreamDestroy(st)
+
+
+def test_workspace_eviction_during_capture(tq, oracle, cuda):
+    """A graph is being captured on one stream while calls on 70 other HIP
+    streams cycle the cache past its 64 streams (evictions with no device
+    synchronization): the capture stays valid, its replays and every eager
+    output equal the oracle."""
+    import ctypes
+    cfg, lp, _ = _cfg(tq, 2, 128)
+    q, pool, slots, ref = _att_case(oracle, 1500, 90)
+    q, pool, slots = q.to(cuda), torch.from_numpy(pool).to(cuda), slots.to(cuda)
+    qb, poolb, slotsb, refb = _att_case(oracle, 3000, 91)
+    qb, poolb, slotsb = qb.to(cuda), torch.from_numpy(poolb).to(cuda), slotsb.to(cuda)
+    tq.release_workspaces()
+    hip = _hip()
+    streams = []
+    for _ in range(70):
+        h = ctypes.c_void_p()
+        assert hip.hipStreamCreate(ctypes.byref(h)) == 0
+        streams.append(h.value)
+    cap = torch.cuda.Stream()
+    out = torch.zeros(8, 2, 128, dtype=torch.float16, device=cuda)
+    outs = [torch.zeros(8, 2, 128, dtype=torch.float16, device=cuda) for _ in streams]
+    torch.cuda.synchronize()
+    try:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=cap, capture_error_mode="relaxed"):
+            tq.fused_attn_output(q, pool, slots, out, lp, cfg, 8, 1500,
+                                 stream=torch.cuda.current_stream().cuda_stream)
+            for st, o in zip(streams, outs):  # eager, on other streams, mid-capture
+                tq.fused_attn_output(qb, poolb, slotsb, o, lp, cfg, 8, 3000, stream=st)
+        torch.cuda.synchronize()
+        for o in outs:
+            assert _rel_err(o.cpu().float().numpy(), refb) < ATT_TOL
+        for rep in range(3):
+            out.zero_()
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert _rel_err(out.cpu().float().numpy(), ref) < ATT_TOL, rep
+        del g
     finally:
         torch.cuda.synchronize()
         tq.release_workspaces()

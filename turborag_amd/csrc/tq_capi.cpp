@@ -293,17 +293,21 @@ int num_cus() {
 // and freed once that event has completed (checked on later calls).  A
 // buffer handed out while its stream was being captured into a graph is
 // referenced by that graph, so it is never freed automatically, only by
-// tq_workspace_release().  More than kMaxStreams cached streams: the devices
-// are synchronized and the buffers no graph references are freed.
+// tq_workspace_release().  Past kMaxStreams cached streams the least recently
+// used buffer that no graph references is evicted the same way: freed at
+// once if its stream is idle, otherwise retired behind an event recorded on
+// its stream.  No launching entry synchronizes a device or another stream.
 namespace {
 struct WsBuf {
     void* p = nullptr;
     size_t n = 0;
     bool captured = false;  // handed out during a stream capture
+    uint64_t last_use = 0;  // handout tick (eviction order)
 };
+uint64_t g_ws_tick = 0;
 struct Retired {
     void* p;
-    hipEvent_t ev;  // null: outgrown during capture, freed only on release
+    hipEvent_t ev;  // null: outgrown during capture, or its stream unknown: freed only on release
     int dev;
 };
 std::mutex g_ws_mu;
@@ -334,6 +338,47 @@ void reap_retired() {
             ++k;
         }
     }
+}
+
+// Evicts the least recently used cached buffer that no captured graph
+// references and whose stream is not being captured (none: the cache grows).
+// Its stream idle: freed now.  Still running work: retired behind an event
+// recorded on that stream.  A stream the runtime no longer knows (destroyed):
+// parked, freed only by tq_workspace_release, since it cannot be ordered
+// behind that stream's last kernels.  Lock held.
+void evict_lru() {
+    auto victim = g_ws.end();
+    for (auto it = g_ws.begin(); it != g_ws.end(); ++it) {
+        if (it->second.captured) continue;
+        if (victim != g_ws.end() && it->second.last_use >= victim->second.last_use) continue;
+        victim = it;
+    }
+    if (victim == g_ws.end()) return;
+    const int dev = victim->first.first;
+    const hipStream_t s = victim->first.second;
+    int cur = 0;
+    (void)hipGetDevice(&cur);
+    (void)hipSetDevice(dev);
+    if (capturing(s)) {  // (its next handout marks it captured)
+        (void)hipSetDevice(cur);
+        return;
+    }
+    Retired r{victim->second.p, nullptr, dev};
+    const hipError_t q = hipStreamQuery(s);
+    if (q == hipSuccess) {
+        (void)hipFree(r.p);
+    } else if (q == hipErrorNotReady &&
+               hipEventCreateWithFlags(&r.ev, hipEventDisableTiming) == hipSuccess &&
+               hipEventRecord(r.ev, s) == hipSuccess) {
+        g_retired.push_back(r);
+    } else {
+        if (r.ev) (void)hipEventDestroy(r.ev);
+        r.ev = nullptr;
+        g_retired.push_back(r);  // parked until tq_workspace_release
+    }
+    (void)hipGetLastError();
+    (void)hipSetDevice(cur);
+    g_ws.erase(victim);
 }
 
 // Synchronizes every device holding a cached buffer and frees them all
@@ -383,11 +428,12 @@ void* workspace(hipStream_t stream, size_t bytes) {
     auto it = g_ws.find({dev, stream});
     if (it != g_ws.end() && it->second.n >= bytes && it->second.p) {
         it->second.captured = it->second.captured || cap;
+        it->second.last_use = ++g_ws_tick;
         return it->second.p;
     }
     if (!cap) {
         reap_retired();
-        if (it == g_ws.end() && g_ws.size() >= kMaxStreams) release_all(/*keep_captured=*/true);
+        if (it == g_ws.end() && g_ws.size() >= kMaxStreams) evict_lru();
     }
     WsBuf& b = g_ws[{dev, stream}];
     size_t n = std::max<size_t>(bytes, 1 << 20);
@@ -412,6 +458,7 @@ void* workspace(hipStream_t stream, size_t bytes) {
     b.p = p;
     b.n = n;
     b.captured = cap;
+    b.last_use = ++g_ws_tick;
     return p;
 }
 
