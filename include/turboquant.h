@@ -287,8 +287,8 @@ int tq_workspace_release(void);
  * semantics, same arguments and result) with its split-K partials in a
  * static 4 MiB device array instead of an allocated workspace; it calls no
  * hipMalloc, hipFree or allocating library routine.  A launch whose
- * partials exceed 4 MiB (more than 993 split workgroups of 8 query rows)
- * returns -2.  Every call on one GPU shares that GPU's array: calls that
+ * partials exceed 4 MiB (more than 1,008 split workgroups of 8 query rows,
+ * 4,160 bytes each) returns -2.  Every call on one GPU shares that GPU's array: calls that
  * overlap on one GPU (other streams, threads or graph replays) race. */
 int tq_launch_turbo_prod_fused_attention_output_noalloc(
     const uint16_t* query, const uint8_t* page_pool, const int32_t* slot_mapping,

@@ -1,7 +1,8 @@
 """The disk-load latency harness (turborag_amd/ttft.py, the counterpart of
 tq_backend/ttft_sim.py:90-147): the layer file it writes is the oracle's pack
-of the same seeded tokens into slots 0..N-1, it is reused on the next call,
-and a scheme without pages gives 0."""
+of the same seeded tokens into slots 0..N-1, it is reused on the next call
+(by the pinned path and by the reference's load steps), and a scheme without
+pages gives 0."""
 from __future__ import annotations
 
 import numpy as np
@@ -28,4 +29,11 @@ def test_disk_load_file_and_timing(tq, oracle, cuda, tmp_path, scheme):
     mtime = path.stat().st_mtime_ns
     assert simulate_disk_load_us(tq, scheme, N, H, D, tmp_path, warmup=0, iters=1) > 0.0
     assert path.stat().st_mtime_ns == mtime  # reused, not rewritten
+    # the reference's load steps on the same file (its figure, comparable
+    # with the reference harness's)
+    assert simulate_disk_load_us(tq, scheme, N, H, D, tmp_path, warmup=0, iters=2,
+                                 mode="reference") > 0.0
+    assert path.stat().st_mtime_ns == mtime
+    with pytest.raises(ValueError):
+        simulate_disk_load_us(tq, scheme, N, H, D, tmp_path, mode="mmap")
     assert simulate_disk_load_us(tq, "fp16", N, H, D, tmp_path) == 0.0

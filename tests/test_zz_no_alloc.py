@@ -86,9 +86,42 @@ def test_noalloc_under_graph_capture(tq, oracle, cuda):
     del g
 
 
+def test_noalloc_scratch_boundary(tq, oracle, cuda):
+    """One kv head and 16 tokens (one split per row group): 1,008 row groups
+    need 1,008 split partials of 4,160 bytes (4,193,280 of the 4,194,304
+    scratch bytes) and are accepted, equal to the allocating entry and the
+    oracle; 1,009 (4,197,440 bytes) are refused with rc -2 and the output
+    untouched."""
+    cfg, lp = _cfg(tq, H=1)
+    N, B = 16, 16
+    k, v = kv_tokens_major(N, 1, 128, seed=95)
+    slots = torch.arange(N, dtype=torch.int32, device=cuda)
+    pool = torch.zeros(lp.page_size_bytes, dtype=torch.uint8, device=cuda)
+    tq.pack(k.to(cuda), v.to(cuda), slots, pool, lp, cfg)
+    for groups, ok in ((1008, True), (1009, False)):
+        print(f"[noalloc boundary] row groups={groups}", flush=True)
+        Q = 8 * groups
+        q = query(Q, 128, seed=96).reshape(Q, 1, 128).to(cuda)
+        out = torch.full((Q, 1, 128), 3.0, dtype=torch.float16, device=cuda)
+        if not ok:
+            with pytest.raises(RuntimeError, match="split-K scratch"):
+                tq.fused_attn_output_noalloc(q, pool, slots, out, lp, cfg, Q, N)
+            torch.cuda.synchronize()
+            assert torch.all(out == 3.0)  # nothing ran
+            continue
+        tq.fused_attn_output_noalloc(q, pool, slots, out, lp, cfg, Q, N)
+        want = torch.zeros_like(out)
+        tq.fused_attn_output(q, pool, slots, want, lp, cfg, Q, N)
+        torch.cuda.synchronize()
+        assert np.array_equal(as_u16(out), as_u16(want))
+        ref = oracle.prod_attention_f64(as_u16(q.cpu()), pool.cpu().numpy(), slots.cpu().numpy(),
+                                        B)
+        assert _rel(out.cpu().float().numpy(), ref) < 1e-3
+
+
 def test_noalloc_rejects_launch_beyond_scratch(tq, cuda):
-    """1000 row groups of 8 rows x 2 kv heads need 1000 split partials of
-    4224 bytes: more than the 4 MiB scratch -> rc -2, nothing launched."""
+    """1000 row groups of 8 rows x 2 kv heads need 2,000 split partials of
+    4,160 bytes: more than the 4 MiB scratch -> rc -2, nothing launched."""
     cfg, lp = _cfg(tq)
     Q, N = 8 * 1000, 16
     q = torch.zeros(Q, 2, 128, dtype=torch.float16, device=cuda)

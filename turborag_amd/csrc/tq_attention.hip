@@ -2432,10 +2432,9 @@ void launch_paged_attention(Scheme s, const uint16_t* query, const uint8_t* pool
     constexpr int kPass = kSplitChunk * kSplitWaves;
     const int Gh = 8 * ((kPagedSegmentsPerCU * num_cus() + 8 * g.H - 1) / (8 * g.H));
     const int G = Gh * g.H;
-    // The plan counts work in int32: at most H * 4 * ceil(max_kv_len / kPass)
-    // per row group.
-    if ((long long)row_groups * g.H * 4 * ((std::max(max_kv_len, 0) + kPass - 1) / kPass) >
-        INT32_MAX)
+    // The plan counts each kv head's work in int32: at most
+    // 4 * ceil(max_kv_len / kPass) per row group (every head has the same).
+    if ((long long)row_groups * 4 * ((std::max(max_kv_len, 0) + kPass - 1) / kPass) > INT32_MAX)
         throw Error("paged attention: too many rows for this max_kv_len");
     // Workspace: the partials (slot (unit + segment) * H + head: fewer than
     // (row_groups + Gh) * H = heads + G slots of kPagedPositions positions),

@@ -21,7 +21,8 @@
 
 namespace {
 
-// 4 MiB: the partials of up to 993 split workgroups (8 query rows each); the
+// 4 MiB: the partials of up to 1,008 split workgroups (8 query rows, 4,160
+// bytes each: 4,194,304 / 4,160 = 1,008.2); the
 // GQA 16/2 decode step at 32K context uses 256 (1.08 MB).
 constexpr size_t kScratchBytes = size_t(4) << 20;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
