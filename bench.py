@@ -5,16 +5,20 @@ A step is one decode-time pass over a 36-layer Qwen2.5-3B-shaped compressed
 KV cache at 32K context: for every layer, dequant of its turbo_prod page pool
 to fp16 K/V [32768, 2, 128] (the layer load that feeds the model's KV cache,
 inputs resident in HBM) and fused GQA 16/2 decode attention over the same
-pool.  The 36 distinct pools (316 MB) and fp16 outputs (2.4 GB) rotate
-through more than the 256 MB Infinity Cache.  Launches are replayed from HIP
-graphs, so host launch cost is not timed.
+pool.  The step runs on one stream: the one-launch dequant of the 36 layers
+(tq_launch_turbo_prod_dequant_kv_layers), then the 36 attention launches.
+The 36 distinct pools (316 MB) and fp16 outputs (2.4 GB) rotate through more
+than the 256 MB Infinity Cache.  Launches are replayed from HIP graphs, so
+host launch cost is not timed.
 
 value = algorithmic bytes of the step / step time (GB/s).  roofline is the
-dominant kernel (dequant): its algorithmic bytes per launch over its average
-launch duration, measured with HIP events around replays of a graph of the 36
-per-layer launches, on the stream the graph runs on.  cpu_baseline times the
-CPU oracle (a C port of the reference's algorithm) on a bounded sample of the
-same work on this host.
+step's dominant kernel, that one-launch dequant: its algorithmic bytes per
+launch over its average launch duration, measured with HIP events around
+replays of a graph of four such launches, on the stream the graph runs on.
+The per-layer dequant launches (the reference's form), and the step with
+those beside the attention chain on a second stream, are second figures.
+cpu_baseline times the CPU oracle (a C port of the reference's algorithm) on
+a bounded sample of the same work on this host.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
        python bench.py --launch-pass   (eager launches only, for rocprofv3)
@@ -158,19 +162,24 @@ class Workload:
             self.attention((start + k) % self.NL)
 
     def step(self):
-        """One step: every layer's dequant and every layer's attention.  The
-        two chains share no data (both only read the pools), so the attention
-        chain runs on a second stream of the same graph, beside the dequant
-        chain: the dequant is store-bound, the attention latency-bound.  The
-        dequant chain is per-layer launches here: attention workgroups fit in
-        between their grids (0.60 ms per step, against 0.70 ms beside the
-        one-launch 36-layer dequant, whose queued grid keeps them out).  The
-        attention chain starts half the layers away from the dequant chain,
-        so the two never read one layer's pages at the same time (no cache
-        hits on the other chain's reads)."""
+        """One step, on one stream: the one-launch dequant of the 36 layers
+        (the roofline kernel), then every layer's attention.  The roofline
+        and the step thus time the same dequant launch."""
+        self.all_dequant()
+        self.all_attention()
+
+    def step_two_streams(self):
+        """The step's other form: the 36 per-layer dequant launches on one
+        stream and the attention chain on a second stream of the same graph
+        (the two share no data; both only read the pools).  Attention
+        workgroups fit in between the per-layer dequant grids; beside the
+        one-launch dequant they cannot (its queued grid keeps them out), so
+        that pairing is slower than running the two one after the other.
+        The attention chain starts half the layers away from the dequant
+        chain, so the two never read one layer's pages at the same time."""
         import torch
         if self.side2 is None:
-            self.serial_step()
+            self.step()
             return
         cur = torch.cuda.current_stream()
         self.side2.wait_stream(cur)
@@ -178,12 +187,6 @@ class Workload:
             self.all_attention(start=self.NL // 2)
         self.all_dequant_per_layer()
         cur.wait_stream(self.side2)
-
-    def serial_step(self):
-        """The step on one stream: the one-launch 36-layer dequant, then the
-        attention chain."""
-        self.all_dequant()
-        self.all_attention()
 
 
 def capture(fn, side):
@@ -281,20 +284,20 @@ def main() -> int:
     w.side2 = torch.cuda.Stream()
     w.side2.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
-        w.serial_step()  # sizes each stream's split-K workspace before capture
+        w.step()  # sizes each stream's split-K workspace before capture
     with torch.cuda.stream(w.side2):
         w.all_attention()
     torch.cuda.synchronize()
     use_graph = not args.no_graph
-    g_step = g_serial = g_att = g_deq1 = None
+    g_step = g_two = g_att = g_deq1 = None
     if use_graph:
         g_step = capture(w.step, side)
-        g_serial = capture(w.serial_step, side)
+        g_two = capture(w.step_two_streams, side)
         g_att = capture(w.all_attention, side)
         g_deq1 = capture(w.all_dequant_per_layer, side)
-        use_graph = None not in (g_step, g_serial, g_att, g_deq1)
+        use_graph = None not in (g_step, g_two, g_att, g_deq1)
     run_step = g_step.replay if use_graph else w.step
-    run_serial = g_serial.replay if use_graph else w.serial_step
+    run_two = g_two.replay if use_graph else w.step_two_streams
     run_att = g_att.replay if use_graph else w.all_attention
     run_deq1 = g_deq1.replay if use_graph else w.all_dequant_per_layer
 
@@ -312,10 +315,10 @@ def main() -> int:
     torch.cuda.synchronize()
     ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
     ev_ms_per_step = ev0.elapsed_time(ev1) / args.steps
-    serial_ms = event_time_us(run_serial, args.steps) / 1e3
+    two_ms = event_time_us(run_two, args.steps) / 1e3
     log(f"[bench] step {ms_per_step:.3f} ms wall, {ev_ms_per_step:.3f} ms events "
-        f"({'graph' if use_graph else 'eager'}; dequant and attention chains on two streams); "
-        f"one stream: {serial_ms:.3f} ms")
+        f"({'graph' if use_graph else 'eager'}; one-launch dequant, then attention, one stream); "
+        f"per-layer dequant beside attention on two streams: {two_ms:.3f} ms")
 
     # Per-kernel averages, replayed from graphs and timed with events: the
     # one-launch dequant of the 36 layers (the roofline kernel), the 36
@@ -451,8 +454,9 @@ def main() -> int:
             "layers": w.NL, "tokens": w.N, "kv_heads": w.H, "q_heads": w.q_heads,
             "head_dim": w.D, "page_tokens": w.B, "scheme": "turbo_prod",
             "graph_replay": bool(use_graph),
-            "streams": "per-layer dequant chain and attention chain on two streams of one graph "
-                       "(step_ms_one_stream: one-launch 36-layer dequant, then attention)",
+            "streams": "one stream: the one-launch 36-layer dequant (the roofline kernel), "
+                       "then the 36 attention launches (step_ms_two_streams: per-layer dequant "
+                       "launches beside the attention chain on a second stream)",
         },
         "roofline": {
             "bound": "hbm",
@@ -491,7 +495,7 @@ def main() -> int:
         "single_query_decode": single,
         "config1": config1,
         "step_ms_events": round(ev_ms_per_step, 4),
-        "step_ms_one_stream": round(serial_ms, 4),
+        "step_ms_two_streams": round(two_ms, 4),
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -193,105 +193,6 @@ __global__ __launch_bounds__(256) void prod_logits_kernel(
     logits[(size_t)row * num_kv_tokens + t] = (s1 * ks + s2 * (ks * re)) * inv;
 }
 
-// D = 128: one workgroup of 8 waves per (128-token tile, kv head, group of up
-// to 8 query rows), so each K cell is read and decoded once for all the rows
-// of its group.  A wave takes 16 tokens, 4 per step: lane l handles token
-// l / 16 and code dword j = l % 16 (dimensions 8j .. 8j + 7), holding those
-// dimensions of every row's rotated query in registers.  Each dimension contributes
-// q_r[d] * (K3[code] +- re) (nibble bit 3: +), the reference's
-// s1*ks + s2*ks*re (:513-531) with the two sums taken together; the 16
-// lanes of a token are summed by a butterfly that halves the rows each lane
-// keeps (rows 4*b3 + 2*b2 + b1 of lane bits b3..b1), so lanes j and j ^ 1
-// end with the total of one row and the even one stores it.
-constexpr int kLogitTile = 128;  // tokens per workgroup
-constexpr int kLogitWaves = 8;   // 16 tokens per wave (7.4 us at 32K, 8.1 with 4 waves of 32)
-__global__ __launch_bounds__(64 * kLogitWaves) void prod_logits_rows_kernel(
-    const uint16_t* __restrict__ query, const uint8_t* __restrict__ pool,
-    const int32_t* __restrict__ slots, float* __restrict__ logits, PageGeom g, int num_queries,
-    int num_kv_tokens, float inv) {
-    constexpr int D = 128, kRowsG = 8, kSteps = kLogitTile / (4 * kLogitWaves);
-    __shared__ float qs[kRowsG][D];
-    __shared__ float tk[8];
-    const int h = blockIdx.y, rg = blockIdx.z;
-    const int nrows = min(kRowsG, num_queries - rg * kRowsG);
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int j = lane & 15, ti = lane >> 4;
-    const int t_base = blockIdx.x * kLogitTile + w * (kLogitTile / kLogitWaves);
-    // Every load of the wave's 16 tokens is issued before any is used: the
-    // slots (lane l: token t_base + l), then per step the lane's code dword
-    // and its token's two scales (tokens past the end or with a negative
-    // slot read the query's first bytes, always valid memory, and are
-    // dropped).
-    const int my_slot = lane < kLogitTile / kLogitWaves && t_base + lane < num_kv_tokens
-                            ? slots[t_base + lane] : -1;
-    uint32_t word[kSteps];
-    uint16_t ksr[kSteps], rer[kSteps];
-#pragma unroll
-    for (int s = 0; s < kSteps; ++s) {
-        const int slot = __shfl(my_slot, 4 * s + ti);
-        int page, tib;
-        split_slot(slot < 0 ? 0 : slot, g, page, tib);
-        const uint64_t base = (uint64_t)page * g.page_size;
-        const uint64_t cell = (uint64_t)(tib * g.H + h);
-        const bool ok = slot >= 0;
-        const uint8_t* dummy = reinterpret_cast<const uint8_t*>(query);
-        word[s] = *reinterpret_cast<const uint32_t*>(
-            ok ? pool + base + g.kc_off + cell * g.code_stride + 4 * j : dummy);
-        ksr[s] = ld_u16(ok ? pool + base + g.ks_off + cell * g.scale_stride : dummy);
-        rer[s] = ld_u16(ok ? pool + base + g.kres_off + cell * g.scale_stride : dummy + 2);
-    }
-    if (threadIdx.x < 8) tk[threadIdx.x] = kK3[threadIdx.x];
-    for (int r = w; r < kRowsG; r += kLogitWaves) {  // wave-uniform
-        float q0 = 0.f, q1 = 0.f;
-        if (r < nrows)
-            rotate_query<D / 2>(query + ((size_t)(rg * kRowsG + r) * g.H + h) * D, h, lane, inv,
-                                q0, q1);
-        qs[r][2 * lane] = q0;
-        qs[r][2 * lane + 1] = q1;
-    }
-    __syncthreads();
-    float qr[kRowsG][8];
-#pragma unroll
-    for (int r = 0; r < kRowsG; ++r)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) qr[r][e] = qs[r][8 * j + e];
-    const int my_row = ((j >> 3) & 1) * 4 + ((j >> 2) & 1) * 2 + ((j >> 1) & 1);
-    const bool writer = (j & 1) == 0 && my_row < nrows;
-    float* out_row = logits + ((size_t)(rg * kRowsG + my_row) * g.H + h) * num_kv_tokens;
-    const bool b3 = (j & 8) != 0, b2 = (j & 4) != 0, b1 = (j & 2) != 0;
-#pragma unroll
-    for (int s = 0; s < kSteps; ++s) {
-        const int t = t_base + 4 * s + ti;
-        const float re = h2f(rer[s]), ks = h2f(ksr[s]);
-        float acc[kRowsG];
-#pragma unroll
-        for (int r = 0; r < kRowsG; ++r) acc[r] = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const uint32_t n = (word[s] >> (4 * e)) & 0xFu;
-            const float v = tk[n & 7u] + ((n & 8u) ? re : -re);
-#pragma unroll
-            for (int r = 0; r < kRowsG; ++r) acc[r] = fmaf(qr[r][e], v, acc[r]);
-        }
-        // 16 lanes of a token -> one row total per lane pair
-        float a4[4], a2[2];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float keep = b3 ? acc[i + 4] : acc[i], send = b3 ? acc[i] : acc[i + 4];
-            a4[i] = keep + lane_xor<8>(send);
-        }
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const float keep = b2 ? a4[i + 2] : a4[i], send = b2 ? a4[i] : a4[i + 2];
-            a2[i] = keep + lane_xor<4>(send);
-        }
-        float a1 = (b1 ? a2[1] : a2[0]) + lane_xor<2>(b1 ? a2[0] : a2[1]);
-        a1 += lane_xor<1>(a1);
-        const int slot = __shfl(my_slot, 4 * s + ti);
-        if (writer && t < num_kv_tokens) out_row[t] = slot < 0 ? -INFINITY : a1 * ks * inv;
-    }
-}
-
 // ===========================================================================
 // Matrix-core path: D = 128, up to 8 query rows per kv head per workgroup.
 //
@@ -430,6 +331,177 @@ __device__ __forceinline__ uint32_t lo_pair(float x0, float x1, uint32_t h) {
     return r;
 }
 }  // namespace mfma
+
+// ---------------------------------------------------------------------------
+// turbo_prod logits on the matrix cores (D = 128; :346-434, 628-648).
+//
+// The 3-bit codebook is odd under c -> 7 - c (K3[7 - c] = -K3[c]), so with
+// u_i = 2 b_i - 1 (bits b2 b1 b0 of c, each +-1) it is exactly
+//     K3[c] = cA u2 + cB u1 + cC u0 + cD u2 u1 u0,
+// the four odd functions of the bits (cA = mean of K3[4..7], cB, cC, cD the
+// other +-1 contrasts of K3[4..7]).  Each term is a +-1 matrix, exact in
+// fp16, built from the code bits with v_perm, and so is the residual sign
+// u3 = +-1 (nibble bit 3).  Per (token, row):
+//     logit = ks * (sum_j c_j S_j + re * S_3) / sqrt(D),  S_j = sum_d u_j(c_d) q_d,
+// the reference's (s1 + s2 re) ks / sqrt(D) with s1 = sum_d q_d K3[c_d] and
+// s2 = sum_d q_d u3(d).  The five S_j are v_mfma_f32_16x16x32_f16 products
+// A_j (16 tokens x 32 dims, +-1) x B (32 dims x 16 columns): column 2r + p
+// holds query row r's fp16 hi (p = 0) or lo (p = 1) part, so a column pair
+// sums to ~22-bit query precision, and the products and fp32 sums carry no
+// other rounding than the reference's own fp32 accumulation does.
+//
+// A workgroup of 8 waves takes 128 tokens of one kv head and one group of up
+// to 8 query rows; wave w takes tokens 16w .. 16w + 15 (one MFMA tile) and
+// rotates query row w.  Lane (i, g) = (lane % 16, lane / 16) holds A rows of
+// token i over dims 32g .. 32g + 31: the contraction runs over the dims in
+// the order (block kk, lane group g, e) -> dim 32g + 8kk + e, so each lane's
+// codes are one 16-byte load (code dword kk = block kk).  The MFMA output
+// lane (n, g) holds tokens 4g .. 4g + 3 of column n; its token scales come
+// from lanes 16g + m (ks) and 16g + 4 + m (re) of its own 16-lane row by
+// DPP row broadcast.
+// ---------------------------------------------------------------------------
+namespace lgt {
+using namespace mfma;
+constexpr int kWaves = 8, kTile = 16, kTokens = kWaves * kTile;  // tokens per workgroup
+constexpr double kq(int c) { return (double)dev::kK3[c]; }
+constexpr float kCA = (float)((kq(4) + kq(5) + kq(6) + kq(7)) / 4);  // u2
+constexpr float kCB = (float)((kq(6) + kq(7) - kq(4) - kq(5)) / 4);  // u1
+constexpr float kCC = (float)((kq(5) + kq(7) - kq(4) - kq(6)) / 4);  // u0
+constexpr float kCD = (float)((kq(4) + kq(7) - kq(5) - kq(6)) / 4);  // u2 u1 u0
+
+// The +-1 fp16 pairs of one code dword for bit plane `src` (bit i of each
+// nibble set = +1), i.e. the 4 dwords of an A operand: dword k holds the
+// values of byte k's low nibble (low half) and high nibble (high half).
+// neg holds, per nibble, the bit to turn into the sign (1 = -1).
+template <int I>
+__device__ __forceinline__ half8 pm1_plane(uint32_t neg) {
+    const uint32_t x = ((neg << (7 - I)) & 0x80808080u) | 0x3C3C3C3Cu;  // low nibbles' signs
+    const uint32_t y = ((neg << (3 - I)) & 0x80808080u) | 0x3C3C3C3Cu;  // high nibbles'
+    return as_h8(__builtin_amdgcn_perm(y, x, 0x040C000Cu), __builtin_amdgcn_perm(y, x, 0x050C010Cu),
+                 __builtin_amdgcn_perm(y, x, 0x060C020Cu), __builtin_amdgcn_perm(y, x, 0x070C030Cu));
+}
+
+template <int N>
+__device__ __forceinline__ float row_bcast(float v) {  // lane N of each 16-lane row
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + N, 0xF, 0xF,
+                                                      false));
+}
+template <int N>
+__device__ __forceinline__ int row_bcast_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, 0x150 + N, 0xF, 0xF, false);
+}
+
+// VEC: the logits rows are 16-byte aligned and num_kv_tokens % 4 == 0.
+template <bool VEC>
+__global__ __launch_bounds__(64 * kWaves) void prod_logits_mfma_kernel(
+    const uint16_t* __restrict__ query, const uint8_t* __restrict__ pool,
+    const int32_t* __restrict__ slots, float* __restrict__ logits, PageGeom g, int num_queries,
+    int num_kv_tokens, float inv) {
+    constexpr int D = 128;
+    __shared__ uint32_t bq[4][64][4];  // B operands: [block kk][lane][dword], fp16 pairs
+    const int h = blockIdx.y, rg = blockIdx.z;
+    const int nrows = min(kRows, num_queries - rg * kRows);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int i = lane & 15, gq = lane >> 4;
+    const int t0 = blockIdx.x * kTokens + w * kTile;
+    // Loads first, in dependency order: the wave's query row (raw), the
+    // slots of the lane's code token (i) and scale token (4 gq + lane % 4),
+    // then the codes and the one scale (ks for lane % 8 < 4, else re).
+    // Dropped tokens read the query's first bytes (always valid memory);
+    // their addresses are selected, then hidden from the optimiser so each
+    // value stays one unconditional load.
+    const uint32_t qq = w < nrows ? *reinterpret_cast<const uint32_t*>(
+                                        query + ((size_t)(rg * kRows + w) * g.H + h) * D + 2 * lane)
+                                  : 0u;
+    const int tc = t0 + i, ts = t0 + 4 * gq + (lane & 3);
+    const int slot_c = tc < num_kv_tokens ? slots[tc] : -1;
+    const int slot_s = ts < num_kv_tokens ? slots[ts] : -1;
+    const uint64_t dummy = reinterpret_cast<uint64_t>(query);
+    uint64_t ac, as;
+    {
+        int page, tib;
+        split_slot(slot_c >= 0 ? slot_c : 0, g, page, tib);
+        ac = slot_c >= 0 ? reinterpret_cast<uint64_t>(pool) + (uint64_t)page * g.page_size +
+                               g.kc_off + (uint64_t)(tib * g.H + h) * g.code_stride + 16 * gq
+                         : dummy;
+        split_slot(slot_s >= 0 ? slot_s : 0, g, page, tib);
+        as = slot_s >= 0 ? reinterpret_cast<uint64_t>(pool) + (uint64_t)page * g.page_size +
+                               ((lane & 4) ? g.kres_off : g.ks_off) +
+                               (uint64_t)(tib * g.H + h) * g.scale_stride
+                         : dummy;
+    }
+    asm volatile("" : "+v"(ac), "+v"(as));
+    // 16 code bytes at a 4-byte aligned address (one multi-dword load; global
+    // loads need dword alignment only).
+    typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+    const u32x4 code = *reinterpret_cast<const __attribute__((address_space(1))) u32x4a4*>(ac);
+    const uint16_t sraw = *reinterpret_cast<const __attribute__((address_space(1))) uint16_t*>(as);
+
+    // Rotate query row w (sign flip, orthonormal WHT) while the codes load;
+    // lane j holds dims 2j, 2j + 1: block kk = (j % 16) / 4, lane group
+    // g = j / 16, dword j % 4 of columns 2w (hi) and 2w + 1 (lo).
+    {
+        const float sh = (h & 1) ? -1.0f : 1.0f;
+        float q0 = h2f(qq & 0xffff) * sh, q1 = h2f(qq >> 16) * (-sh);
+        wht_pair<D / 2>(q0, q1, lane);
+        q0 *= inv;
+        q1 *= inv;
+        const uint32_t hi = pack_h2(q0, q1);
+        const int kk = (lane & 15) >> 2, col = 2 * w + 16 * (lane >> 4);
+        bq[kk][col][lane & 3] = hi;
+        bq[kk][col + 1][lane & 3] = lo_pair(q0, q1, hi);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    half8 b[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+        b[kk] = __builtin_bit_cast(half8, *reinterpret_cast<const u32x4*>(bq[kk][lane]));
+
+    // The five products over the 4 blocks (A_j from code dword kk).
+    f32x4 acc[5];
+#pragma unroll
+    for (int j = 0; j < 5; ++j) acc[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+        const uint32_t v = ~code[kk];                      // per nibble bit: 1 = -1
+        const uint32_t par = v ^ (v >> 1) ^ (v >> 2);      // bit 0: sign of u2 u1 u0
+        acc[0] = mma(pm1_plane<0>(v), b[kk], acc[0]);
+        acc[1] = mma(pm1_plane<1>(v), b[kk], acc[1]);
+        acc[2] = mma(pm1_plane<2>(v), b[kk], acc[2]);
+        acc[3] = mma(pm1_plane<3>(v), b[kk], acc[3]);
+        acc[4] = mma(pm1_plane<0>(par), b[kk], acc[4]);
+    }
+
+    // Lane (n, gq): tokens 4 gq + m of column n; rows r = n / 2 summed over
+    // the hi/lo column pair, then scaled by the token's ks.
+    const float sv = h2f(sraw);
+    const float ksm[4] = {row_bcast<0>(sv), row_bcast<1>(sv), row_bcast<2>(sv), row_bcast<3>(sv)};
+    const float rem[4] = {row_bcast<4>(sv), row_bcast<5>(sv), row_bcast<6>(sv), row_bcast<7>(sv)};
+    const int okm[4] = {row_bcast_i<0>(slot_s), row_bcast_i<1>(slot_s), row_bcast_i<2>(slot_s),
+                        row_bcast_i<3>(slot_s)};
+    float out[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const float s1 = (kCA * acc[2][m] + kCB * acc[1][m]) + (kCC * acc[0][m] + kCD * acc[4][m]);
+        float x = s1 + rem[m] * acc[3][m];
+        x += lane_xor<1>(x);
+        out[m] = okm[m] < 0 ? -INFINITY : x * ksm[m] * inv;
+    }
+    const int r = i >> 1;
+    if ((i & 1) || r >= nrows) return;
+    const int tf = t0 + 4 * gq;
+    float* dst = logits + ((size_t)(rg * kRows + r) * g.H + h) * num_kv_tokens + tf;
+    if (VEC && tf + 3 < num_kv_tokens) {
+        *reinterpret_cast<float4*>(dst) = make_float4(out[0], out[1], out[2], out[3]);
+    } else {
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+            if (tf + m < num_kv_tokens) dst[m] = out[m];
+    }
+}
+}  // namespace lgt
 
 // CH = tokens per wave iteration (32: two QK tiles, one PV step; 64: four and
 // two); NW = waves per workgroup; NP = row groups per workgroup.
@@ -2507,11 +2579,17 @@ void launch_logits(const uint16_t* query, const uint8_t* pool, const int32_t* sl
     const float inv = inv_sqrt_d(g.D);
     const int row_groups = (num_queries + 7) / 8;
     if (g.D == 128 && g.code_stride == 64 && (g.kc_off & 3) == 0 && (g.page_size & 3) == 0 &&
+        (g.ks_off & 1) == 0 && (g.kres_off & 1) == 0 &&
         (reinterpret_cast<uintptr_t>(pool) & 3) == 0 && g.H <= 65535 && row_groups <= 65535) {
-        hipLaunchKernelGGL(prod_logits_rows_kernel,
-                           dim3((num_kv_tokens + kLogitTile - 1) / kLogitTile, g.H, row_groups),
-                           dim3(64 * kLogitWaves), 0, stream, query, pool, slots, logits, g, num_queries,
-                           num_kv_tokens, inv);
+        const bool vec = (num_kv_tokens & 3) == 0 && (reinterpret_cast<uintptr_t>(logits) & 15) == 0;
+        const dim3 grid((num_kv_tokens + lgt::kTokens - 1) / lgt::kTokens, g.H, row_groups);
+        const dim3 block(64 * lgt::kWaves);
+        if (vec)
+            hipLaunchKernelGGL((lgt::prod_logits_mfma_kernel<true>), grid, block, 0, stream, query,
+                               pool, slots, logits, g, num_queries, num_kv_tokens, inv);
+        else
+            hipLaunchKernelGGL((lgt::prod_logits_mfma_kernel<false>), grid, block, 0, stream, query,
+                               pool, slots, logits, g, num_queries, num_kv_tokens, inv);
         check_launch("turbo_prod_fused_attention_logits_kernel");
         return;
     }
