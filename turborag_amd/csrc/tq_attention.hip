@@ -335,50 +335,81 @@ __device__ __forceinline__ uint32_t lo_pair(float x0, float x1, uint32_t h) {
 // ---------------------------------------------------------------------------
 // turbo_prod logits on the matrix cores (D = 128; :346-434, 628-648).
 //
-// The 3-bit codebook is odd under c -> 7 - c (K3[7 - c] = -K3[c]), so with
-// u_i = 2 b_i - 1 (bits b2 b1 b0 of c, each +-1) it is exactly
-//     K3[c] = cA u2 + cB u1 + cC u0 + cD u2 u1 u0,
-// the four odd functions of the bits (cA = mean of K3[4..7], cB, cC, cD the
-// other +-1 contrasts of K3[4..7]).  Each term is a +-1 matrix, exact in
-// fp16, built from the code bits with v_perm, and so is the residual sign
-// u3 = +-1 (nibble bit 3).  Per (token, row):
-//     logit = ks * (sum_j c_j S_j + re * S_3) / sqrt(D),  S_j = sum_d u_j(c_d) q_d,
-// the reference's (s1 + s2 re) ks / sqrt(D) with s1 = sum_d q_d K3[c_d] and
-// s2 = sum_d q_d u3(d).  The five S_j are v_mfma_f32_16x16x32_f16 products
-// A_j (16 tokens x 32 dims, +-1) x B (32 dims x 16 columns): column 2r + p
-// holds query row r's fp16 hi (p = 0) or lo (p = 1) part, so a column pair
-// sums to ~22-bit query precision, and the products and fp32 sums carry no
-// other rounding than the reference's own fp32 accumulation does.
+// Per (token, row): logit = ks (s1 + re s2) / sqrt(D), the reference's
+// s1*ks + s2*ks*re, with s1 = sum_d q_d K3[c_d] and s2 = sum_d q_d u3_d
+// (u3 = +-1: nibble bit 3).  Both are v_mfma_f32_16x16x32_f16 products
+// A (16 tokens x 32 dims) x B (32 dims x 16 columns): column 2r + p holds
+// query row r's fp16 hi (p = 0) or lo (p = 1) part, so a column pair sums to
+// ~22-bit query precision.  For s1, A is K3[c] split the same way into two
+// matrices, fp16(K3[c]) and fp16(K3[c] - fp16(K3[c])), both accumulated into
+// one fp32 sum (the four hi/lo cross products: ~2^-22 relative); for s2, A is
+// the +-1 matrix (exact).
+//
+// K3 is odd under c -> 7 - c (K3[7 - c] = -K3[c]), so K3[c] = +-mag[m] with
+// mag = K3[4..7], m = (c ^ (c < 4 ? 3 : 0)) & 3 and the sign of bit 2.  The
+// fp16 values come from v_perm over a 4-entry register table (low bytes of
+// the 4 magnitudes in one dword, high bytes in another), selected by m, then
+// the sign bit is xor'ed in; the +-1 matrix is 0x3C00 with the sign bit.
 //
 // A workgroup of 8 waves takes 128 tokens of one kv head and one group of up
 // to 8 query rows; wave w takes tokens 16w .. 16w + 15 (one MFMA tile) and
-// rotates query row w.  Lane (i, g) = (lane % 16, lane / 16) holds A rows of
-// token i over dims 32g .. 32g + 31: the contraction runs over the dims in
-// the order (block kk, lane group g, e) -> dim 32g + 8kk + e, so each lane's
-// codes are one 16-byte load (code dword kk = block kk).  The MFMA output
-// lane (n, g) holds tokens 4g .. 4g + 3 of column n; its token scales come
-// from lanes 16g + m (ks) and 16g + 4 + m (re) of its own 16-lane row by
-// DPP row broadcast.
+// rotates query row w.  Lane (i, g) = (lane % 16, lane / 16)
+// holds A rows of token i over dims 32g .. 32g + 31: the contraction runs
+// over the dims in the order (block kk, lane group g, e) -> dim
+// 32g + 8kk + e, so each lane's codes of a tile are one 16-byte load (code
+// dword kk = block kk).  The MFMA output lane (n, g) holds tokens 4g .. 4g + 3
+// of column n; its token scales come from lanes 16g + m (ks) and
+// 16g + 4 + m (re) of its own 16-lane row by DPP row broadcast.
 // ---------------------------------------------------------------------------
 namespace lgt {
 using namespace mfma;
-constexpr int kWaves = 8, kTile = 16, kTokens = kWaves * kTile;  // tokens per workgroup
-constexpr double kq(int c) { return (double)dev::kK3[c]; }
-constexpr float kCA = (float)((kq(4) + kq(5) + kq(6) + kq(7)) / 4);  // u2
-constexpr float kCB = (float)((kq(6) + kq(7) - kq(4) - kq(5)) / 4);  // u1
-constexpr float kCC = (float)((kq(5) + kq(7) - kq(4) - kq(6)) / 4);  // u0
-constexpr float kCD = (float)((kq(4) + kq(7) - kq(5) - kq(6)) / 4);  // u2 u1 u0
+constexpr int kWaves = 8, kTilesW = 1, kTile = 16;  // 4.9 us/layer at 32K; 4 x 2: 5.2, 8 x 2: 5.1
+constexpr int kTokens = kWaves * kTilesW * kTile;  // tokens per workgroup
+constexpr uint16_t f16b(double x) { return __builtin_bit_cast(uint16_t, (_Float16)x); }
+constexpr double f16v(double x) { return (double)(_Float16)x; }
+constexpr double kmag(int m) { return (double)dev::kK3[4 + m]; }
+constexpr uint16_t mag_hi(int m) { return f16b(kmag(m)); }
+constexpr uint16_t mag_lo(int m) { return f16b(kmag(m) - f16v(kmag(m))); }
+constexpr uint32_t bytes4(uint16_t a, uint16_t b, uint16_t c, uint16_t d, int hi_byte) {
+    const int sh = 8 * hi_byte;
+    return ((uint32_t)((a >> sh) & 0xFF)) | ((uint32_t)((b >> sh) & 0xFF) << 8) |
+           ((uint32_t)((c >> sh) & 0xFF) << 16) | ((uint32_t)((d >> sh) & 0xFF) << 24);
+}
+// v_perm tables: byte m of the *L word is the low byte of magnitude m's
+// fp16 value, byte m of the *H word its high byte.
+constexpr uint32_t kHiL = bytes4(mag_hi(0), mag_hi(1), mag_hi(2), mag_hi(3), 0);
+constexpr uint32_t kHiH = bytes4(mag_hi(0), mag_hi(1), mag_hi(2), mag_hi(3), 1);
+constexpr uint32_t kLoL = bytes4(mag_lo(0), mag_lo(1), mag_lo(2), mag_lo(3), 0);
+constexpr uint32_t kLoH = bytes4(mag_lo(0), mag_lo(1), mag_lo(2), mag_lo(3), 1);
 
-// The +-1 fp16 pairs of one code dword for bit plane `src` (bit i of each
-// nibble set = +1), i.e. the 4 dwords of an A operand: dword k holds the
-// values of byte k's low nibble (low half) and high nibble (high half).
-// neg holds, per nibble, the bit to turn into the sign (1 = -1).
-template <int I>
-__device__ __forceinline__ half8 pm1_plane(uint32_t neg) {
-    const uint32_t x = ((neg << (7 - I)) & 0x80808080u) | 0x3C3C3C3Cu;  // low nibbles' signs
-    const uint32_t y = ((neg << (3 - I)) & 0x80808080u) | 0x3C3C3C3Cu;  // high nibbles'
-    return as_h8(__builtin_amdgcn_perm(y, x, 0x040C000Cu), __builtin_amdgcn_perm(y, x, 0x050C010Cu),
-                 __builtin_amdgcn_perm(y, x, 0x060C020Cu), __builtin_amdgcn_perm(y, x, 0x070C030Cu));
+// The three A operands of one code dword W (dims of byte k: low nibble ->
+// low half of dword k, high nibble -> high half).
+struct AOps {
+    half8 hi, lo, u3;
+};
+__device__ __forceinline__ AOps a_ops(uint32_t W, uint32_t hil, uint32_t hih, uint32_t lol,
+                                      uint32_t loh) {
+    const uint32_t V = ~W;
+    const uint32_t t = (V >> 2) & 0x11111111u;                    // 1 where c < 4
+    const uint32_t wm = (W ^ (t | (t << 1))) & 0x33333333u;       // m per nibble
+    const uint32_t E = wm & 0x03030303u, O = (wm >> 4) & 0x03030303u;
+    const uint32_t xs = (V << 5) & 0x80808080u, ys = (V << 1) & 0x80808080u;  // K3 < 0
+    const uint32_t x3 = ((V << 4) & 0x80808080u) | 0x3C3C3C3Cu;   // u3 of low nibbles
+    const uint32_t y3 = (V & 0x80808080u) | 0x3C3C3C3Cu;          // of high nibbles
+    uint32_t h[4], l[4], u[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t sel =
+            __builtin_amdgcn_perm(O, E, (uint32_t)(k | k << 8 | (4 + k) << 16 | (4 + k) << 24)) |
+            0x04000400u;
+        const uint32_t sk = (uint32_t)(0x0C | k << 8 | 0x0C << 16 | (4 + k) << 24);
+        const uint32_t sg = __builtin_amdgcn_perm(ys, xs, sk);
+        h[k] = __builtin_amdgcn_perm(hih, hil, sel) ^ sg;
+        l[k] = __builtin_amdgcn_perm(loh, lol, sel) ^ sg;
+        u[k] = __builtin_amdgcn_perm(y3, x3, sk);
+    }
+    return {as_h8(h[0], h[1], h[2], h[3]), as_h8(l[0], l[1], l[2], l[3]),
+            as_h8(u[0], u[1], u[2], u[3])};
 }
 
 template <int N>
@@ -399,58 +430,87 @@ __global__ __launch_bounds__(64 * kWaves) void prod_logits_mfma_kernel(
     int num_kv_tokens, float inv) {
     constexpr int D = 128;
     __shared__ uint32_t bq[4][64][4];  // B operands: [block kk][lane][dword], fp16 pairs
+    // Every kernel argument the loads need, fetched in the first batch of
+    // scalar loads (one wait) rather than each before its first use.
+    asm volatile("" ::"s"(pool), "s"(slots), "s"(logits), "s"(g.page_size), "s"(g.kc_off),
+                 "s"(g.ks_off), "s"(g.kres_off), "s"(g.H), "s"(g.bs_shift));
     const int h = blockIdx.y, rg = blockIdx.z;
     const int nrows = min(kRows, num_queries - rg * kRows);
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int i = lane & 15, gq = lane >> 4;
-    const int t0 = blockIdx.x * kTokens + w * kTile;
-    // Loads first, in dependency order: the wave's query row (raw), the
-    // slots of the lane's code token (i) and scale token (4 gq + lane % 4),
-    // then the codes and the one scale (ks for lane % 8 < 4, else re).
-    // Dropped tokens read the query's first bytes (always valid memory);
-    // their addresses are selected, then hidden from the optimiser so each
-    // value stays one unconditional load.
-    const uint32_t qq = w < nrows ? *reinterpret_cast<const uint32_t*>(
-                                        query + ((size_t)(rg * kRows + w) * g.H + h) * D + 2 * lane)
-                                  : 0u;
-    const int tc = t0 + i, ts = t0 + 4 * gq + (lane & 3);
-    const int slot_c = tc < num_kv_tokens ? slots[tc] : -1;
-    const int slot_s = ts < num_kv_tokens ? slots[ts] : -1;
-    const uint64_t dummy = reinterpret_cast<uint64_t>(query);
-    uint64_t ac, as;
-    {
-        int page, tib;
-        split_slot(slot_c >= 0 ? slot_c : 0, g, page, tib);
-        ac = slot_c >= 0 ? reinterpret_cast<uint64_t>(pool) + (uint64_t)page * g.page_size +
-                               g.kc_off + (uint64_t)(tib * g.H + h) * g.code_stride + 16 * gq
-                         : dummy;
-        split_slot(slot_s >= 0 ? slot_s : 0, g, page, tib);
-        as = slot_s >= 0 ? reinterpret_cast<uint64_t>(pool) + (uint64_t)page * g.page_size +
-                               ((lane & 4) ? g.kres_off : g.ks_off) +
-                               (uint64_t)(tib * g.H + h) * g.scale_stride
-                         : dummy;
+    const int t0 = blockIdx.x * kTokens + w * (kTilesW * kTile);
+    // Loads first, in dependency order: the wave's two query rows (raw), the
+    // slots of the lane's code token (i) and scale token (4 gq + lane % 4) of
+    // each tile, then the codes and the one scale (ks for lane % 8 < 4, else
+    // re).  Dropped tokens read the query's first bytes (always valid
+    // memory); their addresses are selected, then hidden from the optimiser
+    // so each value stays one unconditional load.
+    constexpr int kRowsW = kRows / kWaves;  // query rows rotated per wave
+    uint32_t qq[kRowsW];
+#pragma unroll
+    for (int e = 0; e < kRowsW; ++e) {
+        const int r = w + kWaves * e;
+        qq[e] = r < nrows ? *reinterpret_cast<const uint32_t*>(
+                                query + ((size_t)(rg * kRows + r) * g.H + h) * D + 2 * lane)
+                          : 0u;
     }
-    asm volatile("" : "+v"(ac), "+v"(as));
-    // 16 code bytes at a 4-byte aligned address (one multi-dword load; global
-    // loads need dword alignment only).
+    int slot_c[kTilesW], slot_s[kTilesW];
+#pragma unroll
+    for (int tt = 0; tt < kTilesW; ++tt) {
+        const int tc = t0 + kTile * tt + i, ts = t0 + kTile * tt + 4 * gq + (lane & 3);
+        slot_c[tt] = tc < num_kv_tokens ? slots[tc] : -1;
+        slot_s[tt] = ts < num_kv_tokens ? slots[ts] : -1;
+    }
+    const uint64_t dummy = reinterpret_cast<uint64_t>(query);
+    const uint64_t soff = (lane & 4) ? g.kres_off : g.ks_off;
     typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
-    const u32x4 code = *reinterpret_cast<const __attribute__((address_space(1))) u32x4a4*>(ac);
-    const uint16_t sraw = *reinterpret_cast<const __attribute__((address_space(1))) uint16_t*>(as);
+    u32x4 code[kTilesW];
+    uint16_t sraw[kTilesW];
+#pragma unroll
+    for (int tt = 0; tt < kTilesW; ++tt) {
+        int page, tib;
+        split_slot(slot_c[tt] >= 0 ? slot_c[tt] : 0, g, page, tib);
+        // (page sizes are below 4 GiB: checked by the launcher)
+        uint64_t ac = slot_c[tt] >= 0
+                          ? reinterpret_cast<uint64_t>(pool) +
+                                (uint64_t)(uint32_t)page * (uint32_t)g.page_size + g.kc_off +
+                                (uint32_t)((tib * g.H + h) * g.code_stride + 16 * gq)
+                          : dummy;
+        split_slot(slot_s[tt] >= 0 ? slot_s[tt] : 0, g, page, tib);
+        uint64_t as = slot_s[tt] >= 0
+                          ? reinterpret_cast<uint64_t>(pool) +
+                                (uint64_t)(uint32_t)page * (uint32_t)g.page_size + soff +
+                                (uint32_t)((tib * g.H + h) * g.scale_stride)
+                          : dummy;
+        asm volatile("" : "+v"(ac), "+v"(as));
+        // 16 code bytes at a 4-byte aligned address (one multi-dword load;
+        // global loads need dword alignment only).
+        code[tt] = *reinterpret_cast<const __attribute__((address_space(1))) u32x4a4*>(ac);
+        sraw[tt] = *reinterpret_cast<const __attribute__((address_space(1))) uint16_t*>(as);
+    }
 
-    // Rotate query row w (sign flip, orthonormal WHT) while the codes load;
-    // lane j holds dims 2j, 2j + 1: block kk = (j % 16) / 4, lane group
-    // g = j / 16, dword j % 4 of columns 2w (hi) and 2w + 1 (lo).
+    // Rotate the wave's query rows w + 8e / kWaves (sign flip, orthonormal
+    // WHT) while the codes load; lane j holds dims 2j, 2j + 1: block kk = (j % 16) / 4, lane group
+    // g = j / 16, dword j % 4 of columns 2r (hi) and 2r + 1 (lo).
     {
         const float sh = (h & 1) ? -1.0f : 1.0f;
-        float q0 = h2f(qq & 0xffff) * sh, q1 = h2f(qq >> 16) * (-sh);
-        wht_pair<D / 2>(q0, q1, lane);
-        q0 *= inv;
-        q1 *= inv;
-        const uint32_t hi = pack_h2(q0, q1);
-        const int kk = (lane & 15) >> 2, col = 2 * w + 16 * (lane >> 4);
-        bq[kk][col][lane & 3] = hi;
-        bq[kk][col + 1][lane & 3] = lo_pair(q0, q1, hi);
+        const int kk = (lane & 15) >> 2, cg = 16 * (lane >> 4);
+#pragma unroll
+        for (int e = 0; e < kRowsW; ++e) {
+            float q0 = h2f(qq[e] & 0xffff) * sh, q1 = h2f(qq[e] >> 16) * (-sh);
+            wht_pair<D / 2>(q0, q1, lane);
+            q0 *= inv;
+            q1 *= inv;
+            const uint32_t hi = pack_h2(q0, q1);
+            const int col = 2 * (w + kWaves * e) + cg;
+            bq[kk][col][lane & 3] = hi;
+            bq[kk][col + 1][lane & 3] = lo_pair(q0, q1, hi);
+        }
     }
+    // Register tables for the K operands (values in VGPRs: v_perm reads at
+    // most one scalar operand).
+    uint32_t hil = kHiL, hih = kHiH, lol = kLoL, loh = kLoH;
+    asm volatile("" : "+v"(hil), "+v"(hih), "+v"(lol), "+v"(loh));
     __builtin_amdgcn_sched_barrier(0);
     lds_barrier();
     __builtin_amdgcn_sched_barrier(0);
@@ -459,46 +519,46 @@ __global__ __launch_bounds__(64 * kWaves) void prod_logits_mfma_kernel(
     for (int kk = 0; kk < 4; ++kk)
         b[kk] = __builtin_bit_cast(half8, *reinterpret_cast<const u32x4*>(bq[kk][lane]));
 
-    // The five products over the 4 blocks (A_j from code dword kk).
-    f32x4 acc[5];
-#pragma unroll
-    for (int j = 0; j < 5; ++j) acc[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-        const uint32_t v = ~code[kk];                      // per nibble bit: 1 = -1
-        const uint32_t par = v ^ (v >> 1) ^ (v >> 2);      // bit 0: sign of u2 u1 u0
-        acc[0] = mma(pm1_plane<0>(v), b[kk], acc[0]);
-        acc[1] = mma(pm1_plane<1>(v), b[kk], acc[1]);
-        acc[2] = mma(pm1_plane<2>(v), b[kk], acc[2]);
-        acc[3] = mma(pm1_plane<3>(v), b[kk], acc[3]);
-        acc[4] = mma(pm1_plane<0>(par), b[kk], acc[4]);
-    }
-
-    // Lane (n, gq): tokens 4 gq + m of column n; rows r = n / 2 summed over
-    // the hi/lo column pair, then scaled by the token's ks.
-    const float sv = h2f(sraw);
-    const float ksm[4] = {row_bcast<0>(sv), row_bcast<1>(sv), row_bcast<2>(sv), row_bcast<3>(sv)};
-    const float rem[4] = {row_bcast<4>(sv), row_bcast<5>(sv), row_bcast<6>(sv), row_bcast<7>(sv)};
-    const int okm[4] = {row_bcast_i<0>(slot_s), row_bcast_i<1>(slot_s), row_bcast_i<2>(slot_s),
-                        row_bcast_i<3>(slot_s)};
-    float out[4];
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-        const float s1 = (kCA * acc[2][m] + kCB * acc[1][m]) + (kCC * acc[0][m] + kCD * acc[4][m]);
-        float x = s1 + rem[m] * acc[3][m];
-        x += lane_xor<1>(x);
-        out[m] = okm[m] < 0 ? -INFINITY : x * ksm[m] * inv;
-    }
     const int r = i >> 1;
-    if ((i & 1) || r >= nrows) return;
-    const int tf = t0 + 4 * gq;
-    float* dst = logits + ((size_t)(rg * kRows + r) * g.H + h) * num_kv_tokens + tf;
-    if (VEC && tf + 3 < num_kv_tokens) {
-        *reinterpret_cast<float4*>(dst) = make_float4(out[0], out[1], out[2], out[3]);
-    } else {
+    const bool writer = (i & 1) == 0 && r < nrows;
+    float* const row_out = logits + ((size_t)(rg * kRows + r) * g.H + h) * num_kv_tokens;
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
-            if (tf + m < num_kv_tokens) dst[m] = out[m];
+    for (int tt = 0; tt < kTilesW; ++tt) {
+        f32x4 s1 = {0.f, 0.f, 0.f, 0.f}, s2 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            const AOps a = a_ops(code[tt][kk], hil, hih, lol, loh);
+            s1 = mma(a.hi, b[kk], s1);
+            s2 = mma(a.u3, b[kk], s2);
+            s1 = mma(a.lo, b[kk], s1);
+        }
+        // Lane (n, gq): tokens 4 gq + m of column n; rows r = n / 2 summed
+        // over the hi/lo column pair, then scaled by the token's ks.
+        const float sv = h2f(sraw[tt]);
+        const float ksm[4] = {row_bcast<0>(sv), row_bcast<1>(sv), row_bcast<2>(sv),
+                              row_bcast<3>(sv)};
+        const float rem[4] = {row_bcast<4>(sv), row_bcast<5>(sv), row_bcast<6>(sv),
+                              row_bcast<7>(sv)};
+        const int okm[4] = {row_bcast_i<0>(slot_s[tt]), row_bcast_i<1>(slot_s[tt]),
+                            row_bcast_i<2>(slot_s[tt]), row_bcast_i<3>(slot_s[tt])};
+        float out[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            float x = s1[m] + rem[m] * s2[m];
+            x += lane_xor<1>(x);
+            out[m] = okm[m] < 0 ? -INFINITY : x * ksm[m] * inv;
+        }
+        const int tf = t0 + kTile * tt + 4 * gq;
+        if (writer) {
+            float* dst = row_out + tf;
+            if (VEC && tf + 3 < num_kv_tokens) {
+                *reinterpret_cast<float4*>(dst) = make_float4(out[0], out[1], out[2], out[3]);
+            } else {
+#pragma unroll
+                for (int m = 0; m < 4; ++m)
+                    if (tf + m < num_kv_tokens) dst[m] = out[m];
+            }
+        }
     }
 }
 }  // namespace lgt
@@ -2580,7 +2640,8 @@ void launch_logits(const uint16_t* query, const uint8_t* pool, const int32_t* sl
     const int row_groups = (num_queries + 7) / 8;
     if (g.D == 128 && g.code_stride == 64 && (g.kc_off & 3) == 0 && (g.page_size & 3) == 0 &&
         (g.ks_off & 1) == 0 && (g.kres_off & 1) == 0 &&
-        (reinterpret_cast<uintptr_t>(pool) & 3) == 0 && g.H <= 65535 && row_groups <= 65535) {
+        (reinterpret_cast<uintptr_t>(pool) & 3) == 0 && g.H <= 65535 && row_groups <= 65535 &&
+        g.page_size <= 0xFFFFFFFFull) {
         const bool vec = (num_kv_tokens & 3) == 0 && (reinterpret_cast<uintptr_t>(logits) & 15) == 0;
         const dim3 grid((num_kv_tokens + lgt::kTokens - 1) / lgt::kTokens, g.H, row_groups);
         const dim3 block(64 * lgt::kWaves);
