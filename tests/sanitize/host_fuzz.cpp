@@ -18,9 +18,11 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <stdexcept>
 #include <string>
 #include <vector>
 
+#include "tq_turbo_prod_launch.h"
 #include "turboquant.h"
 
 namespace {
@@ -67,10 +69,55 @@ void write_all(const std::string& p, const std::string& s) {
 // ---------------------------------------------------------------------------
 // abi
 // ---------------------------------------------------------------------------
+// The C++ launchers (include/tq_turbo_prod.cuh:45-101 semantics): results of
+// the C entries, errors as std::runtime_error with the entry's message.
+template <class F>
+bool throws(F f, const char* needle) {
+    try {
+        f();
+    } catch (const std::runtime_error& e) {
+        return std::strstr(e.what(), needle) != nullptr;
+    }
+    return false;
+}
+
+void run_cxx_launchers(const TQConfig& cfg) {
+    TQTurboProdPageLayout a{};
+    CHECK(tq_make_turbo_prod_layout(&cfg, &a) == 0);
+    const TQTurboProdPageLayout b = make_tq_turbo_prod_page_layout(cfg);
+    CHECK(std::memcmp(&a, &b, sizeof a) == 0);
+    TQConfig bad = cfg;  // the factory computes any shape (as the reference's)
+    bad.head_dim = 3;
+    const TQTurboProdPageLayout c = make_tq_turbo_prod_page_layout(bad);
+    CHECK(tq_make_turbo_prod_layout(&bad, &a) == 0 && std::memcmp(&a, &c, sizeof a) == 0);
+    CHECK(tq_make_turbo_prod_layout(&cfg, &a) == 0);
+    // null pointers and a bad configuration fail before any launch
+    CHECK(throws([&] { launch_tq_turbo_prod_pack_kv(nullptr, nullptr, nullptr, nullptr, a, cfg, 1,
+                                                    nullptr); }, "NULL"));
+    CHECK(throws([&] { launch_tq_turbo_prod_dequant_kv(nullptr, nullptr, nullptr, nullptr, a, cfg,
+                                                       1, nullptr); }, "NULL"));
+    CHECK(throws([&] { launch_tq_turbo_prod_fused_attention_logits(nullptr, nullptr, nullptr,
+                                                                   nullptr, a, cfg, 1, 1,
+                                                                   nullptr); }, "NULL"));
+    CHECK(throws([&] { launch_tq_turbo_prod_fused_attention_output(nullptr, nullptr, nullptr,
+                                                                   nullptr, a, cfg, 1, 1,
+                                                                   nullptr); }, "NULL"));
+    uint16_t h[4] = {};
+    int32_t sl[1] = {0};
+    uint8_t pg[4] = {};
+    float dbg[4] = {};
+    CHECK(throws([&] { launch_tq_turbo_prod_pack_kv(h, h, sl, pg, a, bad, 1, nullptr); },
+                 "head_dim"));
+    // a debug buffer routes the call to the debug pack (a stand-in here)
+    CHECK(throws([&] { launch_tq_turbo_prod_pack_kv(h, h, sl, pg, a, cfg, 1, nullptr, dbg); },
+                 "pack debug"));
+}
+
 int run_abi() {
     TQConfig cfg;
     CHECK(tq_make_default_config(&cfg) == 0);
     CHECK(tq_make_default_config(nullptr) == -1);
+    run_cxx_launchers(cfg);
     // Layout factories over a grid of shapes (no device involved).
     for (int H : {1, 2, 3, 8, 64})
         for (int D : {2, 16, 64, 128, 256})

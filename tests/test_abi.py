@@ -245,3 +245,32 @@ def test_block_table_failed_append_leaves_sequence_unchanged(tq):
     with pytest.raises(RuntimeError, match="out of blocks"):
         t.build_slot_map(1, 40)          # needs 3 more pages, only 1 free
     assert t.num_tokens(1) == 16 and t.blocks(1) == [0] and a.num_free() == 1
+
+
+CXX_LAUNCHERS = ["make_tq_turbo_prod_page_layout", "launch_tq_turbo_prod_pack_kv",
+                 "launch_tq_turbo_prod_dequant_kv", "launch_tq_turbo_prod_fused_attention_logits",
+                 "launch_tq_turbo_prod_fused_attention_output"]
+
+
+def test_cxx_launchers_declared_and_exported(lib_path):
+    """The reference's C-linkage C++ launchers (include/tq_turbo_prod.cuh:45-101)
+    are declared in include/tq_turbo_prod_launch.h and exported unmangled."""
+    text = (ROOT / "include" / "tq_turbo_prod_launch.h").read_text()
+    lib = ctypes.CDLL(str(lib_path))
+    for n in CXX_LAUNCHERS:
+        assert re.search(rf"\b{n}\s*\(", text), n
+        assert hasattr(lib, n), n
+
+
+@pytest.mark.parametrize("H,D,B", [(2, 128, 16), (3, 64, 7), (1, 2, 1)])
+def test_cxx_layout_factory_matches_c_entry(tq, lib_path, H, D, B):
+    from turborag_amd.turboquant_wrapper import TQTurboProdPageLayout
+    lib = ctypes.CDLL(str(lib_path))
+    f = lib.make_tq_turbo_prod_page_layout
+    f.argtypes = [ctypes.c_void_p]  # const TQConfig& (a pointer in the ABI)
+    f.restype = TQTurboProdPageLayout  # returned by value
+    cfg = tq.default_config()
+    cfg.num_kv_heads, cfg.head_dim, cfg.block_size = H, D, B
+    got = f(ctypes.addressof(cfg))
+    want = tq.make_layout_for(cfg)
+    assert bytes(got) == bytes(want)

@@ -17,7 +17,7 @@ import pytest
 ROOT = Path(__file__).resolve().parent.parent
 CSRC = ROOT / "turborag_amd" / "csrc"
 SAN = ROOT / "tests" / "sanitize"
-HOST_SOURCES = ["tq_capi.cpp", "tq_pool.cpp", "tq_loader.cpp", "tq_store.cpp"]
+HOST_SOURCES = ["tq_capi.cpp", "tq_pool.cpp", "tq_loader.cpp", "tq_store.cpp", "tq_launch_cxx.cpp"]
 
 
 @pytest.fixture(scope="module")

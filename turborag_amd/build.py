@@ -36,8 +36,8 @@ HIPCC_FLAGS = [
     f"-I{ROOT / 'include'}", f"-I{CSRC}",
 ]
 
-SOURCES = ["tq_capi.cpp", "tq_pool.cpp", "tq_loader.cpp", "tq_store.cpp", "tq_codec.hip",
-           "tq_legacy.hip", "tq_attention.hip", "tq_noalloc.hip"]
+SOURCES = ["tq_capi.cpp", "tq_pool.cpp", "tq_loader.cpp", "tq_store.cpp", "tq_launch_cxx.cpp",
+           "tq_codec.hip", "tq_legacy.hip", "tq_attention.hip", "tq_noalloc.hip"]
 
 
 def _hipcc() -> str:
