@@ -273,7 +273,10 @@ def test_gqa_decode_matches_sdpa_over_dequant(tq, oracle, cuda):
 @pytest.mark.parametrize("Q,H,D,N,B,seed", [(8, 2, 128, 1000, 16, 41), (3, 8, 64, 300, 16, 42),
                                             (1, 2, 128, 1, 16, 43),
                                             (8, 2, 128, 32768, 16, 44),   # the bench's shape
-                                            (9, 2, 128, 32768 + 77, 16, 45)])  # ragged tile, 2 row groups
+                                            (9, 2, 128, 32768 + 77, 16, 45),  # ragged tile, 2 row groups
+                                            (5, 1, 128, 777, 16, 46),     # one kv head
+                                            (16, 8, 128, 1500, 12, 47),   # 8 heads, 12-token pages
+                                            (24, 2, 128, 4099, 32, 48)])  # 3 row groups
 def test_logits_vs_oracle(tq, oracle, cuda, Q, H, D, N, B, seed):
     print(f"[logits] Q={Q} H={H} D={D} N={N}", flush=True)
     k, v = kv_tokens_major(N, H, D, seed=seed)
