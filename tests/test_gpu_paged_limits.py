@@ -1,10 +1,10 @@
 """The paged decode entry's int32 work-count limit: the plan counts each kv
 head's work (every head has the same) as at most 4 * ceil(max_kv_len / 256)
-per row group in int32.  With max_kv_len = 2^23 (32,768 passes), 16,384 row
-groups reach 2^31 and are refused on the host with the reason, leaving the
-output untouched; 16,383 row groups (2^31 - 2^17) are accepted, with 8 kv
-heads, and sampled row groups equal the slot-mapped entry over the same
-tokens.  Every input is valid for the rows' real kv length (10 tokens on
++ 8 (a unit's setup) per row group in int32.  With max_kv_len = 2^23 (32,768
+passes), 16,384 row groups reach 2^31 + 2^17 and are refused on the host
+with the reason, leaving the output untouched; 16,383 row groups
+(2^31 - 8) are accepted, with 8 kv heads, and sampled row groups equal the
+slot-mapped entry over the same tokens.  Every input is valid for the rows' real kv length (10 tokens on
 page 0), so a launch stays in bounds either way.
 """
 from __future__ import annotations

@@ -3,7 +3,9 @@ item_passes, the split kernel's unit walk and attn_paged_combine_kernel),
 restated in integer Python.
 
 Every kv head has the same work: unit u holds n passes of weight w from work
-position start (a per-head prefix sum).  Each head's work is split into Gh
+position start (a per-head prefix sum), after a lead of positions that no
+pass occupies (a unit's setup cost, 8 in the kernel's plan; 0 for a unit
+without passes).  Each head's work is split into Gh
 segments; workgroup s of a head takes the work positions [bound(s),
 bound(s + 1)) with bound(s) = floor(s * total / Gh), computed as q*s +
 floor(r*s / Gh), and a pass belongs to the segment holding its first
@@ -48,10 +50,12 @@ def test_paged_plan_pieces_partition_every_item():
         U = int(rng.integers(1, 40))
         H = int(rng.choice([1, 2, 4]))
         Gh = int(rng.choice([8, 64, 256, 512]))
+        lead = int(rng.choice([0, 1, 8, 40]))
         units, start = [], 0
         for _u in range(U):
             n = int(rng.choice([0, 1, 2, 17, 128, int(rng.integers(0, 300))]))
             w = int(rng.choice([1, 3, 4]))
+            start += lead if n > 0 else 0
             units.append((start, n, w))
             start += w * n
         total = start
@@ -69,7 +73,8 @@ def test_paged_plan_pieces_partition_every_item():
                 b0, b1 = _bound(seg, total, Gh), _bound(seg + 1, total, Gh)
                 if b0 >= b1:
                     continue
-                u = next(k for k in range(U) if units[k][0] <= b0 < ends[k])
+                # (before the first unit's first pass: unit 0)
+                u = next(k for k in range(U) if (k == 0 or units[k][0] <= b0) and b0 < ends[k])
                 while u < U:
                     S, n, w = units[u]
                     if S >= b1:

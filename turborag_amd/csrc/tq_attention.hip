@@ -1464,11 +1464,11 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
         const Segments sg(total, Gh);
         const int b0 = sg.bound(seg), b1 = sg.bound(seg + 1);
         if (b0 >= b1) return;  // an empty segment (less work than workgroups)
-        // The unit holding work position b0 (exactly one: the units' work
-        // ranges partition [0, total)).
+        // The unit holding work position b0: exactly one u has start(u) <= b0 <
+        // start(u + 1), or b0 lies before the first unit's first pass (unit 0).
         __shared__ int s_unit;
         for (int u = threadIdx.x; u < nu; u += 64 * kWaves)
-            if (pr.units[u].start <= b0 && b0 < pr.units[u + 1].start) s_unit = u;
+            if ((u == 0 || pr.units[u].start <= b0) && b0 < pr.units[u + 1].start) s_unit = u;
         __syncthreads();
         // The walk over the units overlapping the segment, in work order.  Its
         // position lives in LDS (one copy per wave, volatile accesses), so no
@@ -1742,6 +1742,14 @@ __device__ int block_scan_1024(int v, int ident, int* s_tot, Op op) {
     return op(pre, v);
 }
 
+// Paged steps: the work positions a unit's setup counts for (a two-tile pass
+// weighs 4), before its first pass (config 5, 32 sequences: 139 us per step
+// with 0, 135 with 4, 131-133 with 8, 12 or 16).
+#ifndef TQ_PAGED_PIECE_COST
+#define TQ_PAGED_PIECE_COST 8
+#endif
+constexpr int kPieceCost = TQ_PAGED_PIECE_COST;
+
 // The plan of a paged step, one block of 1024 threads.  Row groups (8 rows
 // of one sequence) form units: each run of consecutive groups of one
 // sequence is cut into units of U groups from its start, the last one
@@ -1749,8 +1757,12 @@ __device__ int block_scan_1024(int v, int ident, int* s_tot, Op op) {
 // passes over its longest row (at most max_kv_len), a pass weighing w: with
 // U = 4, 4 for a unit of more than two positions (the two-tile loop) and 3
 // otherwise, about their measured cost ratio.  Work positions are given out
-// in unit order.  The groups are taken 1024 at a time, carrying the run
-// start, the unit count and the work total from window to window.
+// in unit order; a unit with passes first takes kPieceCost positions that no
+// pass occupies (its start is its first pass): a workgroup pays a piece's
+// setup (query rotation, decode tables, a first chunk with nothing in flight)
+// for every unit it starts, so a segment holding unit starts gets less pass
+// work.  The groups are taken 1024 at a time, carrying the run start, the
+// unit count and the work total from window to window.
 template <int U>
 __global__ __launch_bounds__(1024) void paged_plan_kernel(
     const int32_t* __restrict__ row_seq, const int32_t* __restrict__ row_kv_len, int num_rows,
@@ -1799,12 +1811,13 @@ __global__ __launch_bounds__(1024) void paged_plan_kernel(
             }
         const int w = U > 2 ? (c > 2 ? 4 : 3) : 1;
         const int n = (kv + pass - 1) / pass;
-        const int work = start ? w * n : 0;  // per kv head (every head has it)
+        const int lead = n > 0 ? kPieceCost : 0;
+        const int work = start ? lead + w * n : 0;  // per kv head (every head has it)
         const int ui = block_scan_1024(start ? 1 : 0, 0, s_tot, add);
         const int wi = block_scan_1024(work, 0, s_tot, add);
         if (start) {
             const int o = c_units + ui - 1;
-            const mfma::PagedUnit rec{gi, c, kv, c_work + wi - work, n, w, o, 0};
+            const mfma::PagedUnit rec{gi, c, kv, c_work + wi - work + lead, n, w, o, 0};
             units[o] = rec;
             for (int k = 0; k < c; ++k) group_unit[gi + k] = rec;
         }
@@ -2565,8 +2578,11 @@ void launch_paged_attention(Scheme s, const uint16_t* query, const uint8_t* pool
     const int Gh = 8 * ((kPagedSegmentsPerCU * num_cus() + 8 * g.H - 1) / (8 * g.H));
     const int G = Gh * g.H;
     // The plan counts each kv head's work in int32: at most
-    // 4 * ceil(max_kv_len / kPass) per row group (every head has the same).
-    if ((long long)row_groups * 4 * ((std::max(max_kv_len, 0) + kPass - 1) / kPass) > INT32_MAX)
+    // 4 * ceil(max_kv_len / kPass) + kPieceCost per row group (every head has
+    // the same).
+    if ((long long)row_groups *
+            (4LL * ((std::max(max_kv_len, 0) + kPass - 1) / kPass) + kPieceCost) >
+        INT32_MAX)
         throw Error("paged attention: too many rows for this max_kv_len");
     // Workspace: the partials (slot (unit + segment) * H + head: fewer than
     // (row_groups + Gh) * H = heads + G slots of kPagedPositions positions),
