@@ -384,6 +384,12 @@ def main() -> int:
     # two calibrated counter runs (FETCH_SIZE, WRITE_SIZE) summarised in
     # profiles/traffic.json.
     traffic = kernel_traffic(DEQUANT_KERNEL)
+    # The attention layer's HBM bytes (split + combine) from the same summary.
+    att_parts = [kernel_traffic(k) for k in ATTN_KERNELS]
+    att_traffic = ({"bytes": sum(t["bytes"] for t in att_parts),
+                    "ratio_to_algorithmic": round(sum(t["bytes"] for t in att_parts) / w.att_bytes, 3),
+                    "source": "profiles/traffic.json"}
+                   if all(att_parts) else None)
 
     loader = measure_loader(w)
     log(f"[bench] loader: {w.NL} layers host->device + dequant to [1,H,N,D] in "
@@ -484,6 +490,8 @@ def main() -> int:
             "frac_hbm": round(att_gbps / HBM_PEAK_GBPS, 4),
             "algorithmic_bytes": w.att_bytes,
             "kernels_per_layer": 2,
+            "kernels": list(ATTN_KERNELS),
+            "traffic": att_traffic,
             "graph_floor": floor,
         },
         "loader": loader,
