@@ -272,6 +272,10 @@ def main() -> int:
               file=sys.stderr)
         return 2
 
+    # The CPU baseline's build, compiled on this host before anything touches
+    # the GPU (a child process, started while this process has no GPU state).
+    native = None if args.no_cpu_baseline or args.launch_pass else build_native_oracle()
+
     import torch
 
     w = Workload(args.layers, args.tokens)
@@ -437,7 +441,7 @@ def main() -> int:
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(w)
+        cpu = cpu_baseline(w, native)
 
     value = w.step_bytes / (ms_per_step * 1e-3) / 1e9
     line = {
@@ -1030,7 +1034,36 @@ def host_cpu() -> dict:
     return {"nproc": os.cpu_count(), "usable": usable, "model": model}
 
 
-def cpu_baseline(w: Workload, runs: int = 5, layers_per_run: int = 3):
+NATIVE_FLAGS = ["-O2", "-march=native", "-ffp-contract=off"]
+
+
+def build_native_oracle():
+    """The oracle's C restatement compiled on this host with the CPU
+    baseline's flags (-O2 -march=native -ffp-contract=off, no fast-math;
+    -march=native is this host's CPU, so it is built here, into a temporary
+    directory, not shipped).  Returns (path, command), or (None, reason)
+    when gcc is missing or fails; the prebuilt oracle
+    (oracle/build_oracle.sh: -O3 -march=x86-64-v3) is timed instead then."""
+    import shutil
+    import subprocess
+    import tempfile
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        return None, "gcc not found"
+    src = os.path.join(os.path.dirname(os.path.abspath(__file__)), "oracle", "tq_oracle.c")
+    out = os.path.join(tempfile.mkdtemp(prefix="tq_cpu_baseline_"), "libtq_oracle_native.so")
+    cmd = [gcc, *NATIVE_FLAGS, "-std=gnu99", "-fPIC", "-shared", "-o", out, src, "-lm",
+           "-lpthread"]
+    try:
+        r = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
+    except (OSError, subprocess.TimeoutExpired) as e:
+        return None, f"gcc failed: {e}"
+    if r.returncode != 0:
+        return None, f"gcc failed: {r.stderr.strip()[-300:]}"
+    return out, "gcc " + " ".join(NATIVE_FLAGS) + " -std=gnu99 -fPIC -shared oracle/tq_oracle.c"
+
+
+def cpu_baseline(w: Workload, native=None, runs: int = 5, layers_per_run: int = 3):
     """The reference's CPU path for one decode step of this workload, on this
     host: per layer, the dequant (the oracle's C
     restatement of the reference kernel's operation order) to [N, H, D] fp16,
@@ -1039,14 +1072,31 @@ def cpu_baseline(w: Workload, runs: int = 5, layers_per_run: int = 3):
     each of the 16 query heads over its kv head's dequantized K/V.  Timed on
     1 thread and on every usable core (the dequant's token rows and the
     query heads split over threads), each as the median of `runs` runs of
-    `layers_per_run` layers after one warm-up run."""
+    `layers_per_run` layers after one warm-up run.  `native` is
+    build_native_oracle()'s result: that build is timed when there is one
+    (its dequant checked bit-identical to the prebuilt oracle's first)."""
     from concurrent.futures import ThreadPoolExecutor
 
     import numpy as np
 
-    from oracle.oracle import load
+    from oracle.oracle import Oracle, load
     from turborag_amd.synthetic import as_u16
     orc = load()
+    build = "gcc -O3 -march=x86-64-v3 -ffp-contract=off (oracle/build_oracle.sh)"
+    same = None
+    if native is not None and native[0] is not None:
+        nat = Oracle(native[0])
+        p0 = w.pools[0].cpu().numpy()
+        s0 = w.slots.cpu().numpy()
+        a = orc.prod_dequant(p0, s0, w.H, w.D, w.B)
+        b = nat.prod_dequant(p0, s0, w.H, w.D, w.B)
+        same = all(np.array_equal(x.view(np.uint16), y.view(np.uint16)) for x, y in zip(a, b))
+        if same:
+            orc, build = nat, native[1] + " (built on this host)"
+        else:
+            build += "; the -march=native build's dequant differed: not used"
+    elif native is not None:
+        build += f"; the -march=native build: {native[1]}"
     info = host_cpu()
     slots_np = w.slots.cpu().numpy()
     q_heads = as_u16(w.qa).transpose(1, 0, 2).reshape(w.q_heads, w.D)  # [h * rows + g]
@@ -1110,7 +1160,8 @@ def cpu_baseline(w: Workload, runs: int = 5, layers_per_run: int = 3):
         "single_thread": one,
         "all_cores": allc,
         "host": info,
-        "build": "gcc -O3 -march=x86-64-v3 -ffp-contract=off (oracle/build_oracle.sh)",
+        "build": build,
+        "native_build_matches_prebuilt": same,
     }
 
 

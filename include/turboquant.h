@@ -254,9 +254,11 @@ int tq_load_turbo_mse_layers(const uint8_t* const* host_pools, uint8_t* const* d
  * t % block_size of page block_tables[s * max_blocks_per_seq + t /
  * block_size]; pages for every token a row attends must be valid.
  * max_kv_len >= every row_kv_len sizes the launch and must fit in
- * max_blocks_per_seq pages.  Rows with kv length 0 get 0.  head_dim 128,
- * and the pool and page size 16-byte aligned (a turbo_prod page is 134 bytes
- * per token-head: block_size x num_kv_heads a multiple of 8); otherwise -2. */
+ * max_blocks_per_seq pages.  Rows with kv length 0 get 0.  head_dim 128
+ * with the pool and page size 16-byte aligned runs on the matrix cores;
+ * other head_dims and page sizes (a turbo_prod page is 134 bytes per
+ * token-head at head_dim 128, so block_size x num_kv_heads not a multiple of
+ * 8) on the generic split-K decode, one wave per (split, row). */
 int tq_launch_turbo_prod_paged_attention(const uint16_t* query, const uint8_t* page_pool,
                                          const int32_t* block_tables, int max_blocks_per_seq,
                                          const int32_t* row_seq, const int32_t* row_kv_len,

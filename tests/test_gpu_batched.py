@@ -150,3 +150,57 @@ def test_paged_over_a_thousand_row_groups(tq, cuda):
     print(f"    worst rel diff {err:.3e}", flush=True)
     assert err < 2e-3
     b.close()
+
+
+@pytest.mark.parametrize("scheme,H,D,B", [
+    ("turbo_prod", 2, 128, 7),  # 1,876-byte pages: not 16-byte aligned
+    ("turbo_prod", 1, 128, 7),  # 938-byte pages
+    ("turbo_prod", 2, 64, 16),
+    ("turbo_mse", 2, 64, 16),
+    ("turbo_mse", 4, 32, 5),
+])
+def test_paged_generic_geometries(tq, oracle, cuda, scheme, H, D, B):
+    """Geometries the matrix-core kernel does not take (unaligned pages, head
+    dims other than 128) run on the generic split-K decode through the block
+    table: every row against the fp64 oracle over its sequence's first
+    row_kv_len tokens; a row of kv length 0 gives 0 and a row whose length
+    passes max_kv_len attends max_kv_len tokens."""
+    lens, widths = [900, 33, 1500], [2, 1, 3]
+    print(f"[paged generic {scheme}] H={H} D={D} B={B}", flush=True)
+    b = PagedBatch(tq, scheme, lens, widths, kv_heads=H, q_heads=8 * H, head_dim=D,
+                   block_size=B, seed=560, device=cuda)
+    b.append_new_tokens(seed=561)
+    query, row_seq, row_len = b.decode_rows(seed=562)
+    max_kv = max(L + w for L, w in zip(lens, widths))
+    row_len[9] = 0
+    # a row of sequence 1 (34 tokens) given a length past max_kv_len: it attends
+    # max_kv_len positions, those past its pages unmapped (-1 in the block table;
+    # the unwritten cells of its last page read as stored: zero bytes)
+    row_len[17] = max_kv + 5
+    out = torch.full_like(query, 7.0)
+    b.attention(query, row_seq, row_len, b.block_tables(), out)
+    torch.cuda.synchronize()
+    got = out.cpu().float().numpy()
+    pool_np = b.pool.cpu().numpy()
+    q_np = as_u16(query)
+    f64 = oracle.prod_attention_f64 if scheme == "turbo_prod" else oracle.mse_attention_f64
+    seqs, lens_r = row_seq.cpu().numpy(), row_len.cpu().numpy()
+    assert np.all(got[9] == 0.0)
+    worst, worst_row = 0.0, -1
+    for r in range(query.shape[0]):
+        if r == 9:
+            continue
+        s = int(seqs[r])
+        n = min(int(lens_r[r]), max_kv)
+        blocks = np.asarray(b.table.blocks(s), dtype=np.int64)
+        t = np.arange(n)
+        mapped = t // B < blocks.size
+        slots = np.where(mapped, blocks[np.minimum(t // B, blocks.size - 1)] * B + t % B,
+                         -1).astype(np.int32)
+        ref = f64(q_np[r:r + 1].copy(), pool_np, slots, B)
+        e = _rel_err(got[r:r + 1], ref)
+        if e > worst:
+            worst, worst_row = e, r
+    print(f"    worst rel err {worst:.3e} (row {worst_row})", flush=True)
+    assert worst < ATT_TOL
+    b.close()

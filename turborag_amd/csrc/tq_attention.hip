@@ -48,15 +48,54 @@ __device__ __forceinline__ CellPtrs cell_of(const uint8_t* pool, const int32_t* 
     return {pool + (size_t)page * g.page_size, (size_t)(tib * g.H + h)};
 }
 
+// Where the generic decode finds a row's tokens.  Slot-mapped rows all attend
+// tokens [0, n) of one slot list (a negative slot: no token).
+struct SlotTokens {
+    const int32_t* slots;
+    int n;
+    struct Row {
+        int kv;
+    };
+    __device__ Row row(int) const { return {n}; }
+    __device__ bool cell(const Row&, int t, const PageGeom& g, int& page, int& tib) const {
+        const int s = slots[t];
+        if (s < 0) return false;
+        split_slot(s, g, page, tib);
+        return true;
+    }
+};
+// Paged rows: query row q attends the first min(row_kv_len[q], max_kv_len)
+// tokens of sequence row_seq[q]; token t is at position t % B of page
+// block_tables[seq * max_blocks + t / B] (a negative page: no token).
+// max_kv_len <= max_blocks * B (checked on the host) keeps t / B in the row.
+struct PagedTokens {
+    const int32_t* block_tables;
+    const int32_t* row_seq;
+    const int32_t* row_kv_len;
+    int max_blocks, max_kv_len;
+    struct Row {
+        int kv, seq;
+    };
+    __device__ Row row(int q) const { return {min(row_kv_len[q], max_kv_len), row_seq[q]}; }
+    __device__ bool cell(const Row& r, int t, const PageGeom& g, int& page, int& tib) const {
+        const int blk = g.bs_shift >= 0 ? t >> g.bs_shift : t / g.block_size;
+        page = block_tables[(size_t)r.seq * max_blocks + blk];
+        tib = t - blk * g.block_size;
+        return page >= 0;
+    }
+};
+
 // ---------------------------------------------------------------------------
 // Split-K partial: one wave per (split, row = q*H + h).
 // ws[(split * rows + row) * (D + 2) + ...] = acc[0..D), m, l.
+// Any head_dim and page geometry (the matrix-core kernels take D = 128 with
+// aligned pages).
 // ---------------------------------------------------------------------------
-template <int D, bool PROD>
+template <int D, bool PROD, class Tok>
 __global__ __launch_bounds__(64) void attn_partial_kernel(
-    const uint16_t* __restrict__ query, const uint8_t* __restrict__ pool,
-    const int32_t* __restrict__ slots, float* __restrict__ ws, PageGeom g, int rows,
-    int num_kv_tokens, int tokens_per_split, int num_splits, float inv) {
+    const uint16_t* __restrict__ query, const uint8_t* __restrict__ pool, Tok tok,
+    float* __restrict__ ws, PageGeom g, int rows, int tokens_per_split, int num_splits,
+    float inv) {
     constexpr int L = D / 2;
     __shared__ float tk[16], tv[16];
     const int lane = threadIdx.x;
@@ -69,16 +108,18 @@ __global__ __launch_bounds__(64) void attn_partial_kernel(
     const int split = blockIdx.x % num_splits;
     const int row = blockIdx.x / num_splits;
     const int h = row % g.H;
+    const typename Tok::Row tr = tok.row(row / g.H);
 
     float q0, q1;
     rotate_query<L>(query + (size_t)row * D, h, j, inv, q0, q1);
 
     const int t0 = split * tokens_per_split;
-    const int t1 = min(num_kv_tokens, t0 + tokens_per_split);
+    const int t1 = min(tr.kv, t0 + tokens_per_split);
     float m = kInitMax, l = 0.0f, a0 = 0.0f, a1 = 0.0f;
     for (int t = t0; t < t1; ++t) {
-        if (slots[t] < 0) continue;  // unmapped token (wave-uniform)
-        const CellPtrs c = cell_of(pool, slots, t, h, g);
+        int page, tib;
+        if (!tok.cell(tr, t, g, page, tib)) continue;  // no token here (wave-uniform)
+        const CellPtrs c{pool + (size_t)page * g.page_size, (size_t)(tib * g.H + h)};
         const uint32_t kb = c.base[g.kc_off + c.cell * g.code_stride + j];
         const float ks = h2f(ld_u16(c.base + g.ks_off + c.cell * g.scale_stride));
         const uint32_t n0 = kb & 0xf, n1 = kb >> 4;
@@ -2510,6 +2551,45 @@ void launch_decode_attention(const uint16_t* query, const uint8_t* pool, const i
                        0, stream, po, pml, output, g.H, rows, num_kv_tokens > 0 ? splits : 0);
     check_launch(combine_name);
 }
+
+// The generic split-K decode (attn_partial_kernel + attn_combine_kernel, any
+// head_dim and page geometry): one wave per (split, row), enough waves to
+// cover the chip several times, at least 32 tokens per split.
+struct GenericSplit {
+    int splits, tps;
+    size_t ws_bytes;
+};
+GenericSplit generic_split(int rows, int max_tokens, int D) {
+    int splits = (2048 + rows - 1) / rows;
+    splits = std::min(splits, std::max(1, (max_tokens + 31) / 32));
+    splits = std::max(splits, 1);
+    const int tps = max_tokens > 0 ? (max_tokens + splits - 1) / splits : 0;
+    if (tps > 0) splits = (max_tokens + tps - 1) / tps;
+    return {splits, tps, (size_t)splits * rows * (D + 2) * sizeof(float)};
+}
+template <class Tok>
+void launch_generic_attention(Scheme s, const uint16_t* query, const uint8_t* pool, Tok tok,
+                              uint16_t* output, const PageGeom& g, int rows,
+                              const GenericSplit& sp, float* ws, hipStream_t stream,
+                              const char* name) {
+    if ((long long)sp.splits * rows > INT32_MAX)
+        throw Error(std::string(name) + ": too many query rows");
+    const float inv = inv_sqrt_d(g.D);
+    const dim3 grid((unsigned)(sp.splits * rows));
+    if (s == Scheme::Prod) {
+        TQ_DISPATCH_D(g.D, hipLaunchKernelGGL((attn_partial_kernel<kD, true, Tok>), grid, dim3(64),
+                                              0, stream, query, pool, tok, ws, g, rows, sp.tps,
+                                              sp.splits, inv));
+    } else {
+        TQ_DISPATCH_D(g.D, hipLaunchKernelGGL((attn_partial_kernel<kD, false, Tok>), grid, dim3(64),
+                                              0, stream, query, pool, tok, ws, g, rows, sp.tps,
+                                              sp.splits, inv));
+    }
+    check_launch((std::string(name) + "_partial").c_str());
+    TQ_DISPATCH_D(g.D, hipLaunchKernelGGL(attn_combine_kernel<kD>, dim3(rows), dim3(64), 0,
+                                          stream, ws, output, g, rows, sp.splits, inv));
+    check_launch((std::string(name) + "_combine").c_str());
+}
 }  // namespace
 
 void launch_attention(Scheme s, const uint16_t* query, const uint8_t* pool, const int32_t* slots,
@@ -2531,31 +2611,12 @@ void launch_attention(Scheme s, const uint16_t* query, const uint8_t* pool, cons
                                                    "turbo_mse_fused_attn_combine", scratch);
         return;
     }
-    // Enough waves to cover the chip several times, at least 32 tokens each.
-    int splits = (2048 + rows - 1) / rows;
-    splits = std::min(splits, std::max(1, (num_kv_tokens + 31) / 32));
-    splits = std::max(splits, 1);
-    const int tps = num_kv_tokens > 0 ? (num_kv_tokens + splits - 1) / splits : 0;
-    if (tps > 0) splits = (num_kv_tokens + tps - 1) / tps;
-    const size_t ws_bytes = (size_t)splits * rows * (g.D + 2) * sizeof(float);
+    const GenericSplit sp = generic_split(rows, num_kv_tokens, g.D);
     const bool prod = s == Scheme::Prod;
     float* ws = static_cast<float*>(scratch.get(
-        stream, ws_bytes, prod ? "turbo_prod_fused_attn_partial" : "turbo_mse_fused_attn_partial"));
-    if (prod) {
-        TQ_DISPATCH_D(g.D, hipLaunchKernelGGL((attn_partial_kernel<kD, true>),
-                                              dim3(splits * rows), dim3(64), 0, stream, query,
-                                              pool, slots, ws, g, rows, num_kv_tokens, tps,
-                                              splits, inv));
-    } else {
-        TQ_DISPATCH_D(g.D, hipLaunchKernelGGL((attn_partial_kernel<kD, false>),
-                                              dim3(splits * rows), dim3(64), 0, stream, query,
-                                              pool, slots, ws, g, rows, num_kv_tokens, tps,
-                                              splits, inv));
-    }
-    check_launch(prod ? "turbo_prod_fused_attn_partial" : "turbo_mse_fused_attn_partial");
-    TQ_DISPATCH_D(g.D, hipLaunchKernelGGL(attn_combine_kernel<kD>, dim3(rows), dim3(64), 0,
-                                          stream, ws, output, g, rows, splits, inv));
-    check_launch(prod ? "turbo_prod_fused_attn_combine" : "turbo_mse_fused_attn_combine");
+        stream, sp.ws_bytes, prod ? "turbo_prod_fused_attn_partial" : "turbo_mse_fused_attn_partial"));
+    launch_generic_attention(s, query, pool, SlotTokens{slots, num_kv_tokens}, output, g, rows, sp,
+                             ws, stream, prod ? "turbo_prod_fused_attn" : "turbo_mse_fused_attn");
 }
 
 void launch_paged_attention(Scheme s, const uint16_t* query, const uint8_t* pool,
@@ -2564,8 +2625,19 @@ void launch_paged_attention(Scheme s, const uint16_t* query, const uint8_t* pool
                             int num_rows, int max_kv_len, hipStream_t stream) {
     const int rows = num_rows * g.H;
     if (rows <= 0) return;
-    if (!mfma_attention_ok(g, pool))
-        throw Error("paged attention: needs head_dim 128 and 16-byte aligned pages and pool");
+    const bool prod = s == Scheme::Prod;
+    if (!mfma_attention_ok(g, pool)) {
+        // Other head_dims and unaligned pages: the generic split-K decode, its
+        // rows reading their tokens through the block table.
+        const GenericSplit sp = generic_split(rows, std::max(max_kv_len, 0), g.D);
+        float* ws = static_cast<float*>(workspace(stream, sp.ws_bytes));
+        launch_generic_attention(
+            s, query, pool,
+            PagedTokens{block_tables, row_seq, row_kv_len, max_blocks, std::max(max_kv_len, 0)},
+            output, g, rows, sp, ws, stream,
+            prod ? "turbo_prod_paged_attn" : "turbo_mse_paged_attn");
+        return;
+    }
     using namespace mfma;
     const float inv = inv_sqrt_d(g.D);
     const int row_groups = (num_rows + kRows - 1) / kRows;
@@ -2597,7 +2669,6 @@ void launch_paged_attention(Scheme s, const uint16_t* query, const uint8_t* pool
     PagedUnit* group_unit = units + row_groups + 1;
     int32_t* plan = reinterpret_cast<int32_t*>(wsb + part_bytes + unit_bytes);
     const PagedRows pr{block_tables, row_seq, row_kv_len, max_blocks, units, group_unit, plan};
-    const bool prod = s == Scheme::Prod;
     constexpr int kCH = kSplitChunk, kNW = kSplitWaves;
     hipLaunchKernelGGL(paged_plan_kernel<kPagedPositions>, dim3(1), dim3(1024), 0, stream, row_seq,
                        row_kv_len, num_rows, row_groups, kPass, std::max(max_kv_len, 0), units,
