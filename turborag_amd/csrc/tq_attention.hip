@@ -710,16 +710,32 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
         };
         // Token of this lane in the chunk at t0 and its slot (the load is issued
         // here and consumed by fetch, so other work can run in between).  Lanes
-        // past the range re-read the last token of the range.
+        // past the range re-read the last token of the range.  Paged rows: the
+        // token's page table entry, turned into its slot by to_slot inside
+        // fetch; arithmetic on the loaded value here would make the in-order
+        // vector-memory counter wait, right after the next chunk's code loads
+        // are issued, for all of them (129-130 -> 125-127.5 us per config-5
+        // step).
+        auto token_block = [&](int t0, int& t) -> int {
+            t = max(min(t0 + (lane & (kChunk - 1)), t_end - 1), 0);
+            return min(g.bs_shift >= 0 ? t >> g.bs_shift : t / g.block_size, pr.max_blocks - 1);
+        };
         auto load_slot = [&](int t0) -> int {
-            const int t = max(min(t0 + (lane & (kChunk - 1)), t_end - 1), 0);
             if constexpr (PAGED) {  // token t of sequence seq: page table entry t / B
-                const int blk = min(g.bs_shift >= 0 ? t >> g.bs_shift : t / g.block_size,
-                                    pr.max_blocks - 1);
-                const int page = pr.block_tables[(size_t)seq * pr.max_blocks + blk];
-                return page < 0 ? -1 : page * g.block_size + (t - blk * g.block_size);
+                int t;
+                const int blk = token_block(t0, t);
+                return pr.block_tables[(size_t)seq * pr.max_blocks + blk];
             } else {
-                return slots[t];
+                return slots[max(min(t0 + (lane & (kChunk - 1)), t_end - 1), 0)];
+            }
+        };
+        auto to_slot = [&](int t0, int v) -> int {
+            if constexpr (PAGED) {
+                int t;
+                const int blk = token_block(t0, t);
+                return v < 0 ? -1 : v * g.block_size + (t - blk * g.block_size);
+            } else {
+                return v;
             }
         };
         // slot -> cell offsets (exchanged through LDS) -> scale and code loads,
@@ -741,7 +757,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
         auto ld128 = [](const uint8_t* p) -> uint4 {
             return PAGED ? *reinterpret_cast<const uint4*>(p) : ld_u4_nt(p);
         };
-        auto fetch = [&](int t0, int slot, Chunk& c) {
+        auto fetch = [&](int t0, int loaded, Chunk& c) {
+            const int slot = to_slot(t0, loaded);
             c.valid = t0 + (lane & (kChunk - 1)) < t_end && slot >= 0;
             int page, tib;
             split_slot(c.valid ? slot : 0, g, page, tib);
