@@ -677,10 +677,18 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
         int rl_col[NT] = {}, gmin_live = 0x7fffffff;
         if constexpr (PAGED) {
             kv_end = 0;
+            // Every row length and the sequence are loaded unconditionally (rows
+            // past the end re-read the last row), so the loads go out together:
+            // a load under a condition sits in a branch whose join waits for it.
+            int lraw[NP];
+#pragma unroll
+            for (int p = 0; p < NP; ++p)
+                lraw[p] = pr.row_kv_len[min((rg + p) * kRows + (lane & 7), num_queries - 1)];
+            const int seq_raw = pr.row_seq[rg * kRows];
 #pragma unroll
             for (int p = 0; p < NP; ++p) {
                 const int rr = (rg + p) * kRows + (lane & 7);
-                const int lv = p < npos && rr < num_queries ? pr.row_kv_len[rr] : 0;
+                const int lv = p < npos && rr < num_queries ? lraw[p] : 0;
                 rowlen[p] = __shfl(lv, i >> 1);
                 const int lc = __shfl(lv, i & 7);
                 // (one position: both halves of the tile hold its rows, hi and lo)
@@ -695,7 +703,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                 kv_end = max(kv_end, gend[p]);
                 if (p < npos) gmin_live = min(gmin_live, gmin[p]);
             }
-            seq = __builtin_amdgcn_readfirstlane(pr.row_seq[rg * kRows]);
+            seq = __builtin_amdgcn_readfirstlane(seq_raw);
             if (t_begin >= kv_end) return;  // uniform over the workgroup, before any barrier
         }
         const int t_end = min(kv_end, t_cap);
@@ -1530,10 +1538,13 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
         __syncthreads();
         // The walk over the units overlapping the segment, in work order.  Its
         // position lives in LDS (one copy per wave, volatile accesses), so no
-        // walk state is held in registers across an item.
+        // walk state is held in registers across an item.  The pointer is an
+        // LDS one: a generic (flat) access would also wait for the previous
+        // piece's partial stores.
         __shared__ int s_walk[kWaves];
+        typedef __attribute__((address_space(3))) int lds_int;
         const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-        volatile int* walk = &s_walk[wv];
+        volatile lds_int* walk = (volatile lds_int*)&s_walk[wv];
         if ((threadIdx.x & 63) == 0) walk[0] = __builtin_amdgcn_readfirstlane(s_unit);
         for (;;) {
             const int u = __builtin_amdgcn_readfirstlane(walk[0]);
