@@ -11,7 +11,10 @@ element: the decode kernels (turbo_prod, and turbo_mse whose K also carries
 fp16 lo parts) stay within one such ulp (measured: 0.5-1.0, with ~75% of all
 elements equal to the correctly rounded value), so the relative error against
 the 1e-3 bar (3.1e-4 to 4.1e-4 here) is the output format's own rounding, not
-the kernels' arithmetic."""
+the kernels' arithmetic.  The batched paged decode (hi/lo parts stacked along
+the reductions) is measured the same way over every row of a step (measured:
+within 1.0 row-max ulps; rel err 4.5e-4 to 4.7e-4, equal to the rounding of the
+exact result)."""
 from __future__ import annotations
 
 import numpy as np
@@ -77,5 +80,42 @@ def test_attention_output_within_fp16_rounding(tq, oracle, cuda, scheme, Q, H, N
     print(f"    rel err {e_kernel:.3e} (fp16 rounding of the exact result: {e_format:.3e}); "
           f"deviation from the rounded result: max {u.max():.2f} row-max ulps; "
           f"{same:.4f} of the elements equal it", flush=True)
+    assert u.max() <= 1.0
+    assert e_kernel < 1e-3
+
+
+@pytest.mark.parametrize("scheme", ["turbo_prod", "turbo_mse"])
+def test_paged_attention_output_within_fp16_rounding(tq, oracle, cuda, scheme):
+    """The batched paged decode (units of up to four positions, the hi/lo
+    parts stacked along the reductions) measured the same way: every row of a
+    step against the fp64 oracle over its sequence's causal token range, in
+    fp16 ulps of the row's largest element."""
+    from turborag_amd.batched import PagedBatch
+    lens, widths = [3000, 700, 5000, 64, 1500], [8, 3, 5, 1, 4]
+    print(f"[precision paged {scheme}] lens={lens} widths={widths}", flush=True)
+    oracle.nthreads = 16
+    b = PagedBatch(tq, scheme, lens, widths, seed=580, device=cuda)
+    b.append_new_tokens(seed=581)
+    query, row_seq, row_len = b.decode_rows(seed=582)
+    out = torch.zeros_like(query)
+    b.attention(query, row_seq, row_len, b.block_tables(), out)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    pool = b.pool.cpu().numpy()
+    q = as_u16(query)
+    f64 = oracle.prod_attention_f64 if scheme == "turbo_prod" else oracle.mse_attention_f64
+    refs, r = [], 0
+    for s, (L, w) in enumerate(zip(lens, widths)):
+        for j in range(w):
+            refs.append(f64(q[r:r + 8].copy(), pool, b.slots_of(s, L + j + 1), 16))
+            r += 8
+    ref = np.concatenate(refs)
+    u = _row_ulps(got, ref)
+    e_kernel, e_format = _rel(got, ref), _rel(ref.astype(np.float16), ref)
+    same = float(np.mean(got.astype(np.float16) == ref.astype(np.float16)))
+    print(f"    rel err {e_kernel:.3e} (fp16 rounding of the exact result: {e_format:.3e}); "
+          f"deviation from the rounded result: max {u.max():.2f} row-max ulps; "
+          f"{same:.4f} of the elements equal it", flush=True)
+    b.close()
     assert u.max() <= 1.0
     assert e_kernel < 1e-3
