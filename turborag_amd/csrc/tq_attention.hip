@@ -637,22 +637,48 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     // NP >= 2: NT tiles of 16 MFMA columns, (position 2t + i / 8, row i % 8)
     constexpr int NT = NP >= 2 ? NP / 2 : 1;
     constexpr int kMoRows = NP >= 2 ? 16 : kR;  // rows merged per pass (one tile)
-    // Decode tables indexed by a code byte (low nibble = even d), fp16 pairs:
-    // table 0 = K (prod: aK*K3, mse: the lo parts of aV*V4), table 1 = V (aV*V4,
-    // also mse's K hi parts), 32 copies
-    // each.  Entry e of table t, copy c is word e*64 + 32t + c and lane l
-    // reads copy l % 32, so a half-wave's 32 random lookups hit 32 distinct
-    // banks.  After the token loop the space holds the per-wave results for
-    // the merge.
-    __shared__ __attribute__((aligned(256))) uint32_t lut[256][64];
-    __shared__ float qs[kR][128];
+    // Decode tables indexed by a code byte (low nibble = even d), fp16 pairs,
+    // 32 copies each: copy c of entry e at byte 256e + 4c of its table and lane
+    // l reads copy l % 32, so a half-wave's 32 random lookups hit 32 distinct
+    // banks.
+    //  - NP = 1 (QJL): one region of K|V rows, table 0 (the sign octets) in
+    //    bytes 0..127 of each row, table 1 = V (aV*V4) in bytes 128..255.
+    //  - NP >= 2 (turbo_prod, turbo_mse): S rows at byte 0 (prod: the
+    //    residual signs, +-1.0; mse: the lo parts of aV*V4; bytes 0..127 of
+    //    each row) and K|V rows at byte kOffKV (K copies: prod aK*K3, mse the
+    //    hi parts aV*V4; V copies aV*V4 at +128).  One address then reads a
+    //    code byte's S pair (offset 0) and its K pair (offset kOffKV, which no
+    //    two-address LDS read merges with 0), each straight into its MFMA
+    //    operand, and a V lookup's address is that of the byte's S row + 128.
+    //    During the setup the S rows' upper halves hold the rotated queries.
+    // After the token loop the K|V rows hold the per-wave results for the
+    // merge.
+    constexpr bool STAB = NP >= 2;
+    constexpr int kOffKV = STAB ? 65520 : 0;
+    constexpr int kTabWords = STAB ? 32768 : 256 * 64;
+    __shared__ __attribute__((aligned(256))) uint32_t lut[kTabWords];
+    __shared__ float qs_sep[STAB ? 1 : kR][128];
     __shared__ uint4 bqs[NP][4][64];  // QK B operand (fp16 hi/lo q) of k-step s for lane l
     __shared__ uint64_t tko[kWaves][kChunk], tvo[kWaves][kChunk];
     __shared__ float4 tsc[kWaves][kChunk];  // per token: K scale a, residual scale b, vs, bias
     __shared__ float mm[kWaves][kR], ml[kWaves][kR];
     __shared__ uint32_t kstage[256], vstage[256];
-    static_assert(sizeof(float) * kWaves * kMoRows * 128 <= sizeof(lut), "merge space");
-    float(*mo)[kMoRows][128] = reinterpret_cast<float(*)[kMoRows][128]>(&lut[0][0]);
+    static_assert(kOffKV + 256 * 256 <= (int)sizeof(lut), "K|V rows");
+    static_assert(kOffKV + sizeof(float) * kWaves * kMoRows * 128 <= sizeof(lut), "merge space");
+    static_assert(!STAB || 256 * (kR * 128 / 32) <= kOffKV, "queries in the S rows' upper halves");
+    float(*mo)[kMoRows][128] = reinterpret_cast<float(*)[kMoRows][128]>(&lut[kOffKV / 4]);
+    // K|V row e (its 64 words: 32 K copies, then 32 V copies)
+    auto kv_row = [&](int e) -> uint32_t* { return &lut[kOffKV / 4 + 64 * e]; };
+    // Rotated query element (r, d): STAB: float r*128 + d in the upper half of
+    // S row (r*128 + d) / 32.
+    auto qs_at = [&](int r, int d) -> float& {
+        if constexpr (STAB) {
+            const int f = r * 128 + d;
+            return reinterpret_cast<float*>(&lut[64 * (f >> 5) + 32])[f & 31];
+        } else {
+            return qs_sep[r][d];
+        }
+    };
 
     const float ck = inv * kLog2e / (PROD ? kAlphaK : kAlphaV);  // logit scale per unit ks
     const float cr = inv * kLog2e;                                 // residual: ks * re
@@ -859,8 +885,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
             float q0 = qf[k][0], q1 = qf[k][1];
             wht_pair<64>(q0, q1, lane);
             const bool live = r / kRows < npos && rg * kRows + r < num_queries;
-            qs[r][2 * lane] = live ? q0 * inv : 0.0f;
-            qs[r][2 * lane + 1] = live ? q1 * inv : 0.0f;
+            qs_at(r, 2 * lane) = live ? q0 * inv : 0.0f;
+            qs_at(r, 2 * lane + 1) = live ? q1 * inv : 0.0f;
         }
         lds_barrier();  // staged table rows and rotated queries visible
 
@@ -869,11 +895,23 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
             constexpr int kRowsPerWave = 256 / kWaves;
             // (all staged words read before the first store: one LDS round trip)
             uint32_t stv[kRowsPerWave / 4];
+            uint32_t sts[kRowsPerWave / 8];  // STAB: the S entries this lane stores
             if constexpr (!QJL) {
 #pragma unroll
                 for (int k = 0; k < kRowsPerWave; k += 4) {
                     const int e = w * kRowsPerWave + k + (lane >> 4);
-                    stv[k / 4] = (lane & 8) ? vstage[e] : kstage[e];  // words 32..63: V
+                    // words 32..63: V; mse's K copies hold its hi parts (the V pairs)
+                    stv[k / 4] = (lane & 8) || (STAB && !PROD) ? vstage[e] : kstage[e];
+                }
+                if constexpr (STAB) {
+#pragma unroll
+                    for (int k = 0; k < kRowsPerWave; k += 8) {
+                        const int e = w * kRowsPerWave + k + (lane >> 3);
+                        // prod: the residual signs of the two nibbles (bits 3, 7)
+                        sts[k / 8] = PROD ? ((e & 0x08) ? 0x3C00u : 0xBC00u) |
+                                                ((e & 0x80) ? 0x3C000000u : 0xBC000000u)
+                                          : kstage[e];  // mse: the lo parts
+                    }
                 }
             }
 #pragma unroll
@@ -892,10 +930,18 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                                     ((e >> (2 * q + 1)) & 1 ? 0x3C000000u : 0xBC000000u);
                         v4 = make_uint4(wd[0], wd[1], wd[2], wd[3]);
                     }
-                    *reinterpret_cast<uint4*>(&lut[e][4 * (lane & 15)]) = v4;
+                    *reinterpret_cast<uint4*>(kv_row(e) + 4 * (lane & 15)) = v4;
                 } else {
                     const uint32_t v = stv[k / 4];
-                    *reinterpret_cast<uint4*>(&lut[e][4 * (lane & 15)]) = make_uint4(v, v, v, v);
+                    *reinterpret_cast<uint4*>(kv_row(e) + 4 * (lane & 15)) = make_uint4(v, v, v, v);
+                }
+            }
+            if constexpr (STAB) {  // S rows: 8 per store, 8 lanes of 4 copies each
+#pragma unroll
+                for (int k = 0; k < kRowsPerWave; k += 8) {
+                    const int e = w * kRowsPerWave + k + (lane >> 3);
+                    const uint32_t v = sts[k / 8];
+                    *reinterpret_cast<uint4*>(&lut[64 * e + 4 * (lane & 7)]) = make_uint4(v, v, v, v);
                 }
             }
         }
@@ -910,15 +956,15 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                 if (p != 0) continue;
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
-                    b[e] = hi_lo(qs[i & 7][32 * gq + 8 * s + e], (i >> 3) != 0);
+                    b[e] = hi_lo(qs_at(i & 7, 32 * gq + 8 * s + e), (i >> 3) != 0);
             } else if constexpr (NP >= 2) {  // tile p / 2, part p % 2 (hi, lo) of column i's row
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
-                    b[e] = hi_lo(qs[16 * (p >> 1) + i][32 * gq + 8 * s + e], (p & 1) != 0);
+                    b[e] = hi_lo(qs_at(16 * (p >> 1) + i, 32 * gq + 8 * s + e), (p & 1) != 0);
             } else {  // position p, k-step s; column parity picks hi or lo
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
-                    b[e] = hi_lo(qs[p * kRows + (i >> 1)][32 * gq + 8 * s + e], lo_col);
+                    b[e] = hi_lo(qs_at(p * kRows + (i >> 1), 32 * gq + 8 * s + e), lo_col);
             }
             bqs[p][s][lane] = __builtin_bit_cast(uint4, b);
         }
@@ -932,7 +978,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
         }
         // Byte address of this lane's copy of entry 0 of each table; a lookup
         // puts the code byte into byte 1 (entry stride 256 B) with one v_perm.
-        const uint32_t lutk = (uint32_t)reinterpret_cast<uintptr_t>((lds_u32*)&lut[0][lane & 31]);
+        const uint32_t lutk = (uint32_t)reinterpret_cast<uintptr_t>((lds_u32*)(kv_row(0) + (lane & 31)));
         const uint32_t lutv = lutk + 128u;
         const uint32_t lut_hi = lutk & 0xFF00u;  // byte 1 of the base, re-added after the perm
         auto lookup = [&](uint32_t word, int b, int table) -> uint32_t {
@@ -941,9 +987,20 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                 __builtin_amdgcn_perm(word, base, 0x03020000u | ((4u + b) << 8)) + lut_hi;
             return *reinterpret_cast<const lds_u32*>(a);
         };
+        // STAB: the S-row address of byte b of word (this lane's copy; its K pair
+        // at + kOffKV), and that of a V code byte (S row + 128: its V pair at
+        // + kOffKV).
+        const uint32_t luts = (uint32_t)reinterpret_cast<uintptr_t>((lds_u32*)&lut[lane & 31]);
+        const uint32_t luts_hi = luts & 0xFF00u;
+        auto s_addr = [&](uint32_t word, int b, uint32_t off) -> uint32_t {
+            return __builtin_amdgcn_perm(word, luts + off, 0x03020000u | ((4u + b) << 8)) + luts_hi;
+        };
+        auto lds_at = [](uint32_t a, int off) -> uint32_t {
+            return *reinterpret_cast<const lds_u32*>(a + off);
+        };
         // QJL: the fp16 +-1 octet of sign byte b of word (copy lane % 8).
         const uint32_t lutq =
-            (uint32_t)reinterpret_cast<uintptr_t>((lds_u32*)&lut[0][4 * (lane & 7)]);
+            (uint32_t)reinterpret_cast<uintptr_t>((lds_u32*)(kv_row(0) + 4 * (lane & 7)));
         auto signs = [&](uint32_t word, int b) -> half8 {
             const uint32_t a =
                 __builtin_amdgcn_perm(word, lutq, 0x03020000u | ((4u + b) << 8)) + (lutq & 0xFF00u);
@@ -1214,12 +1271,16 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                                             : s == 1 ? kw[tau].y
                                             : s == 2 ? kw[tau].z
                                                      : kw[tau].w;
-                        const int kt = PROD ? 0 : 1;  // mse: the hi parts are the V table
-                        o.a[tau] = as_h8(lookup(wd, 0, kt), lookup(wd, 1, kt), lookup(wd, 2, kt),
-                                         lookup(wd, 3, kt));
-                        if (!PROD)  // mse: the lo parts (table 0)
-                            o.al[tau] = as_h8(lookup(wd, 0, 0), lookup(wd, 1, 0),
-                                              lookup(wd, 2, 0), lookup(wd, 3, 0));
+                        // one address per byte: its K pair (prod aK*K3, mse the hi
+                        // parts) and its S pair (prod the residual signs, mse the lo
+                        // parts)
+                        uint32_t ad[4];
+#pragma unroll
+                        for (int b = 0; b < 4; ++b) ad[b] = s_addr(wd, b, 0);
+                        o.a[tau] = as_h8(lds_at(ad[0], kOffKV), lds_at(ad[1], kOffKV),
+                                         lds_at(ad[2], kOffKV), lds_at(ad[3], kOffKV));
+                        o.al[tau] = as_h8(lds_at(ad[0], 0), lds_at(ad[1], 0), lds_at(ad[2], 0),
+                                          lds_at(ad[3], 0));
                     }
                 };
                 Ops ops[2];
@@ -1246,35 +1307,16 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                     const Ops& o = ops[s & 1];
 #pragma unroll
                     for (int tau = 0; tau < kTiles; ++tau) {
-                        const uint32_t wd = s == 0   ? kw[tau].x
-                                            : s == 1 ? kw[tau].y
-                                            : s == 2 ? kw[tau].z
-                                                     : kw[tau].w;
 #pragma unroll
                         for (int t = 0; t < NTA; ++t) {
                             cb[t][tau] = mma(o.a[tau], o.bk[2 * t], cb[t][tau]);
                             if (!COLS) cb[t][tau] = mma(o.a[tau], o.bk[2 * t + 1], cb[t][tau]);
                         }
-                        if (!PROD) {  // mse: the lo parts into cs
+                        // prod: the +-1 residual signs; mse: the lo parts (into cs)
 #pragma unroll
-                            for (int t = 0; t < NTA; ++t) {
-                                cs[t][tau] = mma(o.al[tau], o.bk[2 * t], cs[t][tau]);
-                                if (!COLS)
-                                    cs[t][tau] = mma(o.al[tau], o.bk[2 * t + 1], cs[t][tau]);
-                            }
-                        }
-                        if (PROD) {
-                            const uint32_t he = ((wd << 4) & 0x80808080u) ^ 0xBCBCBCBCu;  // even d
-                            const uint32_t ho = (wd & 0x80808080u) ^ 0xBCBCBCBCu;         // odd d
-                            const half8 sa = as_h8(__builtin_amdgcn_perm(ho, he, 0x040C000Cu),
-                                                   __builtin_amdgcn_perm(ho, he, 0x050C010Cu),
-                                                   __builtin_amdgcn_perm(ho, he, 0x060C020Cu),
-                                                   __builtin_amdgcn_perm(ho, he, 0x070C030Cu));
-#pragma unroll
-                            for (int t = 0; t < NTA; ++t) {
-                                cs[t][tau] = mma(sa, o.bk[2 * t], cs[t][tau]);
-                                if (!COLS) cs[t][tau] = mma(sa, o.bk[2 * t + 1], cs[t][tau]);
-                            }
+                        for (int t = 0; t < NTA; ++t) {
+                            cs[t][tau] = mma(o.al[tau], o.bk[2 * t], cs[t][tau]);
+                            if (!COLS) cs[t][tau] = mma(o.al[tau], o.bk[2 * t + 1], cs[t][tau]);
                         }
                     }
                     __builtin_amdgcn_sched_barrier(0);
@@ -1308,8 +1350,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                         const uint32_t hib = ((we >> 4) & 0x0F0F0F0Fu) | (wo & 0xF0F0F0F0u);
 #pragma unroll
                         for (int b = 0; b < 4; ++b) {
-                            bv[st][2 * b][q] = lookup(lob, b, 1);
-                            bv[st][2 * b + 1][q] = lookup(hib, b, 1);
+                            bv[st][2 * b][q] = lds_at(s_addr(lob, b, 128u), kOffKV);
+                            bv[st][2 * b + 1][q] = lds_at(s_addr(hib, b, 128u), kOffKV);
                         }
                     }
                 __builtin_amdgcn_sched_barrier(0);
