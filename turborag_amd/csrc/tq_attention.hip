@@ -1244,7 +1244,6 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                 }
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-                Chunk nxt;
                 const int t1 = t0 + kWaves * kChunk;
                 // QK: each decoded A operand against every tile's hi and lo query
                 f32x4 cb[NTA][kTiles], cs[NTA][kTiles];
@@ -1286,13 +1285,6 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                 Ops ops[2];
                 float4 scq[kTiles][4];  // the logits' per-token scales, read during the last k-step
                 load_ops(0, ops[0]);
-                // The next chunk's codes and the slots of the one after, fetched
-                // behind the first k-step's LDS reads (its address exchange
-                // through LDS would otherwise delay them).
-                if (t1 < t_end) {
-                    fetch(t1, slot_nx, nxt);
-                    slot_nx = load_slot(t1 + kWaves * kChunk);
-                }
 #pragma unroll
                 for (int s = 0; s < 4; ++s) {
                     if (s < 3) {
@@ -1355,6 +1347,16 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                         }
                     }
                 __builtin_amdgcn_sched_barrier(0);
+                // This chunk's codes are consumed: the next chunk's codes and the
+                // slots of the one after are fetched into cur's registers, in
+                // flight during the softmax and PV (no copy at the end of the
+                // step, which would wait for them: 128.3 -> 127.1 us turbo_prod,
+                // 129.5 -> 127.1 us turbo_mse against fetching into a second
+                // buffer behind the first k-step).
+                if (t1 < t_end) {
+                    fetch(t1, slot_nx, cur);
+                    slot_nx = load_slot(t1 + kWaves * kChunk);
+                }
                 if (masked) {  // a row of the unit ends in this chunk (wave-uniform)
                     asm volatile("" ::: "memory");  // a branch: no selects on every chunk
 #pragma unroll
@@ -1449,7 +1451,6 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                 }
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-                cur = nxt;
                 t0 = t1;
                 first = false;
             }
