@@ -1778,10 +1778,16 @@ __global__ __launch_bounds__(256) void attn_paged_combine_kernel(
     const int u = un.index;
     const int total = pr.plan[1], G = num_segments;
     const int p = rg - un.first;
+    // The group's longest row: the row lengths are loaded unconditionally (a
+    // row past the end re-reads the last row), so the loads go out together
+    // with the unit's record instead of one after another in branches.
+    int kvr[kRows];
+#pragma unroll
+    for (int k = 0; k < kRows; ++k) kvr[k] = pr.row_kv_len[min(rg * kRows + k, num_queries - 1)];
     int kv = 0;
 #pragma unroll
     for (int k = 0; k < kRows; ++k)
-        kv = max(kv, rg * kRows + k < num_queries ? pr.row_kv_len[rg * kRows + k] : 0);
+        if (rg * kRows + k < num_queries) kv = max(kv, kvr[k]);
     const int S = un.start;  // every head has the unit's work range, in its own segments
     // segments holding the item's first and last pass starts
     int g_lo = 0, g_hi = -1;
@@ -1796,18 +1802,31 @@ __global__ __launch_bounds__(256) void attn_paged_combine_kernel(
     for (int b = g_lo; b <= g_hi; b += 8) {
         float pm[8], pl[8];
         float4 po[8];
+        float2 mlr[8];
+        int okv[8];
+        // (slot gs <= g_hi is one of the item's pieces: the loads are
+        // unconditional and all in flight together; the pieces that wrote
+        // nothing are dropped after, by a per-lane select rather than a branch
+        // whose join would wait for each load in turn)
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const int gs = min(b + k, g_hi);
             int x0, x1;
             item_passes(S, un.n, un.w, sg.bound(gs), sg.bound(gs + 1), x0, x1);
-            const bool ok = b + k <= g_hi && x0 < x1 && x0 * pass < kv;
+            okv[k] = b + k <= g_hi && x0 < x1 && x0 * pass < kv;
             const float* pp =
                 ws + ((((unit0 + gs) * H + h) * positions + p) * kRows + r) * kPartStride;
-            pm[k] = ok ? pp[128] : kInitMax;
-            pl[k] = ok ? pp[129] : 0.f;
-            po[k] = ok ? *reinterpret_cast<const float4*>(pp + d0)
-                       : make_float4(0.f, 0.f, 0.f, 0.f);
+            mlr[k] = *reinterpret_cast<const float2*>(pp + 128);
+            po[k] = *reinterpret_cast<const float4*>(pp + d0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            int ok = okv[k];
+            asm volatile("" : "+v"(ok));
+            pm[k] = ok ? mlr[k].x : kInitMax;
+            pl[k] = ok ? mlr[k].y : 0.f;
+            if (!ok) po[k] = make_float4(0.f, 0.f, 0.f, 0.f);
         }
         float mb = M;
 #pragma unroll
@@ -1885,13 +1904,19 @@ __global__ __launch_bounds__(1024) void paged_plan_kernel(
     constexpr int kWin = 1024;
     __shared__ int s_sq[kWin + U], s_gk[kWin + U], s_tot[16], s_carry[4];
     const int j = threadIdx.x;
-    auto group_kv = [&](int gi) {  // the group's longest row (rows past num_rows: 0)
+    // The group's longest row (rows past num_rows: 0).  The loads are
+    // unconditional (a row past the end re-reads the last row), so the eight
+    // go out together: a load under a condition sits in a branch whose join
+    // waits for it, one memory latency per row.
+    auto load_kv = [&](int gi, int (&v)[kRows]) {
+#pragma unroll
+        for (int k = 0; k < kRows; ++k) v[k] = row_kv_len[min(gi * kRows + k, num_rows - 1)];
+    };
+    auto group_kv = [&](int gi, const int (&v)[kRows]) {
         int m = 0;
 #pragma unroll
-        for (int k = 0; k < kRows; ++k) {
-            const int rr = gi * kRows + k;
-            if (rr < num_rows) m = max(m, row_kv_len[rr]);
-        }
+        for (int k = 0; k < kRows; ++k)
+            if (gi * kRows + k < num_rows) m = max(m, v[k]);
         return min(m, max_kv_len);
     };
     const auto add = [](int a, int b) { return a + b; };
@@ -1900,13 +1925,26 @@ __global__ __launch_bounds__(1024) void paged_plan_kernel(
     for (int base = 0; base < groups; base += kWin) {
         const int gi = base + j;
         const bool in = gi < groups;
-        const int sq = in ? row_seq[(size_t)gi * kRows] : 0;
+        // (groups past the end load the last group, unconditionally, then drop it)
+        const int gc = min(gi, groups - 1);
+        const int gx = min(base + kWin + j, groups - 1);  // look-ahead (threads j < U - 1)
+        int kvr[kRows], kvx[kRows];
+        const int sq_raw = row_seq[(size_t)gc * kRows];
+        const int sqx_raw = row_seq[(size_t)gx * kRows];
+        load_kv(gc, kvr);
+        load_kv(gx, kvx);
+        __builtin_amdgcn_sched_barrier(0);  // all 18 loads in flight before any is used
+        const int gk_raw = group_kv(gc, kvr);
+        const int gkx_raw = group_kv(gx, kvx);
+        const int sq = in ? sq_raw : 0;
         s_sq[j] = sq;
-        s_gk[j] = in ? group_kv(gi) : 0;
-        if (j < U - 1) {  // look-ahead for units that straddle the window's end
-            const int gx = base + kWin + j;
-            s_sq[kWin + j] = gx < groups ? row_seq[(size_t)gx * kRows] : 0;
-            s_gk[kWin + j] = gx < groups ? group_kv(gx) : 0;
+        s_gk[j] = in ? gk_raw : 0;
+        {  // look-ahead for units that straddle the window's end: threads j < U - 1
+            // write slot kWin + j, the others the spare last slot (never read),
+            // so no branch holds the look-ahead loads back
+            const bool inx = j < U - 1 && base + kWin + j < groups;
+            s_sq[kWin + min(j, U - 1)] = inx ? sqx_raw : 0;
+            s_gk[kWin + min(j, U - 1)] = inx ? gkx_raw : 0;
         }
         __syncthreads();
         const int prev = j > 0 ? s_sq[j - 1] : c_sq;
