@@ -314,10 +314,6 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(const PackSet<ML> set
     static_assert(C == 4 || C == 8, "D = 64 or 128");
     constexpr bool PROD = SCH == 1, QJL = SCH == 2;
     __shared__ PackTables tab;
-    if (threadIdx.x < kPackTableWords)
-        reinterpret_cast<uint32_t*>(&tab)[threadIdx.x] =
-            reinterpret_cast<const uint32_t*>(&kPackTables)[threadIdx.x];
-    __syncthreads();
     const int j = pack_lane(threadIdx.x & (R - 1));
     const int row = blockIdx.x * (kBlock / R) + threadIdx.x / R;
     const bool valid = row < num_rows;
@@ -326,12 +322,23 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(const PackSet<ML> set
     const int h = rr - t * g.H;
     const uint32_t* kr = reinterpret_cast<const uint32_t*>(key + (size_t)rr * D) + j;
     const uint32_t* vr = reinterpret_cast<const uint32_t*>(value + (size_t)rr * D) + j;
+    // The table word, the row's K words and its slot go out together; the V
+    // words right after the table is stored, so they arrive during the K
+    // quantization (the compiler had issued the V words after it and the
+    // slot just before the stores: per-layer launches 6.9 -> 6.6 us, one
+    // launch for 36 layers 3.05 -> 2.94 us per layer, config 2 turbo_prod).
+    const uint32_t tw = reinterpret_cast<const uint32_t*>(
+        &kPackTables)[min((int)threadIdx.x, kPackTableWords - 1)];
     uint32_t kw[C], vw[C];
 #pragma unroll
-    for (int c = 0; c < C; ++c) {
-        kw[c] = kr[R * c];
-        vw[c] = vr[R * c];
-    }
+    for (int c = 0; c < C; ++c) kw[c] = kr[R * c];
+    const int slot_raw = slots[t];
+    __builtin_amdgcn_sched_barrier(0);
+    if (threadIdx.x < kPackTableWords) reinterpret_cast<uint32_t*>(&tab)[threadIdx.x] = tw;
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < C; ++c) vw[c] = vr[R * c];
+    __builtin_amdgcn_sched_barrier(0);
     // s(i, h) = (-1)^(i + h) = sh * (-1)^b for element i = 2Rc + 2j + b.  The
     // first butterfly stage on (sh*a, -sh*b) gives (sh*(a - b), sh*(a + b));
     // fp32 rounding is symmetric in sign, so every later value is sh times
@@ -361,7 +368,7 @@ __global__ __launch_bounds__(kBlock) void pack_wide_kernel(const PackSet<ML> set
         }
     }
     if (!valid) return;
-    const int slot = slots[t];
+    const int slot = slot_raw;
     if (slot < 0) return;
     int page, tib;
     split_slot(slot, g, page, tib);
