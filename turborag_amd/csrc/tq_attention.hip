@@ -1867,8 +1867,15 @@ __device__ int block_scan_1024(int v, int ident, int* s_tot, Op op) {
     }
     if (lane == 63) s_tot[wv] = v;
     __syncthreads();
+    // The earlier waves' totals: all 16 read at once (one LDS round trip),
+    // then combined below this wave's index.
+    int tot[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) tot[k] = s_tot[k];
     int pre = ident;
-    for (int k = 0; k < wv; ++k) pre = op(pre, s_tot[k]);
+#pragma unroll
+    for (int k = 0; k < 16; ++k)
+        if (k < wv) pre = op(pre, tot[k]);
     __syncthreads();  // s_tot is reused by the next scan
     return op(pre, v);
 }
