@@ -641,8 +641,10 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     // 32 copies each: copy c of entry e at byte 256e + 4c of its table and lane
     // l reads copy l % 32, so a half-wave's 32 random lookups hit 32 distinct
     // banks.
-    //  - NP = 1 (QJL): one region of K|V rows, table 0 (the sign octets) in
-    //    bytes 0..127 of each row, table 1 = V (aV*V4) in bytes 128..255.
+    //  - NP = 1 (the QJL-1b decode; the layout the one-group loop reads for
+    //    any scheme): one region of K|V rows, table 0 in bytes 0..127 of each
+    //    row (QJL: the sign octets; prod: aK*K3; mse: the lo parts of aV*V4)
+    //    and table 1 = V (aV*V4) in bytes 128..255.
     //  - NP >= 2 (turbo_prod, turbo_mse): S rows at byte 0 (prod: the
     //    residual signs, +-1.0; mse: the lo parts of aV*V4; bytes 0..127 of
     //    each row) and K|V rows at byte kOffKV (K copies: prod aK*K3, mse the
