@@ -682,7 +682,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
         }
     };
 
-    const float ck = inv * kLog2e / (PROD ? kAlphaK : kAlphaV);  // logit scale per unit ks
+    // logit scale per unit ks (log2(e) / alpha folded at compile time: no run-time division)
+    const float ck = inv * (PROD ? kLog2e / kAlphaK : kLog2e / kAlphaV);
     const float cr = inv * kLog2e;                                 // residual: ks * re
     // One work item: kv head h, row groups rg .. rg + npos - 1, tokens
     // [t_begin, t_cap) (paged: and below each row's length), partial slot pid.
@@ -2152,7 +2153,8 @@ __global__ __launch_bounds__(64 * kWaves) void attn_decode_split_kernel(
     const int i = lane & 15, gq = lane >> 4;
     const int t_begin = split * tokens_per_split;
     const int t_end = min(num_kv_tokens, t_begin + tokens_per_split);
-    const float ck = inv * kLog2e / (PROD ? kAlphaK : kAlphaV);  // logit scale per unit ks
+    // logit scale per unit ks (log2(e) / alpha folded at compile time: no run-time division)
+    const float ck = inv * (PROD ? kLog2e / kAlphaK : kLog2e / kAlphaV);
     const float cr = inv * kLog2e;                                 // residual: ks * re
     constexpr float iav = 1.0f / kAlphaV;
 
