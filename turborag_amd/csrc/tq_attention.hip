@@ -321,6 +321,9 @@ struct PagedRows {
     const PagedUnit* units;
     const PagedUnit* group_unit;
     const int32_t* plan;
+    // A page-sized region of the workspace that masked tokens' loads address
+    // (always valid memory; what they read is not used)
+    const uint8_t* spare_page;
 };
 // Workgroup s of G takes the work positions [bound(s), bound(s + 1)) with
 // bound(s) = floor(s * total / G) = q*s + floor(r*s / G) (q, r = total div, mod
@@ -745,41 +748,30 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
             uint16_t ks, re, vs;  // this lane's token's fp16 scales (raw: still in flight)
             bool valid;
         };
-        // Token of this lane in the chunk at t0 and its slot (the load is issued
-        // here and consumed by fetch, so other work can run in between).  Lanes
-        // past the range re-read the last token of the range.  Paged rows: the
-        // token's page table entry, turned into its slot by to_slot inside
-        // fetch; arithmetic on the loaded value here would make the in-order
-        // vector-memory counter wait, right after the next chunk's code loads
-        // are issued, for all of them (129-130 -> 125-127.5 us per config-5
-        // step).
-        auto token_block = [&](int t0, int& t) -> int {
-            t = max(min(t0 + (lane & (kChunk - 1)), t_end - 1), 0);
-            return min(g.bs_shift >= 0 ? t >> g.bs_shift : t / g.block_size, pr.max_blocks - 1);
+        // Token of this lane in the chunk at t0 (lanes past the range re-read the
+        // last token of the range) and its slot, or for paged rows its page
+        // table entry.  The load is issued here and consumed by fetch, so other
+        // work runs in between; arithmetic on the loaded value here would make
+        // the in-order vector-memory counter wait, right after the next chunk's
+        // code loads are issued, for all of them (129-130 -> 125-127.5 us per
+        // config-5 step).
+        auto chunk_token = [&](int t0) -> int {
+            return max(min(t0 + (lane & (kChunk - 1)), t_end - 1), 0);
         };
         auto load_slot = [&](int t0) -> int {
+            const int t = chunk_token(t0);
             if constexpr (PAGED) {  // token t of sequence seq: page table entry t / B
-                int t;
-                const int blk = token_block(t0, t);
-                return pr.block_tables[(size_t)seq * pr.max_blocks + blk];
+                const int blk = g.bs_shift >= 0 ? t >> g.bs_shift : t / g.block_size;
+                return pr.block_tables[(size_t)seq * pr.max_blocks + min(blk, pr.max_blocks - 1)];
             } else {
-                return slots[max(min(t0 + (lane & (kChunk - 1)), t_end - 1), 0)];
-            }
-        };
-        auto to_slot = [&](int t0, int v) -> int {
-            if constexpr (PAGED) {
-                int t;
-                const int blk = token_block(t0, t);
-                return v < 0 ? -1 : v * g.block_size + (t - blk * g.block_size);
-            } else {
-                return v;
+                return slots[t];
             }
         };
         // slot -> cell offsets (exchanged through LDS) -> scale and code loads,
-        // issued for every lane.  Tokens past the range or with a negative slot
-        // read the first bytes of the query instead (always valid memory: the
-        // offset of the query from the pool) and get bias -inf.  The loads stay in
-        // flight until the chunk is computed.
+        // issued for every lane.  Slot-mapped rows: tokens past the range or
+        // with a negative slot read the first bytes of the query instead (always
+        // valid memory: the offset of the query from the pool) and get bias
+        // -inf.  The loads stay in flight until the chunk is computed.
         const uint64_t dummy_off =
             (uint64_t)(reinterpret_cast<uintptr_t>(query) - reinterpret_cast<uintptr_t>(pool));
         // Slot-mapped rows read each pool byte once: non-temporal loads keep
@@ -787,44 +779,79 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
         // Paged rows keep plain loads: the workgroups of the two kv heads of
         // a work segment read each 128-byte code line together, one through
         // the other's L2 copy.
+        typedef __attribute__((address_space(1))) const uint8_t gbyte;
+        typedef __attribute__((address_space(1))) const uint32_t gword;
+        typedef __attribute__((address_space(1))) const u32x4 gquad;
         auto ld16 = [](const uint8_t* p) -> uint16_t { return PAGED ? ld_u16(p) : ld_u16_nt(p); };
-        auto ld32 = [](const uint8_t* p) -> uint32_t {
-            return PAGED ? *reinterpret_cast<const uint32_t*>(p) : ld_u32_nt(p);
+        auto ld32 = [](gbyte* p) -> uint32_t {
+            if constexpr (PAGED) return *reinterpret_cast<gword*>(p);
+            return ld_u32_nt((const uint8_t*)p);
         };
-        auto ld128 = [](const uint8_t* p) -> uint4 {
-            return PAGED ? *reinterpret_cast<const uint4*>(p) : ld_u4_nt(p);
+        auto ld128 = [](gbyte* p) -> uint4 {
+            if constexpr (PAGED) return __builtin_bit_cast(uint4, *reinterpret_cast<gquad*>(p));
+            return ld_u4_nt((const uint8_t*)p);
+        };
+        // The code rows' addresses go through LDS: paged rows as global
+        // addresses, slot-mapped rows as offsets from pool.
+        auto code_row = [&](uint64_t v) -> gbyte* {
+            return PAGED ? reinterpret_cast<gbyte*>(v) : (gbyte*)(pool + v);
         };
         auto fetch = [&](int t0, int loaded, Chunk& c) {
-            const int slot = to_slot(t0, loaded);
-            c.valid = t0 + (lane & (kChunk - 1)) < t_end && slot >= 0;
-            int page, tib;
-            split_slot(c.valid ? slot : 0, g, page, tib);
-            const uint64_t cell = (uint64_t)(tib * g.H + h);
-            const uint64_t pb = (uint64_t)page * g.page_size;
-            // Byte offsets from pool (integer selects: no branches around loads).
-            // (distinct dummy bytes per field, so the three loads stay separate)
-            const uint64_t so = pb + cell * g.scale_stride;
-            c.ks = ld16(pool + (c.valid ? so + g.ks_off : dummy_off));
-            c.vs = ld16(pool + (c.valid ? so + g.vs_off : dummy_off + 2));
-            c.re = PROD ? ld16(pool + (c.valid ? so + g.kres_off : dummy_off + 4)) : (uint16_t)0;
-            // (with 32-token chunks lanes l and l + 32 hold the same token)
-            // K row: code_stride bytes, or QJL's D/8 = 16 sign bytes
-            const uint64_t kstride = QJL ? 16u : (uint64_t)g.code_stride;
-            tko[w][lane & (kChunk - 1)] = c.valid ? pb + g.kc_off + cell * kstride : dummy_off;
-            tvo[w][lane & (kChunk - 1)] =
-                c.valid ? pb + g.vc_off + cell * g.code_stride : dummy_off;
+            if constexpr (PAGED) {
+                // loaded: the token's page table entry.  A cell's bytes are its
+                // page's address plus 32-bit offsets within the page (integer
+                // selects: no branches around loads).  Masked lanes (past the
+                // range, or an unmapped page) address the workspace's spare page
+                // instead: always valid memory, its bytes unused (bias -inf).
+                c.valid = t0 + (lane & (kChunk - 1)) < t_end && loaded >= 0;
+                const int t = chunk_token(t0);
+                const int tib = g.bs_shift >= 0 ? t & (g.block_size - 1) : t % g.block_size;
+                const uint32_t cell = (uint32_t)(tib * g.H + h);
+                const uint8_t* pg =
+                    c.valid ? pool + (uint64_t)(uint32_t)loaded * (uint32_t)g.page_size
+                            : pr.spare_page;
+                const uint32_t so = cell * (uint32_t)g.scale_stride;
+                c.ks = ld16(pg + (so + (uint32_t)g.ks_off));
+                c.vs = ld16(pg + (so + (uint32_t)g.vs_off));
+                c.re = PROD ? ld16(pg + (so + (uint32_t)g.kres_off)) : (uint16_t)0;
+                const uint32_t co = cell * (uint32_t)g.code_stride;
+                tko[w][lane & (kChunk - 1)] = reinterpret_cast<uint64_t>(pg + (co + (uint32_t)g.kc_off));
+                tvo[w][lane & (kChunk - 1)] = reinterpret_cast<uint64_t>(pg + (co + (uint32_t)g.vc_off));
+            } else {
+                const int slot = loaded;
+                c.valid = t0 + (lane & (kChunk - 1)) < t_end && slot >= 0;
+                int page, tib;
+                split_slot(c.valid ? slot : 0, g, page, tib);
+                const uint64_t cell = (uint64_t)(tib * g.H + h);
+                const uint64_t pb = (uint64_t)page * g.page_size;
+                // Byte offsets from pool (integer selects: no branches around loads).
+                // (distinct dummy bytes per field, so the three loads stay separate)
+                const uint64_t so = pb + cell * g.scale_stride;
+                c.ks = ld16(pool + (c.valid ? so + g.ks_off : dummy_off));
+                c.vs = ld16(pool + (c.valid ? so + g.vs_off : dummy_off + 2));
+                c.re = PROD ? ld16(pool + (c.valid ? so + g.kres_off : dummy_off + 4)) : (uint16_t)0;
+                // (with 32-token chunks lanes l and l + 32 hold the same token)
+                // K row: code_stride bytes, or QJL's D/8 = 16 sign bytes
+                const uint64_t kstride = QJL ? 16u : (uint64_t)g.code_stride;
+                tko[w][lane & (kChunk - 1)] = c.valid ? pb + g.kc_off + cell * kstride : dummy_off;
+                tvo[w][lane & (kChunk - 1)] =
+                    c.valid ? pb + g.vc_off + cell * g.code_stride : dummy_off;
+            }
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
             for (int tau = 0; tau < kTiles; ++tau) {
                 if constexpr (QJL)  // sign bytes 4gq .. 4gq + 3: k-steps 0 .. 3
                     c.kw[tau] = make_uint4(
-                        *reinterpret_cast<const uint32_t*>(pool + (tko[w][16 * tau + i] + 4 * gq)),
+                        *reinterpret_cast<gword*>(code_row(tko[w][16 * tau + i]) + 4 * gq),
                         0u,
                         0u, 0u);
                 else
-                    c.kw[tau] = ld128(pool + (tko[w][16 * tau + i] + 16 * gq));
+                    c.kw[tau] = ld128(code_row(tko[w][16 * tau + i]) + 16 * gq);
             }
+            // (the K words first: the QK waits for them while the V words may
+            // still be in flight)
+            __builtin_amdgcn_sched_barrier(0);
             // k-step p covers tiles 2p, 2p+1; k-index 8gq + e is token
             // 32p + 4gq + e (e < 4) or 32p + 16 + 4gq + (e - 4).
 #pragma unroll
@@ -832,7 +859,7 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const int tok = 32 * p + (e < 4 ? 4 * gq + e : 16 + 4 * gq + (e - 4));
-                    c.vw[p][e] = ld32(pool + (tvo[w][tok] + 4 * i));
+                    c.vw[p][e] = ld32(code_row(tvo[w][tok]) + 4 * i);
                 }
         };
 
@@ -2746,7 +2773,14 @@ void launch_paged_attention(Scheme s, const uint16_t* query, const uint8_t* pool
     const int rows = num_rows * g.H;
     if (rows <= 0) return;
     const bool prod = s == Scheme::Prod;
-    if (!mfma_attention_ok(g, pool)) {
+    // Bytes from a page's start that a cell's loads reach (the matrix-core
+    // kernel addresses them as 32-bit offsets, and masked tokens read a spare
+    // region of this size).
+    const uint64_t cells = (uint64_t)g.block_size * (uint64_t)g.H;
+    const uint64_t extent =
+        std::max({g.page_size, std::max({g.ks_off, g.vs_off, g.kres_off}) + cells * g.scale_stride,
+                  std::max(g.kc_off, g.vc_off) + cells * g.code_stride});
+    if (!mfma_attention_ok(g, pool) || extent > 0xFFFFFFFFu) {
         // Other head_dims and unaligned pages: the generic split-K decode, its
         // rows reading their tokens through the block table.
         const GenericSplit sp = generic_split(rows, std::max(max_kv_len, 0), g.D);
@@ -2783,12 +2817,14 @@ void launch_paged_attention(Scheme s, const uint16_t* query, const uint8_t* pool
     const size_t part_bytes =
         ((size_t)heads + G) * kPagedPositions * kRows * kPartStride * sizeof(float);
     const size_t unit_bytes = (2 * (size_t)row_groups + 1) * sizeof(PagedUnit);
-    char* wsb = static_cast<char*>(workspace(stream, part_bytes + unit_bytes + 4 * sizeof(int32_t)));
+    const size_t spare_at = (part_bytes + unit_bytes + 4 * sizeof(int32_t) + 255) & ~(size_t)255;
+    char* wsb = static_cast<char*>(workspace(stream, spare_at + extent));
     float* ws = reinterpret_cast<float*>(wsb);
     PagedUnit* units = reinterpret_cast<PagedUnit*>(wsb + part_bytes);
     PagedUnit* group_unit = units + row_groups + 1;
     int32_t* plan = reinterpret_cast<int32_t*>(wsb + part_bytes + unit_bytes);
-    const PagedRows pr{block_tables, row_seq, row_kv_len, max_blocks, units, group_unit, plan};
+    const PagedRows pr{block_tables, row_seq,    row_kv_len, max_blocks, units, group_unit, plan,
+                       reinterpret_cast<const uint8_t*>(wsb + spare_at)};
     constexpr int kCH = kSplitChunk, kNW = kSplitWaves;
     hipLaunchKernelGGL(paged_plan_kernel<kPagedPositions>, dim3(1), dim3(1024), 0, stream, row_seq,
                        row_kv_len, num_rows, row_groups, kPass, std::max(max_kv_len, 0), units,
