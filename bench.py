@@ -203,12 +203,32 @@ def capture(fn, side):
         return None
 
 
-def event_time_us(run, reps, warm: int = 1):
+SETTLE_MS = 100.0
+
+
+def settle(run, ms: float = SETTLE_MS) -> None:
+    """Untimed calls of run() for `ms` of wall time, 16 queued per
+    synchronisation.  After the host-side set-up of a figure the GPU has
+    idled, and its clocks come back over its first ~30-40 ms of work: per
+    replay of the batched step's graph (10 launches) 1,290-1,400 µs at first,
+    1,105 µs from the 30th on; the 36-layer attention graph 390, then 350,
+    then 337 µs from the 40th on."""
+    import torch
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(16):
+            run()
+        torch.cuda.synchronize()
+
+
+def event_time_us(run, reps, warm: int = 1, settle_ms: float = SETTLE_MS):
     """Mean duration of run() in µs from HIP events on the current stream,
-    after `warm` untimed calls."""
+    after `settle_ms` of untimed calls (the clocks' return from idle) and
+    `warm` more."""
     import torch
     a = torch.cuda.Event(enable_timing=True)
     b = torch.cuda.Event(enable_timing=True)
+    settle(run, settle_ms)
     for _ in range(warm):
         run()
     a.record()
@@ -259,6 +279,9 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--settle-ms", type=float, default=SETTLE_MS,
+                    help="untimed step replays, in ms of wall time, before the warmup steps "
+                         "(the GPU's clocks return from idle over its first ~30-40 ms of work)")
     ap.add_argument("--layers", type=int, default=36)
     ap.add_argument("--tokens", type=int, default=32768)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -306,6 +329,7 @@ def main() -> int:
     run_deq1 = g_deq1.replay if use_graph else w.all_dequant_per_layer
 
     # The timed region: K whole steps.
+    settle(run_step, args.settle_ms)
     for _ in range(args.warmup):
         run_step()
     torch.cuda.synchronize()
@@ -451,6 +475,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_ms": args.settle_ms,
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
