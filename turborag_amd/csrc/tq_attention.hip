@@ -1186,8 +1186,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                                     lg[p][tau][e] = -INFINITY;
                             mloc = fmaxf(mloc, lg[p][tau][e]);
                         }
-                    mloc = fmaxf(mloc, lane_xor<16>(mloc));
-                    mloc = fmaxf(mloc, lane_xor<32>(mloc));
+                    mloc = lane_xor_reduce<16>(mloc, [](float x, float y) { return fmaxf(x, y); });
+                    mloc = lane_xor_reduce<32>(mloc, [](float x, float y) { return fmaxf(x, y); });
                     // v_exp_f32 without denormal handling: arguments are <= 0 and a
                     // weight below 2^-126 of the running maximum is negligible.
                     const float m_new = fmaxf(m_run[p], mloc);
@@ -1405,13 +1405,15 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                 bool grow = false;
 #pragma unroll
                 for (int t = 0; t < NTA; ++t) {
-                    float m = -INFINITY;
+                    // (IEEE maximum: no canonicalising of the lane-exchanged
+                    // values; a NaN logit leaves grow false, as fmaxf would)
+                    float m = lg[t][0][0];
 #pragma unroll
-                    for (int tau = 0; tau < kTiles; ++tau)
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) m = fmaxf(m, lg[t][tau][e]);
-                    m = fmaxf(m, lane_xor<16>(m));
-                    mloc[t] = fmaxf(m, lane_xor<32>(m));
+                    for (int k = 1; k < 4 * kTiles; ++k)
+                        m = __builtin_elementwise_maximum(m, lg[t][k >> 2][k & 3]);
+                    const auto mx = [](float x, float y) { return __builtin_elementwise_maximum(x, y); };
+                    m = lane_xor_reduce<16>(m, mx);
+                    mloc[t] = lane_xor_reduce<32>(m, mx);
                     grow = grow || mloc[t] > m_col[t] + 1.0f;
                 }
                 if (__any(grow)) {  // wave-uniform
@@ -1433,14 +1435,19 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                 }
 #pragma unroll
                 for (int t = 0; t < NTA; ++t) {
-                    float lsum = 0.0f;
 #pragma unroll
                     for (int tau = 0; tau < kTiles; ++tau)
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) {
+                        for (int e = 0; e < 4; ++e)
                             lg[t][tau][e] = __builtin_amdgcn_exp2f(lg[t][tau][e] - m_col[t]);
-                            lsum += lg[t][tau][e];
-                        }
+                    // pairwise: no zero start, and the adds do not wait on one another
+                    float part[kTiles];
+#pragma unroll
+                    for (int tau = 0; tau < kTiles; ++tau)
+                        part[tau] = (lg[t][tau][0] + lg[t][tau][1]) + (lg[t][tau][2] + lg[t][tau][3]);
+                    float lsum = part[0];
+#pragma unroll
+                    for (int tau = 1; tau < kTiles; ++tau) lsum += part[tau];
                     l_col[t] += lsum;
                 }
                 // PV: every tile's hi and lo P against each decoded B operand
@@ -1506,8 +1513,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
         if constexpr (NP >= 2) {
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                float l_tot = l_col[t] + lane_xor<16>(l_col[t]);
-                l_tot += lane_xor<32>(l_tot);
+                float l_tot = lane_xor_reduce<16>(l_col[t], [](float x, float y) { return x + y; });
+                l_tot = lane_xor_reduce<32>(l_tot, [](float x, float y) { return x + y; });
                 if (gq == 0) {
                     mm[w][16 * t + i] = m_col[t];
                     ml[w][16 * t + i] = l_tot;
@@ -1516,8 +1523,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
         } else {
 #pragma unroll
             for (int p = 0; p < NP; ++p) {
-                float l_tot = l_run[p] + lane_xor<16>(l_run[p]);
-                l_tot += lane_xor<32>(l_tot);
+                float l_tot = lane_xor_reduce<16>(l_run[p], [](float x, float y) { return x + y; });
+                l_tot = lane_xor_reduce<32>(l_tot, [](float x, float y) { return x + y; });
                 if (gq == 0 && !lo_col) {
                     mm[w][p * kRows + (i >> 1)] = m_run[p];
                     ml[w][p * kRows + (i >> 1)] = l_tot;
@@ -2411,8 +2418,8 @@ __global__ __launch_bounds__(64 * kWaves) void attn_decode_split_kernel(
                 lg[tau][e] = fmaf(sb, sc.x, fmaf(sr, sc.y, sc.w));
                 mloc = fmaxf(mloc, lg[tau][e]);
             }
-        mloc = fmaxf(mloc, lane_xor<16>(mloc));
-        mloc = fmaxf(mloc, lane_xor<32>(mloc));
+        mloc = lane_xor_reduce<16>(mloc, [](float x, float y) { return fmaxf(x, y); });
+        mloc = lane_xor_reduce<32>(mloc, [](float x, float y) { return fmaxf(x, y); });
         // v_exp_f32 without denormal handling: arguments are <= 0 and a weight
         // below 2^-126 of the running maximum is negligible.
         const float m_new = fmaxf(m_run, mloc);
@@ -2458,8 +2465,8 @@ __global__ __launch_bounds__(64 * kWaves) void attn_decode_split_kernel(
     // from the hi + lo columns.  Then the waves are merged per row, the
     // inverse WHT and sign flip applied, and the partial written.
     {
-        float l_tot = l_run + lane_xor<16>(l_run);
-        l_tot += lane_xor<32>(l_tot);
+        float l_tot = lane_xor_reduce<16>(l_run, [](float x, float y) { return x + y; });
+        l_tot = lane_xor_reduce<32>(l_tot, [](float x, float y) { return x + y; });
         if (gq == 0 && !lo_col) {
             mm[w][i >> 1] = m_run;
             ml[w][i >> 1] = l_tot;

@@ -113,6 +113,24 @@ __device__ __forceinline__ float lane_xor(float v) {
     }
 }
 
+// op(v, lane_xor<M>(v)) for a symmetric op (max, +).  M = 16, 32: a
+// permlane swap of v with itself leaves v's even rows (halves) in one result
+// and its odd rows in the other, each duplicated, so op over the two is the
+// reduction in every lane: one swap, no lane select.
+template <int M, class Op>
+__device__ __forceinline__ float lane_xor_reduce(float v, Op op) {
+    const unsigned x = __float_as_uint(v);
+    if constexpr (M == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+        return op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    } else if constexpr (M == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+        return op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    } else {
+        return op(v, lane_xor<M>(v));
+    }
+}
+
 // lane_xor for an m known after loop unrolling.
 __device__ __forceinline__ float xor_lane(float v, int m) {
     switch (m) {
