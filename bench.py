@@ -206,7 +206,7 @@ def capture(fn, side):
 SETTLE_MS = 100.0
 
 
-def settle(run, ms: float = SETTLE_MS) -> None:
+def settle(run, ms: float | None = None) -> None:
     """Untimed calls of run() for `ms` of wall time, 16 queued per
     synchronisation.  After the host-side set-up of a figure the GPU has
     idled, and its clocks come back over its first ~30-40 ms of work: per
@@ -214,6 +214,7 @@ def settle(run, ms: float = SETTLE_MS) -> None:
     1,105 µs from the 30th on; the 36-layer attention graph 390, then 350,
     then 337 µs from the 40th on."""
     import torch
+    ms = SETTLE_MS if ms is None else ms
     t0 = time.perf_counter()
     while (time.perf_counter() - t0) * 1e3 < ms:
         for _ in range(16):
@@ -221,7 +222,7 @@ def settle(run, ms: float = SETTLE_MS) -> None:
         torch.cuda.synchronize()
 
 
-def event_time_us(run, reps, warm: int = 1, settle_ms: float = SETTLE_MS):
+def event_time_us(run, reps, warm: int = 1, settle_ms: float | None = None):
     """Mean duration of run() in µs from HIP events on the current stream,
     after `settle_ms` of untimed calls (the clocks' return from idle) and
     `warm` more."""
@@ -280,8 +281,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--settle-ms", type=float, default=SETTLE_MS,
-                    help="untimed step replays, in ms of wall time, before the warmup steps "
-                         "(the GPU's clocks return from idle over its first ~30-40 ms of work)")
+                    help="untimed replays, in ms of wall time, before each figure's timed ones "
+                         "(for the step: before its warmup steps); the GPU's clocks return from "
+                         "idle over its first ~30-40 ms of work")
     ap.add_argument("--layers", type=int, default=36)
     ap.add_argument("--tokens", type=int, default=32768)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -289,6 +291,8 @@ def main() -> int:
     ap.add_argument("--launch-pass", action="store_true",
                     help="eager launches only (for rocprofv3 counter runs); no JSON line")
     args = ap.parse_args()
+    global SETTLE_MS
+    SETTLE_MS = args.settle_ms
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the path has no cross-GPU "
               "exchange; each GPU would serve its own layers' pools) — run with --gpus 1",
