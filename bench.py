@@ -276,6 +276,7 @@ def launch_pass(w: Workload, reps: int) -> None:
 
 
 def main() -> int:
+    global SETTLE_MS
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
@@ -291,7 +292,6 @@ def main() -> int:
     ap.add_argument("--launch-pass", action="store_true",
                     help="eager launches only (for rocprofv3 counter runs); no JSON line")
     args = ap.parse_args()
-    global SETTLE_MS
     SETTLE_MS = args.settle_ms
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the path has no cross-GPU "
