@@ -1533,17 +1533,71 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
         }
         const float iav = 1.0f / kAlphaV;
         const float s0 = (!QJL && (h & 1)) ? -inv : inv;
+        // Row rr of tile t from the merge space mt (the 8 waves' o rows): the
+        // waves' (m, l, o) merged, the inverse WHT and sign flip, the partial.
+        auto merge_row = [&](int t, int rr, float(*mt)[kMoRows][128]) {
+            const int r = kMoRows * t + rr;  // row of the workgroup
+            const int p = r / kRows;
+            bool keep = p < npos;
+            if constexpr (PAGED) keep = keep && t_begin < gend[p];
+            if (!keep) return;  // wave-uniform
+            float M = mm[0][r];
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            if (NP >= 2 && t >= ntile) break;  // wave- and workgroup-uniform
-            __syncthreads();  // every wave is done with the tables (or the last pass) mo overwrites
-            if constexpr (NP >= 2) {
+            for (int u = 1; u < kWaves; ++u) M = fmaxf(M, mm[u][r]);
+            float L = 0.f, o0 = 0.f, o1 = 0.f;
+#pragma unroll
+            for (int u = 0; u < kWaves; ++u) {
+                const float wt = __builtin_amdgcn_exp2f(mm[u][r] - M);  // (argument <= 0)
+                L += ml[u][r] * wt;
+                o0 += mt[u][rr][2 * lane] * wt;
+                o1 += mt[u][rr][2 * lane + 1] * wt;
+            }
+            if (NP >= 2 && npos == 1) {  // one position: + its lo columns 8-15
+#pragma unroll
+                for (int u = 0; u < kWaves; ++u) {
+                    const float wt = __builtin_amdgcn_exp2f(mm[u][r] - M);  // (argument <= 0)
+                    o0 += mt[u][rr + kRows][2 * lane] * wt;
+                    o1 += mt[u][rr + kRows][2 * lane + 1] * wt;
+                }
+            }
+            wht_pair<64>(o0, o1, lane);
+            float* part = ws + ((pid * NP + p) * kRows + r % kRows) * kPartStride;
+            part[2 * lane] = o0 * s0;
+            part[2 * lane + 1] = o1 * -s0;
+            if (lane == 0) {
+                part[128] = M;
+                part[129] = L;
+            }
+        };
+        if constexpr (NP >= 2) {
+            // Both tiles at once: tile t's merge space at table word 16384 t
+            // (the tables are no longer read), three barriers per piece instead
+            // of four, and each wave's four rows merged without a barrier
+            // between them.
+            static_assert(NT * sizeof(float) * kWaves * kMoRows * 128 <= sizeof(lut), "merge spaces");
+            auto mot = [&](int t) { return reinterpret_cast<float(*)[kMoRows][128]>(&lut[16384 * t]); };
+            __syncthreads();  // every wave is done with the tables
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                if (t >= ntile) break;  // wave- and workgroup-uniform
 #pragma unroll
                 for (int v = 0; v < 8; ++v)
 #pragma unroll
                     for (int e = 0; e < 4; ++e)  // (x2: the PV operand was P * vs / 2)
-                        mo[w][4 * gq + e][8 * i + v] = acc_col[t][v][e] * (2.0f * iav);
-            } else {
+                        mot(t)[w][4 * gq + e][8 * i + v] = acc_col[t][v][e] * (2.0f * iav);
+            }
+            __syncthreads();
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int k = 0; k < kMoRows / kWaves; ++k) merge_row(t, w + k * kWaves, mot(t));
+            // the next piece's setup writes its rotated queries into the S rows,
+            // which hold tile 0's merge space
+            __syncthreads();
+        } else {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                __syncthreads();  // every wave is done with the tables (or the last pass) mo overwrites
 #pragma unroll
                 for (int p = 0; p < NP; ++p)
 #pragma unroll
@@ -1552,41 +1606,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                         mo[w][p * kRows + 2 * gq + 1][8 * i + v] =
                             (acc[p][v][2] + acc[p][v][3]) * iav;
                     }
-            }
-            __syncthreads();
-            for (int rr = w; rr < kMoRows; rr += kWaves) {
-                const int r = kMoRows * t + rr;  // row of the workgroup
-                const int p = r / kRows;
-                bool keep = p < npos;
-                if constexpr (PAGED) keep = keep && t_begin < gend[p];
-                if (!keep) continue;  // wave-uniform
-                float M = mm[0][r];
-#pragma unroll
-                for (int u = 1; u < kWaves; ++u) M = fmaxf(M, mm[u][r]);
-                float L = 0.f, o0 = 0.f, o1 = 0.f;
-#pragma unroll
-                for (int u = 0; u < kWaves; ++u) {
-                    const float wt = __builtin_amdgcn_exp2f(mm[u][r] - M);  // (argument <= 0)
-                    L += ml[u][r] * wt;
-                    o0 += mo[u][rr][2 * lane] * wt;
-                    o1 += mo[u][rr][2 * lane + 1] * wt;
-                }
-                if (NP >= 2 && npos == 1) {  // one position: + its lo columns 8-15
-#pragma unroll
-                    for (int u = 0; u < kWaves; ++u) {
-                        const float wt = __builtin_amdgcn_exp2f(mm[u][r] - M);  // (argument <= 0)
-                        o0 += mo[u][rr + kRows][2 * lane] * wt;
-                        o1 += mo[u][rr + kRows][2 * lane + 1] * wt;
-                    }
-                }
-                wht_pair<64>(o0, o1, lane);
-                float* part = ws + ((pid * NP + p) * kRows + r % kRows) * kPartStride;
-                part[2 * lane] = o0 * s0;
-                part[2 * lane + 1] = o1 * -s0;
-                if (lane == 0) {
-                    part[128] = M;
-                    part[129] = L;
-                }
+                __syncthreads();
+                for (int rr = w; rr < kMoRows; rr += kWaves) merge_row(t, rr, mo);
             }
         }
     };  // item
