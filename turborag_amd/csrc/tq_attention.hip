@@ -374,6 +374,120 @@ __device__ __forceinline__ uint32_t lo_pair(float x0, float x1, uint32_t h) {
         : "v"(x0), "v"(x1), "v"(h));
     return r;
 }
+constexpr uint16_t f16_bits(float x) { return __builtin_bit_cast(uint16_t, (_Float16)x); }
+constexpr uint32_t f16_pair(float a, float b) {
+    return (uint32_t)f16_bits(a) | ((uint32_t)f16_bits(b) << 16);
+}
+// (x - fp16(x)) * 2^kLoShift, exact in fp32 (mfma::lo_part at compile time).
+constexpr float lo_part_c(float x) { return (x - (float)(_Float16)x) * (float)(1 << kLoShift); }
+
+// fp16 bits of the codebook values the decode tables hold: aK*K3[j],
+// aV*V4[j], and the lo parts (x - fp16(x)) * 2^kLoShift of aV*V4[j].
+struct Fp16Tables {
+    uint32_t k3[8], v4[16], v4lo[16];
+};
+constexpr Fp16Tables make_fp16_tables() {
+    Fp16Tables t{};
+    for (int j = 0; j < 8; ++j) t.k3[j] = f16_bits(kAlphaK * dev::kK3[j]);
+    for (int j = 0; j < 16; ++j) {
+        t.v4[j] = f16_bits(kAlphaV * dev::kV4[j]);
+        t.v4lo[j] = f16_bits(lo_part_c(kAlphaV * dev::kV4[j]));
+    }
+    return t;
+}
+constexpr Fp16Tables kF16 = make_fp16_tables();
+// The fp16 pair (t[j], t[j + 1]).
+template <int N>
+constexpr uint32_t f16_pair_of(const uint32_t (&t)[N], int j) {
+    return t[j] | (t[j + 1] << 16);
+}
+// Selector of entry g < 4 of a 4-entry fp16 table held as two fp16 pairs:
+// bytes 2g, 2g + 1, then zeros.
+__device__ __forceinline__ uint32_t lut4_sel(int g) {
+    return (uint32_t)(2 * g) | ((uint32_t)(2 * g + 1) << 8) | 0x0C0C0000u;
+}
+// t[4m + g] (in the low half) for the 4-entry slice m of t, g given by sel.
+template <int N>
+__device__ __forceinline__ uint32_t lut4(const uint32_t (&t)[N], int m, uint32_t sel) {
+    return __builtin_amdgcn_perm(f16_pair_of(t, 4 * m + 2), f16_pair_of(t, 4 * m), sel);
+}
+// Decode tables in the one-address-two-pairs layout: S rows (256 B each,
+// 32 copies of the entry in bytes 0..127) at byte 0 and K|V rows at byte
+// kOffKV (K copies in bytes 0..127, turbo_prod's V copies in 128..255); entry
+// b holds the fp16 pairs of code byte b (low nibble = even d):
+//   K: turbo_prod (aK*K3[b & 7], aK*K3[(b >> 4) & 7]); turbo_mse the hi
+//      parts fp16(aV*V4[b & 15]), fp16(aV*V4[b >> 4]) (its V lookups read them
+//      too);
+//   S: turbo_prod the residual signs (nibble bit 3 set: +1.0, else -1.0);
+//      turbo_mse the lo parts of aV*V4;
+//   V (turbo_prod): (aV*V4[b & 15], aV*V4[b >> 4]).
+// Wave w of 8 writes rows 32w .. 32w + 31 of each table from registers (no
+// memory traffic): with those rows one nibble of every entry is uniform
+// across the wave and the other comes from a 4-entry fp16 table by v_perm.
+//   S rows, and turbo_mse's K rows: store k < 4 writes row 32w + 8k + lane / 8,
+//     copies 4q .. 4q + 3 (q = lane % 8): low nibble 8(k % 2) + lane / 8, high
+//     nibble 2w + k / 2;
+//   turbo_prod's K | V rows: store k < 8 writes row 32w + 4k + lane / 16, group
+//     lane % 16 (K copies, then V copies): low nibble 4(k % 4) + lane / 16, high
+//     nibble 2w + k / 4.
+template <bool PROD>
+struct TableWords {
+    static constexpr int kR1Stores = PROD ? 8 : 4;
+    uint32_t r0[4], r1[kR1Stores];
+};
+template <bool PROD>
+__device__ __forceinline__ TableWords<PROD> decode_table_words(int w, int lane) {
+    TableWords<PROD> tw;
+    uint32_t(&r0)[4] = tw.r0;
+    uint32_t(&r1)[TableWords<PROD>::kR1Stores] = tw.r1;
+    {
+        const int g4 = lane >> 4, g8 = lane >> 3;
+        const uint32_t sel4 = lut4_sel(g4), sel8 = lut4_sel(g8 & 3);
+        const bool hi8 = (g8 & 4) != 0;
+        if constexpr (PROD) {
+            const uint32_t sh = (w & 4) ? 0x3C000000u : 0xBC000000u;  // row bit 7 = w bit 2
+#pragma unroll
+            for (int k = 0; k < 4; ++k) r0[k] = ((k & 1) ? 0x3C00u : 0xBC00u) | sh;  // row bit 3
+            const bool vq = (lane & 8) != 0;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const uint32_t vpair =
+                    lut4(kF16.v4, k & 3, sel4) | (kF16.v4[2 * w + (k >> 2)] << 16);
+                const uint32_t kpair =
+                    lut4(kF16.k3, k & 1, sel4) | (kF16.k3[(2 * w + (k >> 2)) & 7] << 16);
+                r1[k] = vq ? vpair : kpair;
+            }
+        } else {
+            uint32_t llo[2], vlo[2];
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                llo[hh] = hi8 ? lut4(kF16.v4lo, 2 * hh + 1, sel8) : lut4(kF16.v4lo, 2 * hh, sel8);
+                vlo[hh] = hi8 ? lut4(kF16.v4, 2 * hh + 1, sel8) : lut4(kF16.v4, 2 * hh, sel8);
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                r0[k] = llo[k & 1] | (kF16.v4lo[2 * w + (k >> 1)] << 16);
+                r1[k] = vlo[k & 1] | (kF16.v4[2 * w + (k >> 1)] << 16);
+            }
+        }
+    }
+    return tw;
+}
+template <bool PROD>
+__device__ __forceinline__ void store_decode_tables(uint32_t* lut, int kv_words, int w, int lane,
+                                                    const TableWords<PROD>& tw) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        *reinterpret_cast<u32x4*>(&lut[(32 * w + 8 * k + (lane >> 3)) * 64 + 4 * (lane & 7)]) =
+            (u32x4){tw.r0[k], tw.r0[k], tw.r0[k], tw.r0[k]};
+#pragma unroll
+    for (int k = 0; k < TableWords<PROD>::kR1Stores; ++k) {
+        const int row = PROD ? 32 * w + 4 * k + (lane >> 4) : 32 * w + 8 * k + (lane >> 3);
+        const int q = PROD ? lane & 15 : lane & 7;
+        *reinterpret_cast<u32x4*>(&lut[kv_words + row * 64 + 4 * q]) =
+            (u32x4){tw.r1[k], tw.r1[k], tw.r1[k], tw.r1[k]};
+    }
+}
 }  // namespace mfma
 
 // ---------------------------------------------------------------------------
@@ -648,42 +762,32 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
     //    any scheme): one region of K|V rows, table 0 in bytes 0..127 of each
     //    row (QJL: the sign octets; prod: aK*K3; mse: the lo parts of aV*V4)
     //    and table 1 = V (aV*V4) in bytes 128..255.
-    //  - NP >= 2 (turbo_prod, turbo_mse): S rows at byte 0 (prod: the
-    //    residual signs, +-1.0; mse: the lo parts of aV*V4; bytes 0..127 of
-    //    each row) and K|V rows at byte kOffKV (K copies: prod aK*K3, mse the
-    //    hi parts aV*V4; V copies aV*V4 at +128).  One address then reads a
-    //    code byte's S pair (offset 0) and its K pair (offset kOffKV, which no
-    //    two-address LDS read merges with 0), each straight into its MFMA
-    //    operand, and a V lookup's address is that of the byte's S row + 128.
-    //    During the setup the S rows' upper halves hold the rotated queries.
-    // After the token loop the K|V rows hold the per-wave results for the
-    // merge.
+    //  - NP >= 2 (turbo_prod, turbo_mse): the layout of decode_table_words,
+    //    S rows at byte 0 and K|V rows at byte kOffKV.  One address then reads
+    //    a code byte's S pair (offset 0) and its K pair (offset kOffKV, which
+    //    no two-address LDS read merges with 0), each straight into its MFMA
+    //    operand, and a V lookup's address is that of the byte's S row + 128
+    //    (turbo_prod's V copies; turbo_mse reads its K copies, + 0).
+    // After the token loop the tables' space holds the per-wave results for
+    // the merge (NP = 1: the K|V rows; NP >= 2: one tile in each half).
     constexpr bool STAB = NP >= 2;
     constexpr int kOffKV = STAB ? 65520 : 0;
     constexpr int kTabWords = STAB ? 32768 : 256 * 64;
     __shared__ __attribute__((aligned(256))) uint32_t lut[kTabWords];
-    __shared__ float qs_sep[STAB ? 1 : kR][128];
+    __shared__ float qs_sep[STAB ? 1 : kR][128];  // NP = 1: the rotated queries
     __shared__ uint4 bqs[NP][4][64];  // QK B operand (fp16 hi/lo q) of k-step s for lane l
     __shared__ uint64_t tko[kWaves][kChunk], tvo[kWaves][kChunk];
     __shared__ float4 tsc[kWaves][kChunk];  // per token: K scale a, residual scale b, vs, bias
     __shared__ float mm[kWaves][kR], ml[kWaves][kR];
-    __shared__ uint32_t kstage[256], vstage[256];
+    __shared__ uint32_t kstage[256], vstage[256];  // NP = 1: the staged table entries
     static_assert(kOffKV + 256 * 256 <= (int)sizeof(lut), "K|V rows");
     static_assert(kOffKV + sizeof(float) * kWaves * kMoRows * 128 <= sizeof(lut), "merge space");
-    static_assert(!STAB || 256 * (kR * 128 / 32) <= kOffKV, "queries in the S rows' upper halves");
     float(*mo)[kMoRows][128] = reinterpret_cast<float(*)[kMoRows][128]>(&lut[kOffKV / 4]);
     // K|V row e (its 64 words: 32 K copies, then 32 V copies)
     auto kv_row = [&](int e) -> uint32_t* { return &lut[kOffKV / 4 + 64 * e]; };
-    // Rotated query element (r, d): STAB: float r*128 + d in the upper half of
-    // S row (r*128 + d) / 32.
-    auto qs_at = [&](int r, int d) -> float& {
-        if constexpr (STAB) {
-            const int f = r * 128 + d;
-            return reinterpret_cast<float*>(&lut[64 * (f >> 5) + 32])[f & 31];
-        } else {
-            return qs_sep[r][d];
-        }
-    };
+    // Rotated query element (r, d) (NP = 1; NP >= 2 writes the B operands
+    // directly)
+    auto qs_at = [&](int r, int d) -> float& { return qs_sep[STAB ? 0 : r][d]; };
 
     // logit scale per unit ks (log2(e) / alpha folded at compile time: no run-time division)
     const float ck = inv * (PROD ? kLog2e / kAlphaK : kLog2e / kAlphaV);
@@ -880,8 +984,9 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
         int t0 = t_begin + w * kChunk;
         const int slot0 = load_slot(t0);
 
-        // Decode tables: one entry per thread into a staging row (waves 0-3).
-        if (w < 4) {
+        // NP = 1: decode tables staged one entry per thread (waves 0-3), then
+        // replicated after the first barrier.
+        if (!STAB && w < 4) {
             const int lo = tid & 15, hi = tid >> 4;
             const float vlo = pick(kV4, lo), vhi = pick(kV4, hi);
             const uint32_t vv = pack_h2(kAlphaV * vlo, kAlphaV * vhi);
@@ -906,6 +1011,38 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
         Chunk cur;
         fetch(t0, slot0, cur);  // in flight during the setup below (empty waves: all invalid)
 
+        const bool lo_col = (i & 1) != 0;  // NP = 1: column i holds row i / 2's hi (even) or lo part
+        if constexpr (STAB) {
+            static_assert(kWaves == 8 && kRows == 8, "eight waves, one row per wave and position");
+            __builtin_amdgcn_sched_barrier(0);  // the first chunk's loads go out before the setup
+            // The decode tables from registers, and each wave's rotated rows
+            // (position k: row w of group rg + k) as fp16 hi and lo parts
+            // straight into the QK B operand: one barrier for the setup.  Lane l
+            // holds d = 2l, 2l + 1: k-group l / 16, k-step (l / 4) % 4, halves
+            // 2(l % 4), + 1 of the half8.  Two or more positions: tile k / 2,
+            // column 8(k % 2) + w, hi in operand 2(k / 2), lo in 2(k / 2) + 1;
+            // one position: tile 0, hi in column w, lo in column w + 8.
+            const TableWords<PROD> tw = decode_table_words<PROD>(w, lane);
+            const int s_l = (lane >> 2) & 3, g_l = lane >> 4;
+#pragma unroll
+            for (int k = 0; k < kQPerWave; ++k) {
+                if (k >= 2 * ntile || (npos == 1 && k > 0)) continue;  // never read (wave-uniform)
+                float q0 = qf[k][0], q1 = qf[k][1];
+                wht_pair<64>(q0, q1, lane);
+                const bool live = k < npos && rg * kRows + w + k * kWaves < num_queries;
+                q0 = live ? q0 * inv : 0.0f;
+                q1 = live ? q1 * inv : 0.0f;
+                const uint32_t hi = pack_h2(q0, q1);
+                const uint32_t lo = lo_pair(q0, q1, hi);
+                const int col_hi = npos == 1 ? w : 8 * (k & 1) + w;
+                const int col_lo = npos == 1 ? w + 8 : col_hi;
+                const int op_hi = npos == 1 ? 0 : 2 * (k >> 1);
+                const int op_lo = npos == 1 ? 0 : op_hi + 1;
+                reinterpret_cast<uint32_t*>(&bqs[op_hi][s_l][16 * g_l + col_hi])[lane & 3] = hi;
+                reinterpret_cast<uint32_t*>(&bqs[op_lo][s_l][16 * g_l + col_lo])[lane & 3] = lo;
+            }
+            store_decode_tables<PROD>(lut, kOffKV / 4, w, lane, tw);
+        } else {
         // Rotated query rows of this group (wave w: rows w, w + NW, ...):
         // qrot = WHT(q * s) * inv.
 #pragma unroll
@@ -925,23 +1062,11 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
             constexpr int kRowsPerWave = 256 / kWaves;
             // (all staged words read before the first store: one LDS round trip)
             uint32_t stv[kRowsPerWave / 4];
-            uint32_t sts[kRowsPerWave / 8];  // STAB: the S entries this lane stores
             if constexpr (!QJL) {
 #pragma unroll
                 for (int k = 0; k < kRowsPerWave; k += 4) {
                     const int e = w * kRowsPerWave + k + (lane >> 4);
-                    // words 32..63: V; mse's K copies hold its hi parts (the V pairs)
-                    stv[k / 4] = (lane & 8) || (STAB && !PROD) ? vstage[e] : kstage[e];
-                }
-                if constexpr (STAB) {
-#pragma unroll
-                    for (int k = 0; k < kRowsPerWave; k += 8) {
-                        const int e = w * kRowsPerWave + k + (lane >> 3);
-                        // prod: the residual signs of the two nibbles (bits 3, 7)
-                        sts[k / 8] = PROD ? ((e & 0x08) ? 0x3C00u : 0xBC00u) |
-                                                ((e & 0x80) ? 0x3C000000u : 0xBC000000u)
-                                          : kstage[e];  // mse: the lo parts
-                    }
+                    stv[k / 4] = (lane & 8) ? vstage[e] : kstage[e];  // words 32..63: V
                 }
             }
 #pragma unroll
@@ -966,38 +1091,18 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                     *reinterpret_cast<uint4*>(kv_row(e) + 4 * (lane & 15)) = make_uint4(v, v, v, v);
                 }
             }
-            if constexpr (STAB) {  // S rows: 8 per store, 8 lanes of 4 copies each
-#pragma unroll
-                for (int k = 0; k < kRowsPerWave; k += 8) {
-                    const int e = w * kRowsPerWave + k + (lane >> 3);
-                    const uint32_t v = sts[k / 8];
-                    *reinterpret_cast<uint4*>(&lut[64 * e + 4 * (lane & 7)]) = make_uint4(v, v, v, v);
-                }
-            }
         }
         // B operand of QK, built once per workgroup: column i = row i/2, hi (i
         // even) or lo (i odd) part; k-index 8*gq + e of step s is d = 32*gq + 8*s + e.
-        const bool lo_col = (i & 1) != 0;
         for (int ps = w; ps < 4 * NP; ps += kWaves) {
             const int p = ps >> 2, s = ps & 3;
-            if (NP >= 2 && (p >> 1) >= ntile) break;  // unused tiles (never read)
             half8 b;
-            if (NP >= 2 && npos == 1) {  // one position: columns (part i / 8, row i % 8)
-                if (p != 0) continue;
 #pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    b[e] = hi_lo(qs_at(i & 7, 32 * gq + 8 * s + e), (i >> 3) != 0);
-            } else if constexpr (NP >= 2) {  // tile p / 2, part p % 2 (hi, lo) of column i's row
-#pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    b[e] = hi_lo(qs_at(16 * (p >> 1) + i, 32 * gq + 8 * s + e), (p & 1) != 0);
-            } else {  // position p, k-step s; column parity picks hi or lo
-#pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    b[e] = hi_lo(qs_at(p * kRows + (i >> 1), 32 * gq + 8 * s + e), lo_col);
-            }
+            for (int e = 0; e < 8; ++e)
+                b[e] = hi_lo(qs_at(p * kRows + (i >> 1), 32 * gq + 8 * s + e), lo_col);
             bqs[p][s][lane] = __builtin_bit_cast(uint4, b);
         }
+        }  // !STAB
         lds_barrier();
         // NP = 1: the B operands in registers; NP >= 2 reads them from LDS per
         // k-step (64 registers fewer in the two-tile loop).
@@ -1372,8 +1477,9 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                         const uint32_t hib = ((we >> 4) & 0x0F0F0F0Fu) | (wo & 0xF0F0F0F0u);
 #pragma unroll
                         for (int b = 0; b < 4; ++b) {
-                            bv[st][2 * b][q] = lds_at(s_addr(lob, b, 128u), kOffKV);
-                            bv[st][2 * b + 1][q] = lds_at(s_addr(hib, b, 128u), kOffKV);
+                            // (turbo_prod: the V copies; turbo_mse: its K copies hold aV*V4)
+                            bv[st][2 * b][q] = lds_at(s_addr(lob, b, PROD ? 128u : 0u), kOffKV);
+                            bv[st][2 * b + 1][q] = lds_at(s_addr(hib, b, PROD ? 128u : 0u), kOffKV);
                         }
                     }
                 __builtin_amdgcn_sched_barrier(0);
@@ -2086,51 +2192,7 @@ __global__ __launch_bounds__(1024) void paged_plan_kernel(
 namespace dec {
 using namespace mfma;
 
-constexpr uint16_t f16_bits(float x) { return __builtin_bit_cast(uint16_t, (_Float16)x); }
-constexpr uint32_t f16_pair(float a, float b) {
-    return (uint32_t)f16_bits(a) | ((uint32_t)f16_bits(b) << 16);
-}
-// (x - fp16(x)) * 2^kLoShift, exact in fp32 (mfma::lo_part at compile time).
-constexpr float lo_part_c(float x) { return (x - (float)(_Float16)x) * (float)(1 << kLoShift); }
-
-// fp16 bits of the codebook values the decode tables hold: aK*K3[j],
-// aV*V4[j], and the lo parts (x - fp16(x)) * 2^kLoShift of aV*V4[j].
-struct Fp16Tables {
-    uint32_t k3[8], v4[16], v4lo[16];
-};
-constexpr Fp16Tables make_fp16_tables() {
-    Fp16Tables t{};
-    for (int j = 0; j < 8; ++j) t.k3[j] = f16_bits(kAlphaK * dev::kK3[j]);
-    for (int j = 0; j < 16; ++j) {
-        t.v4[j] = f16_bits(kAlphaV * dev::kV4[j]);
-        t.v4lo[j] = f16_bits(lo_part_c(kAlphaV * dev::kV4[j]));
-    }
-    return t;
-}
-constexpr Fp16Tables kF16 = make_fp16_tables();
-// The fp16 pair (t[j], t[j + 1]).
-template <int N>
-constexpr uint32_t f16_pair_of(const uint32_t (&t)[N], int j) {
-    return t[j] | (t[j + 1] << 16);
-}
-// Selector of entry g < 4 of a 4-entry fp16 table held as two fp16 pairs:
-// bytes 2g, 2g + 1, then zeros.
-__device__ __forceinline__ uint32_t lut4_sel(int g) {
-    return (uint32_t)(2 * g) | ((uint32_t)(2 * g + 1) << 8) | 0x0C0C0000u;
-}
-// t[4m + g] (in the low half) for the 4-entry slice m of t, g given by sel.
-template <int N>
-__device__ __forceinline__ uint32_t lut4(const uint32_t (&t)[N], int m, uint32_t sel) {
-    return __builtin_amdgcn_perm(f16_pair_of(t, 4 * m + 2), f16_pair_of(t, 4 * m), sel);
-}
-// fp16 pairs of the table entries for code byte b (low nibble = even d):
-//   K table: turbo_prod (aK*K3[b & 7], aK*K3[(b >> 4) & 7]); turbo_mse the hi
-//            parts fp16(aV*V4[b & 15]), fp16(aV*V4[b >> 4]) (its V pairs too);
-//   S table: turbo_prod the residual signs (nibble bit 3 set: +1.0, else
-//            -1.0); turbo_mse the lo parts of aV*V4;
-//   V table (turbo_prod): (aV*V4[b & 15], aV*V4[b >> 4]).
-
-// LDS layout of the tables (32 copies of each entry, copy c at 4c; lane l
+// LDS layout of the tables (entries as decode_table_words describes) (32 copies of each entry, copy c at 4c; lane l
 // reads copy l % 32, so a half-wave's random lookups hit distinct banks):
 //   S table: byte 256b + 4c (the rows' upper halves unused: the table ends
 //   below kOffK);
@@ -2264,51 +2326,8 @@ __global__ __launch_bounds__(64 * kWaves) void attn_decode_split_kernel(
     __builtin_amdgcn_sched_barrier(0);  // the code loads go out before any setup work
 
     // The tables' words, computed in registers while the codes are in flight
-    // (no memory traffic).  Each 16-byte store writes four copies; a store
-    // instruction covers whole rows (128 or 256 bytes per 8 or 16 lanes).
-    // With the rows a wave writes, one nibble of every entry is the same
-    // across the wave (a scalar) and the other comes from a 4-entry fp16 table
-    // by v_perm.
-    //   S table, and turbo_mse's K table: store k < 4 of wave w writes row
-    //     32w + 8k + lane / 8, copies 4q .. 4q + 3 (q = lane % 8): low nibble
-    //     8(k % 2) + lane / 8, high nibble 2w + k / 2;
-    //   turbo_prod's K | V rows: store k < 8 writes row 32w + 4k + lane / 16,
-    //     group lane % 16 (K copies, then V copies): low nibble
-    //     4(k % 4) + lane / 16, high nibble 2w + k / 4.
-    constexpr int kR1Stores = PROD ? 8 : 4;
-    uint32_t r0[4], r1[kR1Stores];
-    {
-        const int g4 = lane >> 4, g8 = lane >> 3;
-        const uint32_t sel4 = lut4_sel(g4), sel8 = lut4_sel(g8 & 3);
-        const bool hi8 = (g8 & 4) != 0;
-        if constexpr (PROD) {
-            const uint32_t sh = (w & 4) ? 0x3C000000u : 0xBC000000u;  // row bit 7 = w bit 2
-#pragma unroll
-            for (int k = 0; k < 4; ++k) r0[k] = ((k & 1) ? 0x3C00u : 0xBC00u) | sh;  // row bit 3
-            const bool vq = (lane & 8) != 0;
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const uint32_t vpair =
-                    lut4(kF16.v4, k & 3, sel4) | (kF16.v4[2 * w + (k >> 2)] << 16);
-                const uint32_t kpair =
-                    lut4(kF16.k3, k & 1, sel4) | (kF16.k3[(2 * w + (k >> 2)) & 7] << 16);
-                r1[k] = vq ? vpair : kpair;
-            }
-        } else {
-            uint32_t llo[2], vlo[2];
-#pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                llo[hh] = hi8 ? lut4(kF16.v4lo, 2 * hh + 1, sel8) : lut4(kF16.v4lo, 2 * hh, sel8);
-                vlo[hh] = hi8 ? lut4(kF16.v4, 2 * hh + 1, sel8) : lut4(kF16.v4, 2 * hh, sel8);
-            }
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                r0[k] = llo[k & 1] | (kF16.v4lo[2 * w + (k >> 1)] << 16);
-                r1[k] = vlo[k & 1] | (kF16.v4[2 * w + (k >> 1)] << 16);
-            }
-        }
-    }
-
+    // (no memory traffic; each 16-byte store writes four copies).
+    const TableWords<PROD> tw = decode_table_words<PROD>(w, lane);
     // 3. This wave's query row: qrot = WHT(q * s) * inv, stored as fp16 hi
     //    and lo parts into the B operand (column 2w: hi, 2w + 1: lo; lane l
     //    holds d = 2l, 2l + 1: k-group l / 16, k-step (l / 4) % 4, halves
@@ -2327,17 +2346,7 @@ __global__ __launch_bounds__(64 * kWaves) void attn_decode_split_kernel(
         b[4 + (lane & 3)] = lo;  // the next lane's (column 2w + 1) half8
     }
     // 4. The decode tables.
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-        *reinterpret_cast<u32x4*>(&lut[(32 * w + 8 * k + (lane >> 3)) * 64 + 4 * (lane & 7)]) =
-            (u32x4){r0[k], r0[k], r0[k], r0[k]};
-#pragma unroll
-    for (int k = 0; k < kR1Stores; ++k) {
-        const int row = PROD ? 32 * w + 4 * k + (lane >> 4) : 32 * w + 8 * k + (lane >> 3);
-        const int q = PROD ? lane & 15 : lane & 7;
-        *reinterpret_cast<u32x4*>(&lut[kOffK / 4 + row * 64 + 4 * q]) =
-            (u32x4){r1[k], r1[k], r1[k], r1[k]};
-    }
+    store_decode_tables<PROD>(lut, kOffK / 4, w, lane, tw);
     lds_barrier();
     half8 bq[4];
 #pragma unroll
