@@ -1439,11 +1439,15 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                             cb[t][tau] = mma(o.a[tau], o.bk[2 * t], cb[t][tau]);
                             if (!COLS) cb[t][tau] = mma(o.a[tau], o.bk[2 * t + 1], cb[t][tau]);
                         }
-                        // prod: the +-1 residual signs; mse: the lo parts (into cs)
+                        // prod: the +-1 residual signs against the hi and lo query;
+                        // mse: the codebook's lo parts (into cs) against the hi query
+                        // only: the product of the two lo parts, each below 2^-11
+                        // of its value, is ~2^-22 of the logit
 #pragma unroll
                         for (int t = 0; t < NTA; ++t) {
                             cs[t][tau] = mma(o.al[tau], o.bk[2 * t], cs[t][tau]);
-                            if (!COLS) cs[t][tau] = mma(o.al[tau], o.bk[2 * t + 1], cs[t][tau]);
+                            if (!COLS && PROD)
+                                cs[t][tau] = mma(o.al[tau], o.bk[2 * t + 1], cs[t][tau]);
                         }
                     }
                     __builtin_amdgcn_sched_barrier(0);
