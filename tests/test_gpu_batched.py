@@ -158,15 +158,20 @@ def test_paged_over_a_thousand_row_groups(tq, cuda):
     ("turbo_prod", 2, 64, 16),
     ("turbo_mse", 2, 64, 16),
     ("turbo_mse", 4, 32, 5),
+    # aligned pages, D = 128: the matrix-core kernel
+    ("turbo_prod", 2, 128, 16),
+    ("turbo_mse", 2, 128, 16),
+    ("turbo_prod", 8, 128, 32),
 ])
-def test_paged_generic_geometries(tq, oracle, cuda, scheme, H, D, B):
+def test_paged_geometries(tq, oracle, cuda, scheme, H, D, B):
     """Geometries the matrix-core kernel does not take (unaligned pages, head
     dims other than 128) run on the generic split-K decode through the block
-    table: every row against the fp64 oracle over its sequence's first
-    row_kv_len tokens; a row of kv length 0 gives 0 and a row whose length
-    passes max_kv_len attends max_kv_len tokens."""
+    table, the others on the matrix-core kernel: every row against the fp64
+    oracle over its sequence's first row_kv_len tokens; a row of kv length 0
+    gives 0 and a row whose length passes max_kv_len attends max_kv_len tokens,
+    those past its sequence's pages unmapped (masked)."""
     lens, widths = [900, 33, 1500], [2, 1, 3]
-    print(f"[paged generic {scheme}] H={H} D={D} B={B}", flush=True)
+    print(f"[paged geometry {scheme}] H={H} D={D} B={B}", flush=True)
     b = PagedBatch(tq, scheme, lens, widths, kv_heads=H, q_heads=8 * H, head_dim=D,
                    block_size=B, seed=560, device=cuda)
     b.append_new_tokens(seed=561)
