@@ -811,6 +811,23 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
         int rowlen[NP] = {}, gend[NP] = {}, gmin[NP] = {};
         // NP >= 2: this lane's column row length per tile and the shortest live row
         int rl_col[NT] = {}, gmin_live = 0x7fffffff;
+        // This wave's query rows (row r of the workgroup is row r % 8 of group
+        // rg + r / 8: rows rg * 8 + r), loaded before anything waits: paged rows
+        // issue them right after the row lengths and the sequence, so the
+        // length processing waits only for those (the vector-memory counter is
+        // in order) while the queries are in flight.
+        constexpr int kQPerWave = kR / kWaves;
+        static_assert(kR % kWaves == 0, "rows per wave");
+        uint32_t qraw[kQPerWave];
+        auto load_queries = [&]() {
+#pragma unroll
+            for (int k = 0; k < kQPerWave; ++k) {
+                const int qi = min(rg * kRows + w + k * kWaves, num_queries - 1);
+                qraw[k] = *reinterpret_cast<const uint32_t*>(query + ((size_t)qi * g.H + h) * 128 +
+                                                              2 * lane);
+            }
+        };
+        if constexpr (!PAGED) load_queries();
         if constexpr (PAGED) {
             kv_end = 0;
             // Every row length and the sequence are loaded unconditionally (rows
@@ -821,6 +838,8 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
             for (int p = 0; p < NP; ++p)
                 lraw[p] = pr.row_kv_len[min((rg + p) * kRows + (lane & 7), num_queries - 1)];
             const int seq_raw = pr.row_seq[rg * kRows];
+            load_queries();
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int p = 0; p < NP; ++p) {
                 const int rr = (rg + p) * kRows + (lane & 7);
@@ -840,7 +859,9 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                 if (p < npos) gmin_live = min(gmin_live, gmin[p]);
             }
             seq = __builtin_amdgcn_readfirstlane(seq_raw);
-            if (t_begin >= kv_end) return;  // uniform over the workgroup, before any barrier
+            // (a piece always starts below its unit's kv end: the walk calls
+            // this only for work positions below ceil(kv_end / pass); a piece
+            // past every row would run no chunk and write no partial)
         }
         const int t_end = min(kv_end, t_cap);
         const int ntile = (npos + 1) >> 1;  // NP >= 2: tiles of 16 columns in use
@@ -967,20 +988,9 @@ __global__ __launch_bounds__(64 * NW) void attn_mfma_split_kernel(
                 }
         };
 
-        // Issue order matters (the vector-memory counter is in order): query
-        // rows first, then the first chunk's slots; the decode tables are built
-        // while they are in flight.
-        constexpr int kQPerWave = kR / kWaves;
-        static_assert(kR % kWaves == 0, "rows per wave");
-        // Row r of the workgroup is row r % 8 of group rg + r / 8 (consecutive
-        // groups: rows rg * 8 + r).
-        uint32_t qraw[kQPerWave];
-#pragma unroll
-        for (int k = 0; k < kQPerWave; ++k) {
-            const int qi = min(rg * kRows + w + k * kWaves, num_queries - 1);
-            qraw[k] = *reinterpret_cast<const uint32_t*>(query + ((size_t)qi * g.H + h) * 128 +
-                                                          2 * lane);
-        }
+        // Issue order matters (the vector-memory counter is in order): the
+        // query rows (above), then the first chunk's slots; the decode tables
+        // are built while they are in flight.
         int t0 = t_begin + w * kChunk;
         const int slot0 = load_slot(t0);
 
